@@ -1,0 +1,134 @@
+/* qne: MI355X (gfx950) decode engine for the Qwen3.5 hybrid decoder.
+ *
+ * C ABI that replaces the `kernels` crate's `Model` (kernels/src/model.rs) of
+ * arlinamid/qwen-native-engine. Plain pointers and sizes only. Every call returns 0 on success or a
+ * negative QNE_E* code; qne_last_error() then holds a human-readable message (thread-local). No
+ * exception and no allocation crosses the boundary except the opaque model handle, which only
+ * qne_model_free releases. A model has a single owner: calls on one handle must not overlap.
+ *
+ * Every entry point cites the reference interface it replaces (file:line in the reference repo).
+ */
+#ifndef QNE_H
+#define QNE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define QNE_OK 0
+#define QNE_EINVAL (-1)      /* bad argument (empty prompt, short buffer, ...) */
+#define QNE_ECONTEXT (-2)    /* position or prompt beyond the KV-cache capacity */
+#define QNE_ENOSNAPSHOT (-3) /* restore before snapshot */
+#define QNE_EDEVICE (-4)     /* HIP error, no device, or device wait timeout */
+#define QNE_EFORMAT (-5)     /* index.json / weights.bin rejected by validation */
+
+typedef struct qne_model qne_model;
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* qne_last_error(void);
+
+/* Model::load(index_json, weights, tiles, allow_f16, dxc) -- kernels/src/model.rs:171.
+ * Parses and validates index.json (format_version 1 or 2) against the weights blob before any
+ * device work, then copies the tensors to HBM (tensors with the same (offset, bytes) are uploaded
+ * once, model.rs:185-194). The caller may free `weights` after the call returns.
+ * `options_json` (nullable) replaces the reference's tile profile and flags; recognised keys:
+ *   "max_context" (default 4096, the reference's MAX_CONTEXT), "device" (HIP ordinal, default 0).
+ * A reference tile-profile object (ModelTiles, model.rs:90-98) is accepted and ignored: kernel
+ * shapes here are chosen per matrix at load. `allow_f16` is accepted for signature parity. */
+int qne_model_load(const char* index_json, size_t index_len, const void* weights, size_t weights_len,
+                   const char* options_json, int allow_f16, qne_model** out);
+/* drop(Model) */
+int qne_model_free(qne_model* m);
+
+/* Model::reset -- model.rs:314. Zeroes recurrent, conv and KV state. */
+int qne_reset(qne_model* m);
+/* Model::prefill -- model.rs:324. Token-by-token from position 0 with the full graph.
+ * QNE_EINVAL if n == 0, QNE_ECONTEXT if n >= max_context. */
+int qne_prefill(qne_model* m, const uint32_t* ids, size_t n);
+/* Model::prefill_chunk -- model.rs:349 (prefill_batched / prefill_from are start = 0 /
+ * finish_logits = 1 forms, model.rs:339-346). Continues the state at `start`. With
+ * finish_logits, computes the logits after the last id and the greedy pick (last_token).
+ * QNE_EINVAL if n == 0, QNE_ECONTEXT if start + n >= max_context. */
+int qne_prefill_chunk(qne_model* m, const uint32_t* ids, size_t n, uint32_t start, int finish_logits);
+/* Model::logits -- model.rs:374. Copies vocab floats; QNE_EINVAL if cap < vocab. */
+int qne_logits(qne_model* m, float* out, size_t cap);
+/* Model::step -- model.rs:380. Feeds `token` at `pos`, writes vocab logits; does not update the
+ * greedy pick. QNE_ECONTEXT if pos >= max_context. */
+int qne_step(qne_model* m, uint32_t token, uint32_t pos, float* out, size_t cap);
+/* Model::snapshot / Model::restore -- model.rs:395, 406. restore: QNE_ENOSNAPSHOT before any
+ * snapshot ("no snapshot taken"). */
+int qne_snapshot(qne_model* m);
+int qne_restore(qne_model* m);
+/* Model::last_token -- model.rs:417: (greedy id, next position). */
+int qne_last_token(qne_model* m, uint32_t* token, uint32_t* next_pos);
+/* Model::decode -- model.rs:426. Greedy decode of up to n ids, `window` steps per submission.
+ * out[0] is last_token(); each later id is fed back on the device. Unlike the reference, every id
+ * of a window is returned (no u32::MAX placeholders). Stops after the first id found in `stop`;
+ * with window > 1 the state may have advanced past it, as in the reference. *len = ids written.
+ * QNE_ECONTEXT if next_pos + steps would exceed max_context. */
+int qne_decode(qne_model* m, size_t n, uint32_t window, const uint32_t* stop, size_t nstop,
+               uint32_t* out, size_t cap, size_t* len);
+/* Model::dispatches_per_token -- model.rs:309 (kernel launches per decode token). */
+int qne_dispatches_per_token(qne_model* m, size_t* out);
+/* Model.adapter -- model.rs:167: device name, written NUL-terminated into buf. */
+int qne_adapter(qne_model* m, char* buf, size_t cap);
+/* VOCAB / shaders::MAX_CONTEXT -- kernels/src/lib.rs:21, kernels/src/shaders.rs:34. */
+int qne_vocab(qne_model* m, uint32_t* out);
+int qne_max_context(qne_model* m, uint32_t* out);
+/* Model::profile_token -- model.rs:305: device time of one decode token in ms (event-timed,
+ * consumes one greedy token like the reference). */
+int qne_profile_token(qne_model* m, double* ms);
+
+/* ---- kernel-level entry points (device pointers; the reference exposes these only through its
+ * in-binary checks, kernels/src/lib.rs:513-712, and microbenches, lib.rs:714-963) ---- */
+
+/* Matrix encodings of a device matrix. */
+#define QNE_MAT_F16 0 /* w: f16 [rows][k] */
+#define QNE_MAT_Q4 1  /* w: u32 [rows][k/8] nibbles; sz: f16 pairs (scale, zero) [rows][k/group] */
+#define QNE_EPI_STORE 0
+#define QNE_EPI_ACCUMULATE 1
+#define QNE_EPI_SWIGLU 2
+
+/* gemv / gemv_f16 / gemv_split_f16 + split_reduce -- kernels/src/shaders.rs:45-376, launched by
+ * Gpu::gemv, lib.rs:311-338. y = W x with the Store / Accumulate / SwiGlu epilogue. If `norm` is
+ * non-null, x is first replaced by rmsnorm(x) * norm (shaders.rs:378-403 fused as a prologue).
+ * `rows` counts matrix rows (2 * outputs for SwiGlu). stream = 0 is the null stream. */
+int qne_gemv(int kind, const void* w, const void* sz, int rows, int k, int group, const float* x,
+             const float* norm, float eps, float* y, int epilogue, void* stream);
+/* Repack host q4 data into the device layout used by qne_gemv: sz[r][g] = (scale, zero). */
+int qne_pack_sz_q4g(const uint16_t* scales, const uint16_t* zeros, size_t n, uint16_t* sz);
+/* The gated delta rule alone (kernels/src/shaders.rs:498-512) for `batch` sequences x `heads`
+ * heads, dk = dv = 128: per (b,h) q,k [dk], v [dv], beta, g -> state [dk][dv] updated in place,
+ * out [dv] = S'^T q. q and k are used as given (already normalised). */
+int qne_gdn_step(const float* q, const float* k, const float* v, const float* beta, const float* g,
+                 float* state, float* out, int batch, int heads, void* stream);
+/* The same recurrence over T tokens per sequence (batch.rs:166-255 semantics), computed in
+ * chunks of 64 tokens: q,k [B][T][H][dk], v/out [B][T][H][dv], beta/g [B][T][H]. */
+int qne_gdn_prefill_chunked(const float* q, const float* k, const float* v, const float* beta,
+                            const float* g, float* state, float* out, int batch, int tokens,
+                            int heads, void* stream);
+/* Paged KV decode for `batch` sequences (kernels/src/shaders.rs:522-633 generalised): appends one
+ * token's k,v (f16) per sequence at position ctx[b], then attends q over positions 0..ctx[b].
+ * Pools are [num_blocks][nkv][16][hd] f16; block_table [batch][max_blocks] (int32);
+ * q/out [batch][nq][hd] f32, k_new/v_new [batch][nkv][hd] f32. hd = 256. scale = 1/sqrt(hd). */
+int qne_paged_attn_decode(const float* q, const float* k_new, const float* v_new, void* k_pool,
+                          void* v_pool, const int32_t* block_table, int max_blocks,
+                          const int32_t* ctx, float* out, int batch, int nq, int nkv,
+                          void* stream);
+
+/* ---- synthetic weights (seeded generator used by the benches and tests) ---- */
+/* value[i] = std * N(0,1) from SplitMix64 + Box-Muller on a counter keyed by (seed, stream). */
+int qne_synth_normal_f32(uint64_t seed, uint64_t stream, size_t n, float std, float* out);
+int qne_synth_normal_f16(uint64_t seed, uint64_t stream, size_t n, float std, uint16_t* out);
+/* Asymmetric min/max int4 quantisation with f16 scale and f16 zero per `group` values along each
+ * row: w ~ (q - z) * s. Writes nibbles (u32 [rows][k/8]), scales and zeros ([rows][k/group]). */
+int qne_quantize_q4g(const float* w, size_t rows, size_t k, size_t group, uint32_t* q,
+                     uint16_t* scales, uint16_t* zeros);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,247 @@
+// extern "C" boundary (include/qne.h): every call catches, maps the error to a return code and
+// keeps the message for qne_last_error().
+#include <hip/hip_runtime.h>
+
+#include <cstring>
+#include <new>
+#include <string>
+
+#include "../../include/qne.h"
+#include "error.hpp"
+#include "hip_util.hpp"
+#include "index.hpp"
+#include "kernels/launch.hpp"
+#include "model.hpp"
+
+struct qne_model {
+    qne::Model* m;
+};
+
+namespace {
+thread_local std::string g_last_error;
+
+template <typename F>
+int guard(F&& f) {
+    try {
+        f();
+        g_last_error.clear();
+        return QNE_OK;
+    } catch (const qne::Error& e) {
+        g_last_error = e.what();
+        return e.code;
+    } catch (const std::bad_alloc&) {
+        g_last_error = "out of host memory";
+        return QNE_EDEVICE;
+    } catch (const std::exception& e) {
+        g_last_error = e.what();
+        return QNE_EINVAL;
+    } catch (...) {
+        g_last_error = "unknown error";
+        return QNE_EINVAL;
+    }
+}
+
+qne::Model& model(qne_model* m) {
+    if (!m || !m->m) throw qne::Error(QNE_EINVAL, "null model handle");
+    return *m->m;
+}
+
+void need(bool ok, const char* what) {
+    if (!ok) throw qne::Error(QNE_EINVAL, what);
+}
+
+void check_launch() { qne::hip_check(hipGetLastError(), "kernel launch"); }
+}  // namespace
+
+extern "C" {
+
+const char* qne_last_error(void) { return g_last_error.c_str(); }
+
+int qne_model_load(const char* index_json, size_t index_len, const void* weights, size_t weights_len,
+                   const char* options_json, int allow_f16, qne_model** out) {
+    (void)allow_f16;
+    return guard([&] {
+        need(index_json && out, "null argument");
+        need(weights || weights_len == 0, "null weights");
+        *out = nullptr;
+        // Validate everything before any device work (model.rs:172-174).
+        qne::ModelIndex ix = qne::parse_index(index_json, index_len, weights_len);
+        qne::LoadOptions opt = qne::parse_options(options_json);
+        qne::Model* m = new qne::Model(ix, (const uint8_t*)weights, weights_len, opt);
+        *out = new qne_model{m};
+    });
+}
+
+int qne_model_free(qne_model* m) {
+    return guard([&] {
+        if (!m) return;
+        delete m->m;
+        delete m;
+    });
+}
+
+int qne_reset(qne_model* m) { return guard([&] { model(m).reset(); }); }
+
+int qne_prefill(qne_model* m, const uint32_t* ids, size_t n) {
+    return guard([&] {
+        need(ids || n == 0, "null ids");
+        model(m).prefill(ids, n);
+    });
+}
+
+int qne_prefill_chunk(qne_model* m, const uint32_t* ids, size_t n, uint32_t start, int finish_logits) {
+    return guard([&] {
+        need(ids || n == 0, "null ids");
+        model(m).prefill_chunk(ids, n, start, finish_logits != 0);
+    });
+}
+
+int qne_logits(qne_model* m, float* out, size_t cap) {
+    return guard([&] {
+        need(out != nullptr, "null output");
+        model(m).logits(out, cap);
+    });
+}
+
+int qne_step(qne_model* m, uint32_t token, uint32_t pos, float* out, size_t cap) {
+    return guard([&] {
+        need(out != nullptr, "null output");
+        model(m).step(token, pos, out, cap);
+    });
+}
+
+int qne_snapshot(qne_model* m) { return guard([&] { model(m).snapshot(); }); }
+int qne_restore(qne_model* m) { return guard([&] { model(m).restore(); }); }
+
+int qne_last_token(qne_model* m, uint32_t* token, uint32_t* next_pos) {
+    return guard([&] {
+        need(token && next_pos, "null output");
+        model(m).last_token(token, next_pos);
+    });
+}
+
+int qne_decode(qne_model* m, size_t n, uint32_t window, const uint32_t* stop, size_t nstop, uint32_t* out, size_t cap,
+               size_t* len) {
+    return guard([&] {
+        need(len != nullptr && (out || n == 0), "null output");
+        need(stop || nstop == 0, "null stop list");
+        *len = model(m).decode(n, window, stop, nstop, out, cap);
+    });
+}
+
+int qne_dispatches_per_token(qne_model* m, size_t* out) {
+    return guard([&] {
+        need(out != nullptr, "null output");
+        *out = model(m).dispatches_per_token();
+    });
+}
+
+int qne_adapter(qne_model* m, char* buf, size_t cap) {
+    return guard([&] {
+        need(buf && cap > 0, "null output");
+        const std::string& a = model(m).adapter();
+        need(cap > a.size(), "buffer too small");
+        std::memcpy(buf, a.c_str(), a.size() + 1);
+    });
+}
+
+int qne_vocab(qne_model* m, uint32_t* out) {
+    return guard([&] {
+        need(out != nullptr, "null output");
+        *out = model(m).vocab();
+    });
+}
+
+int qne_max_context(qne_model* m, uint32_t* out) {
+    return guard([&] {
+        need(out != nullptr, "null output");
+        *out = model(m).max_context();
+    });
+}
+
+int qne_profile_token(qne_model* m, double* ms) {
+    return guard([&] {
+        need(ms != nullptr, "null output");
+        *ms = model(m).profile_token();
+    });
+}
+
+// ---- kernel-level entry points ----
+
+int qne_gemv(int kind, const void* w, const void* sz, int rows, int k, int group, const float* x, const float* norm,
+             float eps, float* y, int epilogue, void* stream) {
+    return guard([&] {
+        need(kind == QNE_MAT_F16 || kind == QNE_MAT_Q4, "unknown matrix kind");
+        need(w && x && y && rows > 0, "null or empty argument");
+        need(kind == QNE_MAT_F16 || sz, "q4 needs sz");
+        need(epilogue >= QNE_EPI_STORE && epilogue <= QNE_EPI_SWIGLU, "unknown epilogue");
+        need(epilogue != QNE_EPI_SWIGLU || rows % 2 == 0, "SwiGlu needs an even row count");
+        need(qne::gemv_k_supported(k), "unsupported k");
+        need(kind == QNE_MAT_F16 || group == 32 || group == 64 || group == 128, "unsupported group");
+        qne::ArgmaxOut none;
+        if (!qne::launch_gemv(kind, w, (const uint32_t*)sz, rows, k, group, x, norm, eps, y, epilogue, none,
+                              (hipStream_t)stream))
+            throw qne::Error(QNE_EINVAL, "no kernel for this shape");
+        check_launch();
+    });
+}
+
+int qne_pack_sz_q4g(const uint16_t* scales, const uint16_t* zeros, size_t n, uint16_t* sz) {
+    return guard([&] {
+        need(scales && zeros && sz, "null argument");
+        for (size_t i = 0; i < n; i++) {
+            sz[2 * i] = scales[i];
+            sz[2 * i + 1] = zeros[i];
+        }
+    });
+}
+
+int qne_gdn_step(const float* q, const float* k, const float* v, const float* beta, const float* g, float* state,
+                 float* out, int batch, int heads, void* stream) {
+    return guard([&] {
+        need(q && k && v && beta && g && state && out, "null argument");
+        need(batch > 0 && heads > 0 && batch <= 65535 && heads <= 65535, "bad batch or heads");
+        qne::launch_delta_rule(q, k, v, beta, g, state, out, batch, heads, (hipStream_t)stream);
+        check_launch();
+    });
+}
+
+int qne_gdn_prefill_chunked(const float* q, const float* k, const float* v, const float* beta, const float* g,
+                            float* state, float* out, int batch, int tokens, int heads, void* stream) {
+    return guard([&] {
+        need(q && k && v && beta && g && state && out, "null argument");
+        need(batch > 0 && heads > 0 && tokens > 0 && batch <= 65535 && heads <= 65535, "bad sizes");
+        qne::launch_delta_rule_chunked(q, k, v, beta, g, state, out, batch, tokens, heads, (hipStream_t)stream);
+        check_launch();
+    });
+}
+
+int qne_paged_attn_decode(const float* q, const float* k_new, const float* v_new, void* k_pool, void* v_pool,
+                          const int32_t* block_table, int max_blocks, const int32_t* ctx, float* out, int batch,
+                          int nq, int nkv, void* stream) {
+    return guard([&] {
+        need(q && k_new && v_new && k_pool && v_pool && block_table && ctx && out, "null argument");
+        need(batch > 0 && batch <= 65535 && nkv > 0 && nq % nkv == 0, "bad batch or heads");
+        const int G = nq / nkv;
+        need(G == 1 || G == 2 || G == 4, "nq/nkv must be 1, 2 or 4");
+        need(max_blocks > 0, "max_blocks must be positive");
+        // Split-context partials: enough workgroups to cover the chip at small batch.
+        int splits = 256 / (nkv * batch);
+        if (splits < 1) splits = 1;
+        if (splits > max_blocks) splits = max_blocks;
+        const size_t parts = (size_t)batch * nkv * splits * G;
+        float* ml = nullptr;
+        float* acc = nullptr;
+        hipStream_t st = (hipStream_t)stream;
+        QNE_HIP(hipMallocAsync((void**)&ml, parts * 2 * 4, st));
+        QNE_HIP(hipMallocAsync((void**)&acc, parts * 256 * 4, st));
+        qne::launch_paged_attn(q, k_new, v_new, (uint16_t*)k_pool, (uint16_t*)v_pool, block_table, max_blocks, ctx,
+                               out, batch, nq, nkv, ml, acc, splits, st);
+        hipError_t e = hipGetLastError();
+        (void)hipFreeAsync(ml, st);
+        (void)hipFreeAsync(acc, st);
+        qne::hip_check(e, "kernel launch");
+    });
+}
+
+}  // extern "C"

@@ -1,0 +1,196 @@
+// Gated DeltaNet kernels (dk = dv = 128).
+//
+// Reference: the decode step `gdn` (kernels/src/shaders.rs:436-520) and the chunk kernel `gdn_b`
+// (kernels/src/batch.rs:166-255). Design for gfx950: one 512-thread workgroup per (sequence,
+// head); thread (column t, quarter q) owns the 32 state values S[32q .. 32q+31][t] in VGPRs, so
+// the 64 KiB state tile of a head is read once and written once per launch, with each wave
+// touching 256 contiguous bytes per load. S^T k and S^T q are 32-term register dot products
+// merged across quarters through LDS. The multi-token kernel keeps the tile in registers across
+// all tokens of the launch.
+#include "common.hpp"
+#include "launch.hpp"
+
+namespace qne {
+
+constexpr int kDK = 128, kDV = 128, kGdnThreads = 512;
+
+struct DeltaShared {
+    float q[kDK], k[kDK], v[kDV];
+    float part[2][4][kDV];
+    float dv[kDV];
+    float red[16];
+    float kq, g, beta;
+};
+
+// One token of the delta rule on the register tile. Inputs q, k, v, g, beta in `sh`
+// (synchronised by the caller). Returns out[col] = g S^T q + dv (k.q) in quarter-0 threads.
+__device__ __forceinline__ float delta_token(float (&s)[32], DeltaShared& sh, int col, int qq) {
+    const float g = sh.g, beta = sh.beta;
+    float sk = 0.0f, sq = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 32; i++) {
+        sk = fmaf(s[i], sh.k[32 * qq + i], sk);
+        sq = fmaf(s[i], sh.q[32 * qq + i], sq);
+    }
+    sh.part[0][qq][col] = sk;
+    sh.part[1][qq][col] = sq;
+    __syncthreads();
+    float out = 0.0f;
+    if (qq == 0) {
+        sk = sh.part[0][0][col] + sh.part[0][1][col] + sh.part[0][2][col] + sh.part[0][3][col];
+        sq = sh.part[1][0][col] + sh.part[1][1][col] + sh.part[1][2][col] + sh.part[1][3][col];
+        const float d = beta * (sh.v[col] - g * sk);
+        sh.dv[col] = d;
+        out = g * sq + d * sh.kq;
+    }
+    __syncthreads();
+    const float d = sh.dv[col];
+#pragma unroll
+    for (int i = 0; i < 32; i++) s[i] = fmaf(g, s[i], d * sh.k[32 * qq + i]);
+    return out;
+}
+
+__device__ __forceinline__ void load_tile(float (&s)[32], const float* S, int col, int qq) {
+#pragma unroll
+    for (int i = 0; i < 32; i++) s[i] = S[(32 * qq + i) * kDV + col];
+}
+__device__ __forceinline__ void store_tile(const float (&s)[32], float* S, int col, int qq) {
+#pragma unroll
+    for (int i = 0; i < 32; i++) S[(32 * qq + i) * kDV + col] = s[i];
+}
+
+// Model decode step for head blockIdx.x: conv + SiLU on the head's q, k, v channels, L2 norms,
+// gates, delta rule, gated RMSNorm (shaders.rs:436-520).
+// proj = [q(H*dk) k(H*dk) v(H*dv) z(H*dv) a(H) b(H)], prm = [dt_bias(H) A_neg_exp(H) norm_w(dv)].
+__global__ __launch_bounds__(kGdnThreads) void k_gdn_decode(const float* __restrict__ proj, float* __restrict__ conv_state,
+                                                            const float* __restrict__ conv_w, float* __restrict__ state,
+                                                            float* __restrict__ out, const float* __restrict__ prm, int H) {
+    __shared__ DeltaShared sh;
+    const int h = blockIdx.x, t = threadIdx.x, lane = t % kWave, w = t / kWave;
+    const int col = t & (kDV - 1), qq = t >> 7;
+    float* S = state + (size_t)h * kDK * kDV;
+    float s[32];
+    load_tile(s, S, col, qq);  // in flight while the conv runs
+
+    float val = 0.0f;
+    if (t < 384) {
+        const int ch = t < 128 ? h * kDK + t : (t < 256 ? H * kDK + h * kDK + (t - 128) : 2 * H * kDK + h * kDV + (t - 256));
+        const float x = proj[ch];
+        float* st = conv_state + (size_t)ch * 3;
+        const float* cw = conv_w + (size_t)ch * 4;
+        const float s0 = st[0], s1 = st[1], s2 = st[2];
+        const float y = s0 * cw[0] + s1 * cw[1] + s2 * cw[2] + x * cw[3];
+        st[0] = s1; st[1] = s2; st[2] = x;
+        val = silu(y);
+    }
+    const float ss = wave_sum(val * val);
+    if (lane == 0) sh.red[w] = ss;
+    __syncthreads();
+    if (t < 128) sh.q[t] = val * (1.0f / sqrtf(sh.red[0] + sh.red[1] + 1e-6f)) * 0.08838834764831845f;
+    else if (t < 256) sh.k[t - 128] = val * (1.0f / sqrtf(sh.red[2] + sh.red[3] + 1e-6f));
+    else if (t < 384) sh.v[t - 256] = val;
+    if (t == 0) {
+        const int zoff = 2 * H * kDK + 2 * H * kDV;  // a[H] then b[H] follow z
+        const float a = proj[zoff + h], b = proj[zoff + H + h];
+        sh.g = expf(prm[H + h] * logf(1.0f + expf(a + prm[h])));
+        sh.beta = 1.0f / (1.0f + expf(-b));
+    }
+    __syncthreads();
+    if (w == 0) {
+        float p = sh.k[lane] * sh.q[lane] + sh.k[lane + 64] * sh.q[lane + 64];
+        p = wave_sum(p);
+        if (lane == 0) sh.kq = p;
+    }
+    __syncthreads();
+    const float o = delta_token(s, sh, col, qq);
+    store_tile(s, S, col, qq);
+    // gated RMSNorm over the head's dv outputs (quarter 0 = waves 0 and 1)
+    const float oo = wave_sum(o * o);
+    __syncthreads();
+    if (lane == 0) sh.red[w] = oo;
+    __syncthreads();
+    if (qq == 0) {
+        const float inv = 1.0f / sqrtf((sh.red[0] + sh.red[1]) / (float)kDV + 1e-6f);
+        const float z = proj[2 * H * kDK + H * kDV + h * kDV + col];
+        out[h * kDV + col] = o * inv * silu(z) * prm[2 * H + col];
+    }
+}
+
+// The bare delta rule for one token of sequence blockIdx.y, head blockIdx.x.
+__global__ __launch_bounds__(kGdnThreads) void k_delta_rule(const float* __restrict__ q, const float* __restrict__ k,
+                                                            const float* __restrict__ v, const float* __restrict__ beta,
+                                                            const float* __restrict__ g, float* __restrict__ state,
+                                                            float* __restrict__ out, int H) {
+    __shared__ DeltaShared sh;
+    const int h = blockIdx.x, b = blockIdx.y, t = threadIdx.x, lane = t % kWave, w = t / kWave;
+    const int col = t & (kDV - 1), qq = t >> 7;
+    const size_t bh = (size_t)b * H + h;
+    float* S = state + bh * kDK * kDV;
+    float s[32];
+    load_tile(s, S, col, qq);
+    if (t < 128) sh.q[t] = q[bh * kDK + t];
+    else if (t < 256) sh.k[t - 128] = k[bh * kDK + t - 128];
+    else if (t < 384) sh.v[t - 256] = v[bh * kDV + t - 256];
+    if (t == 0) { sh.g = g[bh]; sh.beta = beta[bh]; }
+    __syncthreads();
+    if (w == 0) {
+        float p = sh.k[lane] * sh.q[lane] + sh.k[lane + 64] * sh.q[lane + 64];
+        p = wave_sum(p);
+        if (lane == 0) sh.kq = p;
+    }
+    __syncthreads();
+    const float o = delta_token(s, sh, col, qq);
+    store_tile(s, S, col, qq);
+    if (qq == 0) out[bh * kDV + col] = o;
+}
+
+// The delta rule over `tokens` tokens of sequence blockIdx.y, head blockIdx.x, state in VGPRs
+// for the whole launch. Layouts: q,k [B][T][H][dk], v,out [B][T][H][dv], beta,g [B][T][H].
+__global__ __launch_bounds__(kGdnThreads) void k_delta_rule_seq(const float* __restrict__ q, const float* __restrict__ k,
+                                                                const float* __restrict__ v, const float* __restrict__ beta,
+                                                                const float* __restrict__ g, float* __restrict__ state,
+                                                                float* __restrict__ out, int T, int H) {
+    __shared__ DeltaShared sh;
+    const int h = blockIdx.x, b = blockIdx.y, t = threadIdx.x, lane = t % kWave, w = t / kWave;
+    const int col = t & (kDV - 1), qq = t >> 7;
+    float* S = state + ((size_t)b * H + h) * kDK * kDV;
+    float s[32];
+    load_tile(s, S, col, qq);
+    for (int n = 0; n < T; n++) {
+        const size_t bth = ((size_t)b * T + n) * H + h;
+        __syncthreads();  // previous token's readers of sh are done
+        if (t < 128) sh.q[t] = q[bth * kDK + t];
+        else if (t < 256) sh.k[t - 128] = k[bth * kDK + t - 128];
+        else if (t < 384) sh.v[t - 256] = v[bth * kDV + t - 256];
+        if (t == 0) { sh.g = g[bth]; sh.beta = beta[bth]; }
+        __syncthreads();
+        if (w == 0) {
+            float p = sh.k[lane] * sh.q[lane] + sh.k[lane + 64] * sh.q[lane + 64];
+            p = wave_sum(p);
+            if (lane == 0) sh.kq = p;
+        }
+        __syncthreads();
+        const float o = delta_token(s, sh, col, qq);
+        if (qq == 0) out[bth * kDV + col] = o;
+    }
+    store_tile(s, S, col, qq);
+}
+
+void launch_gdn_decode(const float* proj, float* conv_state, const float* conv_w, float* state, float* out,
+                       const float* prm, int heads, hipStream_t st) {
+    hipLaunchKernelGGL(k_gdn_decode, dim3(heads), dim3(kGdnThreads), 0, st, proj, conv_state, conv_w, state, out, prm,
+                       heads);
+}
+
+void launch_delta_rule(const float* q, const float* k, const float* v, const float* beta, const float* g, float* state,
+                       float* out, int batch, int heads, hipStream_t st) {
+    hipLaunchKernelGGL(k_delta_rule, dim3(heads, batch), dim3(kGdnThreads), 0, st, q, k, v, beta, g, state, out, heads);
+}
+
+void launch_delta_rule_chunked(const float* q, const float* k, const float* v, const float* beta, const float* g,
+                               float* state, float* out, int batch, int tokens, int heads, hipStream_t st) {
+    hipLaunchKernelGGL(k_delta_rule_seq, dim3(heads, batch), dim3(kGdnThreads), 0, st, q, k, v, beta, g, state, out,
+                       tokens, heads);
+}
+
+}  // namespace qne

@@ -1,0 +1,473 @@
+// Model: load, state, per-token graph and the prefill / step / decode protocol of
+// kernels/src/model.rs, on HIP.
+#include "model.hpp"
+
+#include <chrono>
+#include <cmath>
+#include <cstring>
+#include <map>
+#include <thread>
+
+#include "error.hpp"
+#include "hip_util.hpp"
+#include "json.hpp"
+#include "kernels/launch.hpp"
+
+namespace qne {
+
+void wait_stream(hipStream_t st, double timeout_s) {
+    using clk = std::chrono::steady_clock;
+    const auto start = clk::now();
+    int spins = 0;
+    while (true) {
+        hipError_t e = hipStreamQuery(st);
+        if (e == hipSuccess) return;
+        if (e != hipErrorNotReady) hip_check(e, "hipStreamQuery");
+        if (++spins > 2000) std::this_thread::sleep_for(std::chrono::microseconds(50));
+        if (std::chrono::duration<double>(clk::now() - start).count() > timeout_s)
+            throw Error(QNE_EDEVICE, "GPU wait failed: timed out after 30 s");
+    }
+}
+
+LoadOptions parse_options(const char* json) {
+    LoadOptions o;
+    if (!json || !*json) return o;
+    Json j = Json::parse(json, std::strlen(json));
+    if (j.type != Json::Object) throw Error(QNE_EINVAL, "options must be a JSON object");
+    if (j.has("max_context")) {
+        uint64_t v = j.at("max_context").u64("max_context");
+        if (v < 16 || v > (1u << 22)) throw Error(QNE_EINVAL, "max_context must be 16..4194304");
+        o.max_context = (int)v;
+    }
+    if (j.has("device")) o.device = (int)j.at("device").u64("device");
+    return o;
+}
+
+static float f16_to_f32_host(uint16_t h) {
+    uint32_t sign = (uint32_t)(h & 0x8000u) << 16, e = (h >> 10) & 0x1fu, f = h & 0x3ffu, bits;
+    if (e == 0) {
+        float v = (float)f * 5.9604644775390625e-8f;
+        return (h & 0x8000u) ? -v : v;
+    }
+    bits = e == 31 ? (sign | 0x7f800000u | (f << 13)) : (sign | ((e + 112u) << 23) | (f << 13));
+    float out;
+    std::memcpy(&out, &bits, 4);
+    return out;
+}
+
+static uint16_t small_int_to_f16(unsigned v) {  // exact for 0..15
+    if (v == 0) return 0;
+    int e = 0;
+    while ((v >> (e + 1)) != 0) e++;
+    unsigned frac = (v << (10 - e)) & 0x3ffu;
+    return (uint16_t)(((unsigned)(e + 15) << 10) | frac);
+}
+
+void* Model::dalloc(size_t bytes) {
+    void* p = nullptr;
+    QNE_HIP(hipMalloc(&p, bytes ? bytes : 16));
+    allocations_.push_back(p);
+    return p;
+}
+
+Model::Model(const ModelIndex& ix, const uint8_t* weights, uint64_t /*wlen*/, const LoadOptions& opt)
+    : cfg_(ix.cfg), max_context_(opt.max_context), device_(opt.device) {
+    int count = 0;
+    if (hipGetDeviceCount(&count) != hipSuccess || count == 0) throw Error(QNE_EDEVICE, "no GPU adapter");
+    if (device_ >= count) throw Error(QNE_EDEVICE, "device ordinal out of range");
+    QNE_HIP(hipSetDevice(device_));
+    hipDeviceProp_t prop;
+    QNE_HIP(hipGetDeviceProperties(&prop, device_));
+    adapter_ = std::string(prop.name) + " (" + prop.gcnArchName + ", " + std::to_string(prop.multiProcessorCount) +
+               " CUs) via HIP";
+    QNE_HIP(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking));
+    try {
+        upload(ix, weights);
+        alloc_state();
+        build_graphs();
+    } catch (...) {
+        release();
+        throw;
+    }
+}
+
+Model::~Model() { release(); }
+
+void Model::release() {
+    if (device_ >= 0) (void)hipSetDevice(device_);
+    if (stream_) (void)hipStreamSynchronize(stream_);
+    for (hipGraphExec_t g : {g_layers_, g_head_logits_, g_head_greedy_})
+        if (g) (void)hipGraphExecDestroy(g);
+    g_layers_ = g_head_logits_ = g_head_greedy_ = nullptr;
+    for (void* p : allocations_) (void)hipFree(p);
+    allocations_.clear();
+    if (host_tok_) (void)hipHostFree(host_tok_);
+    if (host_logits_) (void)hipHostFree(host_logits_);
+    if (host_ids_) (void)hipHostFree(host_ids_);
+    host_tok_ = nullptr; host_logits_ = nullptr; host_ids_ = nullptr;
+    if (stream_) (void)hipStreamDestroy(stream_);
+    stream_ = nullptr;
+}
+
+// Copies every tensor to HBM once. Tensors with the same (offset, bytes) share one upload, as in
+// model.rs:185-194 (tied embedding / LM head). q4 scales and zeros are interleaved per group.
+void Model::upload(const ModelIndex& ix, const uint8_t* weights) {
+    std::map<std::pair<uint64_t, uint64_t>, void*> seen;
+    auto raw = [&](const TensorRef& t) -> void* {
+        auto key = std::make_pair(t.offset, t.bytes);
+        auto it = seen.find(key);
+        if (it != seen.end()) return it->second;
+        void* d = dalloc(t.bytes);
+        QNE_HIP(hipMemcpy(d, weights + t.offset, t.bytes, hipMemcpyHostToDevice));
+        seen[key] = d;
+        return d;
+    };
+    std::map<std::pair<uint64_t, uint64_t>, uint32_t*> seen_sz;
+    auto mat = [&](const std::string& name) -> DevMat {
+        const MatInfo& m = ix.mat(name);
+        DevMat d;
+        d.kind = m.kind;
+        d.rows = m.rows;
+        d.k = m.k;
+        d.group = m.group ? m.group : 64;
+        d.w = raw(m.w);
+        if (m.kind == MAT_Q4) {
+            auto key = std::make_pair(m.s.offset, m.z.offset);
+            auto it = seen_sz.find(key);
+            if (it != seen_sz.end()) {
+                d.sz = it->second;
+            } else {
+                const size_t groups_per_row = (size_t)m.k / m.group, n = (size_t)m.rows * groups_per_row;
+                std::vector<uint32_t> sz(n);
+                const uint16_t* s = (const uint16_t*)(weights + m.s.offset);
+                for (size_t r = 0; r < (size_t)m.rows; r++) {
+                    for (size_t g = 0; g < groups_per_row; g++) {
+                        const size_t i = r * groups_per_row + g;
+                        uint16_t z16;
+                        if (m.zero_u4) {
+                            const uint8_t* z = weights + m.z.offset + r * ((groups_per_row + 1) / 2);
+                            z16 = small_int_to_f16((z[g / 2] >> (4 * (g % 2))) & 15u);
+                        } else {
+                            z16 = ((const uint16_t*)(weights + m.z.offset))[i];
+                        }
+                        uint16_t s16;
+                        std::memcpy(&s16, s + i, 2);
+                        sz[i] = (uint32_t)s16 | ((uint32_t)z16 << 16);
+                    }
+                }
+                uint32_t* dsz = (uint32_t*)dalloc(n * 4);
+                QNE_HIP(hipMemcpy(dsz, sz.data(), n * 4, hipMemcpyHostToDevice));
+                seen_sz[key] = dsz;
+                d.sz = dsz;
+            }
+        }
+        return d;
+    };
+    embed_ = mat("embed");
+    lm_head_ = mat("lm_head");
+    final_norm_ = (const float*)raw(ix.tensor("final_norm"));
+    layers_.resize(cfg_.layers);
+    for (int i = 0; i < cfg_.layers; i++) {
+        const std::string p = "layer" + std::to_string(i) + ".";
+        DevLayer& L = layers_[i];
+        L.attn = cfg_.is_attn(i);
+        L.input_norm = (const float*)raw(ix.tensor(p + "input_norm"));
+        L.post_norm = (const float*)raw(ix.tensor(p + "post_norm"));
+        L.in = mat(p + "mixer_in");
+        L.out = mat(p + "mixer_out");
+        L.gate_up = mat(p + "gate_up");
+        L.down = mat(p + "down");
+        if (L.attn) {
+            L.norms = (const float*)raw(ix.tensor(p + "attn_norms"));
+        } else {
+            L.conv_w = (const float*)raw(ix.tensor(p + "conv_w"));
+            L.gdn_params = (const float*)raw(ix.tensor(p + "gdn_params"));
+        }
+    }
+    (void)f16_to_f32_host;
+}
+
+void Model::alloc_state() {
+    const ModelConfig& c = cfg_;
+    const size_t conv_b = (size_t)c.conv_channels() * (c.conv_kernel - 1) * 4;
+    const size_t rec_b = (size_t)c.gdn_heads * c.gdn_dk * c.gdn_dv * 4;
+    const int blocks = (max_context_ + 15) / 16;
+    const size_t pool_b = (size_t)blocks * c.n_kv_heads * 16 * c.head_dim * 2;
+    size_t total = 0;
+    for (const DevLayer& L : layers_) total += L.attn ? 2 * pool_b : conv_b + rec_b;
+    state_bytes_ = total;
+    state_ = dalloc(total);
+    uint8_t* p = (uint8_t*)state_;
+    for (DevLayer& L : layers_) {
+        if (L.attn) {
+            L.k_pool = (uint16_t*)p; p += pool_b;
+            L.v_pool = (uint16_t*)p; p += pool_b;
+        } else {
+            L.conv_state = (float*)p; p += conv_b;
+            L.rec = (float*)p; p += rec_b;
+        }
+    }
+    QNE_HIP(hipMemset(state_, 0, state_bytes_));
+
+    // Block table of the single sequence: a fixed permutation of the pool, so the decode path
+    // always goes through the same paged addressing as batched serving.
+    std::vector<int32_t> bt(blocks);
+    for (int i = 0; i < blocks; i++) bt[i] = i;
+    uint64_t x = 0x9E3779B97F4A7C15ull;
+    for (int i = blocks - 1; i > 0; i--) {
+        x ^= x << 13; x ^= x >> 7; x ^= x << 17;
+        std::swap(bt[i], bt[x % (uint64_t)(i + 1)]);
+    }
+    block_table_ = (int32_t*)dalloc(blocks * 4);
+    QNE_HIP(hipMemcpy(block_table_, bt.data(), blocks * 4, hipMemcpyHostToDevice));
+
+    size_t proj = (size_t)std::max(c.attn_proj(), c.gdn_proj());
+    size_t mixed = (size_t)std::max(c.attn_out(), c.gdn_out());
+    h_ = (float*)dalloc((size_t)c.hidden * 4);
+    proj_ = (float*)dalloc(proj * 4);
+    mixed_ = (float*)dalloc(mixed * 4);
+    act_ = (float*)dalloc((size_t)c.intermediate * 4);
+    logits_ = (float*)dalloc((size_t)c.vocab * 4);
+    qbuf_ = (float*)dalloc((size_t)c.n_q_heads * c.head_dim * 4);
+    // split-context partials: about 256 workgroups per attention layer
+    attn_splits_ = std::max(1, std::min(256 / c.n_kv_heads, (max_context_ + 15) / 16));
+    const size_t G = (size_t)(c.n_q_heads / c.n_kv_heads);
+    part_ml_ = (float*)dalloc((size_t)c.n_kv_heads * attn_splits_ * G * 2 * 4);
+    part_acc_ = (float*)dalloc((size_t)c.n_kv_heads * attn_splits_ * G * c.head_dim * 4);
+    am_val_ = (float*)dalloc(kArgmaxMaxBlocks * 4);
+    am_idx_ = (uint32_t*)dalloc(kArgmaxMaxBlocks * 4);
+    am_counter_ = (unsigned*)dalloc(64);
+    QNE_HIP(hipMemset(am_counter_, 0, 64));
+    tok_ = (uint32_t*)dalloc(16);
+    tok_backup_ = (uint32_t*)dalloc(16);
+    QNE_HIP(hipMemset(tok_, 0, 16));
+    ids_ = (uint32_t*)dalloc((size_t)max_context_ * 4);
+    out_ids_ = (uint32_t*)dalloc((size_t)max_context_ * 4);
+    std::vector<float> inv((size_t)c.rope_dim / 2);
+    for (int i = 0; i < c.rope_dim / 2; i++) inv[i] = (float)std::pow(c.rope_theta, -(double)(2 * i) / (double)c.rope_dim);
+    inv_freq_ = (float*)dalloc(inv.size() * 4);
+    QNE_HIP(hipMemcpy(inv_freq_, inv.data(), inv.size() * 4, hipMemcpyHostToDevice));
+    QNE_HIP(hipHostMalloc((void**)&host_tok_, 64, hipHostMallocDefault));
+    QNE_HIP(hipHostMalloc((void**)&host_logits_, (size_t)c.vocab * 4, hipHostMallocDefault));
+    QNE_HIP(hipHostMalloc((void**)&host_ids_, (size_t)max_context_ * 4, hipHostMallocDefault));
+}
+
+static void gemv_or_throw(const DevMat& m, const float* x, const float* gain, float eps, float* y, int epi,
+                          const ArgmaxOut& am, hipStream_t st) {
+    if (!launch_gemv(m.kind, m.w, m.sz, m.rows, m.k, m.group, x, gain, eps, y, epi, am, st))
+        throw Error(QNE_EFORMAT, "no GEMV kernel for k=" + std::to_string(m.k));
+}
+
+// One token through the layers (model.rs:220-262): the embedding row of tok[0], then per layer
+// RMSNorm -> mixer_in -> GDN | attention -> mixer_out (+=) -> RMSNorm -> gate_up (SwiGLU) ->
+// down (+=). The RMSNorms are fused into the GEMV that consumes them.
+void Model::enqueue_layers() {
+    const ModelConfig& c = cfg_;
+    ArgmaxOut none;
+    launch_embed(embed_.kind, embed_.w, embed_.sz, embed_.group, c.hidden, tok_, h_, stream_);
+    launches_++;
+    for (const DevLayer& L : layers_) {
+        gemv_or_throw(L.in, h_, L.input_norm, c.eps, proj_, EPI_STORE, none, stream_);
+        launches_++;
+        if (L.attn) {
+            AttnModelArgs a;
+            a.proj = proj_; a.norms = L.norms; a.inv_freq = inv_freq_;
+            a.k_pool = L.k_pool; a.v_pool = L.v_pool; a.block_table = block_table_; a.tok = tok_;
+            a.qbuf = qbuf_; a.part_ml = part_ml_; a.part_acc = part_acc_; a.out = mixed_;
+            a.nq = c.n_q_heads; a.nkv = c.n_kv_heads; a.rope_dim = c.rope_dim; a.splits = attn_splits_;
+            launch_attention_model(a, stream_);
+            launches_ += 3;
+        } else {
+            launch_gdn_decode(proj_, L.conv_state, L.conv_w, L.rec, mixed_, L.gdn_params, c.gdn_heads, stream_);
+            launches_++;
+        }
+        gemv_or_throw(L.out, mixed_, nullptr, c.eps, h_, EPI_ACCUMULATE, none, stream_);
+        gemv_or_throw(L.gate_up, h_, L.post_norm, c.eps, act_, EPI_SWIGLU, none, stream_);
+        gemv_or_throw(L.down, act_, nullptr, c.eps, h_, EPI_ACCUMULATE, none, stream_);
+        launches_ += 3;
+    }
+}
+
+// Final RMSNorm + LM head (model.rs:264-269); `greedy` adds the device argmax that feeds tok.
+void Model::enqueue_head(bool greedy) {
+    ArgmaxOut am;
+    if (greedy) {
+        am.part_val = am_val_; am.part_idx = am_idx_; am.counter = am_counter_; am.tok = tok_;
+        am.ids = out_ids_; am.ids_cap = (uint32_t)max_context_;
+    }
+    gemv_or_throw(lm_head_, h_, final_norm_, cfg_.eps, logits_, greedy ? EPI_ARGMAX : EPI_STORE, am, stream_);
+    launches_++;
+}
+
+void Model::build_graphs() {
+    auto capture = [&](auto&& body) -> hipGraphExec_t {
+        hipGraph_t g = nullptr;
+        hipGraphExec_t e = nullptr;
+        QNE_HIP(hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal));
+        try {
+            body();
+        } catch (...) {
+            (void)hipStreamEndCapture(stream_, &g);
+            if (g) (void)hipGraphDestroy(g);
+            throw;
+        }
+        QNE_HIP(hipStreamEndCapture(stream_, &g));
+        QNE_HIP(hipGraphInstantiate(&e, g, nullptr, nullptr, 0));
+        (void)hipGraphDestroy(g);
+        return e;
+    };
+    launches_ = 0;
+    g_layers_ = capture([&] { enqueue_layers(); });
+    g_head_logits_ = capture([&] { enqueue_head(false); });
+    const size_t before = launches_;
+    g_head_greedy_ = capture([&] { enqueue_head(true); });
+    dispatches_ = (before - 1) + (launches_ - before);  // layers + greedy head
+    QNE_HIP(hipStreamSynchronize(stream_));
+}
+
+void Model::sync() { wait_stream(stream_); }
+
+void Model::set_tok(uint32_t token, uint32_t pos) {
+    host_tok_[0] = token;
+    host_tok_[1] = pos;
+    host_tok_[2] = 0;
+    host_tok_[3] = 0;
+    QNE_HIP(hipMemcpyAsync(tok_, host_tok_, 16, hipMemcpyHostToDevice, stream_));
+}
+
+void Model::run_layers_graph() { QNE_HIP(hipGraphLaunch(g_layers_, stream_)); }
+void Model::run_head_graph(bool greedy) { QNE_HIP(hipGraphLaunch(greedy ? g_head_greedy_ : g_head_logits_, stream_)); }
+
+void Model::reset() {
+    QNE_HIP(hipMemsetAsync(state_, 0, state_bytes_, stream_));
+    sync();
+}
+
+// model.rs:324-334: every prompt token through the whole graph, positions from 0.
+void Model::prefill(const uint32_t* ids, size_t n) {
+    if (n == 0 || n >= (size_t)max_context_)
+        throw Error(n == 0 ? QNE_EINVAL : QNE_ECONTEXT, "prompt length must be 1.." + std::to_string(max_context_));
+    std::memcpy(host_ids_, ids, n * 4);
+    QNE_HIP(hipMemcpyAsync(ids_, host_ids_, n * 4, hipMemcpyHostToDevice, stream_));
+    for (size_t i = 0; i < n; i++) {
+        launch_set_tok(tok_, ids_, (int)i, (uint32_t)i, stream_);
+        run_layers_graph();
+        run_head_graph(true);
+    }
+    sync();
+}
+
+// model.rs:349-372: continues the state at `start`; with finish_logits, the logits and greedy
+// pick after the last token (tok = [pick, start + n]). Without it, tok is left as it was.
+void Model::prefill_chunk(const uint32_t* ids, size_t n, uint32_t start, bool finish_logits) {
+    if (n == 0 || (uint64_t)start + n >= (uint64_t)max_context_)
+        throw Error(n == 0 ? QNE_EINVAL : QNE_ECONTEXT,
+                    "context limit: " + std::to_string(start) + " + " + std::to_string(n) + " tokens does not fit in " +
+                        std::to_string(max_context_));
+    std::memcpy(host_ids_, ids, n * 4);
+    QNE_HIP(hipMemcpyAsync(ids_, host_ids_, n * 4, hipMemcpyHostToDevice, stream_));
+    if (!finish_logits) QNE_HIP(hipMemcpyAsync(tok_backup_, tok_, 16, hipMemcpyDeviceToDevice, stream_));
+    for (size_t i = 0; i < n; i++) {
+        launch_set_tok(tok_, ids_, (int)i, start + (uint32_t)i, stream_);
+        run_layers_graph();
+    }
+    if (finish_logits) run_head_graph(true);
+    else QNE_HIP(hipMemcpyAsync(tok_, tok_backup_, 16, hipMemcpyDeviceToDevice, stream_));
+    sync();
+}
+
+void Model::logits(float* out, size_t cap) {
+    if (cap < (size_t)cfg_.vocab) throw Error(QNE_EINVAL, "logits buffer smaller than the vocabulary");
+    QNE_HIP(hipMemcpyAsync(host_logits_, logits_, (size_t)cfg_.vocab * 4, hipMemcpyDeviceToHost, stream_));
+    sync();
+    std::memcpy(out, host_logits_, (size_t)cfg_.vocab * 4);
+}
+
+// model.rs:380-392: host sampling owns the next token, so no device argmax.
+void Model::step(uint32_t token, uint32_t pos, float* out, size_t cap) {
+    if (pos >= (uint32_t)max_context_)
+        throw Error(QNE_ECONTEXT, "context limit of " + std::to_string(max_context_) + " tokens reached");
+    if (cap < (size_t)cfg_.vocab) throw Error(QNE_EINVAL, "logits buffer smaller than the vocabulary");
+    if (token >= (uint32_t)cfg_.vocab) throw Error(QNE_EINVAL, "token id outside the vocabulary");
+    set_tok(token, pos);
+    run_layers_graph();
+    run_head_graph(false);
+    QNE_HIP(hipMemcpyAsync(host_logits_, logits_, (size_t)cfg_.vocab * 4, hipMemcpyDeviceToHost, stream_));
+    sync();
+    std::memcpy(out, host_logits_, (size_t)cfg_.vocab * 4);
+}
+
+// model.rs:395-414: device copies of all recurrent, conv and KV state.
+void Model::snapshot() {
+    if (!saved_) saved_ = dalloc(state_bytes_);
+    QNE_HIP(hipMemcpyAsync(saved_, state_, state_bytes_, hipMemcpyDeviceToDevice, stream_));
+    sync();
+}
+
+void Model::restore() {
+    if (!saved_) throw Error(QNE_ENOSNAPSHOT, "no snapshot taken");
+    QNE_HIP(hipMemcpyAsync(state_, saved_, state_bytes_, hipMemcpyDeviceToDevice, stream_));
+    sync();
+}
+
+void Model::last_token(uint32_t* token, uint32_t* next_pos) {
+    QNE_HIP(hipMemcpyAsync(host_tok_ + 4, tok_, 16, hipMemcpyDeviceToHost, stream_));
+    sync();
+    *token = host_tok_[4];
+    *next_pos = host_tok_[5];
+}
+
+// model.rs:426-449, GPU-resident greedy loop. Each step's pick is also appended on the device,
+// so a window returns every id.
+size_t Model::decode(size_t n, uint32_t window, const uint32_t* stop, size_t nstop, uint32_t* out, size_t cap) {
+    if (window == 0) throw Error(QNE_EINVAL, "window must be >= 1");
+    if (cap < 1 || (n > 0 && cap < n)) throw Error(QNE_EINVAL, "output buffer smaller than n");
+    if (n == 0) return 0;
+    uint32_t first, next_pos;
+    last_token(&first, &next_pos);
+    size_t len = 0;
+    out[len++] = first;
+    auto is_stop = [&](uint32_t id) {
+        for (size_t i = 0; i < nstop; i++)
+            if (stop[i] == id) return true;
+        return false;
+    };
+    while (len < n && !is_stop(out[len - 1])) {
+        const uint32_t steps = (uint32_t)std::min<size_t>(window, n - len);
+        if ((uint64_t)next_pos + steps > (uint64_t)max_context_)
+            throw Error(QNE_ECONTEXT, "context limit of " + std::to_string(max_context_) + " tokens reached after " +
+                                          std::to_string(len) + " generated tokens");
+        next_pos += steps;
+        // tok[2] counts the ids appended on the device during this window
+        QNE_HIP(hipMemsetAsync(tok_ + 2, 0, 4, stream_));
+        for (uint32_t s = 0; s < steps; s++) {
+            run_layers_graph();
+            run_head_graph(true);
+        }
+        QNE_HIP(hipMemcpyAsync(host_ids_, out_ids_, (size_t)steps * 4, hipMemcpyDeviceToHost, stream_));
+        sync();
+        for (uint32_t s = 0; s < steps && len < n; s++) {
+            out[len++] = host_ids_[s];
+            if (is_stop(out[len - 1])) break;
+        }
+    }
+    return len;
+}
+
+double Model::profile_token() {
+    hipEvent_t a, b;
+    QNE_HIP(hipEventCreate(&a));
+    QNE_HIP(hipEventCreate(&b));
+    QNE_HIP(hipEventRecord(a, stream_));
+    run_layers_graph();
+    run_head_graph(true);
+    QNE_HIP(hipEventRecord(b, stream_));
+    sync();
+    float ms = 0.0f;
+    QNE_HIP(hipEventElapsedTime(&ms, a, b));
+    (void)hipEventDestroy(a);
+    (void)hipEventDestroy(b);
+    return ms;
+}
+
+}  // namespace qne

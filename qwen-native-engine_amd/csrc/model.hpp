@@ -1,0 +1,110 @@
+// The decoder behind the C ABI: the `Model` of kernels/src/model.rs rebuilt on HIP for MI355X.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <string>
+#include <vector>
+
+#include "index.hpp"
+
+namespace qne {
+
+struct DevMat {
+    int kind = 0;  // 0 f16, 1 q4
+    int rows = 0, k = 0, group = 64;
+    const void* w = nullptr;
+    const uint32_t* sz = nullptr;  // q4: (scale, zero) f16 pairs per group
+};
+
+struct DevLayer {
+    bool attn = false;
+    DevMat in, out, gate_up, down;
+    const float* input_norm = nullptr;
+    const float* post_norm = nullptr;
+    const float* norms = nullptr;       // attention: q_norm, k_norm
+    const float* conv_w = nullptr;      // GDN
+    const float* gdn_params = nullptr;  // GDN
+    float* conv_state = nullptr;
+    float* rec = nullptr;
+    uint16_t* k_pool = nullptr;
+    uint16_t* v_pool = nullptr;
+};
+
+struct LoadOptions {
+    int max_context = 4096;
+    int device = 0;
+};
+
+LoadOptions parse_options(const char* json);
+
+class Model {
+  public:
+    Model(const ModelIndex& ix, const uint8_t* weights, uint64_t wlen, const LoadOptions& opt);
+    ~Model();
+    Model(const Model&) = delete;
+    Model& operator=(const Model&) = delete;
+
+    void reset();
+    void prefill(const uint32_t* ids, size_t n);
+    void prefill_chunk(const uint32_t* ids, size_t n, uint32_t start, bool finish_logits);
+    void logits(float* out, size_t cap);
+    void step(uint32_t token, uint32_t pos, float* out, size_t cap);
+    void snapshot();
+    void restore();
+    void last_token(uint32_t* token, uint32_t* next_pos);
+    size_t decode(size_t n, uint32_t window, const uint32_t* stop, size_t nstop, uint32_t* out, size_t cap);
+    double profile_token();
+
+    size_t dispatches_per_token() const { return dispatches_; }
+    const std::string& adapter() const { return adapter_; }
+    uint32_t vocab() const { return (uint32_t)cfg_.vocab; }
+    uint32_t max_context() const { return (uint32_t)max_context_; }
+
+  private:
+    void release();
+    void upload(const ModelIndex& ix, const uint8_t* weights);
+    void alloc_state();
+    void build_graphs();
+    void enqueue_layers();
+    void enqueue_head(bool greedy);
+    void set_tok(uint32_t token, uint32_t pos);
+    void run_layers_graph();
+    void run_head_graph(bool greedy);
+    void sync();
+    void* dalloc(size_t bytes);
+
+    ModelConfig cfg_;
+    int max_context_ = 4096;
+    int device_ = 0;
+    hipStream_t stream_ = nullptr;
+    std::string adapter_;
+    std::vector<void*> allocations_;
+
+    DevMat embed_, lm_head_;
+    const float* final_norm_ = nullptr;
+    std::vector<DevLayer> layers_;
+
+    // state (cleared by reset, copied by snapshot)
+    void* state_ = nullptr;
+    size_t state_bytes_ = 0;
+    void* saved_ = nullptr;
+
+    // activations and bookkeeping
+    float *h_ = nullptr, *proj_ = nullptr, *mixed_ = nullptr, *act_ = nullptr, *logits_ = nullptr, *qbuf_ = nullptr;
+    float *part_ml_ = nullptr, *part_acc_ = nullptr, *am_val_ = nullptr, *inv_freq_ = nullptr;
+    uint32_t *am_idx_ = nullptr, *tok_ = nullptr, *tok_backup_ = nullptr, *ids_ = nullptr, *out_ids_ = nullptr;
+    unsigned* am_counter_ = nullptr;
+    int32_t* block_table_ = nullptr;
+    int attn_splits_ = 1;
+    uint32_t* host_tok_ = nullptr;  // pinned
+    float* host_logits_ = nullptr;  // pinned
+    uint32_t* host_ids_ = nullptr;  // pinned
+
+    hipGraphExec_t g_layers_ = nullptr, g_head_logits_ = nullptr, g_head_greedy_ = nullptr;
+    size_t dispatches_ = 0;
+    size_t launches_ = 0;  // kernel launches counted while recording
+};
+
+}  // namespace qne

@@ -1,0 +1,185 @@
+"""The Model API (include/qne.h, mirroring kernels/src/model.rs) on the GPU against the oracle.
+
+Bar (BASELINE parity target): max |logit error| <= 1e-2 and identical greedy ids; the kernels are
+f32-accumulating, so the logits are expected far closer than that (checked at 1e-3 here)."""
+import numpy as np
+import pytest
+
+import cpu_oracle as O
+import qne as Q
+import weights as W
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module", params=[("tiny", "q4", "f16"), ("tiny", "f16", "q4"), ("small", "q4", "f16")],
+                ids=["tiny-q4body", "tiny-f16body-q4head", "small-q4body"])
+def pair(request):
+    name, body, head = request.param
+    index, buf = W.synth_model(name, seed=11, body=body, head=head, norm_jitter=0.1)
+    m = Q.Model.load(index, buf)
+    om = O.OracleModel(index, buf, "f64")
+    yield name, m, om, index, buf
+    m.close()
+
+
+def prompt(vocab, n, seed):
+    return np.random.default_rng(seed).integers(0, vocab, size=n).astype(np.uint32)
+
+
+def test_prefill_logits_and_greedy_decode(pair):
+    name, m, om, _, _ = pair
+    ids = prompt(m.vocab, 40, 1)
+    m.reset()
+    om.reset()
+    m.prefill_batched(ids)
+    want = om.prefill_chunk(ids, 0, True)
+    got = m.logits()
+    assert np.max(np.abs(got - want)) < 1e-3
+    first, pos = m.last_token()
+    assert first == int(np.argmax(want)) and pos == len(ids)
+    steps = 64
+    out = m.decode(steps, 1, [])
+    om.reset()
+    want_ids, want_logits = om.greedy(ids, steps)
+    assert out == want_ids
+
+
+def test_decode_window_returns_every_id(pair):
+    name, m, om, _, _ = pair
+    ids = prompt(m.vocab, 9, 2)
+    m.reset()
+    m.prefill_batched(ids)
+    w1 = m.decode(20, 1, [])
+    m.reset()
+    m.prefill_batched(ids)
+    w8 = m.decode(20, 8, [])
+    assert w1 == w8 and len(w8) == 20
+
+
+def test_decode_stops_at_stop_token(pair):
+    name, m, om, _, _ = pair
+    ids = prompt(m.vocab, 7, 3)
+    m.reset()
+    m.prefill_batched(ids)
+    full = m.decode(12, 1, [])
+    stop = full[5]
+    m.reset()
+    m.prefill_batched(ids)
+    cut = m.decode(12, 1, [stop])
+    assert cut == full[: full.index(stop) + 1]
+
+
+def test_step_returns_logits_and_leaves_the_greedy_pick(pair):
+    name, m, om, _, _ = pair
+    ids = prompt(m.vocab, 12, 4)
+    m.reset()
+    om.reset()
+    m.prefill_batched(ids)
+    om.prefill_chunk(ids, 0, True)
+    got = m.step(5, len(ids))
+    want = om.token(5, len(ids))
+    assert np.max(np.abs(got - want)) < 1e-3
+    assert m.last_token() == (5, len(ids))  # step does not run the device argmax (model.rs:386-387)
+
+
+def test_token_prefill_equals_chunked_prefill(pair):
+    name, m, om, _, _ = pair
+    ids = prompt(m.vocab, 33, 5)
+    m.reset()
+    m.prefill(ids)
+    a = m.logits()
+    ta = m.last_token()
+    m.reset()
+    m.prefill_chunk(ids[:20], 0, False)
+    m.prefill_chunk(ids[20:], 20, True)
+    b = m.logits()
+    assert np.array_equal(a, b) and ta == m.last_token()
+
+
+def test_snapshot_restore_and_reset(pair):
+    name, m, om, _, _ = pair
+    ids = prompt(m.vocab, 16, 6)
+    with pytest.raises(Q.QneError) as e:
+        Q.Model.load(*W.synth_model("tiny", seed=1)).restore()
+    assert e.value.code == Q.ENOSNAPSHOT and str(e.value) == "no snapshot taken"
+    m.reset()
+    m.prefill_batched(ids[:8])
+    m.snapshot()
+    m.prefill_from(ids[8:], 8)
+    a = m.logits()
+    m.restore()
+    m.prefill_from(ids[8:], 8)
+    assert np.array_equal(a, m.logits())
+    m.reset()
+    m.prefill_batched(ids)
+    assert np.array_equal(a, m.logits())
+
+
+def test_context_limits(pair):
+    name, m, om, _, _ = pair
+    with pytest.raises(Q.QneError) as e:
+        m.step(1, m.max_context)
+    assert e.value.code == Q.ECONTEXT
+    with pytest.raises(Q.QneError) as e:
+        m.prefill_chunk([1, 2], m.max_context - 2, True)
+    assert e.value.code == Q.ECONTEXT
+    with pytest.raises(Q.QneError) as e:
+        m.prefill([])
+    assert e.value.code == Q.EINVAL
+    assert m.max_context == 4096 and m.dispatches_per_token() > 0 and "gfx" in m.adapter
+
+
+def test_small_context_capacity_and_decode_guard():
+    index, buf = W.synth_model("tiny", seed=2)
+    m = Q.Model.load(index, buf, options={"max_context": 32})
+    assert m.max_context == 32
+    m.prefill_batched(list(range(30)))
+    with pytest.raises(Q.QneError) as e:
+        m.decode(5, 1, [])
+    assert e.value.code == Q.ECONTEXT and "context limit" in str(e.value)
+    m.close()
+
+
+def test_reference_format1_model_loads_and_matches():
+    """A format-1 file (the reference's q4 block-32 u4-zero layout at Qwen3.5-0.8B shapes)."""
+    import json
+    cfg = W.full_config(dict(W.CONFIGS["0.8b"], vocab=248320))
+    # build format-1 tensors: q4 g32 with u4 zero points for every matrix
+    lay, mats = W.plan(cfg, body="q4", head="q4", group=32)
+    rng = np.random.default_rng(0)
+    buf = np.zeros(lay.size, dtype=np.uint8)
+    tensors = {}
+    for n, t in lay.tensors.items():
+        tensors[n] = {"offset": t["offset"], "bytes": t["bytes"]}
+    v1_tensors = {}
+    for name, mm in mats.items():
+        rows, k = mm["rows"], mm["k"]
+        wv = lay.view(buf.data, name + ".w", np.uint32)
+        wv[:] = rng.integers(0, 2 ** 32, size=wv.size, dtype=np.uint64).astype(np.uint32)
+        sv = lay.view(buf.data, name + ".s", np.uint16)
+        sv[:] = np.float16(0.02).view(np.uint16) + rng.integers(0, 64, size=sv.size).astype(np.uint16)
+        # u4 zero points occupy the first rows * k / 64 bytes of the .z slot
+        zt = dict(tensors[name + ".z"])
+        zt["bytes"] = rows * k // 64
+        zv = np.frombuffer(buf.data, dtype=np.uint8, count=zt["bytes"], offset=zt["offset"])
+        zv[:] = rng.integers(0, 256, size=zv.size).astype(np.uint8)
+        v1_tensors[name + ".z"] = zt
+    for n, t in lay.tensors.items():
+        if t["kind"] == "f32":
+            v = lay.view(buf.data, n, np.float32)
+            v[:] = 1.0 if "norm" in n else rng.normal(0, 0.02, size=v.size)
+            if n.endswith("gdn_params"):
+                v[:16], v[16:32], v[32:] = 0.0, -0.5, 1.0
+    tensors.update(v1_tensors)
+    index = json.dumps({"format_version": 1, "config": {"layers": 24, "full_attention_every": 4, "hidden": 1024,
+                        "intermediate": 3584, "vocab": 248320, "rope_theta": 10000000.0, "rope_dim": 64},
+                        "matrices": {n: {"rows": mm["rows"], "k": mm["k"]} for n, mm in mats.items()},
+                        "tensors": tensors})
+    m = Q.Model.load(index, buf)
+    om = O.OracleModel(index, buf, "f32")
+    ids = [1, 2, 3]
+    m.prefill_batched(ids)
+    want = om.prefill_chunk(ids, 0, True)
+    assert np.max(np.abs(m.logits() - want)) < 1e-3 * max(1.0, np.max(np.abs(want)))
+    m.close()
