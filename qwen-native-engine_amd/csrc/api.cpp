@@ -233,14 +233,15 @@ int qne_paged_attn_decode(const float* q, const float* k_new, const float* v_new
         float* ml = nullptr;
         float* acc = nullptr;
         hipStream_t st = (hipStream_t)stream;
-        QNE_HIP(hipMallocAsync((void**)&ml, parts * 2 * 4, st));
-        QNE_HIP(hipMallocAsync((void**)&acc, parts * 256 * 4, st));
+        QNE_HIP(hipMalloc((void**)&ml, parts * 2 * 4));
+        QNE_HIP(hipMalloc((void**)&acc, parts * 256 * 4));
         qne::launch_paged_attn(q, k_new, v_new, (uint16_t*)k_pool, (uint16_t*)v_pool, block_table, max_blocks, ctx,
                                out, batch, nq, nkv, ml, acc, splits, st);
         hipError_t e = hipGetLastError();
-        (void)hipFreeAsync(ml, st);
-        (void)hipFreeAsync(acc, st);
-        qne::hip_check(e, "kernel launch");
+        if (e == hipSuccess) e = hipStreamSynchronize(st);
+        (void)hipFree(ml);
+        (void)hipFree(acc);
+        qne::hip_check(e, "paged attention");
     });
 }
 

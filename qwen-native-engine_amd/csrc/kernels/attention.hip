@@ -70,6 +70,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_kv_append(const float* __restr
                                                             const int32_t* __restrict__ bt, int max_blocks,
                                                             const int32_t* __restrict__ ctx, int nkv) {
     const int g = blockIdx.x, b = blockIdx.y, t = threadIdx.x;
+    if (ctx[b] < 0 || ctx[b] >= max_blocks * kBlock) return;  // beyond the table: nothing to write
     const size_t at = kv_index(bt + (size_t)b * max_blocks, ctx[b], nkv, g) + t;
     const size_t src = ((size_t)b * nkv + g) * kHD + t;
     k_pool[at] = f2h(k_new[src]);
@@ -88,7 +89,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_partial(const float* __re
     __shared__ float s_acc[4][G][kHD];
     const int split = blockIdx.x, g = blockIdx.y, b = blockIdx.z, splits = gridDim.x;
     const int t = threadIdx.x, lane = t % kWave, w = t / kWave, pg = lane / 16, li = lane % 16;
-    const int len = lens[b] + 1;
+    const int len = max(1, min(lens[b] + 1, max_blocks * kBlock));  // never past the block table
     int per = (len + splits - 1) / splits;
     per = (per + kBlock - 1) / kBlock * kBlock;
     const int p0 = split * per, p1 = min(len, p0 + per);
@@ -230,8 +231,8 @@ void launch_attention_model(const AttnModelArgs& a, hipStream_t st) {
     hipLaunchKernelGGL(k_attn_prep, dim3(a.nq + a.nkv), dim3(kAttnThreads), 0, st, a);
     const int G = a.nq / a.nkv;
     // tok[1] is the position; the partial kernel attends lens[0] + 1 = pos + 1 positions.
-    partial_by_g(G, a.qbuf, a.k_pool, a.v_pool, a.block_table, 0, (const int32_t*)(a.tok + 1), a.nkv, a.part_ml,
-                 a.part_acc, a.splits, 1, st);
+    partial_by_g(G, a.qbuf, a.k_pool, a.v_pool, a.block_table, a.max_blocks, (const int32_t*)(a.tok + 1), a.nkv,
+                 a.part_ml, a.part_acc, a.splits, 1, st);
     hipLaunchKernelGGL(k_attn_combine, dim3(a.nq, 1), dim3(kAttnThreads), 0, st, a.part_ml, a.part_acc, a.nkv, G,
                        a.splits, a.proj + a.nq * kHD, a.out);
 }

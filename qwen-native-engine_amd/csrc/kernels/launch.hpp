@@ -60,6 +60,7 @@ struct AttnModelArgs {
     float* part_acc;        // [nkv][splits][group][hd]
     float* out;             // [nq][hd]
     int nq, nkv, rope_dim, splits;
+    int max_blocks;         // entries of block_table
 };
 void launch_attention_model(const AttnModelArgs& a, hipStream_t st);
 // Raw paged decode for `batch` sequences: append k/v at ctx[b], attend over 0..ctx[b].

@@ -275,6 +275,7 @@ void Model::enqueue_layers() {
             a.k_pool = L.k_pool; a.v_pool = L.v_pool; a.block_table = block_table_; a.tok = tok_;
             a.qbuf = qbuf_; a.part_ml = part_ml_; a.part_acc = part_acc_; a.out = mixed_;
             a.nq = c.n_q_heads; a.nkv = c.n_kv_heads; a.rope_dim = c.rope_dim; a.splits = attn_splits_;
+            a.max_blocks = (max_context_ + 15) / 16;
             launch_attention_model(a, stream_);
             launches_ += 3;
         } else {
@@ -335,6 +336,12 @@ void Model::set_tok(uint32_t token, uint32_t pos) {
     QNE_HIP(hipMemcpyAsync(tok_, host_tok_, 16, hipMemcpyHostToDevice, stream_));
 }
 
+static void check_ids(const uint32_t* ids, size_t n, int vocab) {
+    for (size_t i = 0; i < n; i++)
+        if (ids[i] >= (uint32_t)vocab)
+            throw Error(QNE_EINVAL, "token id " + std::to_string(ids[i]) + " outside the vocabulary");
+}
+
 void Model::run_layers_graph() { QNE_HIP(hipGraphLaunch(g_layers_, stream_)); }
 void Model::run_head_graph(bool greedy) { QNE_HIP(hipGraphLaunch(greedy ? g_head_greedy_ : g_head_logits_, stream_)); }
 
@@ -347,6 +354,7 @@ void Model::reset() {
 void Model::prefill(const uint32_t* ids, size_t n) {
     if (n == 0 || n >= (size_t)max_context_)
         throw Error(n == 0 ? QNE_EINVAL : QNE_ECONTEXT, "prompt length must be 1.." + std::to_string(max_context_));
+    check_ids(ids, n, cfg_.vocab);
     std::memcpy(host_ids_, ids, n * 4);
     QNE_HIP(hipMemcpyAsync(ids_, host_ids_, n * 4, hipMemcpyHostToDevice, stream_));
     for (size_t i = 0; i < n; i++) {
@@ -364,6 +372,7 @@ void Model::prefill_chunk(const uint32_t* ids, size_t n, uint32_t start, bool fi
         throw Error(n == 0 ? QNE_EINVAL : QNE_ECONTEXT,
                     "context limit: " + std::to_string(start) + " + " + std::to_string(n) + " tokens does not fit in " +
                         std::to_string(max_context_));
+    check_ids(ids, n, cfg_.vocab);
     std::memcpy(host_ids_, ids, n * 4);
     QNE_HIP(hipMemcpyAsync(ids_, host_ids_, n * 4, hipMemcpyHostToDevice, stream_));
     if (!finish_logits) QNE_HIP(hipMemcpyAsync(tok_backup_, tok_, 16, hipMemcpyDeviceToDevice, stream_));
