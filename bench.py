@@ -1,0 +1,166 @@
+"""Decode throughput of the Qwen3.5-2B-shaped int4 hybrid decoder at batch 1, context 4096.
+
+Workload (the reference's headline metric on this path): 28 layers [GDN, GDN, GDN, attention] x 7,
+hidden 2048, 16 q / 4 kv heads of 256, GDN 16 heads x 128, intermediate 6144, vocab 151936;
+int4 body (group 64, f16 scale + f16 zero), f16 embedding and LM head, weights N(0, 0.02) from a
+seed; KV cache prefilled with 4000 random ids; then `--steps` greedy decode steps timed as one
+GPU-resident submission (each step's pick is fed back on the device).
+
+One step = one decode token. Prints one JSON line. The CPU baseline is the oracle's C
+restatement (f32, OpenMP) timed on a bounded sample of the same workload: a few decode steps at
+context 4000 with the KV cache and GDN state filled with random values.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path[:0] = [str(ROOT / "qwen-native-engine_amd"), str(ROOT / "oracle")]
+
+PEAK_HBM_GBS = 8000.0  # MI355X HBM3E
+
+
+def algorithmic_bytes_per_token(cfg: dict, mats: dict, ctx: float) -> dict:
+    """Bytes one decode token must move at least once, with no cache credit: every weight byte
+    read once (embedding: one row), the KV cache over `ctx` positions plus the appended row, the
+    GDN recurrent state read and written, the conv state read and written."""
+    w = 0
+    for name, m in mats.items():
+        el = m["rows"] * m["k"]
+        if name == "embed":
+            el = m["k"]  # one row
+        if m["dtype"] == "f16":
+            w += el * 2
+        else:
+            w += el // 2 + 2 * (el // m["group"]) * 2  # nibbles + f16 scale + f16 zero
+    lm = mats["lm_head"]["rows"] * mats["lm_head"]["k"] * 2 if mats["lm_head"]["dtype"] == "f16" else 0
+    n_attn = sum(1 for i in range(cfg["layers"]) if (i + 1) % cfg["full_attention_every"] == 0)
+    n_gdn = cfg["layers"] - n_attn
+    kv_row = cfg["n_kv_heads"] * cfg["head_dim"] * 2 * 2  # K and V, f16
+    kv = n_attn * kv_row * (ctx + 1)
+    gdn = n_gdn * cfg["gdn_heads"] * cfg["gdn_dk"] * cfg["gdn_dv"] * 4 * 2
+    conv_ch = 2 * cfg["gdn_heads"] * cfg["gdn_dk"] + cfg["gdn_heads"] * cfg["gdn_dv"]
+    conv = n_gdn * conv_ch * (cfg["conv_kernel"] - 1) * 4 * 2
+    return {"weights": w - lm, "lm_head": lm, "kv": kv, "gdn_state": gdn, "conv_state": conv,
+            "total": w + kv + gdn + conv}
+
+
+def cpu_baseline(index, buf, cfg, ctx, tokens):
+    import cpu_oracle as O
+    om = O.OracleModel(index, buf, "f32", max_context=4096)
+    L = om.L
+    rng = np.random.default_rng(1)
+    n_attn = sum(1 for i in range(cfg["layers"]) if (i + 1) % cfg["full_attention_every"] == 0)
+    n_gdn = cfg["layers"] - n_attn
+    per = cfg["n_kv_heads"] * 4096 * cfg["head_dim"]
+    for a in range(n_attn):
+        for fn in (L.oc_state_kcache, L.oc_state_vcache):
+            arr = np.ctypeslib.as_array((np.ctypeslib.ctypes.c_uint16 * per).from_address(fn(om.state, a)))
+            arr[:] = rng.normal(size=per).astype(np.float16).view(np.uint16)
+    rec = cfg["gdn_heads"] * cfg["gdn_dk"] * cfg["gdn_dv"]
+    for g in range(n_gdn):
+        arr = np.ctypeslib.as_array((np.ctypeslib.ctypes.c_float * rec).from_address(L.oc_state_recurrent(om.state, g)))
+        arr[:] = rng.normal(0, 0.05, size=rec).astype(np.float32)
+    om.token(1, ctx)  # warm caches and threads
+    t0 = time.perf_counter()
+    tok = 2
+    for i in range(tokens):
+        logits = om.token(tok, ctx + 1 + i)
+        tok = int(np.argmax(logits))
+    dt = time.perf_counter() - t0
+    return tokens / dt, L.oc_num_threads()
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=96)
+    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--ctx", type=int, default=4000)
+    ap.add_argument("--config", default="2b")
+    ap.add_argument("--cpu-tokens", type=int, default=4)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--seed", type=int, default=0)
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py: this engine runs batch-1 decode on one GPU; --gpus above 1 is not supported "
+              "(see DESIGN.md for how the path would shard)", file=sys.stderr)
+        sys.exit(2)
+    import qne
+    import weights as W
+
+    cfg = W.full_config(args.config)
+    t = time.perf_counter()
+    index, buf = W.synth_model(args.config, seed=args.seed, body="q4", head="f16", group=64)
+    mats = json.loads(index)["matrices"]
+    gen_s = time.perf_counter() - t
+    m = qne.Model.load(index, buf, options={"max_context": 4096})
+    rng = np.random.default_rng(args.seed)
+    prompt = rng.integers(0, cfg["vocab"], size=args.ctx).astype(np.uint32)
+    assert args.ctx + max(args.steps, args.warmup) <= 4096, "context + steps must fit in 4096"
+    t = time.perf_counter()
+    for s in range(0, args.ctx - 1, 512):
+        m.prefill_chunk(prompt[s: min(s + 512, args.ctx - 1)], s, False)
+    prefill_s = time.perf_counter() - t
+    # Snapshot after ctx - 1 tokens. The last prompt token is replayed before each decode run to
+    # set the greedy pick and position, which snapshot/restore do not cover (model.rs:394-414).
+    m.snapshot()
+    if args.warmup:
+        m.prefill_chunk(prompt[-1:], args.ctx - 1, True)
+        m.decode(args.warmup + 1, args.warmup, [])
+        m.restore()
+    m.prefill_chunk(prompt[-1:], args.ctx - 1, True)
+    # decode() returns after its stream has drained, so the wall clock brackets the device work
+    t0 = time.perf_counter()
+    ids = m.decode(args.steps + 1, args.steps, [])
+    wall = time.perf_counter() - t0
+    dev_ms, dev_steps = m.last_decode_timing()
+    assert dev_steps == args.steps and len(ids) == args.steps + 1
+    tok_s = args.steps / wall
+    bytes_tok = algorithmic_bytes_per_token(cfg, mats, args.ctx + (args.steps - 1) / 2)
+    achieved = bytes_tok["total"] * args.steps / (dev_ms / 1e3) / 1e9
+    result = {
+        "metric": "decode tok/s @ batch 1, ctx 4096 (2B int4) + % of HBM roofline",
+        "value": round(tok_s, 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(1e3 * wall / args.steps, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": f"Qwen3.5-{args.config.upper()}-shaped hybrid decoder, int4 g64 body, f16 embed/lm_head, "
+                               f"batch 1 greedy decode after a {args.ctx}-token prefill",
+                   "layers": cfg["layers"], "hidden": cfg["hidden"], "vocab": cfg["vocab"], "ctx": args.ctx,
+                   "batch": 1, "window": args.steps},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None,
+                     "kernel": f"decode step ({m.dispatches_per_token()} kernels per token)",
+                     "bytes_per_step": bytes_tok["total"], "device_ms_per_step": round(dev_ms / args.steps, 4)},
+        "detail": {"bytes_per_token": bytes_tok, "weights_gen_s": round(gen_s, 2), "prefill_s": round(prefill_s, 2),
+                   "prefill_tok_s": round((args.ctx - 1) / prefill_s, 1), "adapter": m.adapter},
+    }
+    if not args.no_cpu_baseline:
+        v, cores = cpu_baseline(index, buf, cfg, args.ctx, args.cpu_tokens)
+        result["cpu_baseline"] = {"value": round(v, 4), "unit": "tok/s", "cores": cores, "kind": "port",
+                                  "sample": f"{args.cpu_tokens} greedy decode steps of the same model at context "
+                                            f"{args.ctx} (KV cache and GDN state filled with random values), "
+                                            f"oracle C restatement, f32, OpenMP"}
+    else:
+        result["cpu_baseline"] = None
+    m.close()
+    print(json.dumps(result))
+
+
+if __name__ == "__main__":
+    main()

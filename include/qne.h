@@ -81,6 +81,10 @@ int qne_max_context(qne_model* m, uint32_t* out);
 /* Model::profile_token -- model.rs:305: device time of one decode token in ms (event-timed,
  * consumes one greedy token like the reference). */
 int qne_profile_token(qne_model* m, double* ms);
+/* Device time (HIP events on the model's stream) of the windows of the last qne_decode call, in
+ * ms, and the number of decode steps they ran; the counterpart of timing a submission with
+ * Gpu::time (kernels/src/lib.rs:439-446) without host overhead. */
+int qne_last_decode_timing(qne_model* m, double* ms, size_t* steps);
 
 /* ---- kernel-level entry points (device pointers; the reference exposes these only through its
  * in-binary checks, kernels/src/lib.rs:513-712, and microbenches, lib.rs:714-963) ---- */

@@ -166,6 +166,13 @@ int qne_profile_token(qne_model* m, double* ms) {
     });
 }
 
+int qne_last_decode_timing(qne_model* m, double* ms, size_t* steps) {
+    return guard([&] {
+        need(ms && steps, "null output");
+        model(m).last_decode_timing(ms, steps);
+    });
+}
+
 // ---- kernel-level entry points ----
 
 int qne_gemv(int kind, const void* w, const void* sz, int rows, int k, int group, const float* x, const float* norm,

@@ -4,6 +4,7 @@
 
 #include <chrono>
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <map>
 #include <thread>
@@ -78,9 +79,11 @@ Model::Model(const ModelIndex& ix, const uint8_t* weights, uint64_t /*wlen*/, co
     QNE_HIP(hipSetDevice(device_));
     hipDeviceProp_t prop;
     QNE_HIP(hipGetDeviceProperties(&prop, device_));
-    adapter_ = std::string(prop.name) + " (" + prop.gcnArchName + ", " + std::to_string(prop.multiProcessorCount) +
-               " CUs) via HIP";
+    adapter_ = std::string(prop.name[0] ? prop.name : "AMD GPU") + " (" + prop.gcnArchName + ", " +
+               std::to_string(prop.multiProcessorCount) + " CUs) via HIP";
     QNE_HIP(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking));
+    QNE_HIP(hipEventCreate(&ev_start_));
+    QNE_HIP(hipEventCreate(&ev_stop_));
     try {
         upload(ix, weights);
         alloc_state();
@@ -99,6 +102,9 @@ void Model::release() {
     for (hipGraphExec_t g : {g_layers_, g_head_logits_, g_head_greedy_})
         if (g) (void)hipGraphExecDestroy(g);
     g_layers_ = g_head_logits_ = g_head_greedy_ = nullptr;
+    if (ev_start_) (void)hipEventDestroy(ev_start_);
+    if (ev_stop_) (void)hipEventDestroy(ev_stop_);
+    ev_start_ = ev_stop_ = nullptr;
     for (void* p : allocations_) (void)hipFree(p);
     allocations_.clear();
     if (host_tok_) (void)hipHostFree(host_tok_);
@@ -318,6 +324,18 @@ void Model::build_graphs() {
         return e;
     };
     launches_ = 0;
+    // QNE_NO_GRAPH=1 launches the same kernels directly on the stream (for tracing tools that do
+    // not follow graph launches).
+    const char* ng = std::getenv("QNE_NO_GRAPH");
+    if (ng && *ng && *ng != '0') {
+        use_graphs_ = false;
+        enqueue_layers();
+        const size_t before = launches_;
+        enqueue_head(true);
+        dispatches_ = (before - 1) + (launches_ - before);
+        QNE_HIP(hipStreamSynchronize(stream_));
+        return;
+    }
     g_layers_ = capture([&] { enqueue_layers(); });
     g_head_logits_ = capture([&] { enqueue_head(false); });
     const size_t before = launches_;
@@ -342,8 +360,14 @@ static void check_ids(const uint32_t* ids, size_t n, int vocab) {
             throw Error(QNE_EINVAL, "token id " + std::to_string(ids[i]) + " outside the vocabulary");
 }
 
-void Model::run_layers_graph() { QNE_HIP(hipGraphLaunch(g_layers_, stream_)); }
-void Model::run_head_graph(bool greedy) { QNE_HIP(hipGraphLaunch(greedy ? g_head_greedy_ : g_head_logits_, stream_)); }
+void Model::run_layers_graph() {
+    if (use_graphs_) QNE_HIP(hipGraphLaunch(g_layers_, stream_));
+    else enqueue_layers();
+}
+void Model::run_head_graph(bool greedy) {
+    if (use_graphs_) QNE_HIP(hipGraphLaunch(greedy ? g_head_greedy_ : g_head_logits_, stream_));
+    else enqueue_head(greedy);
+}
 
 void Model::reset() {
     QNE_HIP(hipMemsetAsync(state_, 0, state_bytes_, stream_));
@@ -441,6 +465,8 @@ size_t Model::decode(size_t n, uint32_t window, const uint32_t* stop, size_t nst
             if (stop[i] == id) return true;
         return false;
     };
+    last_decode_ms_ = 0.0;
+    last_decode_steps_ = 0;
     while (len < n && !is_stop(out[len - 1])) {
         const uint32_t steps = (uint32_t)std::min<size_t>(window, n - len);
         if ((uint64_t)next_pos + steps > (uint64_t)max_context_)
@@ -449,12 +475,18 @@ size_t Model::decode(size_t n, uint32_t window, const uint32_t* stop, size_t nst
         next_pos += steps;
         // tok[2] counts the ids appended on the device during this window
         QNE_HIP(hipMemsetAsync(tok_ + 2, 0, 4, stream_));
+        QNE_HIP(hipEventRecord(ev_start_, stream_));
         for (uint32_t s = 0; s < steps; s++) {
             run_layers_graph();
             run_head_graph(true);
         }
+        QNE_HIP(hipEventRecord(ev_stop_, stream_));
         QNE_HIP(hipMemcpyAsync(host_ids_, out_ids_, (size_t)steps * 4, hipMemcpyDeviceToHost, stream_));
         sync();
+        float ms = 0.0f;
+        QNE_HIP(hipEventElapsedTime(&ms, ev_start_, ev_stop_));
+        last_decode_ms_ += ms;
+        last_decode_steps_ += steps;
         for (uint32_t s = 0; s < steps && len < n; s++) {
             out[len++] = host_ids_[s];
             if (is_stop(out[len - 1])) break;

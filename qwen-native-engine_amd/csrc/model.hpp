@@ -56,6 +56,10 @@ class Model {
     void last_token(uint32_t* token, uint32_t* next_pos);
     size_t decode(size_t n, uint32_t window, const uint32_t* stop, size_t nstop, uint32_t* out, size_t cap);
     double profile_token();
+    void last_decode_timing(double* ms, size_t* steps) const {
+        *ms = last_decode_ms_;
+        *steps = last_decode_steps_;
+    }
 
     size_t dispatches_per_token() const { return dispatches_; }
     const std::string& adapter() const { return adapter_; }
@@ -103,6 +107,10 @@ class Model {
     uint32_t* host_ids_ = nullptr;  // pinned
 
     hipGraphExec_t g_layers_ = nullptr, g_head_logits_ = nullptr, g_head_greedy_ = nullptr;
+    hipEvent_t ev_start_ = nullptr, ev_stop_ = nullptr;
+    bool use_graphs_ = true;
+    double last_decode_ms_ = 0.0;
+    size_t last_decode_steps_ = 0;
     size_t dispatches_ = 0;
     size_t launches_ = 0;  // kernel launches counted while recording
 };

@@ -58,6 +58,7 @@ def load_library(path: str | os.PathLike | None = None):
         "qne_vocab": ([c_p, ctypes.POINTER(c_u32)], c_i),
         "qne_max_context": ([c_p, ctypes.POINTER(c_u32)], c_i),
         "qne_profile_token": ([c_p, ctypes.POINTER(ctypes.c_double)], c_i),
+        "qne_last_decode_timing": ([c_p, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(c_sz)], c_i),
         "qne_gemv": ([c_i, c_p, c_p, c_i, c_i, c_i, c_p, c_p, c_f, c_p, c_i, c_p], c_i),
         "qne_pack_sz_q4g": ([c_p, c_p, c_sz, c_p], c_i),
         "qne_gdn_step": ([c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_i, c_i, c_p], c_i),
@@ -198,6 +199,12 @@ class Model:
         v = ctypes.c_double()
         self._c(self._lib.qne_profile_token(self._h, ctypes.byref(v)))
         return v.value
+
+    def last_decode_timing(self):
+        """(device ms, steps) of the windows of the last decode call (HIP events)."""
+        ms, n = ctypes.c_double(), ctypes.c_size_t()
+        self._c(self._lib.qne_last_decode_timing(self._h, ctypes.byref(ms), ctypes.byref(n)))
+        return ms.value, n.value
 
 
 # ---- kernel-level entry points on device pointers (ints) ----
