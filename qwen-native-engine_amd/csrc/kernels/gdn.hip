@@ -58,6 +58,17 @@ __device__ __forceinline__ void store_tile(const float (&s)[32], float* S, int c
 #pragma unroll
     for (int i = 0; i < 32; i++) S[(32 * qq + i) * kDV + col] = s[i];
 }
+// The model keeps each head's state value-major, S_T[t][j] = S[j][t]: the 128 keys of one value
+// column are contiguous, so a column (what one wave updates in the persistent decode kernel) is a
+// single 512-byte read.
+__device__ __forceinline__ void load_tile_t(float (&s)[32], const float* S, int col, int qq) {
+#pragma unroll
+    for (int i = 0; i < 32; i++) s[i] = S[col * kDK + 32 * qq + i];
+}
+__device__ __forceinline__ void store_tile_t(const float (&s)[32], float* S, int col, int qq) {
+#pragma unroll
+    for (int i = 0; i < 32; i++) S[col * kDK + 32 * qq + i] = s[i];
+}
 
 // Model decode step for head blockIdx.x: conv + SiLU on the head's q, k, v channels, L2 norms,
 // gates, delta rule, gated RMSNorm (shaders.rs:436-520).
@@ -70,7 +81,7 @@ __global__ __launch_bounds__(kGdnThreads) void k_gdn_decode(const float* __restr
     const int col = t & (kDV - 1), qq = t >> 7;
     float* S = state + (size_t)h * kDK * kDV;
     float s[32];
-    load_tile(s, S, col, qq);  // in flight while the conv runs
+    load_tile_t(s, S, col, qq);  // in flight while the conv runs
 
     float val = 0.0f;
     if (t < 384) {
@@ -103,7 +114,7 @@ __global__ __launch_bounds__(kGdnThreads) void k_gdn_decode(const float* __restr
     }
     __syncthreads();
     const float o = delta_token(s, sh, col, qq);
-    store_tile(s, S, col, qq);
+    store_tile_t(s, S, col, qq);
     // gated RMSNorm over the head's dv outputs (quarter 0 = waves 0 and 1)
     const float oo = wave_sum(o * o);
     __syncthreads();

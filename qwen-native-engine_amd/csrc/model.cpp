@@ -12,6 +12,7 @@
 #include "error.hpp"
 #include "hip_util.hpp"
 #include "json.hpp"
+#include "kernels/engine.hpp"
 #include "kernels/launch.hpp"
 
 namespace qne {
@@ -41,6 +42,11 @@ LoadOptions parse_options(const char* json) {
         o.max_context = (int)v;
     }
     if (j.has("device")) o.device = (int)j.at("device").u64("device");
+    if (j.has("engine")) {
+        const std::string& e = j.at("engine").string();
+        if (e != "graph" && e != "persistent") throw Error(QNE_EINVAL, "engine must be \"persistent\" or \"graph\"");
+        o.graph_engine = e == "graph";
+    }
     return o;
 }
 
@@ -84,10 +90,12 @@ Model::Model(const ModelIndex& ix, const uint8_t* weights, uint64_t /*wlen*/, co
     QNE_HIP(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking));
     QNE_HIP(hipEventCreate(&ev_start_));
     QNE_HIP(hipEventCreate(&ev_stop_));
+    persistent_ = !opt.graph_engine;
     try {
         upload(ix, weights);
         alloc_state();
-        build_graphs();
+        if (persistent_) setup_engine();
+        else build_graphs();
     } catch (...) {
         release();
         throw;
@@ -110,7 +118,10 @@ void Model::release() {
     if (host_tok_) (void)hipHostFree(host_tok_);
     if (host_logits_) (void)hipHostFree(host_logits_);
     if (host_ids_) (void)hipHostFree(host_ids_);
-    host_tok_ = nullptr; host_logits_ = nullptr; host_ids_ = nullptr;
+    if (host_err_) (void)hipHostFree(host_err_);
+    host_tok_ = nullptr; host_logits_ = nullptr; host_ids_ = nullptr; host_err_ = nullptr;
+    delete (EngineArgs*)engine_args_;
+    engine_args_ = nullptr;
     if (stream_) (void)hipStreamDestroy(stream_);
     stream_ = nullptr;
 }
@@ -344,7 +355,92 @@ void Model::build_graphs() {
     QNE_HIP(hipStreamSynchronize(stream_));
 }
 
-void Model::sync() { wait_stream(stream_); }
+// The persistent engine's view of the model: per-layer descriptors in device memory and the
+// scratch buffers of its phases.
+void Model::setup_engine() {
+    const ModelConfig& c = cfg_;
+    engine_grid_ = engine_max_grid();
+    if (engine_grid_ <= 0) throw Error(QNE_EDEVICE, "the persistent decode kernel cannot be made co-resident");
+    if (c.rope_dim % 8 != 0) throw Error(QNE_EFORMAT, "unsupported model architecture: rope_dim must be a multiple of 8");
+    if (c.hidden > 3968 || c.hidden % 512 != 0)
+        throw Error(QNE_EFORMAT, "unsupported model architecture: the persistent engine needs hidden % 512 == 0 and "
+                                 "hidden <= 3968 (load with {\"engine\": \"graph\"})");
+    auto emat = [](const DevMat& d) {
+        EMat e;
+        e.w = d.w; e.sz = d.sz; e.kind = d.kind; e.rows = d.rows; e.k = d.k; e.group = d.group;
+        return e;
+    };
+    std::vector<ELayer> el(layers_.size());
+    for (size_t i = 0; i < layers_.size(); i++) {
+        const DevLayer& L = layers_[i];
+        ELayer& E = el[i];
+        E.in = emat(L.in); E.out = emat(L.out); E.gu = emat(L.gate_up); E.down = emat(L.down);
+        E.in_norm = L.input_norm; E.post_norm = L.post_norm; E.norms = L.norms;
+        E.conv_w = L.conv_w; E.prm = L.gdn_params; E.conv = L.conv_state; E.rec = L.rec;
+        E.k_pool = L.k_pool; E.v_pool = L.v_pool; E.attn = L.attn ? 1 : 0;
+    }
+    ELayer* d_layers = (ELayer*)dalloc(el.size() * sizeof(ELayer));
+    QNE_HIP(hipMemcpy(d_layers, el.data(), el.size() * sizeof(ELayer), hipMemcpyHostToDevice));
+    EngineArgs* a = new EngineArgs();
+    engine_args_ = a;
+    a->layers = d_layers;
+    a->n_layers = (int)layers_.size();
+    a->embed = emat(embed_);
+    a->lm = emat(lm_head_);
+    a->final_norm = final_norm_;
+    a->hidden = c.hidden; a->inter = c.intermediate; a->vocab = c.vocab;
+    a->nq = c.n_q_heads; a->nkv = c.n_kv_heads; a->rope_dim = c.rope_dim; a->gdn_heads = c.gdn_heads;
+    a->max_blocks = (max_context_ + 15) / 16;
+    a->splits = std::max(1, engine_grid_ / c.n_kv_heads / 2);
+    a->eps = c.eps;
+    a->inv_freq = inv_freq_;
+    a->block_table = block_table_;
+    a->h = h_; a->proj = proj_; a->mixed = mixed_; a->act = act_; a->logits = logits_;
+    a->gdn_sq = (float*)dalloc((size_t)c.gdn_heads * 16 * 4);
+    const size_t G = (size_t)(c.n_q_heads / c.n_kv_heads);
+    a->att_ml = (float*)dalloc((size_t)c.n_kv_heads * a->splits * G * 2 * 4);
+    a->att_acc = (float*)dalloc((size_t)c.n_kv_heads * a->splits * G * c.head_dim * 4);
+    a->att_cnt = (unsigned*)dalloc((size_t)c.n_kv_heads * 4);
+    QNE_HIP(hipMemset(a->att_cnt, 0, (size_t)c.n_kv_heads * 4));
+    a->am_val = (float*)dalloc((size_t)engine_grid_ * 4);
+    a->am_idx = (uint32_t*)dalloc((size_t)engine_grid_ * 4);
+    a->tok = tok_;
+    a->ids = ids_;
+    a->out_ids = out_ids_;
+    a->out_cap = (uint32_t)max_context_;
+    eng_bar_ = (unsigned*)dalloc(64);
+    a->bar = eng_bar_;
+    a->err = eng_bar_ + 1;
+    QNE_HIP(hipHostMalloc((void**)&host_err_, 64, hipHostMallocDefault));
+    host_err_[0] = 0;
+    dispatches_ = 1;  // one launch covers a whole decode window
+    QNE_HIP(hipDeviceSynchronize());
+}
+
+void Model::run_engine(const EngineRun& r) {
+    EngineArgs a = *(const EngineArgs*)engine_args_;
+    a.feed = r.feed;
+    a.head = r.head;
+    a.argmax = r.argmax;
+    a.n_steps = r.n_steps;
+    a.pos0 = r.pos0;
+    a.out_ids = r.record_ids ? out_ids_ : nullptr;
+    QNE_HIP(hipMemsetAsync(eng_bar_, 0, 8, stream_));
+    QNE_HIP(launch_engine(a, engine_grid_, stream_));
+    QNE_HIP(hipMemcpyAsync(host_err_, eng_bar_ + 1, 4, hipMemcpyDeviceToHost, stream_));
+}
+
+void Model::check_engine_error() {
+    if (persistent_ && host_err_ && host_err_[0] != 0) {
+        host_err_[0] = 0;
+        throw Error(QNE_EDEVICE, "GPU wait failed: a grid barrier of the decode kernel timed out");
+    }
+}
+
+void Model::sync() {
+    wait_stream(stream_);
+    check_engine_error();
+}
 
 void Model::set_tok(uint32_t token, uint32_t pos) {
     host_tok_[0] = token;
@@ -381,10 +477,19 @@ void Model::prefill(const uint32_t* ids, size_t n) {
     check_ids(ids, n, cfg_.vocab);
     std::memcpy(host_ids_, ids, n * 4);
     QNE_HIP(hipMemcpyAsync(ids_, host_ids_, n * 4, hipMemcpyHostToDevice, stream_));
-    for (size_t i = 0; i < n; i++) {
-        launch_set_tok(tok_, ids_, (int)i, (uint32_t)i, stream_);
-        run_layers_graph();
-        run_head_graph(true);
+    if (persistent_) {
+        // Only the last token's LM head is observable (logits, greedy pick), so the others are
+        // skipped: the state afterwards is the same.
+        set_tok(ids[0], 0);
+        EngineRun r;
+        r.feed = 0; r.head = 2; r.argmax = 1; r.n_steps = (int)n; r.pos0 = 0;
+        run_engine(r);
+    } else {
+        for (size_t i = 0; i < n; i++) {
+            launch_set_tok(tok_, ids_, (int)i, (uint32_t)i, stream_);
+            run_layers_graph();
+            run_head_graph(true);
+        }
     }
     sync();
 }
@@ -399,6 +504,16 @@ void Model::prefill_chunk(const uint32_t* ids, size_t n, uint32_t start, bool fi
     check_ids(ids, n, cfg_.vocab);
     std::memcpy(host_ids_, ids, n * 4);
     QNE_HIP(hipMemcpyAsync(ids_, host_ids_, n * 4, hipMemcpyHostToDevice, stream_));
+    if (persistent_) {
+        // tok is only written by the greedy pick, so without finish_logits it stays as it was
+        if (finish_logits) QNE_HIP(hipMemsetAsync(tok_ + 2, 0, 4, stream_));
+        EngineRun r;
+        r.feed = 0; r.head = finish_logits ? 2 : 0; r.argmax = finish_logits ? 1 : 0;
+        r.n_steps = (int)n; r.pos0 = start;
+        run_engine(r);
+        sync();
+        return;
+    }
     if (!finish_logits) QNE_HIP(hipMemcpyAsync(tok_backup_, tok_, 16, hipMemcpyDeviceToDevice, stream_));
     for (size_t i = 0; i < n; i++) {
         launch_set_tok(tok_, ids_, (int)i, start + (uint32_t)i, stream_);
@@ -423,8 +538,14 @@ void Model::step(uint32_t token, uint32_t pos, float* out, size_t cap) {
     if (cap < (size_t)cfg_.vocab) throw Error(QNE_EINVAL, "logits buffer smaller than the vocabulary");
     if (token >= (uint32_t)cfg_.vocab) throw Error(QNE_EINVAL, "token id outside the vocabulary");
     set_tok(token, pos);
-    run_layers_graph();
-    run_head_graph(false);
+    if (persistent_) {
+        EngineRun r;
+        r.feed = 1; r.head = 1; r.argmax = 0; r.n_steps = 1; r.pos0 = pos;
+        run_engine(r);
+    } else {
+        run_layers_graph();
+        run_head_graph(false);
+    }
     QNE_HIP(hipMemcpyAsync(host_logits_, logits_, (size_t)cfg_.vocab * 4, hipMemcpyDeviceToHost, stream_));
     sync();
     std::memcpy(out, host_logits_, (size_t)cfg_.vocab * 4);
@@ -476,9 +597,16 @@ size_t Model::decode(size_t n, uint32_t window, const uint32_t* stop, size_t nst
         // tok[2] counts the ids appended on the device during this window
         QNE_HIP(hipMemsetAsync(tok_ + 2, 0, 4, stream_));
         QNE_HIP(hipEventRecord(ev_start_, stream_));
-        for (uint32_t s = 0; s < steps; s++) {
-            run_layers_graph();
-            run_head_graph(true);
+        if (persistent_) {
+            EngineRun r;
+            r.feed = 1; r.head = 1; r.argmax = 1; r.n_steps = (int)steps; r.pos0 = next_pos - steps;
+            r.record_ids = true;
+            run_engine(r);
+        } else {
+            for (uint32_t s = 0; s < steps; s++) {
+                run_layers_graph();
+                run_head_graph(true);
+            }
         }
         QNE_HIP(hipEventRecord(ev_stop_, stream_));
         QNE_HIP(hipMemcpyAsync(host_ids_, out_ids_, (size_t)steps * 4, hipMemcpyDeviceToHost, stream_));
@@ -500,8 +628,18 @@ double Model::profile_token() {
     QNE_HIP(hipEventCreate(&a));
     QNE_HIP(hipEventCreate(&b));
     QNE_HIP(hipEventRecord(a, stream_));
-    run_layers_graph();
-    run_head_graph(true);
+    if (persistent_) {
+        uint32_t t, p;
+        last_token(&t, &p);
+        if (p >= (uint32_t)max_context_) throw Error(QNE_ECONTEXT, "context limit reached");
+        EngineRun r;
+        r.feed = 1; r.head = 1; r.argmax = 1; r.n_steps = 1; r.pos0 = p;
+        QNE_HIP(hipEventRecord(a, stream_));
+        run_engine(r);
+    } else {
+        run_layers_graph();
+        run_head_graph(true);
+    }
     QNE_HIP(hipEventRecord(b, stream_));
     sync();
     float ms = 0.0f;

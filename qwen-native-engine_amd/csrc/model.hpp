@@ -35,6 +35,16 @@ struct DevLayer {
 struct LoadOptions {
     int max_context = 4096;
     int device = 0;
+    bool graph_engine = false;  // per-kernel hipGraph path instead of the persistent kernel
+};
+
+struct EngineRun {
+    int feed = 0;          // 0: ids, 1: greedy feedback from tok[0]
+    int head = 0;          // 0 none, 1 every step, 2 last step
+    int argmax = 0;
+    int n_steps = 1;
+    uint32_t pos0 = 0;
+    bool record_ids = false;
 };
 
 LoadOptions parse_options(const char* json);
@@ -76,6 +86,9 @@ class Model {
     void set_tok(uint32_t token, uint32_t pos);
     void run_layers_graph();
     void run_head_graph(bool greedy);
+    void setup_engine();
+    void run_engine(const EngineRun& r);
+    void check_engine_error();
     void sync();
     void* dalloc(size_t bytes);
 
@@ -109,6 +122,12 @@ class Model {
     hipGraphExec_t g_layers_ = nullptr, g_head_logits_ = nullptr, g_head_greedy_ = nullptr;
     hipEvent_t ev_start_ = nullptr, ev_stop_ = nullptr;
     bool use_graphs_ = true;
+    // persistent engine
+    bool persistent_ = true;
+    int engine_grid_ = 0;
+    void* engine_args_ = nullptr;  // host copy of EngineArgs (opaque here)
+    unsigned* eng_bar_ = nullptr;  // [0] barrier counter, [1] error flag
+    unsigned* host_err_ = nullptr;  // pinned
     double last_decode_ms_ = 0.0;
     size_t last_decode_steps_ = 0;
     size_t dispatches_ = 0;

@@ -12,12 +12,14 @@ import weights as W
 pytestmark = pytest.mark.gpu
 
 
-@pytest.fixture(scope="module", params=[("tiny", "q4", "f16"), ("tiny", "f16", "q4"), ("small", "q4", "f16")],
-                ids=["tiny-q4body", "tiny-f16body-q4head", "small-q4body"])
+@pytest.fixture(scope="module", params=[("tiny", "q4", "f16", "persistent"), ("tiny", "f16", "q4", "persistent"),
+                                        ("small", "q4", "f16", "persistent"), ("tiny", "q4", "f16", "graph"),
+                                        ("small", "q4", "f16", "graph")],
+                ids=["tiny-q4body", "tiny-f16body-q4head", "small-q4body", "tiny-q4body-graph", "small-q4body-graph"])
 def pair(request):
-    name, body, head = request.param
+    name, body, head, engine = request.param
     index, buf = W.synth_model(name, seed=11, body=body, head=head, norm_jitter=0.1)
-    m = Q.Model.load(index, buf)
+    m = Q.Model.load(index, buf, options={"engine": engine})
     om = O.OracleModel(index, buf, "f64")
     yield name, m, om, index, buf
     m.close()
