@@ -762,7 +762,11 @@ __global__ __launch_bounds__(kEngineThreads, 1) void k_engine(EngineArgs a) {
                 const int j = l < a.n_layers ? 4 * l + (k == 0 ? 0 : k - 1) : 4 * a.n_layers;
                 run_job(a, j, token, wg, nwg, wave, lane, smem, cseq, cur, misc);
             }
-            if (!grid_sync(a, epoch, nwg, wave, mixer, &flag)) return;
+            if (!grid_sync(a, epoch, nwg, wave, mixer, &flag)) {
+                // no LDS DMA may still be in flight when the workgroup ends
+                __builtin_amdgcn_s_waitcnt(kWaitAll);
+                return;
+            }
         }
         if (head) {
             if (a.argmax) {
