@@ -88,6 +88,7 @@ def main():
     ap.add_argument("--cpu-tokens", type=int, default=4)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--engine", default="persistent", choices=["persistent", "graph"])
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this engine runs batch-1 decode on one GPU; --gpus above 1 is not supported "
@@ -101,7 +102,7 @@ def main():
     index, buf = W.synth_model(args.config, seed=args.seed, body="q4", head="f16", group=64)
     mats = json.loads(index)["matrices"]
     gen_s = time.perf_counter() - t
-    m = qne.Model.load(index, buf, options={"max_context": 4096})
+    m = qne.Model.load(index, buf, options={"max_context": 4096, "engine": args.engine})
     rng = np.random.default_rng(args.seed)
     prompt = rng.integers(0, cfg["vocab"], size=args.ctx).astype(np.uint32)
     assert args.ctx + max(args.steps, args.warmup) <= 4096, "context + steps must fit in 4096"

@@ -81,6 +81,13 @@ int qne_max_context(qne_model* m, uint32_t* out);
 /* Model::profile_token -- model.rs:305: device time of one decode token in ms (event-timed,
  * consumes one greedy token like the reference). */
 int qne_profile_token(qne_model* m, double* ms);
+/* Model::profile_token -- model.rs:305 (per-label sums of Gpu::profile, kernels/src/lib.rs:366-396):
+ * consumes one greedy token with the device timeline of the persistent decode kernel on and writes
+ * NUL-terminated JSON {"total_ms", "labels": {label: ms}, "work_ms": {...}, "barrier_ms": {...},
+ * "phases": [[label, slowest work ms, fastest work ms, barrier ms], ...]} into buf. Labels are
+ * gdn.* / attn.* per layer phase and lm_head. QNE_EINVAL if cap is too small (the message names
+ * the size) or the model was loaded with the graph engine. Diagnostic only. */
+int qne_profile_token_json(qne_model* m, char* buf, size_t cap);
 /* Device time (HIP events on the model's stream) of the windows of the last qne_decode call, in
  * ms, and the number of decode steps they ran; the counterpart of timing a submission with
  * Gpu::time (kernels/src/lib.rs:439-446) without host overhead. */

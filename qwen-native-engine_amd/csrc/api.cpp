@@ -166,6 +166,15 @@ int qne_profile_token(qne_model* m, double* ms) {
     });
 }
 
+int qne_profile_token_json(qne_model* m, char* buf, size_t cap) {
+    return guard([&] {
+        need(buf != nullptr, "null output");
+        const std::string j = model(m).profile_token_json();
+        if (j.size() + 1 > cap) throw qne::Error(QNE_EINVAL, "buffer too small: need " + std::to_string(j.size() + 1));
+        std::memcpy(buf, j.c_str(), j.size() + 1);
+    });
+}
+
 int qne_last_decode_timing(qne_model* m, double* ms, size_t* steps) {
     return guard([&] {
         need(ms && steps, "null output");

@@ -1,0 +1,1082 @@
+// Persistent decode kernel: every decode step of the hybrid decoder in ONE cooperative launch.
+//
+// Reference: the per-token dispatch list of Model::load (kernels/src/model.rs:220-269) and its
+// kernels (kernels/src/shaders.rs): embed, per layer [rmsnorm, mixer_in GEMV, gdn | attention,
+// mixer_out GEMV (+=), rmsnorm, gate_up GEMV (SwiGLU), down GEMV (+=)], rmsnorm, lm_head GEMV,
+// argmax. A batch-1 token of the 2B-shaped int4 model moves ~1.74 GB in ~150 dependent pieces of
+// 2-14 MB, so a token is latency-bound unless (1) the hand-over between pieces is cheap and
+// (2) HBM keeps streaming while the chip waits for it. Design for MI355X (256 CUs, 8 XCDs with
+// private L2s):
+//  - one workgroup of 8 waves per CU, all co-resident (cooperative launch). The phases of a token
+//    form a fixed program (decode.hpp `Phase`, built once at load);
+//  - hand-over by tagged values: a phase publishes each output f32 together with a 32-bit tag
+//    (its sequence number) in one 8-byte agent-scope store; the next phase polls with agent-scope
+//    16-byte loads until every tag it needs is current. There is no grid barrier and no release /
+//    acquire fence, so no L2 writeback or invalidate: on MI355X those cost ~10 us per barrier
+//    against ~2.4 us for a tagged exchange of a 2048-vector;
+//  - each wave streams the weights of its rows of the NEXT phase into its own 12 KiB of LDS with
+//    global_load_lds_dwordx4 before it starts waiting for that phase's input, so HBM works while
+//    the exchange settles. A wave only ever reads what it loaded itself: no cross-wave handshake;
+//  - rows are spread over waves wave-major (wave w of every workgroup before wave w+1), so every
+//    workgroup owns rows of every vector that all workgroups consume;
+//  - RMSNorm is folded into the input exchange (the poll multiplies by the gain and sums the
+//    squares of the raw values); the GDN causal conv + SiLU runs in the epilogue of the
+//    in-projection rows that own those channels; the residual stream h lives in the registers of
+//    the waves that own its rows and is published after each residual add;
+//  - GDN: one workgroup per (head, 8 value columns), one wave per column, its 512-byte state column
+//    prefetched into LDS; attention: split-context partials per (kv head, split) with GQA reuse,
+//    K/V rows prefetched into LDS through the block table, then a combine phase per (q head,
+//    64 dims) with the sigmoid gate;
+//  - the LM head tracks a per-wave argmax; workgroups publish their best and every workgroup
+//    reduces all of them, so the next step needs no separate broadcast.
+#include "common.hpp"
+#include "decode.hpp"
+
+namespace qne {
+
+namespace {
+
+constexpr int kT = kDecodeThreads;
+constexpr int kNW = kT / kWave;        // 8 waves
+constexpr int kXs = 12288;             // floats of LDS input staging
+constexpr int kRawEmb = 8192;          // xs offset of the raw embedding row (hidden <= 4096)
+constexpr int kRegion = 12 * 1024;     // bytes of LDS per wave (prefetched weights / state / K,V)
+constexpr int kPoll = 6;               // tagged pairs a thread polls at once
+constexpr int kSC1 = 16;               // buffer cache policy: agent-scope coherent access
+constexpr int kBlk = 16;               // KV block size (positions)
+constexpr int kDK = 128;               // GDN dk = dv
+constexpr int kAttnU = kRegion / 2048; // prefetched K/V wave-loads (2 positions each) per wave
+constexpr int kWaitVm0 = 0x0F70;
+constexpr int kWaitAll = 0;
+
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+
+// s_waitcnt until at most N vector-memory operations of this wave are outstanding (gfx9
+// encoding: vmcnt[3:0] at bits 3:0, vmcnt[5:4] at 15:14; expcnt and lgkmcnt left at maximum).
+template <int N>
+__device__ __forceinline__ void wait_vm_n() {
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x70 | 0xF00);
+}
+// Rounds n down to a supported count, so the wait is never shorter than asked for.
+__device__ __forceinline__ void wait_vm(int n) {
+    if (n >= 48) wait_vm_n<48>();
+    else if (n >= 32) wait_vm_n<32>();
+    else if (n >= 24) wait_vm_n<24>();
+    else if (n >= 16) wait_vm_n<16>();
+    else if (n >= 12) wait_vm_n<12>();
+    else if (n >= 8) wait_vm_n<8>();
+    else if (n >= 6) wait_vm_n<6>();
+    else if (n >= 4) wait_vm_n<4>();
+    else if (n >= 3) wait_vm_n<3>();
+    else if (n >= 2) wait_vm_n<2>();
+    else if (n >= 1) wait_vm_n<1>();
+    else wait_vm_n<0>();
+}
+
+// The program and the per-layer parameters are read through the constant address space: they do
+// not change during a launch, so the compiler reads them with scalar loads, which do not wait
+// behind the wave's outstanding weight DMA (vector-memory completion is in order).
+typedef const __attribute__((address_space(4))) Phase CPhase;
+typedef const __attribute__((address_space(4))) float cfloat;
+
+__device__ __forceinline__ void cbar() { asm volatile("" ::: "memory"); }
+// Workgroup barrier for LDS hand-offs only. Unlike __syncthreads it does not wait for the wave's
+// outstanding global loads (the prefetch of the next phase stays in flight).
+__device__ __forceinline__ void bar() {
+    cbar();
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+    cbar();
+}
+
+__device__ __forceinline__ rsrc_t make_rsrc(const void* p, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
+}
+
+__device__ __forceinline__ unsigned ld_agent(const unsigned* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_agent(unsigned* p, unsigned v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Publishes value v at index i of a tagged buffer (write-through to the device coherence point).
+__device__ __forceinline__ void put(uint64_t* buf, uint32_t i, float v, uint32_t tag) {
+    __hip_atomic_store(buf + i, ((uint64_t)tag << 32) | (uint64_t)__float_as_uint(v), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// 16 bytes of K or V stored with an agent-scope (write-through) store.
+__device__ __forceinline__ void st16_agent(uint16_t* p, u32x4 v) {
+    const rsrc_t r = make_rsrc(p, 16);
+    __builtin_amdgcn_raw_buffer_store_b128(v, r, 0, 0, kSC1);
+}
+
+struct Ctl {
+    unsigned* err;
+    unsigned spin;
+    int* bail;  // LDS
+};
+
+// Polls n tagged pairs of `buf` (cap readable u64 entries). Pair q lives at u64 index src(q)
+// (even); fn(q, v0, v1) consumes it. Every thread of the workgroup calls this; the caller ends
+// with a barrier. On a timeout the error flag is raised and *bail set.
+template <class Src, class Fn>
+__device__ __forceinline__ void poll_pairs(const uint64_t* buf, uint32_t cap, int n, uint32_t tag, Src src, Fn fn,
+                                           const Ctl& c) {
+    const rsrc_t rs = make_rsrc(buf, cap * 8u);
+    for (int base = 0; base < n; base += kT * kPoll) {
+        unsigned pend = 0;
+#pragma unroll
+        for (int j = 0; j < kPoll; j++)
+            if (base + j * kT + (int)threadIdx.x < n) pend |= 1u << j;
+        unsigned spins = 0;
+        while (pend) {
+            u32x4 v[kPoll];
+#pragma unroll
+            for (int j = 0; j < kPoll; j++)
+                if ((pend >> j) & 1u) v[j] = __builtin_amdgcn_raw_buffer_load_b128(rs, 8 * src(base + j * kT + (int)threadIdx.x), 0, kSC1);
+#pragma unroll
+            for (int j = 0; j < kPoll; j++) {
+                if (((pend >> j) & 1u) && v[j].y == tag && v[j].w == tag) {
+                    fn(base + j * kT + (int)threadIdx.x, __uint_as_float(v[j].x), __uint_as_float(v[j].z));
+                    pend &= ~(1u << j);
+                }
+            }
+            if (pend && (++spins > c.spin || ((spins & 31u) == 0 && ld_agent(c.err)))) {
+                st_agent(c.err, 1u);
+                *c.bail = 1;
+                return;
+            }
+        }
+    }
+}
+
+// Contiguous share of `rows` for global wave index gw of nw.
+struct Rows {
+    int r0, n;
+};
+__device__ __forceinline__ Rows part(int rows, int gw, int nw) {
+    const int per = rows / nw, rem = rows % nw;
+    return {gw * per + min(gw, rem), per + (gw < rem ? 1 : 0)};
+}
+
+// ---- DMA into the wave's LDS region ----
+
+__device__ __forceinline__ void dma_bytes(const uint8_t* src, int bytes, uint8_t* dst, int lane) {
+    for (int u = 0; u * 1024 < bytes; u++) {
+        const int off = u * 1024 + lane * 16;
+        if (off < bytes)
+            __builtin_amdgcn_global_load_lds((const void*)(src + off), (lds_ptr_t)(dst + u * 1024), 16, 0, 0);
+    }
+}
+
+// Geometry of a GEMV phase's rows in a region.
+struct GemvGeo {
+    int rb, szb, stride, nm, cap;  // row bytes, scale/zero bytes, bytes per row, rows per output, outputs per region
+    int per;                       // DMA instructions per output
+};
+__device__ __forceinline__ GemvGeo geo(CPhase& P) {
+    GemvGeo g;
+    g.rb = P.mkind ? P.k / 2 : P.k * 2;
+    g.szb = P.mkind ? (P.k / P.group) * 4 : 0;
+    g.stride = g.rb + g.szb;
+    g.nm = P.epi == EP_SWIGLU ? 2 : 1;
+    g.cap = kRegion / (g.stride * g.nm);
+    g.per = g.nm * ((g.rb + 1023) / 1024 + (g.szb + 1023) / 1024);
+    return g;
+}
+
+// DMA of outputs [o0, o0 + cnt) (row pairs for SwiGLU) into region slots starting at `slot`.
+__device__ __forceinline__ void dma_rows(CPhase& P, const GemvGeo& g, int o0, int cnt, int slot, uint8_t* reg,
+                                         int lane) {
+    const uint8_t* w = (const uint8_t*)P.w;
+    const uint8_t* sz = (const uint8_t*)P.sz;
+    for (int i = 0; i < cnt; i++) {
+        for (int m = 0; m < g.nm; m++) {
+            const size_t row = (size_t)(o0 + i) + (size_t)m * P.rows;
+            uint8_t* d = reg + ((slot + i) * g.nm + m) * g.stride;
+            dma_bytes(w + row * g.rb, g.rb, d, lane);
+            if (g.szb) dma_bytes(sz + row * g.szb, g.szb, d + g.rb, lane);
+        }
+    }
+}
+
+// ---- input vector slice in registers ----
+
+// The input vector is consumed in steps of at most 32 values per lane, so that only one step's
+// slice of x lives in registers while it is applied to a group of up to 8 rows:
+//  - q4 rows (K <= 6144): step s < n4 is the 2048-column slab s (32 values per lane, 16 bytes of
+//    nibbles), then at most one 1024-column slab (16 values, 8 bytes) and one 512-column slab
+//    (8 values, 4 bytes);
+//  - f16 rows: step j covers the 512-column slabs 4j..4j+3 (8 values, 16 bytes per lane each).
+struct Step {
+    int kind, K, n4, n2, n1, nsteps;
+};
+__device__ __forceinline__ Step make_step(int kind, int K) {
+    Step t;
+    t.kind = kind;
+    t.K = K;
+    t.n4 = K / 2048;
+    t.n2 = (K % 2048) / 1024;
+    t.n1 = (K % 1024) / 512;
+    t.nsteps = kind ? t.n4 + t.n2 + t.n1 : (K + 2047) / 2048;
+    return t;
+}
+
+struct XC {
+    float x[32];
+    float sum;  // q4: sum of the step's values (the zero-point term)
+};
+
+// The lane's values of step j from xs. GDN inputs are scaled per head by the 1/rms computed from
+// the published partial sums of squares at xs[H*128 + h*16 + cb].
+__device__ __forceinline__ void load_step(const float* xs, const Step& t, int j, bool gdn, int H, XC& X, int lane) {
+    auto rn = [&](int c0) {
+        if (!gdn) return 1.0f;
+        const int h = c0 / kDK;
+        float s = 0.0f;
+#pragma unroll
+        for (int b = 0; b < 16; b++) s += xs[H * kDK + h * 16 + b];
+        return 1.0f / sqrtf(s / (float)kDK + 1e-6f);
+    };
+    X.sum = 0.0f;
+    if (t.kind == 1) {
+        int c0, n;
+        if (j < t.n4) { c0 = 2048 * j + 32 * lane; n = 32; }
+        else if (j < t.n4 + t.n2) { c0 = 2048 * t.n4 + 16 * lane; n = 16; }
+        else { c0 = 2048 * t.n4 + 1024 * t.n2 + 8 * lane; n = 8; }
+        const float r = rn(c0);
+#pragma unroll
+        for (int i = 0; i < 32; i += 4) {
+            if (i < n) {
+                const float4 f = *(const float4*)(xs + c0 + i);
+                X.x[i] = f.x * r; X.x[i + 1] = f.y * r; X.x[i + 2] = f.z * r; X.x[i + 3] = f.w * r;
+                X.sum += X.x[i] + X.x[i + 1] + X.x[i + 2] + X.x[i + 3];
+            }
+        }
+    } else {
+        const int ns = t.K / 512;
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const int sl = 4 * j + q;
+            if (sl < ns) {
+                const int c0 = 512 * sl + 8 * lane;
+                const float r = rn(c0);
+                const float4 a = *(const float4*)(xs + c0), b = *(const float4*)(xs + c0 + 4);
+                float* d = &X.x[8 * q];
+                d[0] = a.x * r; d[1] = a.y * r; d[2] = a.z * r; d[3] = a.w * r;
+                d[4] = b.x * r; d[5] = b.y * r; d[6] = b.z * r; d[7] = b.w * r;
+            }
+        }
+    }
+}
+
+__device__ __forceinline__ float dot8(uint32_t w, const float* x) {
+    const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
+    float p = (float)(lo & 0xFFu) * x[0];
+    float q = (float)(hi & 0xFFu) * x[1];
+    p = fmaf((float)((lo >> 8) & 0xFFu), x[2], p);
+    q = fmaf((float)((hi >> 8) & 0xFFu), x[3], q);
+    p = fmaf((float)((lo >> 16) & 0xFFu), x[4], p);
+    q = fmaf((float)((hi >> 16) & 0xFFu), x[5], q);
+    p = fmaf((float)(lo >> 24), x[6], p);
+    q = fmaf((float)(hi >> 24), x[7], q);
+    return p + q;
+}
+
+// The lane's share of step j of the dot product of one row held in LDS (weights at `row`, the
+// row's (scale, zero) pairs at row + rb).
+__device__ __forceinline__ float step_dot(const Step& t, int j, int G, int rb, const uint8_t* row, const XC& X, int lane) {
+    if (t.kind == 1) {
+        const uint8_t* szr = row + rb;
+        if (j < t.n4) {
+            const u32x4 w = *(const u32x4*)(row + 1024 * j + 16 * lane);
+            const uint32_t sz = *(const uint32_t*)(szr + 4 * ((2048 * j + 32 * lane) / G));
+            const float dq = dot8(w.x, &X.x[0]) + dot8(w.y, &X.x[8]) + dot8(w.z, &X.x[16]) + dot8(w.w, &X.x[24]);
+            return lo_h(sz) * (dq - hi_h(sz) * X.sum);
+        }
+        if (j < t.n4 + t.n2) {
+            const u32x2 w = *(const u32x2*)(row + 1024 * t.n4 + 8 * lane);
+            const uint32_t sz = *(const uint32_t*)(szr + 4 * ((2048 * t.n4 + 16 * lane) / G));
+            return lo_h(sz) * (dot8(w.x, &X.x[0]) + dot8(w.y, &X.x[8]) - hi_h(sz) * X.sum);
+        }
+        const uint32_t w = *(const uint32_t*)(row + 1024 * t.n4 + 512 * t.n2 + 4 * lane);
+        const uint32_t sz = *(const uint32_t*)(szr + 4 * ((2048 * t.n4 + 1024 * t.n2 + 8 * lane) / G));
+        return lo_h(sz) * (dot8(w, &X.x[0]) - hi_h(sz) * X.sum);
+    }
+    const int ns = t.K / 512;
+    float a = 0.0f, b = 0.0f;
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        const int sl = 4 * j + q;
+        if (sl < ns) {
+            const u32x4 w = *(const u32x4*)(row + 1024 * sl + 16 * lane);
+            const float* x = &X.x[8 * q];
+            a = fmaf(lo_h(w.x), x[0], a); b = fmaf(hi_h(w.x), x[1], b);
+            a = fmaf(lo_h(w.y), x[2], a); b = fmaf(hi_h(w.y), x[3], b);
+            a = fmaf(lo_h(w.z), x[4], a); b = fmaf(hi_h(w.z), x[5], b);
+            a = fmaf(lo_h(w.w), x[6], a); b = fmaf(hi_h(w.w), x[7], b);
+        }
+    }
+    return a + b;
+}
+
+// Sums 8 per-lane partials across the wave in 10 exchanges: after the call, lanes 8r..8r+7 hold
+// the total of partial r. Halving steps over lane bits 5, 4, 3 (each lane keeps the half its bit
+// selects and adds its partner's copy of it), then a plain sum over lane bits 2, 1, 0.
+__device__ __forceinline__ float reduce8(float (&v)[8], int lane) {
+    float h4[4], h2[2];
+    const bool b5 = lane & 32, b4 = lane & 16, b3 = lane & 8;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const float send = b5 ? v[i] : v[i + 4], keep = b5 ? v[i + 4] : v[i];
+        h4[i] = keep + __shfl_xor(send, 32, kWave);
+    }
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        const float send = b4 ? h4[i] : h4[i + 2], keep = b4 ? h4[i + 2] : h4[i];
+        h2[i] = keep + __shfl_xor(send, 16, kWave);
+    }
+    const float send = b3 ? h2[0] : h2[1], keep = b3 ? h2[1] : h2[0];
+    float t = keep + __shfl_xor(send, 8, kWave);
+    t += __shfl_xor(t, 4, kWave);
+    t += __shfl_xor(t, 2, kWave);
+    t += __shfl_xor(t, 1, kWave);
+    return t;
+}
+
+// Per-wave state carried across phases.
+struct WaveState {
+    float hown[2];       // residual rows this wave owns (uniform across lanes)
+    float conv[7];       // EP_CONV: lane i holds state[3] + weights[4] of its prefetched row i
+    float best;          // argmax of the LM head rows this lane reduced
+    uint32_t best_i;
+};
+
+struct Env {
+    const DecodeArgs* a;
+    int wg, nwg, wave, lane, gwm, nw;
+    float* xs;
+    uint8_t* reg;   // this wave's LDS region
+    uint8_t* regs;  // all regions
+    float* red;
+    int* bail;
+};
+
+__device__ __forceinline__ uint32_t tag_of(const DecodeArgs& a, int step, int p) {
+    return a.tag_base + (uint32_t)step * (uint32_t)a.nph + (uint32_t)p;
+}
+
+// ---- prefetch of a phase's data into the wave's region (and registers) ----
+
+__device__ __forceinline__ void prefetch(const Env& e, CPhase& P, int step, WaveState& ws) {
+    const DecodeArgs& a = *e.a;
+    const int lane = e.lane;
+    if (P.kind == PH_GEMV) {
+        const GemvGeo g = geo(P);
+        const Rows R = part(P.rows, e.gwm, e.nw);
+        const int cnt = min(R.n, g.cap);
+        dma_rows(P, g, R.r0, cnt, 0, e.reg, lane);
+        if (P.epi == EP_CONV && lane < min(R.n, 64)) {
+            const int row = R.r0 + lane;
+            if (row < P.conv_ch) {
+                const float* s = P.conv + (size_t)row * 3;
+                const float* w = P.conv_w + (size_t)row * 4;
+                ws.conv[0] = s[0]; ws.conv[1] = s[1]; ws.conv[2] = s[2];
+                ws.conv[3] = w[0]; ws.conv[4] = w[1]; ws.conv[5] = w[2]; ws.conv[6] = w[3];
+            }
+        }
+    } else if (P.kind == PH_GDN) {
+        const int it = e.wg;
+        if (it < P.heads * 16) {
+            const int h = it / 16, t = (it % 16) * 8 + e.wave;
+            // state column t of head h: S[h][t][0..127] (value-major), 512 bytes
+            dma_bytes((const uint8_t*)(P.rec + ((size_t)h * kDK + t) * kDK), 512, e.reg, lane);
+        }
+    } else if (P.kind == PH_ATTN) {
+        const int nkv = P.kv_heads, S = min(e.nwg / nkv, 128);
+        if (e.wg < nkv * S) {
+            const int g = e.wg / S, sp = e.wg % S;
+            const uint32_t pos = a.pos0 + (uint32_t)step, len = pos + 1;
+            const int p0 = (int)((uint64_t)sp * len / S), p1 = (int)((uint64_t)(sp + 1) * len / S);
+            const int half = lane / 32, li = lane % 32;
+            int bid[kAttnU];
+#pragma unroll
+            for (int u = 0; u < kAttnU; u++) {
+                const int p = p0 + 2 * (e.wave + kNW * u) + half;
+                bid[u] = p < p1 && p < (int)pos ? a.block_table[p / kBlk] : -1;
+            }
+#pragma unroll
+            for (int u = 0; u < kAttnU; u++) {
+                const int p = p0 + 2 * (e.wave + kNW * u) + half;
+                if (bid[u] >= 0) {
+                    const size_t at = (((size_t)bid[u] * nkv + g) * kBlk + p % kBlk) * kHeadDim + 8 * li;
+                    __builtin_amdgcn_global_load_lds((const void*)(P.kp + at), (lds_ptr_t)(e.reg + u * 2048), 16, 0, 0);
+                    __builtin_amdgcn_global_load_lds((const void*)(P.vp + at), (lds_ptr_t)(e.reg + u * 2048 + 1024), 16, 0, 0);
+                }
+            }
+        }
+    }
+}
+
+// ---- phases ----
+
+// Waits for the GEMV input vector and stages it in xs (times the RMSNorm gain); returns 1/rms (or 1).
+__device__ __forceinline__ float gemv_input(const Env& e, CPhase& P, int step, int p, WaveState& ws, const Ctl& c) {
+    const DecodeArgs& a = *e.a;
+    if (P.xin == XI_EMBED) return e.xs[kRawEmb - 1];  // staged with the embedding row
+    const uint32_t tag = tag_of(a, step, p - P.in_rel);
+    const uint64_t* in = P.in + (size_t)(step & 1) * P.in_stride;
+    float ss = 0.0f;
+    float* xs = e.xs;
+    const bool norm = P.xnorm == XN_NORM;
+    // the RMSNorm gains of the pairs this thread will poll, loaded before the poll so that their
+    // latency overlaps it (norm inputs fit one polling round: in_n <= 2 * kT * kPoll)
+    float2 gn[kPoll];
+    if (norm) {
+#pragma unroll
+        for (int j = 0; j < kPoll; j++) {
+            const int q = j * kT + (int)threadIdx.x;
+            gn[j] = 2 * q < P.in_n ? *(const float2*)(P.gain + 2 * q) : make_float2(1.0f, 1.0f);
+        }
+    }
+    poll_pairs(in, P.in_cap, (P.in_n + 1) / 2, tag, [](int q) { return 2 * q; },
+               [&](int q, float v0, float v1) {
+                   if (norm) {
+                       const int j = (q - (int)threadIdx.x) / kT;
+                       float2 g = gn[0];
+#pragma unroll
+                       for (int jj = 1; jj < kPoll; jj++)
+                           if (jj == j) g = gn[jj];
+                       ss += v0 * v0 + v1 * v1;
+                       v0 *= g.x;
+                       v1 *= g.y;
+                   }
+                   xs[2 * q] = v0;
+                   xs[2 * q + 1] = v1;
+               },
+               c);
+    if (norm) {
+        ss = wave_sum(ss);
+        if (e.lane == 0) e.red[e.wave] = ss;
+    }
+    bar();
+    if (!norm) return 1.0f;
+    float t = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kNW; w++) t += e.red[w];
+    return 1.0f / sqrtf(t / (float)P.k + a.eps);
+}
+
+// One GEMV phase for this wave's outputs. Output i sits in region slot i % cap; the first
+// min(n, cap) were prefetched. Outputs are computed in groups of up to 8 rows (8 / nm outputs):
+// for every step of x, the step's slice is read from LDS once and applied to the whole group; the
+// group's 8 partials are then reduced together. The group's slots are refilled with the outputs
+// cap further on, so up to cap - group outputs stay in flight while a group is computed.
+__device__ __forceinline__ void gemv_phase(const Env& e, CPhase& P, int step, int p, WaveState& ws, float inv) {
+    const DecodeArgs& a = *e.a;
+    const int lane = e.lane;
+    const GemvGeo g = geo(P);
+    const Rows R = part(P.rows, e.gwm, e.nw);
+    const uint32_t tag = tag_of(a, step, p);
+    uint64_t* out = P.out ? P.out + (size_t)(step & 1) * P.out_stride : nullptr;
+    if (R.n == 0) return;
+    const Step t = make_step(P.mkind, P.k);
+    const bool gdn = P.xnorm == XN_GDN;
+    const int H = gdn ? P.heads : 0;
+    const int gmax = 8 / g.nm;  // outputs per group
+    const int go = R.n <= g.cap ? min(gmax, R.n) : max(1, min(gmax, g.cap / 2));
+    int issued = min(R.n, g.cap);
+    XC X;
+    if (t.nsteps == 1) load_step(e.xs, t, 0, gdn, H, X, lane);
+    for (int o0 = 0; o0 < R.n; o0 += go) {
+        const int ng = min(go, R.n - o0), nr = ng * g.nm;
+        wait_vm((issued - o0 - ng) * g.per);
+        float acc[8];
+#pragma unroll
+        for (int r = 0; r < 8; r++) acc[r] = 0.0f;
+        for (int j = 0; j < t.nsteps; j++) {
+            if (t.nsteps > 1) load_step(e.xs, t, j, gdn, H, X, lane);
+#pragma unroll
+            for (int r = 0; r < 8; r++) {
+                if (r < nr) {
+                    const int i = r / g.nm, m = r % g.nm;
+                    const uint8_t* row = e.reg + ((o0 + i) % g.cap) * g.nm * g.stride + m * g.stride;
+                    acc[r] += step_dot(t, j, P.group, g.rb, row, X, lane);
+                }
+            }
+        }
+        // refill the group's slots with the outputs cap further on
+        for (int i = 0; i < ng && issued < R.n; i++, issued++) dma_rows(P, g, R.r0 + issued, 1, issued % g.cap, e.reg, lane);
+        const float tot = reduce8(acc, lane) * inv;   // lanes 8r..8r+7: row r of the group
+        const float up = __shfl_down(tot, 8, kWave);  // SwiGLU: the up row of the output
+        const int r = lane >> 3;
+        const int i = r / g.nm;
+        const bool lead = (lane & 7) == 0 && r % g.nm == 0 && i < ng;
+        const int o = R.r0 + o0 + i;
+        // conv state of output i (loaded at prefetch by lane i), moved to the lanes of row i while
+        // every lane is active (a shuffle from an inactive lane reads nothing)
+        float cv[7];
+        if (P.epi == EP_CONV) {
+#pragma unroll
+            for (int q = 0; q < 7; q++) cv[q] = __shfl(ws.conv[q], (o0 + i) & 63, kWave);
+        }
+        float y = tot;
+        if (P.epi == EP_RESID) {
+            // rows of h owned by this wave: outputs 0 and 1
+            const float t0 = __shfl(tot, 0, kWave), t1 = __shfl(tot, 8 * g.nm, kWave);
+            if (o0 == 0) {
+                ws.hown[0] += t0;
+                if (ng > 1) ws.hown[1] += t1;
+            } else {
+                ws.hown[1] += t0;
+            }
+            y = i == 0 && o0 == 0 ? ws.hown[0] : ws.hown[1];
+        }
+        if (lead) {
+            if (P.epi == EP_SWIGLU) y = silu(tot) * up;
+            else if (P.epi == EP_CONV && o < P.conv_ch) {
+                const float tt = cv[0] * cv[3] + cv[1] * cv[4] + cv[2] * cv[5] + tot * cv[6];
+                float* st = P.conv + (size_t)o * 3;
+                st[0] = cv[1]; st[1] = cv[2]; st[2] = tot;
+                y = silu(tt);
+            }
+            if (P.epi == EP_HEAD) {
+                a.logits[o] = y;
+                if (better(y, (uint32_t)o, ws.best, ws.best_i)) { ws.best = y; ws.best_i = (uint32_t)o; }
+            } else {
+                put(out, (uint32_t)o, y, tag);
+            }
+        }
+    }
+}
+
+// Gated DeltaNet step (kernels/src/shaders.rs:436-520 after the conv): workgroup = (head, 8 value
+// columns), wave = one value column t, lane = keys 2l, 2l+1 of the value-major state column.
+__device__ __forceinline__ void gdn_phase(const Env& e, CPhase& P, int step, int p, const Ctl& c) {
+    const DecodeArgs& a = *e.a;
+    const int H = P.heads, lane = e.lane;
+    const uint32_t tin = tag_of(a, step, p - P.in_rel), tag = tag_of(a, step, p);
+    const uint64_t* in = P.in + (size_t)(step & 1) * P.in_stride;
+    uint64_t* out = P.out + (size_t)(step & 1) * P.out_stride;
+    for (int it = e.wg; it < H * 16; it += e.nwg) {
+        const int h = it / 16, cb = it % 16;
+        // inputs: q_h, k_h (64 pairs each), v and z of the 8 columns (4 pairs each), a_h and b_h
+        const int qa = h * kDK, ka = H * kDK + h * kDK, va = 2 * H * kDK + h * kDK + cb * 8;
+        const int za = 3 * H * kDK + h * kDK + cb * 8, aa = 4 * H * kDK + h, ba = 4 * H * kDK + H + h;
+        float* xs = e.xs;
+        poll_pairs(in, P.in_cap, 138, tin,
+                   [&](int q) {
+                       if (q < 64) return qa + 2 * q;
+                       if (q < 128) return ka + 2 * (q - 64);
+                       if (q < 132) return va + 2 * (q - 128);
+                       if (q < 136) return za + 2 * (q - 132);
+                       return q == 136 ? (aa & ~1) : (ba & ~1);
+                   },
+                   [&](int q, float v0, float v1) {
+                       xs[2 * q] = v0;
+                       xs[2 * q + 1] = v1;
+                   },
+                   c);
+        bar();
+        if (*e.bail) return;
+        const int t = cb * 8 + e.wave;
+        const float2 q2 = *(const float2*)(xs + 2 * lane);
+        const float2 k2 = *(const float2*)(xs + 128 + 2 * lane);
+        const float v = xs[256 + e.wave], z = xs[264 + e.wave];
+        const float av = xs[272 + (aa & 1)], bv = xs[274 + (ba & 1)];
+        float* Sg = P.rec + ((size_t)h * kDK + t) * kDK + 2 * lane;
+        float2 s;
+        if (it == e.wg) {
+            __builtin_amdgcn_s_waitcnt(kWaitVm0);
+            s = *(const float2*)(e.reg + 8 * lane);
+        } else {
+            s = *(const float2*)Sg;
+        }
+        const float nq = 1.0f / sqrtf(wave_sum(q2.x * q2.x + q2.y * q2.y) + 1e-6f) * rsqrtf((float)kDK);
+        const float nk = 1.0f / sqrtf(wave_sum(k2.x * k2.x + k2.y * k2.y) + 1e-6f);
+        const float qx = q2.x * nq, qy = q2.y * nq, kx = k2.x * nk, ky = k2.y * nk;
+        const float kq = wave_sum(kx * qx + ky * qy);
+        cfloat* prm = (cfloat*)P.gain;
+        const float gg = expf(prm[H + h] * logf(1.0f + expf(av + prm[h])));
+        const float beta = 1.0f / (1.0f + expf(-bv));
+        const float sk = wave_sum(s.x * kx + s.y * ky);
+        const float sq = wave_sum(s.x * qx + s.y * qy);
+        const float d = beta * (v - gg * sk);
+        float2 sn;
+        sn.x = fmaf(gg, s.x, d * kx);
+        sn.y = fmaf(gg, s.y, d * ky);
+        *(float2*)Sg = sn;
+        const float o = gg * sq + d * kq;
+        if (lane == 0) {
+            put(out, (uint32_t)(h * kDK + t), o * silu(z) * prm[2 * H + t], tag);
+            e.red[e.wave] = o * o;
+        }
+        bar();
+        if (threadIdx.x == 0) {
+            float ss = 0.0f;
+            for (int w = 0; w < kNW; w++) ss += e.red[w];
+            put(out, (uint32_t)(H * kDK + h * 16 + cb), ss, tag);
+        }
+        bar();
+    }
+}
+
+// RMSNorm (weight w) + rotate-half RoPE of one 256-vector held 4 values per lane
+// (kernels/src/shaders.rs:575-593).
+__device__ __forceinline__ void norm_rope4(float (&v)[4], const float* w, const DecodeArgs& a, uint32_t pos, int lane) {
+    float ss = v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3];
+    ss = wave_sum(ss);
+    const float inv = 1.0f / sqrtf(ss / (float)kHeadDim + 1e-6f);
+    const float4 g = *(const float4*)(w + 4 * lane);
+    v[0] = v[0] * inv * g.x; v[1] = v[1] * inv * g.y; v[2] = v[2] * inv * g.z; v[3] = v[3] * inv * g.w;
+    const int half = a.rope_dim / 2, partner = half / 4;
+    float o[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int d = 4 * lane + i;
+        const float other_lo = __shfl_down(v[i], partner, kWave);  // value at d + half
+        const float other_hi = __shfl_up(v[i], partner, kWave);    // value at d - half
+        o[i] = v[i];
+        if (d < a.rope_dim) {
+            const int fi = d < half ? d : d - half;
+            float sn, cs;
+            sincosf((float)pos * a.inv_freq[fi], &sn, &cs);
+            o[i] = d < half ? v[i] * cs - other_lo * sn : v[i] * cs + other_hi * sn;
+        }
+    }
+    v[0] = o[0]; v[1] = o[1]; v[2] = o[2]; v[3] = o[3];
+}
+
+// Attention partials (kernels/src/shaders.rs:522-633 split over the context): workgroup =
+// (kv head g, split sp) over positions [p0, p1) of 0..pos; publishes (max, sum, acc[256]) per
+// q head of the group.
+__device__ __forceinline__ void attn_phase(const Env& e, CPhase& P, int step, int p, const Ctl& c) {
+    const DecodeArgs& a = *e.a;
+    const int nq = P.heads, nkv = P.kv_heads, G = nq / nkv, S = min(e.nwg / nkv, 128), lane = e.lane;
+    if (e.wg >= nkv * S) return;
+    const int g = e.wg / S, sp = e.wg % S;
+    const uint32_t pos = a.pos0 + (uint32_t)step, len = pos + 1;
+    const int p0 = (int)((uint64_t)sp * len / S), p1 = (int)((uint64_t)(sp + 1) * len / S);
+    const uint32_t tin = tag_of(a, step, p - P.in_rel), tag = tag_of(a, step, p);
+    const uint64_t* in = P.in + (size_t)(step & 1) * P.in_stride;
+    uint64_t* out = P.out + (size_t)(step & 1) * P.out_stride;
+    float* xs = e.xs;
+    // q of the group's heads -> xs[0, G*256), k -> xs[1024, 1280), v -> xs[1280, 1536)
+    const int qa = g * G * kHeadDim, ka = 2 * nq * kHeadDim + g * kHeadDim, va = ka + nkv * kHeadDim;
+    const int nqp = G * kHeadDim / 2;
+    poll_pairs(in, P.in_cap, nqp + 256, tin,
+               [&](int q) { return q < nqp ? qa + 2 * q : (q < nqp + 128 ? ka + 2 * (q - nqp) : va + 2 * (q - nqp - 128)); },
+               [&](int q, float v0, float v1) {
+                   const int d = q < nqp ? 2 * q : 1024 + 2 * (q - nqp);
+                   xs[d] = v0;
+                   xs[d + 1] = v1;
+               },
+               c);
+    bar();
+    if (*e.bail) return;
+    float* qs = xs + 1536;  // [G][256], normed, rotated, pre-scaled by 1/sqrt(256)
+    float* kc = xs + 2560;  // current key and value, f16-rounded
+    float* vc = xs + 2816;
+    if (e.wave < G) {
+        float v[4];
+        const float4 f = *(const float4*)(xs + e.wave * kHeadDim + 4 * lane);
+        v[0] = f.x; v[1] = f.y; v[2] = f.z; v[3] = f.w;
+        norm_rope4(v, P.gain, a, pos, lane);
+#pragma unroll
+        for (int i = 0; i < 4; i++) qs[e.wave * kHeadDim + 4 * lane + i] = v[i] * 0.0625f;
+    } else if (e.wave == G) {
+        float v[4];
+        const float4 f = *(const float4*)(xs + 1024 + 4 * lane);
+        v[0] = f.x; v[1] = f.y; v[2] = f.z; v[3] = f.w;
+        norm_rope4(v, P.gain + kHeadDim, a, pos, lane);
+        const float4 vv = *(const float4*)(xs + 1280 + 4 * lane);
+        const float val[4] = {vv.x, vv.y, vv.z, vv.w};
+        uint16_t kh[4], vh[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            kh[i] = f2h(v[i]);
+            vh[i] = f2h(val[i]);
+            kc[4 * lane + i] = h2f(kh[i]);
+            vc[4 * lane + i] = h2f(vh[i]);
+        }
+        if (sp == S - 1) {
+            // append at pos: two lanes' 8-byte halves form one 16-byte agent-scope store
+            const size_t at = (((size_t)a.block_table[pos / kBlk] * nkv + g) * kBlk + pos % kBlk) * kHeadDim;
+            const uint32_t k01 = (uint32_t)kh[0] | ((uint32_t)kh[1] << 16), k23 = (uint32_t)kh[2] | ((uint32_t)kh[3] << 16);
+            const uint32_t v01 = (uint32_t)vh[0] | ((uint32_t)vh[1] << 16), v23 = (uint32_t)vh[2] | ((uint32_t)vh[3] << 16);
+            const uint32_t nk01 = __shfl_down(k01, 1, kWave), nk23 = __shfl_down(k23, 1, kWave);
+            const uint32_t nv01 = __shfl_down(v01, 1, kWave), nv23 = __shfl_down(v23, 1, kWave);
+            if ((lane & 1) == 0) {
+                u32x4 kw, vw;
+                kw.x = k01; kw.y = k23; kw.z = nk01; kw.w = nk23;
+                vw.x = v01; vw.y = v23; vw.z = nv01; vw.w = nv23;
+                st16_agent(P.kp + at + 4 * lane, kw);
+                st16_agent(P.vp + at + 4 * lane, vw);
+            }
+        }
+    }
+    bar();
+    // wave: positions p0 + 2*(wave + 8u) + half; 32 lanes per position, 8 dims per lane
+    const int half = lane / 32, li = lane % 32;
+    float qr[4][8], acc[4][8], m[4], l[4];
+#pragma unroll
+    for (int gi = 0; gi < 4; gi++) {
+        m[gi] = -INFINITY;
+        l[gi] = 0.0f;
+#pragma unroll
+        for (int d = 0; d < 8; d++) {
+            qr[gi][d] = gi < G ? qs[gi * kHeadDim + 8 * li + d] : 0.0f;
+            acc[gi][d] = 0.0f;
+        }
+    }
+    __builtin_amdgcn_s_waitcnt(kWaitVm0);  // prefetched K/V rows
+    for (int u = 0;; u++) {
+        const int pp = p0 + 2 * (e.wave + kNW * u);
+        if (pp >= p1) break;  // wave-uniform
+        const int ps = pp + half;
+        const bool valid = ps < p1;
+        float kf[8], vf[8];
+        if (ps == (int)pos) {
+#pragma unroll
+            for (int d = 0; d < 8; d++) { kf[d] = kc[8 * li + d]; vf[d] = vc[8 * li + d]; }
+        } else if (valid) {
+            u32x4 kw, vw;
+            if (u < kAttnU) {
+                kw = *(const u32x4*)(e.reg + u * 2048 + 16 * lane);
+                vw = *(const u32x4*)(e.reg + u * 2048 + 1024 + 16 * lane);
+            } else {
+                const size_t at = (((size_t)a.block_table[ps / kBlk] * nkv + g) * kBlk + ps % kBlk) * kHeadDim + 8 * li;
+                kw = *(const u32x4*)(P.kp + at);
+                vw = *(const u32x4*)(P.vp + at);
+            }
+            kf[0] = lo_h(kw.x); kf[1] = hi_h(kw.x); kf[2] = lo_h(kw.y); kf[3] = hi_h(kw.y);
+            kf[4] = lo_h(kw.z); kf[5] = hi_h(kw.z); kf[6] = lo_h(kw.w); kf[7] = hi_h(kw.w);
+            vf[0] = lo_h(vw.x); vf[1] = hi_h(vw.x); vf[2] = lo_h(vw.y); vf[3] = hi_h(vw.y);
+            vf[4] = lo_h(vw.z); vf[5] = hi_h(vw.z); vf[6] = lo_h(vw.w); vf[7] = hi_h(vw.w);
+        } else {
+#pragma unroll
+            for (int d = 0; d < 8; d++) { kf[d] = 0.0f; vf[d] = 0.0f; }
+        }
+#pragma unroll
+        for (int gi = 0; gi < 4; gi++) {
+            if (gi < G) {
+                float s = 0.0f;
+#pragma unroll
+                for (int d = 0; d < 8; d++) s = fmaf(qr[gi][d], kf[d], s);
+#pragma unroll
+                for (int mk = 16; mk >= 1; mk >>= 1) s += __shfl_xor(s, mk, kWave);  // 32-lane sum
+                if (valid) {
+                    const float mn = fmaxf(m[gi], s);
+                    const float corr = expf(m[gi] - mn), pw = expf(s - mn);
+                    m[gi] = mn;
+                    l[gi] = l[gi] * corr + pw;
+#pragma unroll
+                    for (int d = 0; d < 8; d++) acc[gi][d] = fmaf(pw, vf[d], acc[gi][d] * corr);
+                }
+            }
+        }
+    }
+    // merge the two position halves of the wave, then write the wave's partial into its region
+    float* wp = (float*)e.reg;  // [G][258]: m, l, acc[256]
+#pragma unroll
+    for (int gi = 0; gi < 4; gi++) {
+        if (gi < G) {
+            const float mo = __shfl_xor(m[gi], 32, kWave), lo = __shfl_xor(l[gi], 32, kWave);
+            const float mn = fmaxf(m[gi], mo);
+            const float ca = mn == -INFINITY ? 0.0f : expf(m[gi] - mn), cb = mn == -INFINITY ? 0.0f : expf(mo - mn);
+#pragma unroll
+            for (int d = 0; d < 8; d++) acc[gi][d] = acc[gi][d] * ca + __shfl_xor(acc[gi][d], 32, kWave) * cb;
+            l[gi] = l[gi] * ca + lo * cb;
+            m[gi] = mn;
+            if (half == 0) {
+#pragma unroll
+                for (int d = 0; d < 8; d++) wp[gi * 258 + 2 + 8 * li + d] = acc[gi][d];
+                if (li == 0) { wp[gi * 258] = m[gi]; wp[gi * 258 + 1] = l[gi]; }
+            }
+        }
+    }
+    bar();
+    // merge the 8 waves; threads 0..255 = dims
+    if (threadIdx.x < kHeadDim) {
+        const int t = threadIdx.x;
+        for (int gi = 0; gi < G; gi++) {
+            float mn = -INFINITY;
+            for (int w = 0; w < kNW; w++) mn = fmaxf(mn, ((const float*)(e.regs + w * kRegion))[gi * 258]);
+            float ls = 0.0f, ac = 0.0f;
+            for (int w = 0; w < kNW; w++) {
+                const float* pw = (const float*)(e.regs + w * kRegion) + gi * 258;
+                const float cw = pw[0] == -INFINITY ? 0.0f : expf(pw[0] - mn);
+                ls += pw[1] * cw;
+                ac += pw[2 + t] * cw;
+            }
+            const uint32_t base = (uint32_t)(((g * S + sp) * G + gi) * 258);
+            put(out, base + 2 + t, ac, tag);
+            if (t == 0) {
+                put(out, base, mn, tag);
+                put(out, base + 1, ls, tag);
+            }
+        }
+    }
+    bar();  // the regions are free again
+}
+
+// Combine of the attention partials: workgroup = (q head h, 64 dims c); times sigmoid(gate).
+__device__ __forceinline__ void comb_phase(const Env& e, CPhase& P, int step, int p, const Ctl& c) {
+    const DecodeArgs& a = *e.a;
+    const int nq = P.heads, nkv = P.kv_heads, G = nq / nkv, S = min(e.nwg / nkv, 128);
+    if (e.wg >= nq * 4) return;
+    const int h = e.wg / 4, cq = e.wg % 4, g = h / G, gi = h % G;
+    const uint32_t tin = tag_of(a, step, p - P.in_rel), tin2 = tag_of(a, step, p - P.in2_rel), tag = tag_of(a, step, p);
+    const uint64_t* in = P.in + (size_t)(step & 1) * P.in_stride;
+    const uint64_t* in2 = P.in2 + (size_t)(step & 1) * P.in2_stride;
+    uint64_t* out = P.out + (size_t)(step & 1) * P.out_stride;
+    float* xs = e.xs;
+    // xs: ml[2S] then acc[S][64] then gate[64]
+    poll_pairs(in, P.in_cap, S * 33, tin,
+               [&](int q) {
+                   const int s = q / 33, j = q % 33;
+                   const int base = ((g * S + s) * G + gi) * 258;
+                   return j == 0 ? base : base + 2 + 64 * cq + 2 * (j - 1);
+               },
+               [&](int q, float v0, float v1) {
+                   const int s = q / 33, j = q % 33;
+                   const int d = j == 0 ? 2 * s : 2 * S + 64 * s + 2 * (j - 1);
+                   xs[d] = v0;
+                   xs[d + 1] = v1;
+               },
+               c);
+    const int ga = nq * kHeadDim + h * kHeadDim + 64 * cq;
+    poll_pairs(in2, P.in2_cap, 32, tin2, [&](int q) { return ga + 2 * q; },
+               [&](int q, float v0, float v1) {
+                   xs[2 * S + 64 * S + 2 * q] = v0;
+                   xs[2 * S + 64 * S + 2 * q + 1] = v1;
+               },
+               c);
+    bar();
+    if (*e.bail) return;
+    if (threadIdx.x < 64) {
+        const int d = threadIdx.x;
+        float mn = -INFINITY;
+        for (int s = 0; s < S; s++) mn = fmaxf(mn, xs[2 * s]);
+        float ls = 0.0f, ac = 0.0f;
+        for (int s = 0; s < S; s++) {
+            const float ms = xs[2 * s];
+            if (ms == -INFINITY) continue;
+            const float cw = expf(ms - mn);
+            ls += xs[2 * s + 1] * cw;
+            ac += xs[2 * S + 64 * s + d] * cw;
+        }
+        const float gate = xs[2 * S + 64 * S + d];
+        put(out, (uint32_t)(h * kHeadDim + 64 * cq + d), ac / ls / (1.0f + expf(-gate)), tag);
+    }
+    bar();
+}
+
+__device__ __forceinline__ float embed_val(const DecodeArgs& a, uint32_t tok, int c) {
+    if (a.emb_kind == 0) return h2f(((const uint16_t*)a.emb_w)[(size_t)tok * a.hidden + c]);
+    const uint32_t word = ((const uint32_t*)a.emb_w)[(size_t)tok * (a.hidden / 8) + c / 8];
+    const uint32_t sz = a.emb_sz[(size_t)tok * (a.hidden / a.emb_group) + c / a.emb_group];
+    return ((float)((word >> (4 * (c % 8))) & 15u) - hi_h(sz)) * lo_h(sz);
+}
+
+__device__ __forceinline__ void trace_done(const Env& e, int inst) {
+    const DecodeArgs& a = *e.a;
+    if (a.trace && inst < a.trace_cap) {
+        bar();
+        if (threadIdx.x == 0) {
+            const unsigned long long t = __builtin_amdgcn_s_memrealtime();
+            atomicMax(a.trace + 2 + 3 * inst, t);
+            atomicMin(a.trace + 3 + 3 * inst, t);
+        }
+    }
+}
+__device__ __forceinline__ void trace_in(const Env& e, int inst) {
+    const DecodeArgs& a = *e.a;
+    if (a.trace && inst < a.trace_cap && e.wg == 0 && threadIdx.x == 0) a.trace[4 + 3 * inst] = __builtin_amdgcn_s_memrealtime();
+}
+
+}  // namespace
+
+__global__ __launch_bounds__(kT, 1) void k_decode(DecodeArgs a) {
+    __shared__ __attribute__((aligned(16))) float xs[kXs];
+    __shared__ __attribute__((aligned(16))) uint8_t regs[kNW * kRegion];
+    __shared__ float red[2 * kNW];
+    __shared__ uint32_t redi[kNW];
+    __shared__ int bail;
+    Env e;
+    e.a = &a;
+    e.wg = blockIdx.x;
+    e.nwg = gridDim.x;
+    e.wave = threadIdx.x / kWave;
+    e.lane = threadIdx.x % kWave;
+    e.gwm = e.wave * e.nwg + e.wg;
+    e.nw = e.nwg * kNW;
+    e.xs = xs;
+    e.reg = regs + e.wave * kRegion;
+    e.regs = regs;
+    e.red = red;
+    e.bail = &bail;
+    Ctl c{a.err, a.spin_limit, &bail};
+    CPhase* prog = (CPhase*)a.prog;
+    if (threadIdx.x == 0) bail = 0;
+    if (a.trace && e.wg == 0 && threadIdx.x == 0) a.trace[0] = __builtin_amdgcn_s_memrealtime();
+    WaveState ws;
+    ws.hown[0] = ws.hown[1] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 7; i++) ws.conv[i] = 0.0f;
+    ws.best = -INFINITY;
+    ws.best_i = 0xFFFFFFFFu;
+    const Rows own = part(a.hidden, e.gwm, e.nw);  // residual rows of this wave (<= 2)
+    bar();
+
+    uint32_t token = a.feed ? a.tok[0] : a.ids[0];
+    prefetch(e, prog[0], 0, ws);
+    int pf = 0;
+    for (int step = 0; step < a.n_steps; step++) {
+        if (pf == a.nph) pf = 0;
+        const uint32_t pos = a.pos0 + (uint32_t)step;
+        const bool head = a.head == 1 || (a.head == 2 && step == a.n_steps - 1);
+        // embedding row (kernels/src/shaders.rs:405-434): raw at xs[kRawEmb..], times the first
+        // layer's input-norm gain at xs[0..]; 1/rms at xs[kRawEmb - 1]
+        {
+            CPhase& P0 = prog[0];
+            float ss = 0.0f;
+            for (int cc = threadIdx.x; cc < a.hidden; cc += kT) {
+                const float v = embed_val(a, token, cc);
+                xs[kRawEmb + cc] = v;
+                xs[cc] = v * P0.gain[cc];
+                ss += v * v;
+            }
+            ss = wave_sum(ss);
+            if (e.lane == 0) red[e.wave] = ss;
+            bar();
+            if (threadIdx.x == 0) {
+                float t = 0.0f;
+                for (int w = 0; w < kNW; w++) t += red[w];
+                xs[kRawEmb - 1] = 1.0f / sqrtf(t / (float)a.hidden + a.eps);
+            }
+            if (own.n > 0) ws.hown[0] = xs[kRawEmb + own.r0];
+            if (own.n > 1) ws.hown[1] = xs[kRawEmb + own.r0 + 1];
+            bar();
+        }
+        ws.best = -INFINITY;
+        ws.best_i = 0xFFFFFFFFu;
+        for (int p = 0; p < a.nph; p++) {
+            CPhase& P = prog[p];
+            if (P.is_head && !head) continue;
+            const int inst = step * a.nph + p;
+            switch (P.kind) {
+                case PH_GEMV: {
+                    const float inv = gemv_input(e, P, step, p, ws, c);
+                    if (bail) { __builtin_amdgcn_s_waitcnt(kWaitAll); return; }
+                    trace_in(e, inst);
+                    gemv_phase(e, P, step, p, ws, inv);
+                    break;
+                }
+                case PH_GDN: trace_in(e, inst); gdn_phase(e, P, step, p, c); break;
+                case PH_ATTN: trace_in(e, inst); attn_phase(e, P, step, p, c); break;
+                default: trace_in(e, inst); comb_phase(e, P, step, p, c); break;
+            }
+            if (bail) { __builtin_amdgcn_s_waitcnt(kWaitAll); return; }
+            trace_done(e, inst);
+            // prefetch the next phase that uses the regions (a combine does not): later in this
+            // step, or phase 0 of the next step
+            int np = p + 1;
+            while (np < a.nph && ((prog[np].is_head && !head) || prog[np].kind == PH_COMB)) np++;
+            if (np < a.nph) {
+                if (np != pf) {
+                    prefetch(e, prog[np], step, ws);
+                    pf = np;
+                }
+            } else if (step + 1 < a.n_steps && pf != a.nph) {
+                prefetch(e, prog[0], step + 1, ws);
+                pf = a.nph;  // phase 0 of the next step
+            }
+        }
+        if (head) {
+            // greedy pick over the LM head rows (argmax_partial / argmax_final,
+            // kernels/src/shaders.rs:635-699): waves -> workgroup -> every workgroup
+            if (a.argmax) {
+#pragma unroll
+                for (int mk = 32; mk >= 1; mk >>= 1) {
+                    const float ov = __shfl_xor(ws.best, mk, kWave);
+                    const uint32_t oi = (uint32_t)__shfl_xor((int)ws.best_i, mk, kWave);
+                    if (better(ov, oi, ws.best, ws.best_i)) { ws.best = ov; ws.best_i = oi; }
+                }
+                if (e.lane == 0) { red[e.wave] = ws.best; redi[e.wave] = ws.best_i; }
+                bar();
+                const uint32_t tag = tag_of(a, step, a.nph - 1) ;
+                uint64_t* am = a.am + (size_t)(step & 1) * a.am_stride;
+                if (threadIdx.x == 0) {
+                    float b = red[0];
+                    uint32_t bi = redi[0];
+                    for (int w = 1; w < kNW; w++)
+                        if (better(red[w], redi[w], b, bi)) { b = red[w]; bi = redi[w]; }
+                    put(am, 2 * e.wg, b, tag);
+                    put(am, 2 * e.wg + 1, __uint_as_float(bi), tag);
+                }
+                float b = -INFINITY;
+                uint32_t bi = 0xFFFFFFFFu;
+                poll_pairs(am, 2 * e.nwg, e.nwg, tag, [](int q) { return 2 * q; },
+                           [&](int q, float v0, float v1) {
+                               const uint32_t i1 = __float_as_uint(v1);
+                               if (better(v0, i1, b, bi)) { b = v0; bi = i1; }
+                           },
+                           c);
+#pragma unroll
+                for (int mk = 32; mk >= 1; mk >>= 1) {
+                    const float ov = __shfl_xor(b, mk, kWave);
+                    const uint32_t oi = (uint32_t)__shfl_xor((int)bi, mk, kWave);
+                    if (better(ov, oi, b, bi)) { b = ov; bi = oi; }
+                }
+                bar();
+                if (e.lane == 0) { red[e.wave] = b; redi[e.wave] = bi; }
+                bar();
+                if (bail) { __builtin_amdgcn_s_waitcnt(kWaitAll); return; }
+                float bb = red[0];
+                uint32_t bbi = redi[0];
+                for (int w = 1; w < kNW; w++)
+                    if (better(red[w], redi[w], bb, bbi)) { bb = red[w]; bbi = redi[w]; }
+                const uint32_t pick = bbi == 0xFFFFFFFFu ? 0u : bbi;
+                if (e.wg == 0 && threadIdx.x == 0) {
+                    a.tok[0] = pick;
+                    a.tok[1] = pos + 1;
+                    if (a.out_ids) {
+                        const uint32_t n = a.tok[2];
+                        if (n < a.out_cap) a.out_ids[n] = pick;
+                        a.tok[2] = n + 1;
+                    }
+                }
+                token = pick;
+                bar();
+            }
+        }
+        if (step + 1 < a.n_steps && !a.feed) token = a.ids[step + 1];
+    }
+    __builtin_amdgcn_s_waitcnt(kWaitAll);
+    if (a.trace && e.wg == 0 && threadIdx.x == 0) a.trace[1] = __builtin_amdgcn_s_memrealtime();
+}
+
+int decode_gemv_variant(int kind, int k) {
+    if (k <= 0 || k % 512 != 0) return -1;
+    if (kind == 1) return k <= 6144 ? 1 : -1;  // the x slice layout holds up to 96 values per lane
+    return k <= 6144 ? 0 : -1;
+}
+
+hipError_t launch_decode(const DecodeArgs& a, int grid, hipStream_t st) {
+    void* args[] = {(void*)&a};
+    return hipLaunchCooperativeKernel((const void*)k_decode, dim3(grid), dim3(kT), args, 0, st);
+}
+
+int decode_max_grid() {
+    int dev = 0, cus = 0, per = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, (const void*)k_decode, kT, 0) != hipSuccess) return 0;
+    return per >= 1 ? cus : 0;
+}
+
+}  // namespace qne

@@ -1,0 +1,100 @@
+// Host-visible description of the persistent decode kernel (kernels/decode.hip).
+//
+// A decode window runs as ONE cooperative launch. The per-token work is a fixed program of
+// phases (built once at load, kept in LDS by the kernel); each phase consumes a vector published
+// by the previous phase and publishes its own. Vectors are handed over as tagged values: every f32
+// is stored next to a 32-bit tag (the phase's sequence number) in one 8-byte agent-scope store,
+// and a consumer polls until every tag it needs carries the expected number. No grid barrier and
+// no cache-maintenance fence is needed: the tag proves the value next to it is the new one.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace qne {
+
+enum PhaseKind { PH_GEMV = 0, PH_GDN = 1, PH_ATTN = 2, PH_COMB = 3 };
+// Input of a GEMV phase: the previous phase's published vector, or the step's embedding row.
+enum { XI_EXCH = 0, XI_EMBED = 1 };
+// Transform of that input: none, RMSNorm with `gain`, or the GDN output norm (per-head 1/rms from
+// the published partial sums of squares).
+enum { XN_PLAIN = 0, XN_NORM = 1, XN_GDN = 2 };
+// Output of a GEMV phase: plain store, GDN causal conv + SiLU (first conv_ch rows), residual add
+// into the rows of h the wave owns, SwiGLU of (gate, up) row pairs, LM head (logits + argmax).
+enum { EP_STORE = 0, EP_CONV = 1, EP_RESID = 2, EP_SWIGLU = 3, EP_HEAD = 4 };
+
+constexpr int kDecodeThreads = 512;
+constexpr int kMaxPhases = 192;
+constexpr int kHeadDim = 256;  // attention head size the kernel is written for
+
+// One phase. `variant` selects the compiled GEMV shape (matrix kind and K).
+struct Phase {
+    int kind = 0, variant = -1;
+    int mkind = 0, k = 0, group = 64, rows = 0;  // GEMV matrix; rows = outputs (SwiGLU: pairs)
+    int xin = XI_EXCH, xnorm = XN_PLAIN, epi = EP_STORE;
+    int in_n = 0;       // values of the input vector (GEMV)
+    int conv_ch = 0;    // EP_CONV: rows that go through the causal conv
+    int heads = 0;      // GDN heads, or attention q heads
+    int kv_heads = 0;   // attention
+    int in_rel = 1;     // the input was published `in_rel` phases earlier in the same step
+    int in2_rel = 0;    // second input (COMB: the gate in the in-projection output)
+    int is_head = 0;    // phase runs only on steps that compute logits
+    const void* w = nullptr;
+    const uint32_t* sz = nullptr;
+    const float* gain = nullptr;    // XN_NORM gain; GDN: dt_bias, A_neg_exp, norm_w; ATTN: q_norm, k_norm
+    const float* conv_w = nullptr;  // EP_CONV [conv_ch][4]
+    float* conv = nullptr;          // EP_CONV state [conv_ch][3]
+    float* rec = nullptr;           // GDN state [heads][dv][dk] (value-major)
+    uint16_t* kp = nullptr;         // attention pools [blocks][kv_heads][16][256]
+    uint16_t* vp = nullptr;
+    uint64_t* in = nullptr;         // input exchange buffer (step parity 0; parity 1 at + in_stride)
+    uint64_t* in2 = nullptr;
+    uint64_t* out = nullptr;        // output exchange buffer
+    uint32_t in_stride = 0, in2_stride = 0, out_stride = 0;  // u64 entries
+    uint32_t in_cap = 0, in2_cap = 0;  // entries readable from in / in2 (bounds of the polling loads)
+};
+
+struct DecodeArgs {
+    const Phase* prog = nullptr;
+    int nph = 0;  // phases per token
+    // embedding (read by every workgroup at the start of a step)
+    const void* emb_w = nullptr;
+    const uint32_t* emb_sz = nullptr;
+    int emb_kind = 0, emb_group = 64;
+    int hidden = 0, vocab = 0;
+    float eps = 1e-6f;
+    int rope_dim = 64;
+    const float* inv_freq = nullptr;
+    const int32_t* block_table = nullptr;
+    int max_blocks = 0;
+    float* logits = nullptr;
+    uint64_t* am = nullptr;  // argmax exchange: 2 entries per workgroup, parity stride am_stride
+    uint32_t am_stride = 0;
+    // tokens
+    uint32_t* tok = nullptr;        // {token, pos, n_out, 0}
+    const uint32_t* ids = nullptr;  // feed 0: token of step s is ids[s]
+    uint32_t* out_ids = nullptr;    // greedy picks appended at tok[2]
+    uint32_t out_cap = 0;
+    int n_steps = 1;
+    uint32_t pos0 = 0;
+    int feed = 0;    // 0: tokens from ids, 1: greedy feedback
+    int head = 0;    // 0: no LM head, 1: every step, 2: last step only
+    int argmax = 0;  // greedy pick after the LM head
+    uint32_t tag_base = 1;  // tag of phase p of step s = tag_base + s * nph + p
+    unsigned* err = nullptr;  // [0] set on a polling timeout
+    unsigned spin_limit = 1u << 20;
+    // Optional device timeline (ticks of the constant-rate wall clock): trace[0] start, trace[1]
+    // end (workgroup 0); for phase instance i = step * nph + p: trace[2 + 3i] latest and
+    // trace[3 + 3i] earliest completion over workgroups, trace[4 + 3i] when workgroup 0 had its
+    // input. `trace_cap` phase instances are recorded.
+    unsigned long long* trace = nullptr;
+    int trace_cap = 0;
+};
+
+// GEMV shapes compiled into the kernel: variant id of (matrix kind, K), or -1.
+int decode_gemv_variant(int kind, int k);
+hipError_t launch_decode(const DecodeArgs& a, int grid, hipStream_t st);
+// Largest cooperative grid for the decode kernel on the current device (one workgroup per CU).
+int decode_max_grid();
+
+}  // namespace qne

@@ -12,7 +12,7 @@
 #include "error.hpp"
 #include "hip_util.hpp"
 #include "json.hpp"
-#include "kernels/engine.hpp"
+#include "kernels/decode.hpp"
 #include "kernels/launch.hpp"
 
 namespace qne {
@@ -120,7 +120,7 @@ void Model::release() {
     if (host_ids_) (void)hipHostFree(host_ids_);
     if (host_err_) (void)hipHostFree(host_err_);
     host_tok_ = nullptr; host_logits_ = nullptr; host_ids_ = nullptr; host_err_ = nullptr;
-    delete (EngineArgs*)engine_args_;
+    delete (DecodeArgs*)engine_args_;
     engine_args_ = nullptr;
     if (stream_) (void)hipStreamDestroy(stream_);
     stream_ = nullptr;
@@ -355,85 +355,212 @@ void Model::build_graphs() {
     QNE_HIP(hipStreamSynchronize(stream_));
 }
 
-// The persistent engine's view of the model: per-layer descriptors in device memory and the
-// scratch buffers of its phases.
+// The persistent decode kernel's program: one Phase per piece of the token graph of
+// model.rs:220-269, with its exchange buffers. Every (layer, phase) publishes into a buffer of its
+// own, doubled by step parity, so a buffer is rewritten two steps after it was last read.
 void Model::setup_engine() {
     const ModelConfig& c = cfg_;
-    engine_grid_ = engine_max_grid();
+    engine_grid_ = decode_max_grid();
     if (engine_grid_ <= 0) throw Error(QNE_EDEVICE, "the persistent decode kernel cannot be made co-resident");
-    if (c.rope_dim % 8 != 0) throw Error(QNE_EFORMAT, "unsupported model architecture: rope_dim must be a multiple of 8");
-    if (c.hidden > 3968 || c.hidden % 512 != 0)
-        throw Error(QNE_EFORMAT, "unsupported model architecture: the persistent engine needs hidden % 512 == 0 and "
-                                 "hidden <= 3968 (load with {\"engine\": \"graph\"})");
-    auto emat = [](const DevMat& d) {
-        EMat e;
-        e.w = d.w; e.sz = d.sz; e.kind = d.kind; e.rows = d.rows; e.k = d.k; e.group = d.group;
-        return e;
+    const int grid = engine_grid_, nw = grid * (kDecodeThreads / 64);
+    auto unsupported = [](const std::string& why) {
+        return Error(QNE_EFORMAT, "unsupported model architecture for the persistent decode kernel: " + why +
+                                      " (load with {\"engine\": \"graph\"})");
     };
-    std::vector<ELayer> el(layers_.size());
-    for (size_t i = 0; i < layers_.size(); i++) {
+    if (c.hidden % 512 != 0 || c.hidden > 4096) throw unsupported("hidden must be a multiple of 512 and <= 4096");
+    if (c.hidden > 2 * nw || c.hidden < grid) throw unsupported("hidden must lie in [workgroups, 2 * waves]");
+    if (c.head_dim != kHeadDim) throw unsupported("head_dim must be 256");
+    if (c.n_kv_heads <= 0 || c.n_q_heads % c.n_kv_heads != 0 || c.n_q_heads / c.n_kv_heads > 4)
+        throw unsupported("n_q_heads / n_kv_heads must be 1..4");
+    if (c.n_q_heads * 4 > grid) throw unsupported("too many attention heads for the grid");
+    if (c.rope_dim % 8 != 0 || c.rope_dim > c.head_dim) throw unsupported("rope_dim must be a multiple of 8");
+    if (c.gdn_dk != 128 || c.gdn_dv != 128) throw unsupported("GDN dk and dv must be 128");
+    if (c.conv_kernel != 4) throw unsupported("the GDN conv kernel must be 4");
+    const int S = std::min(grid / c.n_kv_heads, 128), G = c.n_q_heads / c.n_kv_heads;
+    if (S < 1) throw unsupported("too many kv heads");
+    const int H = c.gdn_heads;
+    if (H * 128 + H * 16 > 12288) throw unsupported("too many GDN heads");
+    if (2 * S + 64 * S + 64 > 12288) throw unsupported("too many attention splits");
+
+    // exchange buffers: sizes per (layer, phase), allocated in one arena
+    struct Buf {
+        uint32_t n;
+        size_t off;
+    };
+    std::vector<Buf> bufs;
+    size_t total = 0;
+    auto buf = [&](uint32_t n) {
+        n = (n + 1) & ~1u;
+        bufs.push_back({n, total});
+        total += 2 * (size_t)n;
+        return (int)bufs.size() - 1;
+    };
+    std::vector<Phase> prog;
+    auto gemv = [&](const DevMat& m, int rows, int epi) {
+        Phase P;
+        P.kind = PH_GEMV;
+        P.mkind = m.kind; P.k = m.k; P.group = m.group; P.rows = rows; P.epi = epi;
+        P.w = m.w; P.sz = m.sz;
+        if (decode_gemv_variant(m.kind, m.k) < 0) throw unsupported("matrix width " + std::to_string(m.k));
+        const int rb = m.kind ? m.k / 2 : m.k * 2, szb = m.kind ? (m.k / m.group) * 4 : 0;
+        if ((rb + szb) * (epi == EP_SWIGLU ? 2 : 1) > 12 * 1024) throw unsupported("rows too wide for the LDS region");
+        if (m.kind == MAT_Q4 && m.group != 32 && m.group != 64 && m.group != 128)
+            throw unsupported("q4 group size " + std::to_string(m.group));
+        if (epi == EP_CONV && (rows + nw - 1) / nw > 64) throw unsupported("too many in-projection rows per wave");
+        return P;
+    };
+    // input links: (phase index, buffer id) of each published vector
+    std::vector<int> out_buf;
+    int h_prev = -1;  // buffer of the residual stream published by the previous layer's down
+    for (int i = 0; i < c.layers; i++) {
         const DevLayer& L = layers_[i];
-        ELayer& E = el[i];
-        E.in = emat(L.in); E.out = emat(L.out); E.gu = emat(L.gate_up); E.down = emat(L.down);
-        E.in_norm = L.input_norm; E.post_norm = L.post_norm; E.norms = L.norms;
-        E.conv_w = L.conv_w; E.prm = L.gdn_params; E.conv = L.conv_state; E.rec = L.rec;
-        E.k_pool = L.k_pool; E.v_pool = L.v_pool; E.attn = L.attn ? 1 : 0;
+        // mixer_in
+        Phase in = gemv(L.in, L.in.rows, L.attn ? EP_STORE : EP_CONV);
+        in.xin = i == 0 ? XI_EMBED : XI_EXCH;
+        in.xnorm = XN_NORM;
+        in.gain = L.input_norm;
+        in.in_n = c.hidden;
+        if (!L.attn) {
+            in.conv_ch = c.conv_channels();
+            in.conv = L.conv_state;
+            in.conv_w = L.conv_w;
+        }
+        const int b_proj = buf((uint32_t)L.in.rows);
+        prog.push_back(in); out_buf.push_back(b_proj);
+        int b_mixed;
+        int in_rel_out = 1;
+        if (!L.attn) {
+            Phase g;
+            g.kind = PH_GDN;
+            g.heads = H;
+            g.gain = L.gdn_params;
+            g.rec = L.rec;
+            b_mixed = buf((uint32_t)(H * 128 + H * 16));
+            prog.push_back(g); out_buf.push_back(b_mixed);
+        } else {
+            Phase at;
+            at.kind = PH_ATTN;
+            at.heads = c.n_q_heads;
+            at.kv_heads = c.n_kv_heads;
+            at.gain = L.norms;
+            at.kp = L.k_pool;
+            at.vp = L.v_pool;
+            const int b_part = buf((uint32_t)(c.n_kv_heads * S * G * 258));
+            prog.push_back(at); out_buf.push_back(b_part);
+            Phase cb;
+            cb.kind = PH_COMB;
+            cb.heads = c.n_q_heads;
+            cb.kv_heads = c.n_kv_heads;
+            cb.in2_rel = 2;
+            b_mixed = buf((uint32_t)(c.n_q_heads * 256));
+            prog.push_back(cb); out_buf.push_back(b_mixed);
+        }
+        Phase mo = gemv(L.out, c.hidden, EP_RESID);
+        mo.xnorm = L.attn ? XN_PLAIN : XN_GDN;
+        mo.heads = H;
+        mo.in_n = L.attn ? c.attn_out() : H * 128 + H * 16;
+        mo.in_rel = in_rel_out;
+        const int b_h1 = buf((uint32_t)c.hidden);
+        prog.push_back(mo); out_buf.push_back(b_h1);
+        if (L.gate_up.rows != 2 * c.intermediate) throw unsupported("gate_up rows");
+        Phase gu = gemv(L.gate_up, c.intermediate, EP_SWIGLU);
+        gu.xnorm = XN_NORM;
+        gu.gain = L.post_norm;
+        gu.in_n = c.hidden;
+        const int b_act = buf((uint32_t)c.intermediate);
+        prog.push_back(gu); out_buf.push_back(b_act);
+        Phase dn = gemv(L.down, c.hidden, EP_RESID);
+        dn.in_n = c.intermediate;
+        h_prev = buf((uint32_t)c.hidden);
+        prog.push_back(dn); out_buf.push_back(h_prev);
     }
-    ELayer* d_layers = (ELayer*)dalloc(el.size() * sizeof(ELayer));
-    QNE_HIP(hipMemcpy(d_layers, el.data(), el.size() * sizeof(ELayer), hipMemcpyHostToDevice));
-    EngineArgs* a = new EngineArgs();
+    Phase hd = gemv(lm_head_, c.vocab, EP_HEAD);
+    hd.xnorm = XN_NORM;
+    hd.gain = final_norm_;
+    hd.in_n = c.hidden;
+    hd.is_head = 1;
+    prog.push_back(hd); out_buf.push_back(-1);
+    if ((int)prog.size() > kMaxPhases) throw unsupported("too many layers");
+    for (const Phase& P : prog)
+        if (P.kind == PH_GEMV && (P.in_n > 12288 || P.in_n > P.k + 2048 * (P.xnorm == XN_GDN)))
+            throw unsupported("input vector too long");
+
+    exch_ = (uint64_t*)dalloc(total * 8);
+    exch_bytes_ = total * 8;
+    QNE_HIP(hipMemset(exch_, 0, exch_bytes_));
+    auto base = [&](int b) { return exch_ + bufs[b].off; };
+    for (size_t p = 0; p < prog.size(); p++) {
+        Phase& P = prog[p];
+        if (out_buf[p] >= 0) {
+            P.out = base(out_buf[p]);
+            P.out_stride = bufs[out_buf[p]].n;
+        }
+        if (P.kind == PH_GEMV && P.xin == XI_EMBED) continue;
+        const int src = (int)p - P.in_rel;
+        if (src < 0 || out_buf[src] < 0) throw Error(QNE_EINVAL, "decode program: bad input link");
+        P.in = base(out_buf[src]);
+        P.in_stride = P.in_cap = bufs[out_buf[src]].n;
+        if (P.in2_rel > 0) {
+            const int s2 = (int)p - P.in2_rel;
+            P.in2 = base(out_buf[s2]);
+            P.in2_stride = P.in2_cap = bufs[out_buf[s2]].n;
+        }
+    }
+    nph_ = (int)prog.size();
+    Phase* d_prog = (Phase*)dalloc(prog.size() * sizeof(Phase));
+    QNE_HIP(hipMemcpy(d_prog, prog.data(), prog.size() * sizeof(Phase), hipMemcpyHostToDevice));
+    am_ = (uint64_t*)dalloc((size_t)4 * grid * 8);
+    QNE_HIP(hipMemset(am_, 0, (size_t)4 * grid * 8));
+
+    DecodeArgs* a = new DecodeArgs();
     engine_args_ = a;
-    a->layers = d_layers;
-    a->n_layers = (int)layers_.size();
-    a->embed = emat(embed_);
-    a->lm = emat(lm_head_);
-    a->final_norm = final_norm_;
-    a->hidden = c.hidden; a->inter = c.intermediate; a->vocab = c.vocab;
-    a->nq = c.n_q_heads; a->nkv = c.n_kv_heads; a->rope_dim = c.rope_dim; a->gdn_heads = c.gdn_heads;
-    a->max_blocks = (max_context_ + 15) / 16;
-    a->splits = std::max(1, engine_grid_ / c.n_kv_heads / 2);
-    a->eps = c.eps;
-    a->inv_freq = inv_freq_;
-    a->block_table = block_table_;
-    a->h = h_; a->proj = proj_; a->mixed = mixed_; a->act = act_; a->logits = logits_;
-    a->gdn_sq = (float*)dalloc((size_t)c.gdn_heads * 16 * 4);
-    const size_t G = (size_t)(c.n_q_heads / c.n_kv_heads);
-    a->att_ml = (float*)dalloc((size_t)c.n_kv_heads * a->splits * G * 2 * 4);
-    a->att_acc = (float*)dalloc((size_t)c.n_kv_heads * a->splits * G * c.head_dim * 4);
-    a->att_cnt = (unsigned*)dalloc((size_t)c.n_kv_heads * 4);
-    QNE_HIP(hipMemset(a->att_cnt, 0, (size_t)c.n_kv_heads * 4));
-    a->am_val = (float*)dalloc((size_t)engine_grid_ * 4);
-    a->am_idx = (uint32_t*)dalloc((size_t)engine_grid_ * 4);
-    a->tok = tok_;
-    a->ids = ids_;
-    a->out_ids = out_ids_;
-    a->out_cap = (uint32_t)max_context_;
+    a->prog = d_prog;
+    a->nph = nph_;
+    a->emb_w = embed_.w; a->emb_sz = embed_.sz; a->emb_kind = embed_.kind; a->emb_group = embed_.group;
+    a->hidden = c.hidden; a->vocab = c.vocab; a->eps = c.eps;
+    a->rope_dim = c.rope_dim; a->inv_freq = inv_freq_;
+    a->block_table = block_table_; a->max_blocks = (max_context_ + 15) / 16;
+    a->logits = logits_;
+    a->am = am_; a->am_stride = (uint32_t)(2 * grid);
+    a->tok = tok_; a->ids = ids_; a->out_ids = out_ids_; a->out_cap = (uint32_t)max_context_;
     eng_bar_ = (unsigned*)dalloc(64);
-    a->bar = eng_bar_;
-    a->err = eng_bar_ + 1;
+    QNE_HIP(hipMemset(eng_bar_, 0, 64));
+    a->err = eng_bar_;
     QNE_HIP(hipHostMalloc((void**)&host_err_, 64, hipHostMallocDefault));
     host_err_[0] = 0;
+    tag_base_ = 1;
     dispatches_ = 1;  // one launch covers a whole decode window
     QNE_HIP(hipDeviceSynchronize());
 }
 
 void Model::run_engine(const EngineRun& r) {
-    EngineArgs a = *(const EngineArgs*)engine_args_;
+    DecodeArgs a = *(const DecodeArgs*)engine_args_;
+    const uint64_t tags = (uint64_t)r.n_steps * (uint64_t)nph_;
+    if ((uint64_t)tag_base_ + tags >= 0xFFFF0000ull) {
+        // tags would wrap: clear every exchange buffer and start again
+        QNE_HIP(hipMemsetAsync(exch_, 0, exch_bytes_, stream_));
+        QNE_HIP(hipMemsetAsync(am_, 0, (size_t)4 * engine_grid_ * 8, stream_));
+        tag_base_ = 1;
+    }
     a.feed = r.feed;
     a.head = r.head;
     a.argmax = r.argmax;
     a.n_steps = r.n_steps;
     a.pos0 = r.pos0;
     a.out_ids = r.record_ids ? out_ids_ : nullptr;
+    a.trace = r.trace;
+    a.trace_cap = r.trace_cap;
+    a.tag_base = tag_base_;
+    tag_base_ += (uint32_t)tags;
     QNE_HIP(hipMemsetAsync(eng_bar_, 0, 8, stream_));
-    QNE_HIP(launch_engine(a, engine_grid_, stream_));
-    QNE_HIP(hipMemcpyAsync(host_err_, eng_bar_ + 1, 4, hipMemcpyDeviceToHost, stream_));
+    QNE_HIP(launch_decode(a, engine_grid_, stream_));
+    QNE_HIP(hipMemcpyAsync(host_err_, eng_bar_, 4, hipMemcpyDeviceToHost, stream_));
 }
 
 void Model::check_engine_error() {
     if (persistent_ && host_err_ && host_err_[0] != 0) {
         host_err_[0] = 0;
-        throw Error(QNE_EDEVICE, "GPU wait failed: a grid barrier of the decode kernel timed out");
+        throw Error(QNE_EDEVICE, "GPU wait failed: a phase of the decode kernel timed out waiting for its input");
     }
 }
 
@@ -647,6 +774,74 @@ double Model::profile_token() {
     (void)hipEventDestroy(a);
     (void)hipEventDestroy(b);
     return ms;
+}
+
+// Per-phase device times of one greedy decode token (the counterpart of Gpu::profile's
+// per-label timestamp sums, kernels/src/lib.rs:366-396). For every phase the timeline gives when
+// workgroup 0 had its input and when the slowest and the fastest workgroup were done:
+//   work_ms = slowest done - input ready, exchange_ms = input ready - previous slowest done.
+std::string Model::profile_token_json() {
+    if (!persistent_) throw Error(QNE_EINVAL, "the phase profile needs the persistent engine");
+    uint32_t t, p;
+    last_token(&t, &p);
+    if (p >= (uint32_t)max_context_) throw Error(QNE_ECONTEXT, "context limit reached");
+    const int nph = nph_;
+    const size_t n = 2 + 3 * (size_t)nph;
+    std::vector<unsigned long long> tr(n, 0ull);
+    for (int b = 0; b < nph; b++) tr[3 + 3 * b] = ~0ull;
+    unsigned long long* d = (unsigned long long*)dalloc(n * 8);
+    QNE_HIP(hipMemcpy(d, tr.data(), n * 8, hipMemcpyHostToDevice));
+    EngineRun r;
+    r.feed = 1; r.head = 1; r.argmax = 1; r.n_steps = 1; r.pos0 = p;
+    r.trace = d;
+    r.trace_cap = nph;
+    run_engine(r);
+    sync();
+    QNE_HIP(hipMemcpy(tr.data(), d, n * 8, hipMemcpyDeviceToHost));
+    int khz = 0;
+    QNE_HIP(hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, device_));
+    const double tick_ms = khz > 0 ? 1.0 / (double)khz : 1e-5;
+    auto ms = [&](unsigned long long a, unsigned long long b) { return b > a ? (double)(b - a) * tick_ms : 0.0; };
+    std::map<std::string, double> total, work, wait;
+    std::string phases = "[";
+    unsigned long long prev = tr[0];
+    int l = 0, k = 0;
+    for (int b = 0; b < nph; b++) {
+        std::string label;
+        if (l >= cfg_.layers) {
+            label = "lm_head";
+        } else {
+            const bool at = layers_[l].attn;
+            static const char* gdn_names[5] = {"mixer_in", "gdn", "mixer_out", "gate_up", "down"};
+            static const char* attn_names[6] = {"mixer_in", "attention", "combine", "mixer_out", "gate_up", "down"};
+            label = std::string(at ? "attn." : "gdn.") + (at ? attn_names[k] : gdn_names[k]);
+            if (++k == (at ? 6 : 5)) { k = 0; l++; }
+        }
+        const unsigned long long dmax = tr[2 + 3 * b], dmin = tr[3 + 3 * b], in = tr[4 + 3 * b];
+        total[label] += ms(prev, dmax);
+        work[label] += ms(in, dmax);
+        wait[label] += ms(prev, in);
+        char buf[192];
+        std::snprintf(buf, sizeof buf, "%s[\"%s\",%.5f,%.5f,%.5f]", b ? "," : "", label.c_str(), ms(in, dmax),
+                      ms(in, dmin), ms(prev, in));
+        phases += buf;
+        prev = dmax;
+    }
+    phases += "]";
+    auto obj = [](const std::map<std::string, double>& m) {
+        std::string o = "{";
+        for (auto& kv : m) {
+            char buf[96];
+            std::snprintf(buf, sizeof buf, "%s\"%s\":%.5f", o.size() > 1 ? "," : "", kv.first.c_str(), kv.second);
+            o += buf;
+        }
+        return o + "}";
+    };
+    char head[160];
+    std::snprintf(head, sizeof head, "{\"total_ms\":%.5f,\"tail_ms\":%.5f,\"tick_ms\":%.3g,", ms(tr[0], tr[1]),
+                  ms(prev, tr[1]), tick_ms);
+    return std::string(head) + "\"labels\":" + obj(total) + ",\"work_ms\":" + obj(work) + ",\"exchange_ms\":" +
+           obj(wait) + ",\"phases\":" + phases + "}";
 }
 
 }  // namespace qne

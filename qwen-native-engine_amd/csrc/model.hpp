@@ -45,6 +45,8 @@ struct EngineRun {
     int n_steps = 1;
     uint32_t pos0 = 0;
     bool record_ids = false;
+    unsigned long long* trace = nullptr;
+    int trace_cap = 0;
 };
 
 LoadOptions parse_options(const char* json);
@@ -66,6 +68,9 @@ class Model {
     void last_token(uint32_t* token, uint32_t* next_pos);
     size_t decode(size_t n, uint32_t window, const uint32_t* stop, size_t nstop, uint32_t* out, size_t cap);
     double profile_token();
+    // One greedy decode token with the device timeline on; JSON of per-phase times (persistent
+    // engine only).
+    std::string profile_token_json();
     void last_decode_timing(double* ms, size_t* steps) const {
         *ms = last_decode_ms_;
         *steps = last_decode_steps_;
@@ -125,8 +130,13 @@ class Model {
     // persistent engine
     bool persistent_ = true;
     int engine_grid_ = 0;
-    void* engine_args_ = nullptr;  // host copy of EngineArgs (opaque here)
-    unsigned* eng_bar_ = nullptr;  // [0] barrier counter, [1] error flag
+    void* engine_args_ = nullptr;  // host copy of DecodeArgs (opaque here)
+    unsigned* eng_bar_ = nullptr;  // [0] error flag of the decode kernel
+    uint64_t* exch_ = nullptr;     // tagged exchange buffers of the decode program
+    size_t exch_bytes_ = 0;
+    uint64_t* am_ = nullptr;       // argmax exchange
+    int nph_ = 0;                  // phases per token
+    uint32_t tag_base_ = 1;
     unsigned* host_err_ = nullptr;  // pinned
     double last_decode_ms_ = 0.0;
     size_t last_decode_steps_ = 0;

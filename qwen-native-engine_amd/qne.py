@@ -58,6 +58,7 @@ def load_library(path: str | os.PathLike | None = None):
         "qne_vocab": ([c_p, ctypes.POINTER(c_u32)], c_i),
         "qne_max_context": ([c_p, ctypes.POINTER(c_u32)], c_i),
         "qne_profile_token": ([c_p, ctypes.POINTER(ctypes.c_double)], c_i),
+        "qne_profile_token_json": ([c_p, ctypes.c_char_p, c_sz], c_i),
         "qne_last_decode_timing": ([c_p, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(c_sz)], c_i),
         "qne_gemv": ([c_i, c_p, c_p, c_i, c_i, c_i, c_p, c_p, c_f, c_p, c_i, c_p], c_i),
         "qne_pack_sz_q4g": ([c_p, c_p, c_sz, c_p], c_i),
@@ -199,6 +200,17 @@ class Model:
         v = ctypes.c_double()
         self._c(self._lib.qne_profile_token(self._h, ctypes.byref(v)))
         return v.value
+
+    def profile_token_detail(self) -> dict:
+        """Model::profile_token (model.rs:305) with the per-phase timeline: consumes one greedy token."""
+        import json
+        buf = ctypes.create_string_buffer(1 << 16)
+        self._c(self._lib.qne_profile_token_json(self._h, buf, len(buf)))
+        return json.loads(buf.value.decode())
+
+    def profile_labels(self) -> dict:
+        """label -> ms for one greedy token, as the reference's profile_token returns."""
+        return self.profile_token_detail()["labels"]
 
     def last_decode_timing(self):
         """(device ms, steps) of the windows of the last decode call (HIP events)."""
