@@ -21,6 +21,34 @@ __device__ __forceinline__ float hi_h(uint32_t w) { return h2f((uint16_t)(w >> 1
 __device__ __forceinline__ float silu(float x) { return x / (1.0f + expf(-x)); }
 __device__ __forceinline__ float sigmoid(float x) { return 1.0f / (1.0f + expf(-x)); }
 
+// Cross-lane moves without the LDS crossbar: DPP within rows of 16 lanes, and the gfx950
+// permlane swaps across rows (v_permlane16_swap: lane ^ 16, v_permlane32_swap: lane ^ 32).
+#define QNE_DPP(v, ctrl) __uint_as_float(__builtin_amdgcn_update_dpp(0u, __float_as_uint(v), (ctrl), 0xF, 0xF, false))
+constexpr int kDppXor1 = 0xB1;        // quad_perm [1,0,3,2]
+constexpr int kDppXor2 = 0x4E;        // quad_perm [2,3,0,1]
+constexpr int kDppHalfMirror = 0x141;  // lane i <-> 7 - i within 8
+constexpr int kDppMirror = 0x140;      // lane i <-> 15 - i within 16
+constexpr int kDppRor8 = 0x128;        // lane i <- (i + 8) % 16 within 16, i.e. lane ^ 8
+__device__ __forceinline__ float lane_xor32(float v, int lane) {
+    const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float((lane & 32) ? p[0] : p[1]);
+}
+__device__ __forceinline__ float lane_xor16(float v, int lane) {
+    const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float((lane & 16) ? p[0] : p[1]);
+}
+// Sum over the 64 lanes of a wave with DPP and permlane swaps; every lane receives the total.
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+    const int lane = (int)__lane_id();
+    v += QNE_DPP(v, kDppXor1);
+    v += QNE_DPP(v, kDppXor2);
+    v += QNE_DPP(v, kDppHalfMirror);
+    v += QNE_DPP(v, kDppMirror);
+    v += lane_xor16(v, lane);
+    v += lane_xor32(v, lane);
+    return v;
+}
+
 // Sum over the 64 lanes of a wave; every lane receives the total.
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll

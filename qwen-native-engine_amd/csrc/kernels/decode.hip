@@ -31,6 +31,7 @@
 //    reduces all of them, so the next step needs no separate broadcast.
 #include "common.hpp"
 #include "decode.hpp"
+#include "gemv.hpp"
 
 namespace qne {
 
@@ -38,14 +39,15 @@ namespace {
 
 constexpr int kT = kDecodeThreads;
 constexpr int kNW = kT / kWave;        // 8 waves
-constexpr int kXs = 12288;             // floats of LDS input staging
-constexpr int kRawEmb = 8192;          // xs offset of the raw embedding row (hidden <= 4096)
-constexpr int kRegion = 12 * 1024;     // bytes of LDS per wave (prefetched weights / state / K,V)
+constexpr int kXs = 6144;              // floats of LDS input staging
+constexpr int kHalf = 8 * 1024;        // bytes of one half of a wave's LDS region
+constexpr int kWaveLds = 2 * kHalf;    // a wave's region: the running phase's half and the next one's
 constexpr int kPoll = 6;               // tagged pairs a thread polls at once
-constexpr int kSC1 = 16;               // buffer cache policy: agent-scope coherent access
+constexpr int kSC1 = 16;               // cache policy: agent-scope coherent access
+constexpr int kNT = 2;                 // cache policy: non-temporal (streamed once; keeps L2 for reused data)
 constexpr int kBlk = 16;               // KV block size (positions)
 constexpr int kDK = 128;               // GDN dk = dv
-constexpr int kAttnU = kRegion / 2048; // prefetched K/V wave-loads (2 positions each) per wave
+constexpr int kAttnU = kHalf / 2048;   // prefetched K/V wave-loads (2 positions each) per wave
 constexpr int kWaitVm0 = 0x0F70;
 constexpr int kWaitAll = 0;
 
@@ -164,18 +166,21 @@ __device__ __forceinline__ Rows part(int rows, int gw, int nw) {
 
 // ---- DMA into the wave's LDS region ----
 
+// Weights and recurrent state are streamed once per token, so they are loaded non-temporal: the
+// L2 then keeps the small data every phase re-reads (program, norms, block table, conv weights).
 __device__ __forceinline__ void dma_bytes(const uint8_t* src, int bytes, uint8_t* dst, int lane) {
     for (int u = 0; u * 1024 < bytes; u++) {
         const int off = u * 1024 + lane * 16;
         if (off < bytes)
-            __builtin_amdgcn_global_load_lds((const void*)(src + off), (lds_ptr_t)(dst + u * 1024), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds((const void*)(src + off), (lds_ptr_t)(dst + u * 1024), 16, 0, kNT);
     }
 }
 
 // Geometry of a GEMV phase's rows in a region.
 struct GemvGeo {
-    int rb, szb, stride, nm, cap;  // row bytes, scale/zero bytes, bytes per row, rows per output, outputs per region
+    int rb, szb, stride, nm, cap;  // row bytes, scale/zero bytes, bytes per row, rows per output, outputs per half
     int per;                       // DMA instructions per output
+    int conv;                      // EP_CONV: bytes of conv state + weights per output (16 + 16)
 };
 __device__ __forceinline__ GemvGeo geo(CPhase& P) {
     GemvGeo g;
@@ -183,13 +188,14 @@ __device__ __forceinline__ GemvGeo geo(CPhase& P) {
     g.szb = P.mkind ? (P.k / P.group) * 4 : 0;
     g.stride = g.rb + g.szb;
     g.nm = P.epi == EP_SWIGLU ? 2 : 1;
-    g.cap = kRegion / (g.stride * g.nm);
+    g.conv = P.epi == EP_CONV ? 32 : 0;
+    g.cap = kHalf / (g.stride * g.nm + g.conv);
     g.per = g.nm * ((g.rb + 1023) / 1024 + (g.szb + 1023) / 1024);
     return g;
 }
 
 // DMA of outputs [o0, o0 + cnt) (row pairs for SwiGLU) into region slots starting at `slot`.
-__device__ __forceinline__ void dma_rows(CPhase& P, const GemvGeo& g, int o0, int cnt, int slot, uint8_t* reg,
+__device__ __forceinline__ void dma_rows(CPhase& P, const GemvGeo& g, int o0, int cnt, int slot, uint8_t* __restrict__ reg,
                                          int lane) {
     const uint8_t* w = (const uint8_t*)P.w;
     const uint8_t* sz = (const uint8_t*)P.sz;
@@ -210,7 +216,7 @@ __device__ __forceinline__ void dma_rows(CPhase& P, const GemvGeo& g, int o0, in
 //  - q4 rows (K <= 6144): step s < n4 is the 2048-column slab s (32 values per lane, 16 bytes of
 //    nibbles), then at most one 1024-column slab (16 values, 8 bytes) and one 512-column slab
 //    (8 values, 4 bytes);
-//  - f16 rows: step j covers the 512-column slabs 4j..4j+3 (8 values, 16 bytes per lane each).
+//  - f16 rows: step j is the 512-column slab j (8 values, 16 bytes per lane).
 struct Step {
     int kind, K, n4, n2, n1, nsteps;
 };
@@ -221,8 +227,27 @@ __device__ __forceinline__ Step make_step(int kind, int K) {
     t.n4 = K / 2048;
     t.n2 = (K % 2048) / 1024;
     t.n1 = (K % 1024) / 512;
-    t.nsteps = kind ? t.n4 + t.n2 + t.n1 : (K + 2047) / 2048;
+    t.nsteps = kind ? t.n4 + t.n2 + t.n1 : K / 512;
     return t;
+}
+
+// Position in xs of input value k of a GEMV of this shape. Each slab's lane slices are stored
+// chunk-major: chunk c (4 values) of lane l at slab_base + 256c + 4l, so a wave reading chunk c of
+// its slices touches 64 consecutive 16-byte words (no LDS bank conflicts). Values past K (the GDN
+// partial sums of squares) keep their index.
+__device__ __forceinline__ int xs_slot(const Step& t, int k) {
+    if (k >= t.K) return k;
+    int base, sh;  // slab base and log2(values per lane)
+    if (t.kind == 1) {
+        if (k < 2048 * t.n4) { base = k & ~2047; sh = 5; }
+        else if (k < 2048 * t.n4 + 1024 * t.n2) { base = 2048 * t.n4; sh = 4; }
+        else { base = 2048 * t.n4 + 1024 * t.n2; sh = 3; }
+    } else {
+        base = k & ~511;
+        sh = 3;
+    }
+    const int w = k - base, l = w >> sh, i = w & ((1 << sh) - 1);
+    return base + ((i >> 2) << 8) + (l << 2) + (i & 3);
 }
 
 struct XC {
@@ -242,33 +267,23 @@ __device__ __forceinline__ void load_step(const float* xs, const Step& t, int j,
         return 1.0f / sqrtf(s / (float)kDK + 1e-6f);
     };
     X.sum = 0.0f;
+    int base, nch, cpl;  // slab base, chunks of 4 per lane, values per lane
     if (t.kind == 1) {
-        int c0, n;
-        if (j < t.n4) { c0 = 2048 * j + 32 * lane; n = 32; }
-        else if (j < t.n4 + t.n2) { c0 = 2048 * t.n4 + 16 * lane; n = 16; }
-        else { c0 = 2048 * t.n4 + 1024 * t.n2 + 8 * lane; n = 8; }
-        const float r = rn(c0);
-#pragma unroll
-        for (int i = 0; i < 32; i += 4) {
-            if (i < n) {
-                const float4 f = *(const float4*)(xs + c0 + i);
-                X.x[i] = f.x * r; X.x[i + 1] = f.y * r; X.x[i + 2] = f.z * r; X.x[i + 3] = f.w * r;
-                X.sum += X.x[i] + X.x[i + 1] + X.x[i + 2] + X.x[i + 3];
-            }
-        }
+        if (j < t.n4) { base = 2048 * j; nch = 8; cpl = 32; }
+        else if (j < t.n4 + t.n2) { base = 2048 * t.n4; nch = 4; cpl = 16; }
+        else { base = 2048 * t.n4 + 1024 * t.n2; nch = 2; cpl = 8; }
     } else {
-        const int ns = t.K / 512;
+        base = 512 * j;
+        nch = 2;
+        cpl = 8;
+    }
+    const float r = rn(base + cpl * lane);
 #pragma unroll
-        for (int q = 0; q < 4; q++) {
-            const int sl = 4 * j + q;
-            if (sl < ns) {
-                const int c0 = 512 * sl + 8 * lane;
-                const float r = rn(c0);
-                const float4 a = *(const float4*)(xs + c0), b = *(const float4*)(xs + c0 + 4);
-                float* d = &X.x[8 * q];
-                d[0] = a.x * r; d[1] = a.y * r; d[2] = a.z * r; d[3] = a.w * r;
-                d[4] = b.x * r; d[5] = b.y * r; d[6] = b.z * r; d[7] = b.w * r;
-            }
+    for (int c = 0; c < 8; c++) {
+        if (c < nch) {
+            const float4 f = *(const float4*)(xs + base + 256 * c + 4 * lane);
+            X.x[4 * c] = f.x * r; X.x[4 * c + 1] = f.y * r; X.x[4 * c + 2] = f.z * r; X.x[4 * c + 3] = f.w * r;
+            X.sum += X.x[4 * c] + X.x[4 * c + 1] + X.x[4 * c + 2] + X.x[4 * c + 3];
         }
     }
 }
@@ -306,52 +321,44 @@ __device__ __forceinline__ float step_dot(const Step& t, int j, int G, int rb, c
         const uint32_t sz = *(const uint32_t*)(szr + 4 * ((2048 * t.n4 + 1024 * t.n2 + 8 * lane) / G));
         return lo_h(sz) * (dot8(w, &X.x[0]) - hi_h(sz) * X.sum);
     }
-    const int ns = t.K / 512;
-    float a = 0.0f, b = 0.0f;
-#pragma unroll
-    for (int q = 0; q < 4; q++) {
-        const int sl = 4 * j + q;
-        if (sl < ns) {
-            const u32x4 w = *(const u32x4*)(row + 1024 * sl + 16 * lane);
-            const float* x = &X.x[8 * q];
-            a = fmaf(lo_h(w.x), x[0], a); b = fmaf(hi_h(w.x), x[1], b);
-            a = fmaf(lo_h(w.y), x[2], a); b = fmaf(hi_h(w.y), x[3], b);
-            a = fmaf(lo_h(w.z), x[4], a); b = fmaf(hi_h(w.z), x[5], b);
-            a = fmaf(lo_h(w.w), x[6], a); b = fmaf(hi_h(w.w), x[7], b);
-        }
-    }
+    const u32x4 w = *(const u32x4*)(row + 1024 * j + 16 * lane);
+    const float* x = &X.x[0];
+    float a = lo_h(w.x) * x[0], b = hi_h(w.x) * x[1];
+    a = fmaf(lo_h(w.y), x[2], a); b = fmaf(hi_h(w.y), x[3], b);
+    a = fmaf(lo_h(w.z), x[4], a); b = fmaf(hi_h(w.z), x[5], b);
+    a = fmaf(lo_h(w.w), x[6], a); b = fmaf(hi_h(w.w), x[7], b);
     return a + b;
 }
 
-// Sums 8 per-lane partials across the wave in 10 exchanges: after the call, lanes 8r..8r+7 hold
-// the total of partial r. Halving steps over lane bits 5, 4, 3 (each lane keeps the half its bit
-// selects and adds its partner's copy of it), then a plain sum over lane bits 2, 1, 0.
+// Sums 8 per-lane partials across the wave: after the call, lanes 8r..8r+7 hold the total of
+// partial r. Halving steps over lane bits 5, 4, 3 (each lane keeps the half its bit selects and
+// adds its partner's copy of it, exchanged with permlane swaps and DPP), then a plain sum over
+// lane bits 2, 1, 0 with DPP.
 __device__ __forceinline__ float reduce8(float (&v)[8], int lane) {
     float h4[4], h2[2];
     const bool b5 = lane & 32, b4 = lane & 16, b3 = lane & 8;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         const float send = b5 ? v[i] : v[i + 4], keep = b5 ? v[i + 4] : v[i];
-        h4[i] = keep + __shfl_xor(send, 32, kWave);
+        h4[i] = keep + lane_xor32(send, lane);
     }
 #pragma unroll
     for (int i = 0; i < 2; i++) {
         const float send = b4 ? h4[i] : h4[i + 2], keep = b4 ? h4[i + 2] : h4[i];
-        h2[i] = keep + __shfl_xor(send, 16, kWave);
+        h2[i] = keep + lane_xor16(send, lane);
     }
     const float send = b3 ? h2[0] : h2[1], keep = b3 ? h2[1] : h2[0];
-    float t = keep + __shfl_xor(send, 8, kWave);
-    t += __shfl_xor(t, 4, kWave);
-    t += __shfl_xor(t, 2, kWave);
-    t += __shfl_xor(t, 1, kWave);
+    float t = keep + QNE_DPP(send, kDppRor8);
+    t += QNE_DPP(t, kDppXor1);
+    t += QNE_DPP(t, kDppXor2);
+    t += QNE_DPP(t, kDppHalfMirror);
     return t;
 }
 
 // Per-wave state carried across phases.
 struct WaveState {
-    float hown[2];       // residual rows this wave owns (uniform across lanes)
-    float conv[7];       // EP_CONV: lane i holds state[3] + weights[4] of its prefetched row i
-    float best;          // argmax of the LM head rows this lane reduced
+    float hown[2];   // residual rows this wave owns (uniform across lanes)
+    float best;      // argmax of the LM head rows this lane reduced
     uint32_t best_i;
 };
 
@@ -359,8 +366,7 @@ struct Env {
     const DecodeArgs* a;
     int wg, nwg, wave, lane, gwm, nw;
     float* xs;
-    uint8_t* reg;   // this wave's LDS region
-    uint8_t* regs;  // all regions
+    uint8_t* regs;  // all waves' regions
     float* red;
     int* bail;
 };
@@ -369,23 +375,52 @@ __device__ __forceinline__ uint32_t tag_of(const DecodeArgs& a, int step, int p)
     return a.tag_base + (uint32_t)step * (uint32_t)a.nph + (uint32_t)p;
 }
 
-// ---- prefetch of a phase's data into the wave's region (and registers) ----
+// Whether the LM head has a register-streaming path (else it goes through the LDS region).
+__device__ __forceinline__ bool head_fast(CPhase& P) {
+    return P.epi == EP_HEAD && (P.mkind == 0 || P.group == 64) && (P.k == 512 || P.k == 1024 || P.k == 2048);
+}
+// Phases whose data is prefetched into a wave's LDS half.
+__device__ __forceinline__ bool uses_region(CPhase& P) {
+    return (P.kind == PH_GEMV && !head_fast(P)) || P.kind == PH_GDN || P.kind == PH_ATTN;
+}
+__device__ __forceinline__ bool head_at(const DecodeArgs& a, int step) {
+    return a.head == 1 || (a.head == 2 && step == a.n_steps - 1);
+}
+// The next phase after (step, p) that reads the regions, or false past the window.
+__device__ __forceinline__ bool next_region_phase(const DecodeArgs& a, CPhase* prog, int step, int p, int& ns, int& np) {
+    ns = step;
+    np = p;
+    for (int guard = 0; guard <= a.nph; guard++) {
+        if (++np >= a.nph) {
+            np = 0;
+            if (++ns >= a.n_steps) return false;
+        }
+        CPhase& Q = prog[np];
+        if (Q.is_head && !head_at(a, ns)) continue;
+        if (uses_region(Q)) return true;
+    }
+    return false;
+}
 
-__device__ __forceinline__ void prefetch(const Env& e, CPhase& P, int step, WaveState& ws) {
+// ---- prefetch of a phase's data into one half of the wave's LDS region ----
+// GEMV: the wave's first outputs (rows, then their scale/zero pairs; for the GDN in-projection the
+// conv state and conv weights of those rows after them). GDN: the wave's 512-byte state column.
+// Attention: the K/V rows of the wave's positions, through the block table.
+__device__ __forceinline__ void prefetch(const Env& e, CPhase& P, int step, uint8_t* __restrict__ nxt) {
     const DecodeArgs& a = *e.a;
     const int lane = e.lane;
     if (P.kind == PH_GEMV) {
         const GemvGeo g = geo(P);
         const Rows R = part(P.rows, e.gwm, e.nw);
         const int cnt = min(R.n, g.cap);
-        dma_rows(P, g, R.r0, cnt, 0, e.reg, lane);
-        if (P.epi == EP_CONV && lane < min(R.n, 64)) {
-            const int row = R.r0 + lane;
-            if (row < P.conv_ch) {
-                const float* s = P.conv + (size_t)row * 3;
-                const float* w = P.conv_w + (size_t)row * 4;
-                ws.conv[0] = s[0]; ws.conv[1] = s[1]; ws.conv[2] = s[2];
-                ws.conv[3] = w[0]; ws.conv[4] = w[1]; ws.conv[5] = w[2]; ws.conv[6] = w[3];
+        dma_rows(P, g, R.r0, cnt, 0, nxt, lane);
+        if (P.epi == EP_CONV && cnt > 0) {
+            // conv state [ch][4] and weights [ch][4] of the prefetched rows, 16 bytes each
+            uint8_t* cv = nxt + cnt * g.nm * g.stride;
+            const int row = min(R.r0 + lane, P.conv_ch - 1);
+            if (lane < cnt) {
+                __builtin_amdgcn_global_load_lds((const void*)(P.conv + (size_t)row * 4), (lds_ptr_t)cv, 16, 0, 0);
+                __builtin_amdgcn_global_load_lds((const void*)(P.conv_w + (size_t)row * 4), (lds_ptr_t)(cv + 16 * cnt), 16, 0, 0);
             }
         }
     } else if (P.kind == PH_GDN) {
@@ -393,10 +428,10 @@ __device__ __forceinline__ void prefetch(const Env& e, CPhase& P, int step, Wave
         if (it < P.heads * 16) {
             const int h = it / 16, t = (it % 16) * 8 + e.wave;
             // state column t of head h: S[h][t][0..127] (value-major), 512 bytes
-            dma_bytes((const uint8_t*)(P.rec + ((size_t)h * kDK + t) * kDK), 512, e.reg, lane);
+            dma_bytes((const uint8_t*)(P.rec + ((size_t)h * kDK + t) * kDK), 512, nxt, lane);
         }
     } else if (P.kind == PH_ATTN) {
-        const int nkv = P.kv_heads, S = min(e.nwg / nkv, 128);
+        const int nkv = P.kv_heads, S = min(e.nwg / nkv, kMaxSplits);
         if (e.wg < nkv * S) {
             const int g = e.wg / S, sp = e.wg % S;
             const uint32_t pos = a.pos0 + (uint32_t)step, len = pos + 1;
@@ -405,16 +440,16 @@ __device__ __forceinline__ void prefetch(const Env& e, CPhase& P, int step, Wave
             int bid[kAttnU];
 #pragma unroll
             for (int u = 0; u < kAttnU; u++) {
-                const int p = p0 + 2 * (e.wave + kNW * u) + half;
-                bid[u] = p < p1 && p < (int)pos ? a.block_table[p / kBlk] : -1;
+                const int pp = p0 + 2 * (e.wave + kNW * u) + half;
+                bid[u] = pp < p1 && pp < (int)pos ? a.block_table[pp / kBlk] : -1;
             }
 #pragma unroll
             for (int u = 0; u < kAttnU; u++) {
-                const int p = p0 + 2 * (e.wave + kNW * u) + half;
+                const int pp = p0 + 2 * (e.wave + kNW * u) + half;
                 if (bid[u] >= 0) {
-                    const size_t at = (((size_t)bid[u] * nkv + g) * kBlk + p % kBlk) * kHeadDim + 8 * li;
-                    __builtin_amdgcn_global_load_lds((const void*)(P.kp + at), (lds_ptr_t)(e.reg + u * 2048), 16, 0, 0);
-                    __builtin_amdgcn_global_load_lds((const void*)(P.vp + at), (lds_ptr_t)(e.reg + u * 2048 + 1024), 16, 0, 0);
+                    const size_t at = (((size_t)bid[u] * nkv + g) * kBlk + pp % kBlk) * kHeadDim + 8 * li;
+                    __builtin_amdgcn_global_load_lds((const void*)(P.kp + at), (lds_ptr_t)(nxt + u * 2048), 16, 0, 0);
+                    __builtin_amdgcn_global_load_lds((const void*)(P.vp + at), (lds_ptr_t)(nxt + u * 2048 + 1024), 16, 0, 0);
                 }
             }
         }
@@ -424,14 +459,16 @@ __device__ __forceinline__ void prefetch(const Env& e, CPhase& P, int step, Wave
 // ---- phases ----
 
 // Waits for the GEMV input vector and stages it in xs (times the RMSNorm gain); returns 1/rms (or 1).
-__device__ __forceinline__ float gemv_input(const Env& e, CPhase& P, int step, int p, WaveState& ws, const Ctl& c) {
+__device__ __forceinline__ float gemv_input(const Env& e, CPhase& P, int step, int p, const Ctl& c) {
     const DecodeArgs& a = *e.a;
-    if (P.xin == XI_EMBED) return e.xs[kRawEmb - 1];  // staged with the embedding row
+    if (P.xin == XI_EMBED) return e.red[2 * kNW - 1];  // staged with the embedding row
     const uint32_t tag = tag_of(a, step, p - P.in_rel);
     const uint64_t* in = P.in + (size_t)(step & 1) * P.in_stride;
     float ss = 0.0f;
     float* xs = e.xs;
     const bool norm = P.xnorm == XN_NORM;
+    const Step st = make_step(P.mkind, P.k);
+    const bool cm = !head_fast(P);  // the LDS-region GEMV reads chunk-major slices
     // the RMSNorm gains of the pairs this thread will poll, loaded before the poll so that their
     // latency overlaps it (norm inputs fit one polling round: in_n <= 2 * kT * kPoll)
     float2 gn[kPoll];
@@ -454,12 +491,13 @@ __device__ __forceinline__ float gemv_input(const Env& e, CPhase& P, int step, i
                        v0 *= g.x;
                        v1 *= g.y;
                    }
-                   xs[2 * q] = v0;
-                   xs[2 * q + 1] = v1;
+                   const int d = cm ? xs_slot(st, 2 * q) : 2 * q;  // 2q even: 2q + 1 is the next slot
+                   xs[d] = v0;
+                   xs[d + 1] = v1;
                },
                c);
     if (norm) {
-        ss = wave_sum(ss);
+        ss = wave_sum_dpp(ss);
         if (e.lane == 0) e.red[e.wave] = ss;
     }
     bar();
@@ -470,14 +508,73 @@ __device__ __forceinline__ float gemv_input(const Env& e, CPhase& P, int step, i
     return 1.0f / sqrtf(t / (float)P.k + a.eps);
 }
 
-// One GEMV phase for this wave's outputs. Output i sits in region slot i % cap; the first
-// min(n, cap) were prefetched. Outputs are computed in groups of up to 8 rows (8 / nm outputs):
-// for every step of x, the step's slice is read from LDS once and applied to the whole group; the
-// group's 8 partials are then reduced together. The group's slots are refilled with the outputs
-// cap further on, so up to cap - group outputs stay in flight while a group is computed.
-__device__ __forceinline__ void gemv_phase(const Env& e, CPhase& P, int step, int p, WaveState& ws, float inv) {
+// LM head rows streamed straight into registers (the kernel's longest phase: vocab rows of width
+// hidden). Two rows are computed while the next two load; the register file, not the LDS region,
+// holds the bytes in flight.
+template <int KIND, int K>
+__device__ __forceinline__ void head_rows(const Env& e, CPhase& P, WaveState& ws, float inv, const Rows& R,
+                                          const float* __restrict__ xs) {
     const DecodeArgs& a = *e.a;
     const int lane = e.lane;
+    float xr[K / 64];
+    load_x<KIND, K>(xs, nullptr, 0.0f, xr, lane);
+    float xsum[KIND == KIND_Q4 ? Q4Plan<K>::NS : 1];
+    if constexpr (KIND == KIND_Q4) slab_sums<K>(xr, xsum);
+    constexpr int NB = 2;
+    RowRaw<KIND, K> cur[NB], nxt[NB];
+#pragma unroll
+    for (int k = 0; k < NB; k++) load_row<KIND, K, 64>(cur[k], P.w, P.sz, R.r0 + min(k, R.n - 1), lane);
+    for (int i = 0; i < R.n; i += NB) {
+        if (i + NB < R.n) {
+#pragma unroll
+            for (int k = 0; k < NB; k++) load_row<KIND, K, 64>(nxt[k], P.w, P.sz, R.r0 + min(i + NB + k, R.n - 1), lane);
+        }
+#pragma unroll
+        for (int k = 0; k < NB; k++) {
+            const float v = wave_sum_dpp(row_partial<KIND, K>(cur[k], xr, xsum)) * inv;
+            const int o = R.r0 + i + k;
+            if (i + k < R.n) {
+                if (lane == 0) a.logits[o] = v;
+                if (better(v, (uint32_t)o, ws.best, ws.best_i)) { ws.best = v; ws.best_i = (uint32_t)o; }
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < NB; k++) cur[k] = nxt[k];
+    }
+}
+
+__device__ __forceinline__ void head_phase(const Env& e, CPhase& P, WaveState& ws, float inv) {
+    const Rows R = part(P.rows, e.gwm, e.nw);
+    if (R.n == 0) return;
+    if (P.mkind == 0) {
+        if (P.k == 512) head_rows<KIND_F16, 512>(e, P, ws, inv, R, e.xs);
+        else if (P.k == 1024) head_rows<KIND_F16, 1024>(e, P, ws, inv, R, e.xs);
+        else head_rows<KIND_F16, 2048>(e, P, ws, inv, R, e.xs);
+    } else {
+        if (P.k == 512) head_rows<KIND_Q4, 512>(e, P, ws, inv, R, e.xs);
+        else if (P.k == 1024) head_rows<KIND_Q4, 1024>(e, P, ws, inv, R, e.xs);
+        else head_rows<KIND_Q4, 2048>(e, P, ws, inv, R, e.xs);
+    }
+}
+
+// One GEMV phase for this wave's outputs, rows read from `cur` (this phase's half); the next
+// region phase's data is first sent to `nxt`. Output i sits in slot i % cap; the first
+// min(n, cap) were prefetched (with more outputs than fit, slots are refilled as groups finish).
+// Outputs are computed in groups of up to 8 rows (8 / nm outputs): for every step of x, the step's
+// slice is read from LDS once and applied to the whole group, then the group is reduced together.
+// cur, nxt and xs are __restrict__: the compiler then knows that the reads of cur and xs do not
+// touch the half being filled, so they do not wait for that DMA.
+__device__ __forceinline__ void gemv_body(const Env& e, CPhase& P, int step, int p, WaveState& ws, float inv,
+                                          const uint8_t* __restrict__ cur, uint8_t* __restrict__ nxt,
+                                          const float* __restrict__ xs, CPhase* pn, int pn_step) {
+    const DecodeArgs& a = *e.a;
+    const int lane = e.lane;
+    unsigned long long tt[6];
+    tt[0] = __builtin_amdgcn_s_memrealtime();
+    __builtin_amdgcn_s_waitcnt(kWaitAll);  // this phase's rows (issued a phase ago) are in
+    tt[1] = __builtin_amdgcn_s_memrealtime();
+    if (pn) prefetch(e, *pn, pn_step, nxt);
+    tt[2] = __builtin_amdgcn_s_memrealtime();
     const GemvGeo g = geo(P);
     const Rows R = part(P.rows, e.gwm, e.nw);
     const uint32_t tag = tag_of(a, step, p);
@@ -487,42 +584,46 @@ __device__ __forceinline__ void gemv_phase(const Env& e, CPhase& P, int step, in
     const bool gdn = P.xnorm == XN_GDN;
     const int H = gdn ? P.heads : 0;
     const int gmax = 8 / g.nm;  // outputs per group
-    const int go = R.n <= g.cap ? min(gmax, R.n) : max(1, min(gmax, g.cap / 2));
-    int issued = min(R.n, g.cap);
+    const int pre = min(R.n, g.cap);  // outputs prefetched
+    const bool stream = R.n > g.cap;
+    const int go = stream ? max(1, min(gmax, g.cap / 2)) : min(gmax, R.n);
+    const uint8_t* cvs = cur + pre * g.nm * g.stride;  // EP_CONV: conv state / weights of the prefetched rows
+    uint8_t* curw = const_cast<uint8_t*>(cur);
+    int issued = pre;
     XC X;
-    if (t.nsteps == 1) load_step(e.xs, t, 0, gdn, H, X, lane);
+    if (t.nsteps == 1) load_step(xs, t, 0, gdn, H, X, lane);
+    asm volatile("" ::"v"(X.x[0]), "v"(X.x[31]));
+    tt[3] = __builtin_amdgcn_s_memrealtime();
+    tt[4] = tt[3];
     for (int o0 = 0; o0 < R.n; o0 += go) {
         const int ng = min(go, R.n - o0), nr = ng * g.nm;
-        wait_vm((issued - o0 - ng) * g.per);
+        if (o0 + ng > pre) wait_vm((issued - o0 - ng) * g.per);  // refilled group
         float acc[8];
 #pragma unroll
         for (int r = 0; r < 8; r++) acc[r] = 0.0f;
         for (int j = 0; j < t.nsteps; j++) {
-            if (t.nsteps > 1) load_step(e.xs, t, j, gdn, H, X, lane);
+            if (t.nsteps > 1) load_step(xs, t, j, gdn, H, X, lane);
 #pragma unroll
             for (int r = 0; r < 8; r++) {
                 if (r < nr) {
                     const int i = r / g.nm, m = r % g.nm;
-                    const uint8_t* row = e.reg + ((o0 + i) % g.cap) * g.nm * g.stride + m * g.stride;
-                    acc[r] += step_dot(t, j, P.group, g.rb, row, X, lane);
+                    const int slot = stream ? (o0 + i) % g.cap : o0 + i;
+                    acc[r] += step_dot(t, j, P.group, g.rb, cur + slot * g.nm * g.stride + m * g.stride, X, lane);
                 }
             }
         }
+        if (o0 == 0) {
+            asm volatile("" ::"v"(acc[0]), "v"(acc[1]), "v"(acc[7]));
+            tt[4] = __builtin_amdgcn_s_memrealtime();
+        }
         // refill the group's slots with the outputs cap further on
-        for (int i = 0; i < ng && issued < R.n; i++, issued++) dma_rows(P, g, R.r0 + issued, 1, issued % g.cap, e.reg, lane);
+        for (int i = 0; i < ng && issued < R.n; i++, issued++) dma_rows(P, g, R.r0 + issued, 1, issued % g.cap, curw, lane);
         const float tot = reduce8(acc, lane) * inv;   // lanes 8r..8r+7: row r of the group
         const float up = __shfl_down(tot, 8, kWave);  // SwiGLU: the up row of the output
         const int r = lane >> 3;
         const int i = r / g.nm;
         const bool lead = (lane & 7) == 0 && r % g.nm == 0 && i < ng;
         const int o = R.r0 + o0 + i;
-        // conv state of output i (loaded at prefetch by lane i), moved to the lanes of row i while
-        // every lane is active (a shuffle from an inactive lane reads nothing)
-        float cv[7];
-        if (P.epi == EP_CONV) {
-#pragma unroll
-            for (int q = 0; q < 7; q++) cv[q] = __shfl(ws.conv[q], (o0 + i) & 63, kWave);
-        }
         float y = tot;
         if (P.epi == EP_RESID) {
             // rows of h owned by this wave: outputs 0 and 1
@@ -538,9 +639,19 @@ __device__ __forceinline__ void gemv_phase(const Env& e, CPhase& P, int step, in
         if (lead) {
             if (P.epi == EP_SWIGLU) y = silu(tot) * up;
             else if (P.epi == EP_CONV && o < P.conv_ch) {
-                const float tt = cv[0] * cv[3] + cv[1] * cv[4] + cv[2] * cv[5] + tot * cv[6];
-                float* st = P.conv + (size_t)o * 3;
-                st[0] = cv[1]; st[1] = cv[2]; st[2] = tot;
+                // conv state s0..s2 and weights w0..w3 of the output's channel
+                const int k = o0 + i;
+                float4 st, cw;
+                if (k < pre) {
+                    st = *(const float4*)(cvs + 16 * k);
+                    cw = *(const float4*)(cvs + 16 * pre + 16 * k);
+                } else {
+                    st = *(const float4*)(P.conv + (size_t)o * 4);
+                    cw = *(const float4*)(P.conv_w + (size_t)o * 4);
+                }
+                const float tt = st.x * cw.x + st.y * cw.y + st.z * cw.z + tot * cw.w;
+                float* sp = P.conv + (size_t)o * 4;
+                sp[0] = st.y; sp[1] = st.z; sp[2] = tot;
                 y = silu(tt);
             }
             if (P.epi == EP_HEAD) {
@@ -551,59 +662,75 @@ __device__ __forceinline__ void gemv_phase(const Env& e, CPhase& P, int step, in
             }
         }
     }
+    tt[5] = __builtin_amdgcn_s_memrealtime();
+    if (a.sub && e.wave == 0 && lane == 0 && step * a.nph + p < a.trace_cap) {
+        unsigned long long* sb = a.sub + 8 * ((size_t)(step * a.nph + p) * e.nwg + e.wg);
+        for (int k = 0; k < 6; k++) sb[k] = tt[k];
+    }
+}
+
+// The inputs of GDN item `it` (head h, value columns 8cb..8cb+7): q_h, k_h (64 pairs each), v and
+// z of the 8 columns (4 pairs each), a_h and b_h; staged at xs[0..276).
+__device__ __forceinline__ void gdn_input(const Env& e, CPhase& P, int step, int p, int it, const Ctl& c) {
+    const DecodeArgs& a = *e.a;
+    const int H = P.heads, h = it / 16, cb = it % 16;
+    const uint32_t tin = tag_of(a, step, p - P.in_rel);
+    const uint64_t* in = P.in + (size_t)(step & 1) * P.in_stride;
+    const int qa = h * kDK, ka = H * kDK + h * kDK, va = 2 * H * kDK + h * kDK + cb * 8;
+    const int za = 3 * H * kDK + h * kDK + cb * 8, aa = 4 * H * kDK + h, ba = 4 * H * kDK + H + h;
+    float* xs = e.xs;
+    poll_pairs(in, P.in_cap, 138, tin,
+               [&](int q) {
+                   if (q < 64) return qa + 2 * q;
+                   if (q < 128) return ka + 2 * (q - 64);
+                   if (q < 132) return va + 2 * (q - 128);
+                   if (q < 136) return za + 2 * (q - 132);
+                   return q == 136 ? (aa & ~1) : (ba & ~1);
+               },
+               [&](int q, float v0, float v1) {
+                   xs[2 * q] = v0;
+                   xs[2 * q + 1] = v1;
+               },
+               c);
+    bar();
 }
 
 // Gated DeltaNet step (kernels/src/shaders.rs:436-520 after the conv): workgroup = (head, 8 value
 // columns), wave = one value column t, lane = keys 2l, 2l+1 of the value-major state column.
-__device__ __forceinline__ void gdn_phase(const Env& e, CPhase& P, int step, int p, const Ctl& c) {
+// The first item's inputs are staged by gdn_input and its state column is in `cur`.
+__device__ __forceinline__ void gdn_body(const Env& e, CPhase& P, int step, int p, const Ctl& c,
+                                         const uint8_t* __restrict__ cur, uint8_t* __restrict__ nxt,
+                                         const float* __restrict__ xs, float* __restrict__ red, CPhase* pn,
+                                         int pn_step) {
     const DecodeArgs& a = *e.a;
+    __builtin_amdgcn_s_waitcnt(kWaitAll);  // the state column (issued a phase ago) is in
+    if (pn) prefetch(e, *pn, pn_step, nxt);
     const int H = P.heads, lane = e.lane;
-    const uint32_t tin = tag_of(a, step, p - P.in_rel), tag = tag_of(a, step, p);
-    const uint64_t* in = P.in + (size_t)(step & 1) * P.in_stride;
+    const uint32_t tag = tag_of(a, step, p);
     uint64_t* out = P.out + (size_t)(step & 1) * P.out_stride;
+    cfloat* prm = (cfloat*)P.gain;
     for (int it = e.wg; it < H * 16; it += e.nwg) {
+        if (it != e.wg) {
+            gdn_input(e, P, step, p, it, c);
+            if (*e.bail) return;
+        }
         const int h = it / 16, cb = it % 16;
-        // inputs: q_h, k_h (64 pairs each), v and z of the 8 columns (4 pairs each), a_h and b_h
-        const int qa = h * kDK, ka = H * kDK + h * kDK, va = 2 * H * kDK + h * kDK + cb * 8;
-        const int za = 3 * H * kDK + h * kDK + cb * 8, aa = 4 * H * kDK + h, ba = 4 * H * kDK + H + h;
-        float* xs = e.xs;
-        poll_pairs(in, P.in_cap, 138, tin,
-                   [&](int q) {
-                       if (q < 64) return qa + 2 * q;
-                       if (q < 128) return ka + 2 * (q - 64);
-                       if (q < 132) return va + 2 * (q - 128);
-                       if (q < 136) return za + 2 * (q - 132);
-                       return q == 136 ? (aa & ~1) : (ba & ~1);
-                   },
-                   [&](int q, float v0, float v1) {
-                       xs[2 * q] = v0;
-                       xs[2 * q + 1] = v1;
-                   },
-                   c);
-        bar();
-        if (*e.bail) return;
+        const int aa = 4 * H * kDK + h, ba = 4 * H * kDK + H + h;
         const int t = cb * 8 + e.wave;
         const float2 q2 = *(const float2*)(xs + 2 * lane);
         const float2 k2 = *(const float2*)(xs + 128 + 2 * lane);
         const float v = xs[256 + e.wave], z = xs[264 + e.wave];
         const float av = xs[272 + (aa & 1)], bv = xs[274 + (ba & 1)];
         float* Sg = P.rec + ((size_t)h * kDK + t) * kDK + 2 * lane;
-        float2 s;
-        if (it == e.wg) {
-            __builtin_amdgcn_s_waitcnt(kWaitVm0);
-            s = *(const float2*)(e.reg + 8 * lane);
-        } else {
-            s = *(const float2*)Sg;
-        }
-        const float nq = 1.0f / sqrtf(wave_sum(q2.x * q2.x + q2.y * q2.y) + 1e-6f) * rsqrtf((float)kDK);
-        const float nk = 1.0f / sqrtf(wave_sum(k2.x * k2.x + k2.y * k2.y) + 1e-6f);
+        const float2 s = it == e.wg ? *(const float2*)(cur + 8 * lane) : *(const float2*)Sg;
+        const float nq = 1.0f / sqrtf(wave_sum_dpp(q2.x * q2.x + q2.y * q2.y) + 1e-6f) * rsqrtf((float)kDK);
+        const float nk = 1.0f / sqrtf(wave_sum_dpp(k2.x * k2.x + k2.y * k2.y) + 1e-6f);
         const float qx = q2.x * nq, qy = q2.y * nq, kx = k2.x * nk, ky = k2.y * nk;
-        const float kq = wave_sum(kx * qx + ky * qy);
-        cfloat* prm = (cfloat*)P.gain;
+        const float kq = wave_sum_dpp(kx * qx + ky * qy);
         const float gg = expf(prm[H + h] * logf(1.0f + expf(av + prm[h])));
         const float beta = 1.0f / (1.0f + expf(-bv));
-        const float sk = wave_sum(s.x * kx + s.y * ky);
-        const float sq = wave_sum(s.x * qx + s.y * qy);
+        const float sk = wave_sum_dpp(s.x * kx + s.y * ky);
+        const float sq = wave_sum_dpp(s.x * qx + s.y * qy);
         const float d = beta * (v - gg * sk);
         float2 sn;
         sn.x = fmaf(gg, s.x, d * kx);
@@ -612,12 +739,12 @@ __device__ __forceinline__ void gdn_phase(const Env& e, CPhase& P, int step, int
         const float o = gg * sq + d * kq;
         if (lane == 0) {
             put(out, (uint32_t)(h * kDK + t), o * silu(z) * prm[2 * H + t], tag);
-            e.red[e.wave] = o * o;
+            red[e.wave] = o * o;
         }
         bar();
         if (threadIdx.x == 0) {
             float ss = 0.0f;
-            for (int w = 0; w < kNW; w++) ss += e.red[w];
+            for (int w = 0; w < kNW; w++) ss += red[w];
             put(out, (uint32_t)(H * kDK + h * 16 + cb), ss, tag);
         }
         bar();
@@ -628,7 +755,7 @@ __device__ __forceinline__ void gdn_phase(const Env& e, CPhase& P, int step, int
 // (kernels/src/shaders.rs:575-593).
 __device__ __forceinline__ void norm_rope4(float (&v)[4], const float* w, const DecodeArgs& a, uint32_t pos, int lane) {
     float ss = v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3];
-    ss = wave_sum(ss);
+    ss = wave_sum_dpp(ss);
     const float inv = 1.0f / sqrtf(ss / (float)kHeadDim + 1e-6f);
     const float4 g = *(const float4*)(w + 4 * lane);
     v[0] = v[0] * inv * g.x; v[1] = v[1] * inv * g.y; v[2] = v[2] * inv * g.z; v[3] = v[3] * inv * g.w;
@@ -653,10 +780,15 @@ __device__ __forceinline__ void norm_rope4(float (&v)[4], const float* w, const 
 // Attention partials (kernels/src/shaders.rs:522-633 split over the context): workgroup =
 // (kv head g, split sp) over positions [p0, p1) of 0..pos; publishes (max, sum, acc[256]) per
 // q head of the group.
-__device__ __forceinline__ void attn_phase(const Env& e, CPhase& P, int step, int p, const Ctl& c) {
+__device__ __forceinline__ void attn_phase(const Env& e, CPhase& P, int step, int p, const Ctl& c, int rh,
+                                           CPhase* pn, int pn_step) {
+    uint8_t* cur = e.regs + e.wave * kWaveLds + rh * kHalf;
     const DecodeArgs& a = *e.a;
-    const int nq = P.heads, nkv = P.kv_heads, G = nq / nkv, S = min(e.nwg / nkv, 128), lane = e.lane;
-    if (e.wg >= nkv * S) return;
+    const int nq = P.heads, nkv = P.kv_heads, G = nq / nkv, S = min(e.nwg / nkv, kMaxSplits), lane = e.lane;
+    if (e.wg >= nkv * S) {
+        if (pn) prefetch(e, *pn, pn_step, e.regs + e.wave * kWaveLds + (1 - rh) * kHalf);
+        return;
+    }
     const int g = e.wg / S, sp = e.wg % S;
     const uint32_t pos = a.pos0 + (uint32_t)step, len = pos + 1;
     const int p0 = (int)((uint64_t)sp * len / S), p1 = (int)((uint64_t)(sp + 1) * len / S);
@@ -745,8 +877,8 @@ __device__ __forceinline__ void attn_phase(const Env& e, CPhase& P, int step, in
         } else if (valid) {
             u32x4 kw, vw;
             if (u < kAttnU) {
-                kw = *(const u32x4*)(e.reg + u * 2048 + 16 * lane);
-                vw = *(const u32x4*)(e.reg + u * 2048 + 1024 + 16 * lane);
+                kw = *(const u32x4*)(cur + u * 2048 + 16 * lane);
+                vw = *(const u32x4*)(cur + u * 2048 + 1024 + 16 * lane);
             } else {
                 const size_t at = (((size_t)a.block_table[ps / kBlk] * nkv + g) * kBlk + ps % kBlk) * kHeadDim + 8 * li;
                 kw = *(const u32x4*)(P.kp + at);
@@ -780,7 +912,7 @@ __device__ __forceinline__ void attn_phase(const Env& e, CPhase& P, int step, in
         }
     }
     // merge the two position halves of the wave, then write the wave's partial into its region
-    float* wp = (float*)e.reg;  // [G][258]: m, l, acc[256]
+    float* wp = (float*)cur;  // [G][258]: m, l, acc[256]
 #pragma unroll
     for (int gi = 0; gi < 4; gi++) {
         if (gi < G) {
@@ -804,10 +936,10 @@ __device__ __forceinline__ void attn_phase(const Env& e, CPhase& P, int step, in
         const int t = threadIdx.x;
         for (int gi = 0; gi < G; gi++) {
             float mn = -INFINITY;
-            for (int w = 0; w < kNW; w++) mn = fmaxf(mn, ((const float*)(e.regs + w * kRegion))[gi * 258]);
+            for (int w = 0; w < kNW; w++) mn = fmaxf(mn, ((const float*)(e.regs + w * kWaveLds + rh * kHalf))[gi * 258]);
             float ls = 0.0f, ac = 0.0f;
             for (int w = 0; w < kNW; w++) {
-                const float* pw = (const float*)(e.regs + w * kRegion) + gi * 258;
+                const float* pw = (const float*)(e.regs + w * kWaveLds + rh * kHalf) + gi * 258;
                 const float cw = pw[0] == -INFINITY ? 0.0f : expf(pw[0] - mn);
                 ls += pw[1] * cw;
                 ac += pw[2 + t] * cw;
@@ -821,12 +953,14 @@ __device__ __forceinline__ void attn_phase(const Env& e, CPhase& P, int step, in
         }
     }
     bar();  // the regions are free again
+    if (pn) prefetch(e, *pn, pn_step, e.regs + e.wave * kWaveLds + (1 - rh) * kHalf);
 }
 
 // Combine of the attention partials: workgroup = (q head h, 64 dims c); times sigmoid(gate).
+// Combine of the attention partials: workgroup = (q head h, 64 dims c); times sigmoid(gate).
 __device__ __forceinline__ void comb_phase(const Env& e, CPhase& P, int step, int p, const Ctl& c) {
     const DecodeArgs& a = *e.a;
-    const int nq = P.heads, nkv = P.kv_heads, G = nq / nkv, S = min(e.nwg / nkv, 128);
+    const int nq = P.heads, nkv = P.kv_heads, G = nq / nkv, S = min(e.nwg / nkv, kMaxSplits);
     if (e.wg >= nq * 4) return;
     const int h = e.wg / 4, cq = e.wg % 4, g = h / G, gi = h % G;
     const uint32_t tin = tag_of(a, step, p - P.in_rel), tin2 = tag_of(a, step, p - P.in2_rel), tag = tag_of(a, step, p);
@@ -886,23 +1020,20 @@ __device__ __forceinline__ void trace_done(const Env& e, int inst) {
     const DecodeArgs& a = *e.a;
     if (a.trace && inst < a.trace_cap) {
         bar();
-        if (threadIdx.x == 0) {
-            const unsigned long long t = __builtin_amdgcn_s_memrealtime();
-            atomicMax(a.trace + 2 + 3 * inst, t);
-            atomicMin(a.trace + 3 + 3 * inst, t);
-        }
+        if (threadIdx.x == 0) a.trace[2 + 2 * ((size_t)inst * e.nwg + e.wg) + 1] = __builtin_amdgcn_s_memrealtime();
     }
 }
 __device__ __forceinline__ void trace_in(const Env& e, int inst) {
     const DecodeArgs& a = *e.a;
-    if (a.trace && inst < a.trace_cap && e.wg == 0 && threadIdx.x == 0) a.trace[4 + 3 * inst] = __builtin_amdgcn_s_memrealtime();
+    if (a.trace && inst < a.trace_cap && threadIdx.x == 0)
+        a.trace[2 + 2 * ((size_t)inst * e.nwg + e.wg)] = __builtin_amdgcn_s_memrealtime();
 }
 
 }  // namespace
 
 __global__ __launch_bounds__(kT, 1) void k_decode(DecodeArgs a) {
     __shared__ __attribute__((aligned(16))) float xs[kXs];
-    __shared__ __attribute__((aligned(16))) uint8_t regs[kNW * kRegion];
+    __shared__ __attribute__((aligned(16))) uint8_t regs[kNW * kWaveLds];
     __shared__ float red[2 * kNW];
     __shared__ uint32_t redi[kNW];
     __shared__ int bail;
@@ -915,7 +1046,6 @@ __global__ __launch_bounds__(kT, 1) void k_decode(DecodeArgs a) {
     e.gwm = e.wave * e.nwg + e.wg;
     e.nw = e.nwg * kNW;
     e.xs = xs;
-    e.reg = regs + e.wave * kRegion;
     e.regs = regs;
     e.red = red;
     e.bail = &bail;
@@ -925,41 +1055,43 @@ __global__ __launch_bounds__(kT, 1) void k_decode(DecodeArgs a) {
     if (a.trace && e.wg == 0 && threadIdx.x == 0) a.trace[0] = __builtin_amdgcn_s_memrealtime();
     WaveState ws;
     ws.hown[0] = ws.hown[1] = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 7; i++) ws.conv[i] = 0.0f;
     ws.best = -INFINITY;
     ws.best_i = 0xFFFFFFFFu;
     const Rows own = part(a.hidden, e.gwm, e.nw);  // residual rows of this wave (<= 2)
+    auto region = [&](int half) { return regs + e.wave * kWaveLds + half * kHalf; };
     bar();
 
     uint32_t token = a.feed ? a.tok[0] : a.ids[0];
-    prefetch(e, prog[0], 0, ws);
-    int pf = 0;
+    int half = 0;  // half holding the data of the next region phase
+    {
+        int ns, np;
+        if (uses_region(prog[0])) prefetch(e, prog[0], 0, region(0));
+        else if (next_region_phase(a, prog, 0, 0, ns, np)) prefetch(e, prog[np], ns, region(0));
+    }
     for (int step = 0; step < a.n_steps; step++) {
-        if (pf == a.nph) pf = 0;
         const uint32_t pos = a.pos0 + (uint32_t)step;
-        const bool head = a.head == 1 || (a.head == 2 && step == a.n_steps - 1);
-        // embedding row (kernels/src/shaders.rs:405-434): raw at xs[kRawEmb..], times the first
-        // layer's input-norm gain at xs[0..]; 1/rms at xs[kRawEmb - 1]
+        const bool head = head_at(a, step);
+        // embedding row (kernels/src/shaders.rs:405-434) times the first layer's input-norm gain,
+        // in the layout the first in-projection reads; 1/rms in red[2 kNW - 1]
         {
             CPhase& P0 = prog[0];
+            const Step st0 = make_step(P0.mkind, P0.k);
             float ss = 0.0f;
             for (int cc = threadIdx.x; cc < a.hidden; cc += kT) {
                 const float v = embed_val(a, token, cc);
-                xs[kRawEmb + cc] = v;
-                xs[cc] = v * P0.gain[cc];
+                xs[xs_slot(st0, cc)] = v * P0.gain[cc];
                 ss += v * v;
             }
-            ss = wave_sum(ss);
+            ss = wave_sum_dpp(ss);
             if (e.lane == 0) red[e.wave] = ss;
+            if (own.n > 0) ws.hown[0] = embed_val(a, token, own.r0);
+            if (own.n > 1) ws.hown[1] = embed_val(a, token, own.r0 + 1);
             bar();
             if (threadIdx.x == 0) {
                 float t = 0.0f;
                 for (int w = 0; w < kNW; w++) t += red[w];
-                xs[kRawEmb - 1] = 1.0f / sqrtf(t / (float)a.hidden + a.eps);
+                red[2 * kNW - 1] = 1.0f / sqrtf(t / (float)a.hidden + a.eps);
             }
-            if (own.n > 0) ws.hown[0] = xs[kRawEmb + own.r0];
-            if (own.n > 1) ws.hown[1] = xs[kRawEmb + own.r0 + 1];
             bar();
         }
         ws.best = -INFINITY;
@@ -968,91 +1100,97 @@ __global__ __launch_bounds__(kT, 1) void k_decode(DecodeArgs a) {
             CPhase& P = prog[p];
             if (P.is_head && !head) continue;
             const int inst = step * a.nph + p;
+            int ns = 0, np = 0;
+            const bool more = next_region_phase(a, prog, step, p, ns, np);
+            CPhase* pn = more ? &prog[np] : nullptr;
             switch (P.kind) {
                 case PH_GEMV: {
-                    const float inv = gemv_input(e, P, step, p, ws, c);
+                    const float inv = gemv_input(e, P, step, p, c);
                     if (bail) { __builtin_amdgcn_s_waitcnt(kWaitAll); return; }
                     trace_in(e, inst);
-                    gemv_phase(e, P, step, p, ws, inv);
+                    if (head_fast(P)) {
+                        head_phase(e, P, ws, inv);
+                    } else {
+                        gemv_body(e, P, step, p, ws, inv, region(half), region(1 - half), xs, pn, ns);
+                        half ^= 1;
+                    }
                     break;
                 }
-                case PH_GDN: trace_in(e, inst); gdn_phase(e, P, step, p, c); break;
-                case PH_ATTN: trace_in(e, inst); attn_phase(e, P, step, p, c); break;
-                default: trace_in(e, inst); comb_phase(e, P, step, p, c); break;
+                case PH_GDN:
+                    if (e.wg < P.heads * 16) gdn_input(e, P, step, p, e.wg, c);
+                    if (bail) { __builtin_amdgcn_s_waitcnt(kWaitAll); return; }
+                    trace_in(e, inst);
+                    gdn_body(e, P, step, p, c, region(half), region(1 - half), xs, red, pn, ns);
+                    half ^= 1;
+                    break;
+                case PH_ATTN:
+                    trace_in(e, inst);
+                    attn_phase(e, P, step, p, c, half, pn, ns);
+                    half ^= 1;
+                    break;
+                default:
+                    trace_in(e, inst);
+                    comb_phase(e, P, step, p, c);
+                    break;
             }
             if (bail) { __builtin_amdgcn_s_waitcnt(kWaitAll); return; }
             trace_done(e, inst);
-            // prefetch the next phase that uses the regions (a combine does not): later in this
-            // step, or phase 0 of the next step
-            int np = p + 1;
-            while (np < a.nph && ((prog[np].is_head && !head) || prog[np].kind == PH_COMB)) np++;
-            if (np < a.nph) {
-                if (np != pf) {
-                    prefetch(e, prog[np], step, ws);
-                    pf = np;
-                }
-            } else if (step + 1 < a.n_steps && pf != a.nph) {
-                prefetch(e, prog[0], step + 1, ws);
-                pf = a.nph;  // phase 0 of the next step
-            }
         }
-        if (head) {
+        if (head && a.argmax) {
             // greedy pick over the LM head rows (argmax_partial / argmax_final,
-            // kernels/src/shaders.rs:635-699): waves -> workgroup -> every workgroup
-            if (a.argmax) {
+            // kernels/src/shaders.rs:635-699): lanes -> waves -> workgroup -> every workgroup
 #pragma unroll
-                for (int mk = 32; mk >= 1; mk >>= 1) {
-                    const float ov = __shfl_xor(ws.best, mk, kWave);
-                    const uint32_t oi = (uint32_t)__shfl_xor((int)ws.best_i, mk, kWave);
-                    if (better(ov, oi, ws.best, ws.best_i)) { ws.best = ov; ws.best_i = oi; }
-                }
-                if (e.lane == 0) { red[e.wave] = ws.best; redi[e.wave] = ws.best_i; }
-                bar();
-                const uint32_t tag = tag_of(a, step, a.nph - 1) ;
-                uint64_t* am = a.am + (size_t)(step & 1) * a.am_stride;
-                if (threadIdx.x == 0) {
-                    float b = red[0];
-                    uint32_t bi = redi[0];
-                    for (int w = 1; w < kNW; w++)
-                        if (better(red[w], redi[w], b, bi)) { b = red[w]; bi = redi[w]; }
-                    put(am, 2 * e.wg, b, tag);
-                    put(am, 2 * e.wg + 1, __uint_as_float(bi), tag);
-                }
-                float b = -INFINITY;
-                uint32_t bi = 0xFFFFFFFFu;
-                poll_pairs(am, 2 * e.nwg, e.nwg, tag, [](int q) { return 2 * q; },
-                           [&](int q, float v0, float v1) {
-                               const uint32_t i1 = __float_as_uint(v1);
-                               if (better(v0, i1, b, bi)) { b = v0; bi = i1; }
-                           },
-                           c);
-#pragma unroll
-                for (int mk = 32; mk >= 1; mk >>= 1) {
-                    const float ov = __shfl_xor(b, mk, kWave);
-                    const uint32_t oi = (uint32_t)__shfl_xor((int)bi, mk, kWave);
-                    if (better(ov, oi, b, bi)) { b = ov; bi = oi; }
-                }
-                bar();
-                if (e.lane == 0) { red[e.wave] = b; redi[e.wave] = bi; }
-                bar();
-                if (bail) { __builtin_amdgcn_s_waitcnt(kWaitAll); return; }
-                float bb = red[0];
-                uint32_t bbi = redi[0];
-                for (int w = 1; w < kNW; w++)
-                    if (better(red[w], redi[w], bb, bbi)) { bb = red[w]; bbi = redi[w]; }
-                const uint32_t pick = bbi == 0xFFFFFFFFu ? 0u : bbi;
-                if (e.wg == 0 && threadIdx.x == 0) {
-                    a.tok[0] = pick;
-                    a.tok[1] = pos + 1;
-                    if (a.out_ids) {
-                        const uint32_t n = a.tok[2];
-                        if (n < a.out_cap) a.out_ids[n] = pick;
-                        a.tok[2] = n + 1;
-                    }
-                }
-                token = pick;
-                bar();
+            for (int mk = 32; mk >= 1; mk >>= 1) {
+                const float ov = __shfl_xor(ws.best, mk, kWave);
+                const uint32_t oi = (uint32_t)__shfl_xor((int)ws.best_i, mk, kWave);
+                if (better(ov, oi, ws.best, ws.best_i)) { ws.best = ov; ws.best_i = oi; }
             }
+            if (e.lane == 0) { red[e.wave] = ws.best; redi[e.wave] = ws.best_i; }
+            bar();
+            const uint32_t tag = tag_of(a, step, a.nph - 1);
+            uint64_t* am = a.am + (size_t)(step & 1) * a.am_stride;
+            if (threadIdx.x == 0) {
+                float b = red[0];
+                uint32_t bi = redi[0];
+                for (int w = 1; w < kNW; w++)
+                    if (better(red[w], redi[w], b, bi)) { b = red[w]; bi = redi[w]; }
+                put(am, 2 * e.wg, b, tag);
+                put(am, 2 * e.wg + 1, __uint_as_float(bi), tag);
+            }
+            float b = -INFINITY;
+            uint32_t bi = 0xFFFFFFFFu;
+            poll_pairs(am, 2 * e.nwg, e.nwg, tag, [](int q) { return 2 * q; },
+                       [&](int q, float v0, float v1) {
+                           const uint32_t i1 = __float_as_uint(v1);
+                           if (better(v0, i1, b, bi)) { b = v0; bi = i1; }
+                       },
+                       c);
+#pragma unroll
+            for (int mk = 32; mk >= 1; mk >>= 1) {
+                const float ov = __shfl_xor(b, mk, kWave);
+                const uint32_t oi = (uint32_t)__shfl_xor((int)bi, mk, kWave);
+                if (better(ov, oi, b, bi)) { b = ov; bi = oi; }
+            }
+            bar();
+            if (e.lane == 0) { red[e.wave] = b; redi[e.wave] = bi; }
+            bar();
+            if (bail) { __builtin_amdgcn_s_waitcnt(kWaitAll); return; }
+            float bb = red[0];
+            uint32_t bbi = redi[0];
+            for (int w = 1; w < kNW; w++)
+                if (better(red[w], redi[w], bb, bbi)) { bb = red[w]; bbi = redi[w]; }
+            const uint32_t pick = bbi == 0xFFFFFFFFu ? 0u : bbi;
+            if (e.wg == 0 && threadIdx.x == 0) {
+                a.tok[0] = pick;
+                a.tok[1] = pos + 1;
+                if (a.out_ids) {
+                    const uint32_t n = a.tok[2];
+                    if (n < a.out_cap) a.out_ids[n] = pick;
+                    a.tok[2] = n + 1;
+                }
+            }
+            token = pick;
+            bar();
         }
         if (step + 1 < a.n_steps && !a.feed) token = a.ids[step + 1];
     }
@@ -1062,8 +1200,8 @@ __global__ __launch_bounds__(kT, 1) void k_decode(DecodeArgs a) {
 
 int decode_gemv_variant(int kind, int k) {
     if (k <= 0 || k % 512 != 0) return -1;
-    if (kind == 1) return k <= 6144 ? 1 : -1;  // the x slice layout holds up to 96 values per lane
-    return k <= 6144 ? 0 : -1;
+    if (kind == 1) return k <= 6144 ? 1 : -1;  // a q4 row of 6144 is 3456 bytes of LDS
+    return k <= 4096 ? 0 : -1;                 // an f16 row of 4096 fills an 8 KiB half
 }
 
 hipError_t launch_decode(const DecodeArgs& a, int grid, hipStream_t st) {

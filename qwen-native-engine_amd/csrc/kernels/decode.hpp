@@ -1,8 +1,8 @@
 // Host-visible description of the persistent decode kernel (kernels/decode.hip).
 //
 // A decode window runs as ONE cooperative launch. The per-token work is a fixed program of
-// phases (built once at load, kept in LDS by the kernel); each phase consumes a vector published
-// by the previous phase and publishes its own. Vectors are handed over as tagged values: every f32
+// phases (built once at load, read by the kernel through the constant address space); each phase
+// consumes a vector published by the previous phase and publishes its own. Vectors are handed over as tagged values: every f32
 // is stored next to a 32-bit tag (the phase's sequence number) in one 8-byte agent-scope store,
 // and a consumer polls until every tag it needs carries the expected number. No grid barrier and
 // no cache-maintenance fence is needed: the tag proves the value next to it is the new one.
@@ -26,6 +26,7 @@ enum { EP_STORE = 0, EP_CONV = 1, EP_RESID = 2, EP_SWIGLU = 3, EP_HEAD = 4 };
 constexpr int kDecodeThreads = 512;
 constexpr int kMaxPhases = 192;
 constexpr int kHeadDim = 256;  // attention head size the kernel is written for
+constexpr int kMaxSplits = 92;  // attention context splits per kv head (the combine stages 66 floats each)
 
 // One phase. `variant` selects the compiled GEMV shape (matrix kind and K).
 struct Phase {
@@ -43,7 +44,7 @@ struct Phase {
     const uint32_t* sz = nullptr;
     const float* gain = nullptr;    // XN_NORM gain; GDN: dt_bias, A_neg_exp, norm_w; ATTN: q_norm, k_norm
     const float* conv_w = nullptr;  // EP_CONV [conv_ch][4]
-    float* conv = nullptr;          // EP_CONV state [conv_ch][3]
+    float* conv = nullptr;          // EP_CONV state [conv_ch][4] (3 used)
     float* rec = nullptr;           // GDN state [heads][dv][dk] (value-major)
     uint16_t* kp = nullptr;         // attention pools [blocks][kv_heads][16][256]
     uint16_t* vp = nullptr;
@@ -84,11 +85,16 @@ struct DecodeArgs {
     unsigned* err = nullptr;  // [0] set on a polling timeout
     unsigned spin_limit = 1u << 20;
     // Optional device timeline (ticks of the constant-rate wall clock): trace[0] start, trace[1]
-    // end (workgroup 0); for phase instance i = step * nph + p: trace[2 + 3i] latest and
-    // trace[3 + 3i] earliest completion over workgroups, trace[4 + 3i] when workgroup 0 had its
-    // input. `trace_cap` phase instances are recorded.
+    // end (workgroup 0); for phase instance i = step * nph + p and workgroup w:
+    // trace[2 + 2 (i * grid + w)] when w had its input, trace[3 + 2 (i * grid + w)] when w was
+    // done. `trace_cap` phase instances are recorded.
     unsigned long long* trace = nullptr;
     int trace_cap = 0;
+    // Optional finer timeline of GEMV phases (wave 0 of every workgroup, kept in registers and
+    // stored when the phase ends): for phase instance i and workgroup w, sub[8 (i * grid + w) + k]
+    // for k = 0 entry, 1 own rows landed, 2 next phase's DMA issued, 3 x slice loaded, 4 first
+    // group's rows done, 5 end.
+    unsigned long long* sub = nullptr;
 };
 
 // GEMV shapes compiled into the kernel: variant id of (matrix kind, K), or -1.

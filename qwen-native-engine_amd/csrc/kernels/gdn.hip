@@ -87,7 +87,7 @@ __global__ __launch_bounds__(kGdnThreads) void k_gdn_decode(const float* __restr
     if (t < 384) {
         const int ch = t < 128 ? h * kDK + t : (t < 256 ? H * kDK + h * kDK + (t - 128) : 2 * H * kDK + h * kDV + (t - 256));
         const float x = proj[ch];
-        float* st = conv_state + (size_t)ch * 3;
+        float* st = conv_state + (size_t)ch * 4;
         const float* cw = conv_w + (size_t)ch * 4;
         const float s0 = st[0], s1 = st[1], s2 = st[2];
         const float y = s0 * cw[0] + s1 * cw[1] + s2 * cw[2] + x * cw[3];

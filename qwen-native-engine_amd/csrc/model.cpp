@@ -2,6 +2,7 @@
 // kernels/src/model.rs, on HIP.
 #include "model.hpp"
 
+#include <algorithm>
 #include <chrono>
 #include <cmath>
 #include <cstdlib>
@@ -206,7 +207,8 @@ void Model::upload(const ModelIndex& ix, const uint8_t* weights) {
 
 void Model::alloc_state() {
     const ModelConfig& c = cfg_;
-    const size_t conv_b = (size_t)c.conv_channels() * (c.conv_kernel - 1) * 4;
+    // conv state: 3 values per channel at a 4-float stride (16-byte rows the decode kernel DMAs)
+    const size_t conv_b = (size_t)c.conv_channels() * 4 * 4;
     const size_t rec_b = (size_t)c.gdn_heads * c.gdn_dk * c.gdn_dv * 4;
     const int blocks = (max_context_ + 15) / 16;
     const size_t pool_b = (size_t)blocks * c.n_kv_heads * 16 * c.head_dim * 2;
@@ -376,11 +378,10 @@ void Model::setup_engine() {
     if (c.rope_dim % 8 != 0 || c.rope_dim > c.head_dim) throw unsupported("rope_dim must be a multiple of 8");
     if (c.gdn_dk != 128 || c.gdn_dv != 128) throw unsupported("GDN dk and dv must be 128");
     if (c.conv_kernel != 4) throw unsupported("the GDN conv kernel must be 4");
-    const int S = std::min(grid / c.n_kv_heads, 128), G = c.n_q_heads / c.n_kv_heads;
+    const int S = std::min(grid / c.n_kv_heads, kMaxSplits), G = c.n_q_heads / c.n_kv_heads;
     if (S < 1) throw unsupported("too many kv heads");
     const int H = c.gdn_heads;
-    if (H * 128 + H * 16 > 12288) throw unsupported("too many GDN heads");
-    if (2 * S + 64 * S + 64 > 12288) throw unsupported("too many attention splits");
+    if (H * 128 + H * 16 > 6144) throw unsupported("too many GDN heads");
 
     // exchange buffers: sizes per (layer, phase), allocated in one arena
     struct Buf {
@@ -403,7 +404,8 @@ void Model::setup_engine() {
         P.w = m.w; P.sz = m.sz;
         if (decode_gemv_variant(m.kind, m.k) < 0) throw unsupported("matrix width " + std::to_string(m.k));
         const int rb = m.kind ? m.k / 2 : m.k * 2, szb = m.kind ? (m.k / m.group) * 4 : 0;
-        if ((rb + szb) * (epi == EP_SWIGLU ? 2 : 1) > 12 * 1024) throw unsupported("rows too wide for the LDS region");
+        if ((rb + szb) * (epi == EP_SWIGLU ? 2 : 1) + (epi == EP_CONV ? 32 : 0) > 8 * 1024)
+            throw unsupported("rows too wide for the LDS region");
         if (m.kind == MAT_Q4 && m.group != 32 && m.group != 64 && m.group != 128)
             throw unsupported("q4 group size " + std::to_string(m.group));
         if (epi == EP_CONV && (rows + nw - 1) / nw > 64) throw unsupported("too many in-projection rows per wave");
@@ -482,7 +484,7 @@ void Model::setup_engine() {
     prog.push_back(hd); out_buf.push_back(-1);
     if ((int)prog.size() > kMaxPhases) throw unsupported("too many layers");
     for (const Phase& P : prog)
-        if (P.kind == PH_GEMV && (P.in_n > 12288 || P.in_n > P.k + 2048 * (P.xnorm == XN_GDN)))
+        if (P.kind == PH_GEMV && (P.in_n > 6144 || P.in_n > P.k + 2048 * (P.xnorm == XN_GDN)))
             throw unsupported("input vector too long");
 
     exch_ = (uint64_t*)dalloc(total * 8);
@@ -549,6 +551,7 @@ void Model::run_engine(const EngineRun& r) {
     a.pos0 = r.pos0;
     a.out_ids = r.record_ids ? out_ids_ : nullptr;
     a.trace = r.trace;
+    a.sub = r.sub;
     a.trace_cap = r.trace_cap;
     a.tag_base = tag_base_;
     tag_base_ += (uint32_t)tags;
@@ -777,32 +780,45 @@ double Model::profile_token() {
 }
 
 // Per-phase device times of one greedy decode token (the counterpart of Gpu::profile's
-// per-label timestamp sums, kernels/src/lib.rs:366-396). For every phase the timeline gives when
-// workgroup 0 had its input and when the slowest and the fastest workgroup were done:
-//   work_ms = slowest done - input ready, exchange_ms = input ready - previous slowest done.
+// per-label timestamp sums, kernels/src/lib.rs:366-396). For every phase and workgroup the
+// timeline has the moment the workgroup had its input and the moment it was done. Reported per
+// phase: the phase's span (latest done minus the previous phase's latest done), the median and
+// maximum per-workgroup compute time (done - input), and the median and maximum hand-over latency
+// (input - previous phase's latest done).
 std::string Model::profile_token_json() {
     if (!persistent_) throw Error(QNE_EINVAL, "the phase profile needs the persistent engine");
     uint32_t t, p;
     last_token(&t, &p);
     if (p >= (uint32_t)max_context_) throw Error(QNE_ECONTEXT, "context limit reached");
-    const int nph = nph_;
-    const size_t n = 2 + 3 * (size_t)nph;
+    const int nph = nph_, grid = engine_grid_;
+    const size_t n = 2 + 2 * (size_t)nph * grid;
     std::vector<unsigned long long> tr(n, 0ull);
-    for (int b = 0; b < nph; b++) tr[3 + 3 * b] = ~0ull;
     unsigned long long* d = (unsigned long long*)dalloc(n * 8);
     QNE_HIP(hipMemcpy(d, tr.data(), n * 8, hipMemcpyHostToDevice));
     EngineRun r;
     r.feed = 1; r.head = 1; r.argmax = 1; r.n_steps = 1; r.pos0 = p;
     r.trace = d;
     r.trace_cap = nph;
+    const size_t nsub = 8 * (size_t)nph * grid;
+    std::vector<unsigned long long> sub(nsub, 0ull);
+    unsigned long long* dsub = (unsigned long long*)dalloc(nsub * 8);
+    QNE_HIP(hipMemcpy(dsub, sub.data(), nsub * 8, hipMemcpyHostToDevice));
+    r.sub = dsub;
     run_engine(r);
     sync();
     QNE_HIP(hipMemcpy(tr.data(), d, n * 8, hipMemcpyDeviceToHost));
+    QNE_HIP(hipMemcpy(sub.data(), dsub, nsub * 8, hipMemcpyDeviceToHost));
     int khz = 0;
     QNE_HIP(hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, device_));
     const double tick_ms = khz > 0 ? 1.0 / (double)khz : 1e-5;
     auto ms = [&](unsigned long long a, unsigned long long b) { return b > a ? (double)(b - a) * tick_ms : 0.0; };
-    std::map<std::string, double> total, work, wait;
+    auto med = [](std::vector<double> v) {
+        if (v.empty()) return 0.0;
+        std::sort(v.begin(), v.end());
+        return v[v.size() / 2];
+    };
+    std::map<std::string, double> span_l, comp_l, exch_l;
+    std::map<std::string, std::vector<double>> sub_l;
     std::string phases = "[";
     unsigned long long prev = tr[0];
     int l = 0, k = 0;
@@ -817,13 +833,35 @@ std::string Model::profile_token_json() {
             label = std::string(at ? "attn." : "gdn.") + (at ? attn_names[k] : gdn_names[k]);
             if (++k == (at ? 6 : 5)) { k = 0; l++; }
         }
-        const unsigned long long dmax = tr[2 + 3 * b], dmin = tr[3 + 3 * b], in = tr[4 + 3 * b];
-        total[label] += ms(prev, dmax);
-        work[label] += ms(in, dmax);
-        wait[label] += ms(prev, in);
-        char buf[192];
-        std::snprintf(buf, sizeof buf, "%s[\"%s\",%.5f,%.5f,%.5f]", b ? "," : "", label.c_str(), ms(in, dmax),
-                      ms(in, dmin), ms(prev, in));
+        unsigned long long dmax = 0;
+        std::vector<double> comp, exch;
+        for (int w = 0; w < grid; w++) {
+            const unsigned long long in = tr[2 + 2 * ((size_t)b * grid + w)], done = tr[3 + 2 * ((size_t)b * grid + w)];
+            dmax = std::max(dmax, done);
+            comp.push_back(ms(in, done));
+            exch.push_back(ms(prev, in));
+        }
+        {
+            std::vector<double> parts[5];
+            for (int w = 0; w < grid; w++) {
+                const unsigned long long* q = sub.data() + 8 * ((size_t)b * grid + w);
+                if (q[0] == 0 || q[5] == 0) continue;
+                for (int k2 = 0; k2 < 5; k2++) parts[k2].push_back(ms(q[k2], q[k2 + 1]));
+            }
+            if (!parts[0].empty()) {
+                auto& v = sub_l[label];
+                v.resize(5, 0.0);
+                for (int k2 = 0; k2 < 5; k2++) v[k2] += med(parts[k2]);
+            }
+        }
+        const double span = ms(prev, dmax), cm = med(comp), em = med(exch);
+        const double cx = *std::max_element(comp.begin(), comp.end()), ex = *std::max_element(exch.begin(), exch.end());
+        span_l[label] += span;
+        comp_l[label] += cm;
+        exch_l[label] += em;
+        char buf[224];
+        std::snprintf(buf, sizeof buf, "%s[\"%s\",%.5f,%.5f,%.5f,%.5f,%.5f]", b ? "," : "", label.c_str(), span, cm, cx,
+                      em, ex);
         phases += buf;
         prev = dmax;
     }
@@ -837,11 +875,21 @@ std::string Model::profile_token_json() {
         }
         return o + "}";
     };
-    char head[160];
+    char head[200];
     std::snprintf(head, sizeof head, "{\"total_ms\":%.5f,\"tail_ms\":%.5f,\"tick_ms\":%.3g,", ms(tr[0], tr[1]),
                   ms(prev, tr[1]), tick_ms);
-    return std::string(head) + "\"labels\":" + obj(total) + ",\"work_ms\":" + obj(work) + ",\"exchange_ms\":" +
-           obj(wait) + ",\"phases\":" + phases + "}";
+    std::string subs = "{";
+    for (auto& kv : sub_l) {
+        char buf[160];
+        std::snprintf(buf, sizeof buf, "%s\"%s\":[%.5f,%.5f,%.5f,%.5f,%.5f]", subs.size() > 1 ? "," : "",
+                      kv.first.c_str(), kv.second[0], kv.second[1], kv.second[2], kv.second[3], kv.second[4]);
+        subs += buf;
+    }
+    subs += "}";
+    return std::string(head) + "\"gemv_steps_median_ms\":" + subs + ",\"labels\":" + obj(span_l) + ",\"compute_median_ms\":" + obj(comp_l) +
+           ",\"handover_median_ms\":" + obj(exch_l) +
+           ",\"phase_columns\":[\"label\",\"span\",\"compute_median\",\"compute_max\",\"handover_median\",\"handover_max\"]" +
+           ",\"phases\":" + phases + "}";
 }
 
 }  // namespace qne

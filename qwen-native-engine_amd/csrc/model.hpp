@@ -46,6 +46,7 @@ struct EngineRun {
     uint32_t pos0 = 0;
     bool record_ids = false;
     unsigned long long* trace = nullptr;
+    unsigned long long* sub = nullptr;
     int trace_cap = 0;
 };
 
