@@ -78,21 +78,66 @@ def cpu_baseline(index, buf, cfg, ctx, tokens):
     return tokens / dt, L.oc_num_threads()
 
 
+TRAFFIC_PROFILE = ROOT / "profiles" / "k_decode_2b_int4_ctx4000_hbm_traffic.md"
+
+
+def profiled_traffic(steps: int):
+    """HBM bytes per decode launch measured by the FETCH_SIZE / WRITE_SIZE counter passes recorded
+    in the profile summary (scaled by a plain copy of known size), when that profile covers launches
+    of the same window length; else None."""
+    try:
+        text = TRAFFIC_PROFILE.read_text()
+    except OSError:
+        return None
+    vals = {}
+    for line in text.splitlines():
+        if line.startswith("traffic_") and ":" in line:
+            k, v = line.split(":", 1)
+            vals[k.strip()] = float(v)
+    if int(vals.get("traffic_steps_per_launch", -1)) != steps or "traffic_bytes_per_launch" not in vals:
+        return None
+    return vals["traffic_bytes_per_launch"]
+
+
+def copy_calibration(mib: int) -> None:
+    """A plain device-to-device copy of a known size: under a hardware-counter profiler its
+    FETCH_SIZE / WRITE_SIZE readings per dispatch, divided into the bytes it must move, give the
+    scale factor applied to the decode kernel's readings."""
+    import torch
+    n = mib << 20
+    src = torch.empty(n, dtype=torch.uint8, device="cuda").fill_(1)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes": n, "dispatches": 3}))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=96)
-    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--warmup", type=int, default=None,
+                    help="untimed warmup steps, run as one window (default: as many as --steps, so that "
+                         "every decode window a profile sees has the timed length)")
     ap.add_argument("--ctx", type=int, default=4000)
     ap.add_argument("--config", default="2b")
     ap.add_argument("--cpu-tokens", type=int, default=4)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--engine", default="persistent", choices=["persistent", "graph"])
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only run a plain device copy of MIB MiB three times (scales the HBM byte counters)")
     args = ap.parse_args()
+    if args.warmup is None:
+        args.warmup = args.steps
+    if args.copy_calibration:
+        copy_calibration(args.copy_calibration)
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this engine runs batch-1 decode on one GPU; --gpus above 1 is not supported "
-              "(see DESIGN.md for how the path would shard)", file=sys.stderr)
+              "(the decode path is measured on one GPU only)", file=sys.stderr)
         sys.exit(2)
     import qne
     import weights as W
@@ -126,7 +171,9 @@ def main():
     assert dev_steps == args.steps and len(ids) == args.steps + 1
     tok_s = args.steps / wall
     bytes_tok = algorithmic_bytes_per_token(cfg, mats, args.ctx + (args.steps - 1) / 2)
+    # one k_decode launch covers the whole timed window: bytes per launch / launch duration
     achieved = bytes_tok["total"] * args.steps / (dev_ms / 1e3) / 1e9
+    traffic = profiled_traffic(args.steps) if args.ctx == 4000 and args.config == "2b" else None
     result = {
         "metric": "decode tok/s @ batch 1, ctx 4096 (2B int4) + % of HBM roofline",
         "value": round(tok_s, 2),
@@ -145,9 +192,13 @@ def main():
                    "layers": cfg["layers"], "hidden": cfg["hidden"], "vocab": cfg["vocab"], "ctx": args.ctx,
                    "batch": 1, "window": args.steps},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                     "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None,
-                     "kernel": f"decode step ({m.dispatches_per_token()} kernels per token)",
-                     "bytes_per_step": bytes_tok["total"], "device_ms_per_step": round(dev_ms / args.steps, 4)},
+                     "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": traffic,
+                     "traffic_source": TRAFFIC_PROFILE.name if traffic else None,
+                     "kernel": f"k_decode, one launch per {args.steps}-token window"
+                               if args.engine == "persistent" else
+                               f"decode step ({m.dispatches_per_token()} kernels per token)",
+                     "bytes_per_launch": bytes_tok["total"] * args.steps, "bytes_per_step": bytes_tok["total"],
+                     "device_ms_per_launch": round(dev_ms, 3), "device_ms_per_step": round(dev_ms / args.steps, 4)},
         "detail": {"bytes_per_token": bytes_tok, "weights_gen_s": round(gen_s, 2), "prefill_s": round(prefill_s, 2),
                    "prefill_tok_s": round((args.ctx - 1) / prefill_s, 1), "adapter": m.adapter},
     }

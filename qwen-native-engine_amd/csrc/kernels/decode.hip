@@ -1031,7 +1031,9 @@ __device__ __forceinline__ void trace_in(const Env& e, int inst) {
 
 }  // namespace
 
-__global__ __launch_bounds__(kT, 1) void k_decode(DecodeArgs a) {
+// The program body; instantiated by the two kernels below so that profiles tell prompt-token runs
+// from greedy decode windows.
+__device__ __forceinline__ void decode_program(const DecodeArgs& a) {
     __shared__ __attribute__((aligned(16))) float xs[kXs];
     __shared__ __attribute__((aligned(16))) uint8_t regs[kNW * kWaveLds];
     __shared__ float red[2 * kNW];
@@ -1198,6 +1200,11 @@ __global__ __launch_bounds__(kT, 1) void k_decode(DecodeArgs a) {
     if (a.trace && e.wg == 0 && threadIdx.x == 0) a.trace[1] = __builtin_amdgcn_s_memrealtime();
 }
 
+// Greedy decode windows and single steps (feed 1).
+__global__ __launch_bounds__(kT, 1) void k_decode(DecodeArgs a) { decode_program(a); }
+// Prompt tokens taken from `ids` (feed 0): prefill and prefill_chunk.
+__global__ __launch_bounds__(kT, 1) void k_prefill_tokens(DecodeArgs a) { decode_program(a); }
+
 int decode_gemv_variant(int kind, int k) {
     if (k <= 0 || k % 512 != 0) return -1;
     if (kind == 1) return k <= 6144 ? 1 : -1;  // a q4 row of 6144 is 3456 bytes of LDS
@@ -1206,15 +1213,18 @@ int decode_gemv_variant(int kind, int k) {
 
 hipError_t launch_decode(const DecodeArgs& a, int grid, hipStream_t st) {
     void* args[] = {(void*)&a};
-    return hipLaunchCooperativeKernel((const void*)k_decode, dim3(grid), dim3(kT), args, 0, st);
+    const void* fn = a.feed ? (const void*)k_decode : (const void*)k_prefill_tokens;
+    return hipLaunchCooperativeKernel(fn, dim3(grid), dim3(kT), args, 0, st);
 }
 
 int decode_max_grid() {
     int dev = 0, cus = 0, per = 0;
     if (hipGetDevice(&dev) != hipSuccess) return 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, (const void*)k_decode, kT, 0) != hipSuccess) return 0;
-    return per >= 1 ? cus : 0;
+    for (const void* fn : {(const void*)k_decode, (const void*)k_prefill_tokens}) {
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, fn, kT, 0) != hipSuccess || per < 1) return 0;
+    }
+    return cus;
 }
 
 }  // namespace qne
