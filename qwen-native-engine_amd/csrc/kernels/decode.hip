@@ -14,9 +14,13 @@
 //    16-byte loads until every tag it needs is current. There is no grid barrier and no release /
 //    acquire fence, so no L2 writeback or invalidate: on MI355X those cost ~10 us per barrier
 //    against ~2.4 us for a tagged exchange of a 2048-vector;
-//  - each wave streams the weights of its rows of the NEXT phase into its own 12 KiB of LDS with
-//    global_load_lds_dwordx4 before it starts waiting for that phase's input, so HBM works while
-//    the exchange settles. A wave only ever reads what it loaded itself: no cross-wave handshake;
+//  - each wave owns 16 KiB of LDS in two 8 KiB halves; the phases that read prefetched data
+//    ("region phases": LDS GEMVs, GDN, attention) alternate between the halves. When a region
+//    phase has done its last LDS read it sends the data of the region phase two ahead into the
+//    half it just freed (global_load_lds_dwordx4), and only then waits for the next phase's input:
+//    the weight stream then overlaps the hand-over, and nothing the phase computes waits behind it
+//    (vector-memory completion is in order, and the compiler makes any LDS read that follows an
+//    LDS DMA wait for it). A wave only ever reads what it loaded itself: no cross-wave handshake;
 //  - rows are spread over waves wave-major (wave w of every workgroup before wave w+1), so every
 //    workgroup owns rows of every vector that all workgroups consume;
 //  - RMSNorm is folded into the input exchange (the poll multiplies by the gain and sums the
@@ -163,6 +167,10 @@ __device__ __forceinline__ Rows part(int rows, int gw, int nw) {
     const int per = rows / nw, rem = rows % nw;
     return {gw * per + min(gw, rem), per + (gw < rem ? 1 : 0)};
 }
+// The same for a phase's outputs (rows / waves precomputed on the host).
+__device__ __forceinline__ Rows part_p(CPhase& P, int gw) {
+    return {gw * P.rper + min(gw, P.rrem), P.rper + (gw < P.rrem ? 1 : 0)};
+}
 
 // ---- DMA into the wave's LDS region ----
 
@@ -184,13 +192,13 @@ struct GemvGeo {
 };
 __device__ __forceinline__ GemvGeo geo(CPhase& P) {
     GemvGeo g;
-    g.rb = P.mkind ? P.k / 2 : P.k * 2;
-    g.szb = P.mkind ? (P.k / P.group) * 4 : 0;
-    g.stride = g.rb + g.szb;
-    g.nm = P.epi == EP_SWIGLU ? 2 : 1;
-    g.conv = P.epi == EP_CONV ? 32 : 0;
-    g.cap = kHalf / (g.stride * g.nm + g.conv);
-    g.per = g.nm * ((g.rb + 1023) / 1024 + (g.szb + 1023) / 1024);
+    g.rb = P.rb;
+    g.szb = P.szb;
+    g.stride = P.stride;
+    g.nm = P.nm;
+    g.conv = P.convb;
+    g.cap = P.cap;
+    g.per = P.dper;
     return g;
 }
 
@@ -220,14 +228,14 @@ __device__ __forceinline__ void dma_rows(CPhase& P, const GemvGeo& g, int o0, in
 struct Step {
     int kind, K, n4, n2, n1, nsteps;
 };
-__device__ __forceinline__ Step make_step(int kind, int K) {
+__device__ __forceinline__ Step make_step(CPhase& P) {
     Step t;
-    t.kind = kind;
-    t.K = K;
-    t.n4 = K / 2048;
-    t.n2 = (K % 2048) / 1024;
-    t.n1 = (K % 1024) / 512;
-    t.nsteps = kind ? t.n4 + t.n2 + t.n1 : K / 512;
+    t.kind = P.mkind;
+    t.K = P.k;
+    t.n4 = P.n4;
+    t.n2 = P.n2;
+    t.n1 = P.n1;
+    t.nsteps = P.nsteps;
     return t;
 }
 
@@ -302,23 +310,23 @@ __device__ __forceinline__ float dot8(uint32_t w, const float* x) {
 }
 
 // The lane's share of step j of the dot product of one row held in LDS (weights at `row`, the
-// row's (scale, zero) pairs at row + rb).
-__device__ __forceinline__ float step_dot(const Step& t, int j, int G, int rb, const uint8_t* row, const XC& X, int lane) {
+// row's (scale, zero) pairs at row + rb; gs = log2 of the group size).
+__device__ __forceinline__ float step_dot(const Step& t, int j, int gs, int rb, const uint8_t* row, const XC& X, int lane) {
     if (t.kind == 1) {
         const uint8_t* szr = row + rb;
         if (j < t.n4) {
             const u32x4 w = *(const u32x4*)(row + 1024 * j + 16 * lane);
-            const uint32_t sz = *(const uint32_t*)(szr + 4 * ((2048 * j + 32 * lane) / G));
+            const uint32_t sz = *(const uint32_t*)(szr + 4 * ((2048 * j + 32 * lane) >> gs));
             const float dq = dot8(w.x, &X.x[0]) + dot8(w.y, &X.x[8]) + dot8(w.z, &X.x[16]) + dot8(w.w, &X.x[24]);
             return lo_h(sz) * (dq - hi_h(sz) * X.sum);
         }
         if (j < t.n4 + t.n2) {
             const u32x2 w = *(const u32x2*)(row + 1024 * t.n4 + 8 * lane);
-            const uint32_t sz = *(const uint32_t*)(szr + 4 * ((2048 * t.n4 + 16 * lane) / G));
+            const uint32_t sz = *(const uint32_t*)(szr + 4 * ((2048 * t.n4 + 16 * lane) >> gs));
             return lo_h(sz) * (dot8(w.x, &X.x[0]) + dot8(w.y, &X.x[8]) - hi_h(sz) * X.sum);
         }
         const uint32_t w = *(const uint32_t*)(row + 1024 * t.n4 + 512 * t.n2 + 4 * lane);
-        const uint32_t sz = *(const uint32_t*)(szr + 4 * ((2048 * t.n4 + 1024 * t.n2 + 8 * lane) / G));
+        const uint32_t sz = *(const uint32_t*)(szr + 4 * ((2048 * t.n4 + 1024 * t.n2 + 8 * lane) >> gs));
         return lo_h(sz) * (dot8(w, &X.x[0]) - hi_h(sz) * X.sum);
     }
     const u32x4 w = *(const u32x4*)(row + 1024 * j + 16 * lane);
@@ -376,13 +384,9 @@ __device__ __forceinline__ uint32_t tag_of(const DecodeArgs& a, int step, int p)
 }
 
 // Whether the LM head has a register-streaming path (else it goes through the LDS region).
-__device__ __forceinline__ bool head_fast(CPhase& P) {
-    return P.epi == EP_HEAD && (P.mkind == 0 || P.group == 64) && (P.k == 512 || P.k == 1024 || P.k == 2048);
-}
+__device__ __forceinline__ bool head_fast(CPhase& P) { return P.fast_head != 0; }
 // Phases whose data is prefetched into a wave's LDS half.
-__device__ __forceinline__ bool uses_region(CPhase& P) {
-    return (P.kind == PH_GEMV && !head_fast(P)) || P.kind == PH_GDN || P.kind == PH_ATTN;
-}
+__device__ __forceinline__ bool uses_region(CPhase& P) { return P.region != 0; }
 __device__ __forceinline__ bool head_at(const DecodeArgs& a, int step) {
     return a.head == 1 || (a.head == 2 && step == a.n_steps - 1);
 }
@@ -402,7 +406,10 @@ __device__ __forceinline__ bool next_region_phase(const DecodeArgs& a, CPhase* p
     return false;
 }
 
-// ---- prefetch of a phase's data into one half of the wave's LDS region ----
+// First position of context split sp of S over len positions (sp * len < 2^32: len <= 2^16, S <= 92).
+__device__ __forceinline__ int split_at(int sp, uint32_t len, int S) { return (int)(((uint32_t)sp * len) / (uint32_t)S); }
+
+// ---- prefetch of a region phase's data into one half of the wave's LDS region ----
 // GEMV: the wave's first outputs (rows, then their scale/zero pairs; for the GDN in-projection the
 // conv state and conv weights of those rows after them). GDN: the wave's 512-byte state column.
 // Attention: the K/V rows of the wave's positions, through the block table.
@@ -411,7 +418,7 @@ __device__ __forceinline__ void prefetch(const Env& e, CPhase& P, int step, uint
     const int lane = e.lane;
     if (P.kind == PH_GEMV) {
         const GemvGeo g = geo(P);
-        const Rows R = part(P.rows, e.gwm, e.nw);
+        const Rows R = part_p(P, e.gwm);
         const int cnt = min(R.n, g.cap);
         dma_rows(P, g, R.r0, cnt, 0, nxt, lane);
         if (P.epi == EP_CONV && cnt > 0) {
@@ -431,11 +438,11 @@ __device__ __forceinline__ void prefetch(const Env& e, CPhase& P, int step, uint
             dma_bytes((const uint8_t*)(P.rec + ((size_t)h * kDK + t) * kDK), 512, nxt, lane);
         }
     } else if (P.kind == PH_ATTN) {
-        const int nkv = P.kv_heads, S = min(e.nwg / nkv, kMaxSplits);
+        const int nkv = P.kv_heads, S = P.splits;
         if (e.wg < nkv * S) {
             const int g = e.wg / S, sp = e.wg % S;
             const uint32_t pos = a.pos0 + (uint32_t)step, len = pos + 1;
-            const int p0 = (int)((uint64_t)sp * len / S), p1 = (int)((uint64_t)(sp + 1) * len / S);
+            const int p0 = split_at(sp, len, S), p1 = split_at(sp + 1, len, S);
             const int half = lane / 32, li = lane % 32;
             int bid[kAttnU];
 #pragma unroll
@@ -467,7 +474,7 @@ __device__ __forceinline__ float gemv_input(const Env& e, CPhase& P, int step, i
     float ss = 0.0f;
     float* xs = e.xs;
     const bool norm = P.xnorm == XN_NORM;
-    const Step st = make_step(P.mkind, P.k);
+    const Step st = make_step(P);
     const bool cm = !head_fast(P);  // the LDS-region GEMV reads chunk-major slices
     // the RMSNorm gains of the pairs this thread will poll, loaded before the poll so that their
     // latency overlaps it (norm inputs fit one polling round: in_n <= 2 * kT * kPoll)
@@ -544,7 +551,7 @@ __device__ __forceinline__ void head_rows(const Env& e, CPhase& P, WaveState& ws
 }
 
 __device__ __forceinline__ void head_phase(const Env& e, CPhase& P, WaveState& ws, float inv) {
-    const Rows R = part(P.rows, e.gwm, e.nw);
+    const Rows R = part_p(P, e.gwm);
     if (R.n == 0) return;
     if (P.mkind == 0) {
         if (P.k == 512) head_rows<KIND_F16, 512>(e, P, ws, inv, R, e.xs);
@@ -557,115 +564,110 @@ __device__ __forceinline__ void head_phase(const Env& e, CPhase& P, WaveState& w
     }
 }
 
-// One GEMV phase for this wave's outputs, rows read from `cur` (this phase's half); the next
-// region phase's data is first sent to `nxt`. Output i sits in slot i % cap; the first
-// min(n, cap) were prefetched (with more outputs than fit, slots are refilled as groups finish).
-// Outputs are computed in groups of up to 8 rows (8 / nm outputs): for every step of x, the step's
-// slice is read from LDS once and applied to the whole group, then the group is reduced together.
-// cur, nxt and xs are __restrict__: the compiler then knows that the reads of cur and xs do not
-// touch the half being filled, so they do not wait for that DMA.
+// One GEMV phase for this wave's outputs, rows read from `cur` (this phase's half). Output i sits
+// in slot i % cap; the first min(n, cap) were prefetched (with more outputs than fit, slots are
+// refilled as groups finish). Outputs are computed in groups of up to 8 rows (8 / nm outputs): for
+// every step of x, the step's slice is read from LDS once and applied to the whole group, then the
+// group is reduced together. The caller then sends the data of the region phase two ahead into `cur`.
 __device__ __forceinline__ void gemv_body(const Env& e, CPhase& P, int step, int p, WaveState& ws, float inv,
-                                          const uint8_t* __restrict__ cur, uint8_t* __restrict__ nxt,
-                                          const float* __restrict__ xs, CPhase* pn, int pn_step) {
+                                          uint8_t* cur, const float* xs) {
     const DecodeArgs& a = *e.a;
     const int lane = e.lane;
     unsigned long long tt[6];
     tt[0] = __builtin_amdgcn_s_memrealtime();
-    __builtin_amdgcn_s_waitcnt(kWaitAll);  // this phase's rows (issued a phase ago) are in
-    tt[1] = __builtin_amdgcn_s_memrealtime();
-    if (pn) prefetch(e, *pn, pn_step, nxt);
-    tt[2] = __builtin_amdgcn_s_memrealtime();
+    __builtin_amdgcn_s_waitcnt(kWaitAll);  // this phase's rows (issued two region phases ago) are in
     const GemvGeo g = geo(P);
-    const Rows R = part(P.rows, e.gwm, e.nw);
-    const uint32_t tag = tag_of(a, step, p);
-    uint64_t* out = P.out ? P.out + (size_t)(step & 1) * P.out_stride : nullptr;
-    if (R.n == 0) return;
-    const Step t = make_step(P.mkind, P.k);
-    const bool gdn = P.xnorm == XN_GDN;
-    const int H = gdn ? P.heads : 0;
-    const int gmax = 8 / g.nm;  // outputs per group
-    const int pre = min(R.n, g.cap);  // outputs prefetched
-    const bool stream = R.n > g.cap;
-    const int go = stream ? max(1, min(gmax, g.cap / 2)) : min(gmax, R.n);
-    const uint8_t* cvs = cur + pre * g.nm * g.stride;  // EP_CONV: conv state / weights of the prefetched rows
-    uint8_t* curw = const_cast<uint8_t*>(cur);
-    int issued = pre;
-    XC X;
-    if (t.nsteps == 1) load_step(xs, t, 0, gdn, H, X, lane);
-    asm volatile("" ::"v"(X.x[0]), "v"(X.x[31]));
-    tt[3] = __builtin_amdgcn_s_memrealtime();
-    tt[4] = tt[3];
-    for (int o0 = 0; o0 < R.n; o0 += go) {
-        const int ng = min(go, R.n - o0), nr = ng * g.nm;
-        if (o0 + ng > pre) wait_vm((issued - o0 - ng) * g.per);  // refilled group
-        float acc[8];
+    const Rows R = part_p(P, e.gwm);
+    tt[1] = tt[2] = tt[3] = tt[0];
+    if (R.n > 0) {
+        const uint32_t tag = tag_of(a, step, p);
+        uint64_t* out = P.out ? P.out + (size_t)(step & 1) * P.out_stride : nullptr;
+        const Step t = make_step(P);
+        const bool gdn = P.xnorm == XN_GDN;
+        const int H = gdn ? P.heads : 0;
+        const int gmax = 8 / g.nm;  // outputs per group
+        const int pre = min(R.n, g.cap);  // outputs prefetched
+        const bool stream = R.n > g.cap;
+        const int go = stream ? max(1, min(gmax, g.cap / 2)) : min(gmax, R.n);
+        const uint8_t* cvs = cur + pre * g.nm * g.stride;  // EP_CONV: conv state / weights of the prefetched rows
+        int issued = pre;
+        XC X;
+        if (t.nsteps == 1) load_step(xs, t, 0, gdn, H, X, lane);
+        asm volatile("" ::"v"(X.x[0]), "v"(X.x[31]));
+        tt[1] = __builtin_amdgcn_s_memrealtime();
+        tt[2] = tt[1];
+        for (int o0 = 0; o0 < R.n; o0 += go) {
+            const int ng = min(go, R.n - o0), nr = ng * g.nm;
+            if (o0 + ng > pre) wait_vm((issued - o0 - ng) * g.per);  // refilled group
+            float acc[8];
 #pragma unroll
-        for (int r = 0; r < 8; r++) acc[r] = 0.0f;
-        for (int j = 0; j < t.nsteps; j++) {
-            if (t.nsteps > 1) load_step(xs, t, j, gdn, H, X, lane);
+            for (int r = 0; r < 8; r++) acc[r] = 0.0f;
+            for (int j = 0; j < t.nsteps; j++) {
+                if (t.nsteps > 1) load_step(xs, t, j, gdn, H, X, lane);
 #pragma unroll
-            for (int r = 0; r < 8; r++) {
-                if (r < nr) {
-                    const int i = r / g.nm, m = r % g.nm;
-                    const int slot = stream ? (o0 + i) % g.cap : o0 + i;
-                    acc[r] += step_dot(t, j, P.group, g.rb, cur + slot * g.nm * g.stride + m * g.stride, X, lane);
+                for (int r = 0; r < 8; r++) {
+                    if (r < nr) {
+                        const int i = r / g.nm, m = r % g.nm;
+                        const int slot = stream ? (o0 + i) % g.cap : o0 + i;
+                        acc[r] += step_dot(t, j, P.gshift, g.rb, cur + slot * g.nm * g.stride + m * g.stride, X, lane);
+                    }
                 }
             }
-        }
-        if (o0 == 0) {
-            asm volatile("" ::"v"(acc[0]), "v"(acc[1]), "v"(acc[7]));
-            tt[4] = __builtin_amdgcn_s_memrealtime();
-        }
-        // refill the group's slots with the outputs cap further on
-        for (int i = 0; i < ng && issued < R.n; i++, issued++) dma_rows(P, g, R.r0 + issued, 1, issued % g.cap, curw, lane);
-        const float tot = reduce8(acc, lane) * inv;   // lanes 8r..8r+7: row r of the group
-        const float up = __shfl_down(tot, 8, kWave);  // SwiGLU: the up row of the output
-        const int r = lane >> 3;
-        const int i = r / g.nm;
-        const bool lead = (lane & 7) == 0 && r % g.nm == 0 && i < ng;
-        const int o = R.r0 + o0 + i;
-        float y = tot;
-        if (P.epi == EP_RESID) {
-            // rows of h owned by this wave: outputs 0 and 1
-            const float t0 = __shfl(tot, 0, kWave), t1 = __shfl(tot, 8 * g.nm, kWave);
             if (o0 == 0) {
-                ws.hown[0] += t0;
-                if (ng > 1) ws.hown[1] += t1;
-            } else {
-                ws.hown[1] += t0;
+                asm volatile("" ::"v"(acc[0]), "v"(acc[1]), "v"(acc[7]));
+                tt[2] = __builtin_amdgcn_s_memrealtime();
             }
-            y = i == 0 && o0 == 0 ? ws.hown[0] : ws.hown[1];
-        }
-        if (lead) {
-            if (P.epi == EP_SWIGLU) y = silu(tot) * up;
-            else if (P.epi == EP_CONV && o < P.conv_ch) {
-                // conv state s0..s2 and weights w0..w3 of the output's channel
-                const int k = o0 + i;
-                float4 st, cw;
-                if (k < pre) {
-                    st = *(const float4*)(cvs + 16 * k);
-                    cw = *(const float4*)(cvs + 16 * pre + 16 * k);
+            // refill the group's slots with the outputs cap further on
+            for (int i = 0; i < ng && issued < R.n; i++, issued++) dma_rows(P, g, R.r0 + issued, 1, issued % g.cap, cur, lane);
+            const float tot = reduce8(acc, lane) * inv;   // lanes 8r..8r+7: row r of the group
+            const float up = __shfl_down(tot, 8, kWave);  // SwiGLU: the up row of the output
+            const int r = lane >> 3;
+            const int i = r / g.nm;
+            const bool lead = (lane & 7) == 0 && r % g.nm == 0 && i < ng;
+            const int o = R.r0 + o0 + i;
+            float y = tot;
+            if (P.epi == EP_RESID) {
+                // rows of h owned by this wave: outputs 0 and 1
+                const float t0 = __shfl(tot, 0, kWave), t1 = __shfl(tot, 8 * g.nm, kWave);
+                if (o0 == 0) {
+                    ws.hown[0] += t0;
+                    if (ng > 1) ws.hown[1] += t1;
                 } else {
-                    st = *(const float4*)(P.conv + (size_t)o * 4);
-                    cw = *(const float4*)(P.conv_w + (size_t)o * 4);
+                    ws.hown[1] += t0;
                 }
-                const float tt = st.x * cw.x + st.y * cw.y + st.z * cw.z + tot * cw.w;
-                float* sp = P.conv + (size_t)o * 4;
-                sp[0] = st.y; sp[1] = st.z; sp[2] = tot;
-                y = silu(tt);
+                y = i == 0 && o0 == 0 ? ws.hown[0] : ws.hown[1];
             }
-            if (P.epi == EP_HEAD) {
-                a.logits[o] = y;
-                if (better(y, (uint32_t)o, ws.best, ws.best_i)) { ws.best = y; ws.best_i = (uint32_t)o; }
-            } else {
-                put(out, (uint32_t)o, y, tag);
+            if (lead) {
+                if (P.epi == EP_SWIGLU) y = silu(tot) * up;
+                else if (P.epi == EP_CONV && o < P.conv_ch) {
+                    // conv state s0..s2 and weights w0..w3 of the output's channel
+                    const int k = o0 + i;
+                    float4 st, cw;
+                    if (k < pre) {
+                        st = *(const float4*)(cvs + 16 * k);
+                        cw = *(const float4*)(cvs + 16 * pre + 16 * k);
+                    } else {
+                        st = *(const float4*)(P.conv + (size_t)o * 4);
+                        cw = *(const float4*)(P.conv_w + (size_t)o * 4);
+                    }
+                    const float cv = st.x * cw.x + st.y * cw.y + st.z * cw.z + tot * cw.w;
+                    float* sp = P.conv + (size_t)o * 4;
+                    sp[0] = st.y; sp[1] = st.z; sp[2] = tot;
+                    y = silu(cv);
+                }
+                if (P.epi == EP_HEAD) {
+                    a.logits[o] = y;
+                    if (better(y, (uint32_t)o, ws.best, ws.best_i)) { ws.best = y; ws.best_i = (uint32_t)o; }
+                } else {
+                    put(out, (uint32_t)o, y, tag);
+                }
             }
         }
+        tt[3] = __builtin_amdgcn_s_memrealtime();
     }
-    tt[5] = __builtin_amdgcn_s_memrealtime();
     if (a.sub && e.wave == 0 && lane == 0 && step * a.nph + p < a.trace_cap) {
         unsigned long long* sb = a.sub + 8 * ((size_t)(step * a.nph + p) * e.nwg + e.wg);
-        for (int k = 0; k < 6; k++) sb[k] = tt[k];
+        for (int k = 0; k < 4; k++) sb[k] = tt[k];
     }
 }
 
@@ -698,13 +700,10 @@ __device__ __forceinline__ void gdn_input(const Env& e, CPhase& P, int step, int
 // Gated DeltaNet step (kernels/src/shaders.rs:436-520 after the conv): workgroup = (head, 8 value
 // columns), wave = one value column t, lane = keys 2l, 2l+1 of the value-major state column.
 // The first item's inputs are staged by gdn_input and its state column is in `cur`.
-__device__ __forceinline__ void gdn_body(const Env& e, CPhase& P, int step, int p, const Ctl& c,
-                                         const uint8_t* __restrict__ cur, uint8_t* __restrict__ nxt,
-                                         const float* __restrict__ xs, float* __restrict__ red, CPhase* pn,
-                                         int pn_step) {
+__device__ __forceinline__ void gdn_body(const Env& e, CPhase& P, int step, int p, const Ctl& c, const uint8_t* cur,
+                                         const float* xs, float* red) {
     const DecodeArgs& a = *e.a;
-    __builtin_amdgcn_s_waitcnt(kWaitAll);  // the state column (issued a phase ago) is in
-    if (pn) prefetch(e, *pn, pn_step, nxt);
+    __builtin_amdgcn_s_waitcnt(kWaitAll);  // the state column (issued two region phases ago) is in
     const int H = P.heads, lane = e.lane;
     const uint32_t tag = tag_of(a, step, p);
     uint64_t* out = P.out + (size_t)(step & 1) * P.out_stride;
@@ -712,7 +711,7 @@ __device__ __forceinline__ void gdn_body(const Env& e, CPhase& P, int step, int 
     for (int it = e.wg; it < H * 16; it += e.nwg) {
         if (it != e.wg) {
             gdn_input(e, P, step, p, it, c);
-            if (*e.bail) return;
+            if (*e.bail) break;
         }
         const int h = it / 16, cb = it % 16;
         const int aa = 4 * H * kDK + h, ba = 4 * H * kDK + H + h;
@@ -752,8 +751,9 @@ __device__ __forceinline__ void gdn_body(const Env& e, CPhase& P, int step, int 
 }
 
 // RMSNorm (weight w) + rotate-half RoPE of one 256-vector held 4 values per lane
-// (kernels/src/shaders.rs:575-593).
-__device__ __forceinline__ void norm_rope4(float (&v)[4], const float* w, const DecodeArgs& a, uint32_t pos, int lane) {
+// (kernels/src/shaders.rs:575-593). rope = {cos[64], sin[64]} of the step's angles.
+__device__ __forceinline__ void norm_rope4(float (&v)[4], const float* w, const DecodeArgs& a, const float* rope,
+                                           int lane) {
     float ss = v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3];
     ss = wave_sum_dpp(ss);
     const float inv = 1.0f / sqrtf(ss / (float)kHeadDim + 1e-6f);
@@ -769,8 +769,7 @@ __device__ __forceinline__ void norm_rope4(float (&v)[4], const float* w, const 
         o[i] = v[i];
         if (d < a.rope_dim) {
             const int fi = d < half ? d : d - half;
-            float sn, cs;
-            sincosf((float)pos * a.inv_freq[fi], &sn, &cs);
+            const float cs = rope[fi], sn = rope[64 + fi];
             o[i] = d < half ? v[i] * cs - other_lo * sn : v[i] * cs + other_hi * sn;
         }
     }
@@ -779,19 +778,17 @@ __device__ __forceinline__ void norm_rope4(float (&v)[4], const float* w, const 
 
 // Attention partials (kernels/src/shaders.rs:522-633 split over the context): workgroup =
 // (kv head g, split sp) over positions [p0, p1) of 0..pos; publishes (max, sum, acc[256]) per
-// q head of the group.
+// q head of the group. The K/V rows prefetched into half `rh` are read from it and the waves'
+// partials merged through it.
 __device__ __forceinline__ void attn_phase(const Env& e, CPhase& P, int step, int p, const Ctl& c, int rh,
-                                           CPhase* pn, int pn_step) {
+                                           const float* rope) {
     uint8_t* cur = e.regs + e.wave * kWaveLds + rh * kHalf;
     const DecodeArgs& a = *e.a;
-    const int nq = P.heads, nkv = P.kv_heads, G = nq / nkv, S = min(e.nwg / nkv, kMaxSplits), lane = e.lane;
-    if (e.wg >= nkv * S) {
-        if (pn) prefetch(e, *pn, pn_step, e.regs + e.wave * kWaveLds + (1 - rh) * kHalf);
-        return;
-    }
+    const int nq = P.heads, nkv = P.kv_heads, G = nq / nkv, S = P.splits, lane = e.lane;
+    if (e.wg >= nkv * S) return;
     const int g = e.wg / S, sp = e.wg % S;
     const uint32_t pos = a.pos0 + (uint32_t)step, len = pos + 1;
-    const int p0 = (int)((uint64_t)sp * len / S), p1 = (int)((uint64_t)(sp + 1) * len / S);
+    const int p0 = split_at(sp, len, S), p1 = split_at(sp + 1, len, S);
     const uint32_t tin = tag_of(a, step, p - P.in_rel), tag = tag_of(a, step, p);
     const uint64_t* in = P.in + (size_t)(step & 1) * P.in_stride;
     uint64_t* out = P.out + (size_t)(step & 1) * P.out_stride;
@@ -816,14 +813,14 @@ __device__ __forceinline__ void attn_phase(const Env& e, CPhase& P, int step, in
         float v[4];
         const float4 f = *(const float4*)(xs + e.wave * kHeadDim + 4 * lane);
         v[0] = f.x; v[1] = f.y; v[2] = f.z; v[3] = f.w;
-        norm_rope4(v, P.gain, a, pos, lane);
+        norm_rope4(v, P.gain, a, rope, lane);
 #pragma unroll
         for (int i = 0; i < 4; i++) qs[e.wave * kHeadDim + 4 * lane + i] = v[i] * 0.0625f;
     } else if (e.wave == G) {
         float v[4];
         const float4 f = *(const float4*)(xs + 1024 + 4 * lane);
         v[0] = f.x; v[1] = f.y; v[2] = f.z; v[3] = f.w;
-        norm_rope4(v, P.gain + kHeadDim, a, pos, lane);
+        norm_rope4(v, P.gain + kHeadDim, a, rope, lane);
         const float4 vv = *(const float4*)(xs + 1280 + 4 * lane);
         const float val[4] = {vv.x, vv.y, vv.z, vv.w};
         uint16_t kh[4], vh[4];
@@ -953,14 +950,12 @@ __device__ __forceinline__ void attn_phase(const Env& e, CPhase& P, int step, in
         }
     }
     bar();  // the regions are free again
-    if (pn) prefetch(e, *pn, pn_step, e.regs + e.wave * kWaveLds + (1 - rh) * kHalf);
 }
 
 // Combine of the attention partials: workgroup = (q head h, 64 dims c); times sigmoid(gate).
-// Combine of the attention partials: workgroup = (q head h, 64 dims c); times sigmoid(gate).
 __device__ __forceinline__ void comb_phase(const Env& e, CPhase& P, int step, int p, const Ctl& c) {
     const DecodeArgs& a = *e.a;
-    const int nq = P.heads, nkv = P.kv_heads, G = nq / nkv, S = min(e.nwg / nkv, kMaxSplits);
+    const int nq = P.heads, nkv = P.kv_heads, G = nq / nkv, S = P.splits;
     if (e.wg >= nq * 4) return;
     const int h = e.wg / 4, cq = e.wg % 4, g = h / G, gi = h % G;
     const uint32_t tin = tag_of(a, step, p - P.in_rel), tin2 = tag_of(a, step, p - P.in2_rel), tag = tag_of(a, step, p);
@@ -1038,6 +1033,7 @@ __device__ __forceinline__ void decode_program(const DecodeArgs& a) {
     __shared__ __attribute__((aligned(16))) uint8_t regs[kNW * kWaveLds];
     __shared__ float red[2 * kNW];
     __shared__ uint32_t redi[kNW];
+    __shared__ float rope[2 * 64];  // cos, sin of the step's RoPE angles
     __shared__ int bail;
     Env e;
     e.a = &a;
@@ -1064,11 +1060,15 @@ __device__ __forceinline__ void decode_program(const DecodeArgs& a) {
     bar();
 
     uint32_t token = a.feed ? a.tok[0] : a.ids[0];
-    int half = 0;  // half holding the data of the next region phase
+    int half = 0;  // half of the next region phase (region phases alternate between the halves)
     {
-        int ns, np;
-        if (uses_region(prog[0])) prefetch(e, prog[0], 0, region(0));
-        else if (next_region_phase(a, prog, 0, 0, ns, np)) prefetch(e, prog[np], ns, region(0));
+        // the first two region phases
+        int ps = 0, pp = 0;
+        bool more = uses_region(prog[0]) || next_region_phase(a, prog, 0, 0, ps, pp);
+        for (int k = 0; k < 2 && more; k++) {
+            prefetch(e, prog[pp], ps, region(k));
+            more = next_region_phase(a, prog, ps, pp, ps, pp);
+        }
     }
     for (int step = 0; step < a.n_steps; step++) {
         const uint32_t pos = a.pos0 + (uint32_t)step;
@@ -1077,7 +1077,13 @@ __device__ __forceinline__ void decode_program(const DecodeArgs& a) {
         // in the layout the first in-projection reads; 1/rms in red[2 kNW - 1]
         {
             CPhase& P0 = prog[0];
-            const Step st0 = make_step(P0.mkind, P0.k);
+            const Step st0 = make_step(P0);
+            if ((int)threadIdx.x < a.rope_dim / 2) {
+                float sn, cs;
+                sincosf((float)pos * a.inv_freq[threadIdx.x], &sn, &cs);
+                rope[threadIdx.x] = cs;
+                rope[64 + threadIdx.x] = sn;
+            }
             float ss = 0.0f;
             for (int cc = threadIdx.x; cc < a.hidden; cc += kT) {
                 const float v = embed_val(a, token, cc);
@@ -1102,33 +1108,25 @@ __device__ __forceinline__ void decode_program(const DecodeArgs& a) {
             CPhase& P = prog[p];
             if (P.is_head && !head) continue;
             const int inst = step * a.nph + p;
-            int ns = 0, np = 0;
-            const bool more = next_region_phase(a, prog, step, p, ns, np);
-            CPhase* pn = more ? &prog[np] : nullptr;
+            const int rh = half;
             switch (P.kind) {
                 case PH_GEMV: {
                     const float inv = gemv_input(e, P, step, p, c);
                     if (bail) { __builtin_amdgcn_s_waitcnt(kWaitAll); return; }
                     trace_in(e, inst);
-                    if (head_fast(P)) {
-                        head_phase(e, P, ws, inv);
-                    } else {
-                        gemv_body(e, P, step, p, ws, inv, region(half), region(1 - half), xs, pn, ns);
-                        half ^= 1;
-                    }
+                    if (head_fast(P)) head_phase(e, P, ws, inv);
+                    else gemv_body(e, P, step, p, ws, inv, region(half), xs);
                     break;
                 }
                 case PH_GDN:
                     if (e.wg < P.heads * 16) gdn_input(e, P, step, p, e.wg, c);
                     if (bail) { __builtin_amdgcn_s_waitcnt(kWaitAll); return; }
                     trace_in(e, inst);
-                    gdn_body(e, P, step, p, c, region(half), region(1 - half), xs, red, pn, ns);
-                    half ^= 1;
+                    gdn_body(e, P, step, p, c, region(half), xs, red);
                     break;
                 case PH_ATTN:
                     trace_in(e, inst);
-                    attn_phase(e, P, step, p, c, half, pn, ns);
-                    half ^= 1;
+                    attn_phase(e, P, step, p, c, half, rope);
                     break;
                 default:
                     trace_in(e, inst);
@@ -1136,6 +1134,16 @@ __device__ __forceinline__ void decode_program(const DecodeArgs& a) {
                     break;
             }
             if (bail) { __builtin_amdgcn_s_waitcnt(kWaitAll); return; }
+            if (uses_region(P)) {
+                // this phase's LDS reads are done: send the data of the region phase two ahead
+                // into its half (the next region phase's data is in the other half)
+                int ns = 0, np = 0;
+                if (next_region_phase(a, prog, step, p, ns, np) && next_region_phase(a, prog, ns, np, ns, np))
+                    prefetch(e, prog[np], ns, region(rh));
+                if (a.sub && P.kind == PH_GEMV && e.wave == 0 && e.lane == 0 && inst < a.trace_cap)
+                    a.sub[8 * ((size_t)inst * e.nwg + e.wg) + 4] = __builtin_amdgcn_s_memrealtime();
+                half ^= 1;
+            }
             trace_done(e, inst);
         }
         if (head && a.argmax) {
@@ -1209,6 +1217,31 @@ int decode_gemv_variant(int kind, int k) {
     if (k <= 0 || k % 512 != 0) return -1;
     if (kind == 1) return k <= 6144 ? 1 : -1;  // a q4 row of 6144 is 3456 bytes of LDS
     return k <= 4096 ? 0 : -1;                 // an f16 row of 4096 fills an 8 KiB half
+}
+
+void finalize_phase(Phase& P, int grid) {
+    const int nw = grid * kNW;
+    if (P.kind == PH_GEMV) {
+        P.fast_head = P.epi == EP_HEAD && (P.mkind == 0 || P.group == 64) && (P.k == 512 || P.k == 1024 || P.k == 2048);
+        P.rper = P.rows / nw;
+        P.rrem = P.rows % nw;
+        P.rb = P.mkind ? P.k / 2 : P.k * 2;
+        P.szb = P.mkind ? (P.k / P.group) * 4 : 0;
+        P.stride = P.rb + P.szb;
+        P.nm = P.epi == EP_SWIGLU ? 2 : 1;
+        P.convb = P.epi == EP_CONV ? 32 : 0;
+        P.cap = kHalf / (P.stride * P.nm + P.convb);
+        P.dper = P.nm * ((P.rb + 1023) / 1024 + (P.szb + 1023) / 1024);
+        int gs = 0;
+        while (P.mkind && (1 << gs) < P.group) gs++;
+        P.gshift = gs;
+        P.n4 = P.k / 2048;
+        P.n2 = (P.k % 2048) / 1024;
+        P.n1 = (P.k % 1024) / 512;
+        P.nsteps = P.mkind ? P.n4 + P.n2 + P.n1 : P.k / 512;
+    }
+    if ((P.kind == PH_ATTN || P.kind == PH_COMB) && P.kv_heads > 0) P.splits = std::min(grid / P.kv_heads, kMaxSplits);
+    P.region = (P.kind == PH_GEMV && !P.fast_head) || P.kind == PH_GDN || P.kind == PH_ATTN;
 }
 
 hipError_t launch_decode(const DecodeArgs& a, int grid, hipStream_t st) {

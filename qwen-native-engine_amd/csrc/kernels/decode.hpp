@@ -53,7 +53,20 @@ struct Phase {
     uint64_t* out = nullptr;        // output exchange buffer
     uint32_t in_stride = 0, in2_stride = 0, out_stride = 0;  // u64 entries
     uint32_t in_cap = 0, in2_cap = 0;  // entries readable from in / in2 (bounds of the polling loads)
+    // Derived by finalize_phase from the fields above and the launch grid, so the kernel reads
+    // constants instead of dividing:
+    int region = 0;     // the phase reads data prefetched into an LDS half (LDS GEMV, GDN, attention)
+    int fast_head = 0;  // LM head streamed through registers instead of an LDS half
+    int rper = 0, rrem = 0;  // GEMV outputs per wave: rows / waves and rows % waves
+    int rb = 0, szb = 0, stride = 0, nm = 1;  // GEMV row bytes, scale/zero bytes, their sum, rows per output
+    int cap = 0, dper = 0, convb = 0;  // outputs per LDS half, DMA instructions per output, conv bytes per output
+    int gshift = 6;     // log2(group)
+    int n4 = 0, n2 = 0, n1 = 0, nsteps = 0;  // x steps: 2048/1024/512-column slabs (q4) or 512 (f16)
+    int splits = 0;     // attention: context splits per kv head
 };
+
+// Fills the derived fields of P for a launch of `grid` workgroups (kDecodeThreads / 64 waves each).
+void finalize_phase(Phase& P, int grid);
 
 struct DecodeArgs {
     const Phase* prog = nullptr;
@@ -92,8 +105,8 @@ struct DecodeArgs {
     int trace_cap = 0;
     // Optional finer timeline of GEMV phases (wave 0 of every workgroup, kept in registers and
     // stored when the phase ends): for phase instance i and workgroup w, sub[8 (i * grid + w) + k]
-    // for k = 0 entry, 1 own rows landed, 2 next phase's DMA issued, 3 x slice loaded, 4 first
-    // group's rows done, 5 end.
+    // for k = 0 entry, 1 x slice loaded, 2 first group's rows done, 3 all rows published, 4 the
+    // DMA of the region phase two ahead issued.
     unsigned long long* sub = nullptr;
 };
 

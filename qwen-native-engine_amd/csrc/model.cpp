@@ -508,6 +508,7 @@ void Model::setup_engine() {
             P.in2_stride = P.in2_cap = bufs[out_buf[s2]].n;
         }
     }
+    for (Phase& P : prog) finalize_phase(P, grid);
     nph_ = (int)prog.size();
     Phase* d_prog = (Phase*)dalloc(prog.size() * sizeof(Phase));
     QNE_HIP(hipMemcpy(d_prog, prog.data(), prog.size() * sizeof(Phase), hipMemcpyHostToDevice));
@@ -842,16 +843,17 @@ std::string Model::profile_token_json() {
             exch.push_back(ms(prev, in));
         }
         {
-            std::vector<double> parts[5];
+            // GEMV sub-steps of wave 0 per workgroup: entry, x loaded, first group, rows done, prefetch issued
+            std::vector<double> parts[4];
             for (int w = 0; w < grid; w++) {
                 const unsigned long long* q = sub.data() + 8 * ((size_t)b * grid + w);
-                if (q[0] == 0 || q[5] == 0) continue;
-                for (int k2 = 0; k2 < 5; k2++) parts[k2].push_back(ms(q[k2], q[k2 + 1]));
+                if (q[0] == 0 || q[4] == 0) continue;
+                for (int k2 = 0; k2 < 4; k2++) parts[k2].push_back(ms(q[k2], q[k2 + 1]));
             }
             if (!parts[0].empty()) {
                 auto& v = sub_l[label];
-                v.resize(5, 0.0);
-                for (int k2 = 0; k2 < 5; k2++) v[k2] += med(parts[k2]);
+                v.resize(4, 0.0);
+                for (int k2 = 0; k2 < 4; k2++) v[k2] += med(parts[k2]);
             }
         }
         const double span = ms(prev, dmax), cm = med(comp), em = med(exch);
@@ -881,12 +883,14 @@ std::string Model::profile_token_json() {
     std::string subs = "{";
     for (auto& kv : sub_l) {
         char buf[160];
-        std::snprintf(buf, sizeof buf, "%s\"%s\":[%.5f,%.5f,%.5f,%.5f,%.5f]", subs.size() > 1 ? "," : "",
-                      kv.first.c_str(), kv.second[0], kv.second[1], kv.second[2], kv.second[3], kv.second[4]);
+        std::snprintf(buf, sizeof buf, "%s\"%s\":[%.5f,%.5f,%.5f,%.5f]", subs.size() > 1 ? "," : "",
+                      kv.first.c_str(), kv.second[0], kv.second[1], kv.second[2], kv.second[3]);
         subs += buf;
     }
     subs += "}";
-    return std::string(head) + "\"gemv_steps_median_ms\":" + subs + ",\"labels\":" + obj(span_l) + ",\"compute_median_ms\":" + obj(comp_l) +
+    return std::string(head) +
+           "\"gemv_step_names\":[\"x load\",\"first group\",\"other groups\",\"prefetch issue\"]," +
+           "\"gemv_steps_median_ms\":" + subs + ",\"labels\":" + obj(span_l) + ",\"compute_median_ms\":" + obj(comp_l) +
            ",\"handover_median_ms\":" + obj(exch_l) +
            ",\"phase_columns\":[\"label\",\"span\",\"compute_median\",\"compute_max\",\"handover_median\",\"handover_max\"]" +
            ",\"phases\":" + phases + "}";
