@@ -383,6 +383,14 @@ __device__ __forceinline__ uint32_t tag_of(const DecodeArgs& a, int step, int p)
     return a.tag_base + (uint32_t)step * (uint32_t)a.nph + (uint32_t)p;
 }
 
+// Profiling only: timestamp k of the phase instance (step, p), taken by thread 0.
+__device__ __forceinline__ void mark(const Env& e, int step, int p, int k) {
+    const DecodeArgs& a = *e.a;
+    const int inst = step * a.nph + p;
+    if (a.sub && threadIdx.x == 0 && inst < a.trace_cap)
+        a.sub[8 * ((size_t)inst * e.nwg + e.wg) + k] = __builtin_amdgcn_s_memrealtime();
+}
+
 // Whether the LM head has a register-streaming path (else it goes through the LDS region).
 __device__ __forceinline__ bool head_fast(CPhase& P) { return P.fast_head != 0; }
 // Phases whose data is prefetched into a wave's LDS half.
@@ -786,6 +794,7 @@ __device__ __forceinline__ void attn_phase(const Env& e, CPhase& P, int step, in
     const DecodeArgs& a = *e.a;
     const int nq = P.heads, nkv = P.kv_heads, G = nq / nkv, S = P.splits, lane = e.lane;
     if (e.wg >= nkv * S) return;
+    mark(e, step, p, 0);
     const int g = e.wg / S, sp = e.wg % S;
     const uint32_t pos = a.pos0 + (uint32_t)step, len = pos + 1;
     const int p0 = split_at(sp, len, S), p1 = split_at(sp + 1, len, S);
@@ -806,6 +815,7 @@ __device__ __forceinline__ void attn_phase(const Env& e, CPhase& P, int step, in
                c);
     bar();
     if (*e.bail) return;
+    mark(e, step, p, 1);
     float* qs = xs + 1536;  // [G][256], normed, rotated, pre-scaled by 1/sqrt(256)
     float* kc = xs + 2560;  // current key and value, f16-rounded
     float* vc = xs + 2816;
@@ -848,6 +858,7 @@ __device__ __forceinline__ void attn_phase(const Env& e, CPhase& P, int step, in
         }
     }
     bar();
+    mark(e, step, p, 2);
     // wave: positions p0 + 2*(wave + 8u) + half; 32 lanes per position, 8 dims per lane
     const int half = lane / 32, li = lane % 32;
     float qr[4][8], acc[4][8], m[4], l[4];
@@ -908,6 +919,7 @@ __device__ __forceinline__ void attn_phase(const Env& e, CPhase& P, int step, in
             }
         }
     }
+    mark(e, step, p, 3);
     // merge the two position halves of the wave, then write the wave's partial into its region
     float* wp = (float*)cur;  // [G][258]: m, l, acc[256]
 #pragma unroll
@@ -950,6 +962,7 @@ __device__ __forceinline__ void attn_phase(const Env& e, CPhase& P, int step, in
         }
     }
     bar();  // the regions are free again
+    mark(e, step, p, 4);
 }
 
 // Combine of the attention partials: workgroup = (q head h, 64 dims c); times sigmoid(gate).
@@ -957,6 +970,7 @@ __device__ __forceinline__ void comb_phase(const Env& e, CPhase& P, int step, in
     const DecodeArgs& a = *e.a;
     const int nq = P.heads, nkv = P.kv_heads, G = nq / nkv, S = P.splits;
     if (e.wg >= nq * 4) return;
+    mark(e, step, p, 0);
     const int h = e.wg / 4, cq = e.wg % 4, g = h / G, gi = h % G;
     const uint32_t tin = tag_of(a, step, p - P.in_rel), tin2 = tag_of(a, step, p - P.in2_rel), tag = tag_of(a, step, p);
     const uint64_t* in = P.in + (size_t)(step & 1) * P.in_stride;
@@ -977,6 +991,7 @@ __device__ __forceinline__ void comb_phase(const Env& e, CPhase& P, int step, in
                    xs[d + 1] = v1;
                },
                c);
+    mark(e, step, p, 1);
     const int ga = nq * kHeadDim + h * kHeadDim + 64 * cq;
     poll_pairs(in2, P.in2_cap, 32, tin2, [&](int q) { return ga + 2 * q; },
                [&](int q, float v0, float v1) {
@@ -986,6 +1001,7 @@ __device__ __forceinline__ void comb_phase(const Env& e, CPhase& P, int step, in
                c);
     bar();
     if (*e.bail) return;
+    mark(e, step, p, 2);
     if (threadIdx.x < 64) {
         const int d = threadIdx.x;
         float mn = -INFINITY;
@@ -1002,6 +1018,7 @@ __device__ __forceinline__ void comb_phase(const Env& e, CPhase& P, int step, in
         put(out, (uint32_t)(h * kHeadDim + 64 * cq + d), ac / ls / (1.0f + expf(-gate)), tag);
     }
     bar();
+    mark(e, step, p, 3);
 }
 
 __device__ __forceinline__ float embed_val(const DecodeArgs& a, uint32_t tok, int c) {
@@ -1119,10 +1136,13 @@ __device__ __forceinline__ void decode_program(const DecodeArgs& a) {
                     break;
                 }
                 case PH_GDN:
+                    mark(e, step, p, 0);
                     if (e.wg < P.heads * 16) gdn_input(e, P, step, p, e.wg, c);
+                    mark(e, step, p, 1);
                     if (bail) { __builtin_amdgcn_s_waitcnt(kWaitAll); return; }
                     trace_in(e, inst);
                     gdn_body(e, P, step, p, c, region(half), xs, red);
+                    mark(e, step, p, 2);
                     break;
                 case PH_ATTN:
                     trace_in(e, inst);
@@ -1140,8 +1160,7 @@ __device__ __forceinline__ void decode_program(const DecodeArgs& a) {
                 int ns = 0, np = 0;
                 if (next_region_phase(a, prog, step, p, ns, np) && next_region_phase(a, prog, ns, np, ns, np))
                     prefetch(e, prog[np], ns, region(rh));
-                if (a.sub && P.kind == PH_GEMV && e.wave == 0 && e.lane == 0 && inst < a.trace_cap)
-                    a.sub[8 * ((size_t)inst * e.nwg + e.wg) + 4] = __builtin_amdgcn_s_memrealtime();
+                mark(e, step, p, 7);
                 half ^= 1;
             }
             trace_done(e, inst);

@@ -843,17 +843,23 @@ std::string Model::profile_token_json() {
             exch.push_back(ms(prev, in));
         }
         {
-            // GEMV sub-steps of wave 0 per workgroup: entry, x loaded, first group, rows done, prefetch issued
-            std::vector<double> parts[4];
+            // sub-steps: intervals between the consecutive stamped slots of each workgroup
+            std::vector<std::vector<double>> parts;
             for (int w = 0; w < grid; w++) {
                 const unsigned long long* q = sub.data() + 8 * ((size_t)b * grid + w);
-                if (q[0] == 0 || q[4] == 0) continue;
-                for (int k2 = 0; k2 < 4; k2++) parts[k2].push_back(ms(q[k2], q[k2 + 1]));
+                if (q[0] == 0) continue;
+                int last = 0, n = 0;
+                for (int k2 = 1; k2 < 8; k2++) {
+                    if (q[k2] == 0) continue;
+                    if ((int)parts.size() <= n) parts.resize(n + 1);
+                    parts[n++].push_back(ms(q[last], q[k2]));
+                    last = k2;
+                }
             }
-            if (!parts[0].empty()) {
+            if (!parts.empty()) {
                 auto& v = sub_l[label];
-                v.resize(4, 0.0);
-                for (int k2 = 0; k2 < 4; k2++) v[k2] += med(parts[k2]);
+                if (v.size() < parts.size()) v.resize(parts.size(), 0.0);
+                for (size_t k2 = 0; k2 < parts.size(); k2++) v[k2] += med(parts[k2]);
             }
         }
         const double span = ms(prev, dmax), cm = med(comp), em = med(exch);
@@ -882,15 +888,21 @@ std::string Model::profile_token_json() {
                   ms(prev, tr[1]), tick_ms);
     std::string subs = "{";
     for (auto& kv : sub_l) {
-        char buf[160];
-        std::snprintf(buf, sizeof buf, "%s\"%s\":[%.5f,%.5f,%.5f,%.5f]", subs.size() > 1 ? "," : "",
-                      kv.first.c_str(), kv.second[0], kv.second[1], kv.second[2], kv.second[3]);
-        subs += buf;
+        subs += (subs.size() > 1 ? ",\"" : "\"") + kv.first + "\":[";
+        for (size_t k2 = 0; k2 < kv.second.size(); k2++) {
+            char buf[32];
+            std::snprintf(buf, sizeof buf, "%s%.5f", k2 ? "," : "", kv.second[k2]);
+            subs += buf;
+        }
+        subs += "]";
     }
     subs += "}";
     return std::string(head) +
-           "\"gemv_step_names\":[\"x load\",\"first group\",\"other groups\",\"prefetch issue\"]," +
-           "\"gemv_steps_median_ms\":" + subs + ",\"labels\":" + obj(span_l) + ",\"compute_median_ms\":" + obj(comp_l) +
+           "\"sub_step_names\":{\"gemv\":[\"x load\",\"first group\",\"other groups\",\"prefetch issue\"],"
+           "\"gdn\":[\"input\",\"state update\",\"prefetch issue\"],"
+           "\"attention\":[\"input\",\"q/k prep\",\"context loop\",\"merge + publish\",\"prefetch issue\"],"
+           "\"combine\":[\"partials\",\"gate\",\"combine + publish\"]}," +
+           "\"sub_steps_median_ms\":" + subs + ",\"labels\":" + obj(span_l) + ",\"compute_median_ms\":" + obj(comp_l) +
            ",\"handover_median_ms\":" + obj(exch_l) +
            ",\"phase_columns\":[\"label\",\"span\",\"compute_median\",\"compute_max\",\"handover_median\",\"handover_max\"]" +
            ",\"phases\":" + phases + "}";
