@@ -49,6 +49,16 @@ __device__ __forceinline__ float wave_sum_dpp(float v) {
     return v;
 }
 
+// Sum over each half (32 lanes) of a wave; every lane receives its half's total.
+__device__ __forceinline__ float half_sum_dpp(float v, int lane) {
+    v += QNE_DPP(v, kDppXor1);
+    v += QNE_DPP(v, kDppXor2);
+    v += QNE_DPP(v, kDppHalfMirror);
+    v += QNE_DPP(v, kDppMirror);
+    v += lane_xor16(v, lane);
+    return v;
+}
+
 // Sum over the 64 lanes of a wave; every lane receives the total.
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll

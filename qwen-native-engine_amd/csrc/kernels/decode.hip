@@ -52,18 +52,19 @@ constexpr int kNT = 2;                 // cache policy: non-temporal (streamed o
 constexpr int kBlk = 16;               // KV block size (positions)
 constexpr int kDK = 128;               // GDN dk = dv
 constexpr int kAttnU = kHalf / 2048;   // prefetched K/V wave-loads (2 positions each) per wave
-constexpr int kWaitVm0 = 0x0F70;
-constexpr int kWaitAll = 0;
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 typedef __amdgpu_buffer_rsrc_t rsrc_t;
 
-// s_waitcnt until at most N vector-memory operations of this wave are outstanding (gfx9
-// encoding: vmcnt[3:0] at bits 3:0, vmcnt[5:4] at 15:14; expcnt and lgkmcnt left at maximum).
+// s_waitcnt until at most N vector-memory operations of this wave are outstanding. Written as
+// asm with a memory clobber: the compiler then keeps every load of LDS data the wait protects
+// (rows landed by LDS DMA) after it.
 template <int N>
 __device__ __forceinline__ void wait_vm_n() {
-    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x70 | 0xF00);
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
+// Every counter to zero (all of this wave's memory operations done), with the same ordering.
+__device__ __forceinline__ void wait_all() { asm volatile("s_waitcnt vmcnt(0) expcnt(0) lgkmcnt(0)" ::: "memory"); }
 // Rounds n down to a supported count, so the wait is never shorter than asked for.
 __device__ __forceinline__ void wait_vm(int n) {
     if (n >= 48) wait_vm_n<48>();
@@ -398,18 +399,19 @@ __device__ __forceinline__ bool uses_region(CPhase& P) { return P.region != 0; }
 __device__ __forceinline__ bool head_at(const DecodeArgs& a, int step) {
     return a.head == 1 || (a.head == 2 && step == a.n_steps - 1);
 }
-// The next phase after (step, p) that reads the regions, or false past the window.
-__device__ __forceinline__ bool next_region_phase(const DecodeArgs& a, CPhase* prog, int step, int p, int& ns, int& np) {
-    ns = step;
-    np = p;
-    for (int guard = 0; guard <= a.nph; guard++) {
-        if (++np >= a.nph) {
-            np = 0;
-            if (++ns >= a.n_steps) return false;
-        }
-        CPhase& Q = prog[np];
-        if (Q.is_head && !head_at(a, ns)) continue;
-        if (uses_region(Q)) return true;
+// The k-th (1 or 2) region phase after phase p of `step`, from the links set on the host: the
+// step's own next region phases, then the LM head when it runs on this step, then the next step's
+// first two. False past the window.
+__device__ __forceinline__ bool region_after(const DecodeArgs& a, CPhase& P, int step, int p, int k, int& ns, int& np) {
+    int c = 0;
+    for (int i = 0; i < 2; i++) {
+        if (P.nr[i] < 0) break;
+        if (++c == k) { ns = step; np = P.nr[i]; return true; }
+    }
+    if (a.head_reg >= 0 && p < a.head_reg && head_at(a, step) && ++c == k) { ns = step; np = a.head_reg; return true; }
+    if (step + 1 < a.n_steps) {
+        if (++c == k) { ns = step + 1; np = a.reg0; return true; }
+        if (++c == k) { ns = step + 1; np = a.reg1; return true; }
     }
     return false;
 }
@@ -583,7 +585,7 @@ __device__ __forceinline__ void gemv_body(const Env& e, CPhase& P, int step, int
     const int lane = e.lane;
     unsigned long long tt[6];
     tt[0] = __builtin_amdgcn_s_memrealtime();
-    __builtin_amdgcn_s_waitcnt(kWaitAll);  // this phase's rows (issued two region phases ago) are in
+    wait_all();  // this phase's rows (issued two region phases ago) are in
     const GemvGeo g = geo(P);
     const Rows R = part_p(P, e.gwm);
     tt[1] = tt[2] = tt[3] = tt[0];
@@ -604,22 +606,26 @@ __device__ __forceinline__ void gemv_body(const Env& e, CPhase& P, int step, int
         asm volatile("" ::"v"(X.x[0]), "v"(X.x[31]));
         tt[1] = __builtin_amdgcn_s_memrealtime();
         tt[2] = tt[1];
+        const int ns = g.nm - 1;  // log2(rows per output): 0 or 1 (SwiGLU)
         for (int o0 = 0; o0 < R.n; o0 += go) {
-            const int ng = min(go, R.n - o0), nr = ng * g.nm;
+            const int ng = min(go, R.n - o0), nr = ng << ns;
             if (o0 + ng > pre) wait_vm((issued - o0 - ng) * g.per);  // refilled group
+            // LDS offsets of the group's rows (row r = row m of output i)
+            int roff[8];
+#pragma unroll
+            for (int r = 0; r < 8; r++) {
+                int slot = o0 + (r >> ns);
+                if (stream) slot = slot < g.cap ? slot : slot % g.cap;
+                roff[r] = ((slot << ns) + (r & ns)) * g.stride;
+            }
             float acc[8];
 #pragma unroll
             for (int r = 0; r < 8; r++) acc[r] = 0.0f;
             for (int j = 0; j < t.nsteps; j++) {
                 if (t.nsteps > 1) load_step(xs, t, j, gdn, H, X, lane);
 #pragma unroll
-                for (int r = 0; r < 8; r++) {
-                    if (r < nr) {
-                        const int i = r / g.nm, m = r % g.nm;
-                        const int slot = stream ? (o0 + i) % g.cap : o0 + i;
-                        acc[r] += step_dot(t, j, P.gshift, g.rb, cur + slot * g.nm * g.stride + m * g.stride, X, lane);
-                    }
-                }
+                for (int r = 0; r < 8; r++)
+                    if (r < nr) acc[r] += step_dot(t, j, P.gshift, g.rb, cur + roff[r], X, lane);
             }
             if (o0 == 0) {
                 asm volatile("" ::"v"(acc[0]), "v"(acc[1]), "v"(acc[7]));
@@ -630,8 +636,8 @@ __device__ __forceinline__ void gemv_body(const Env& e, CPhase& P, int step, int
             const float tot = reduce8(acc, lane) * inv;   // lanes 8r..8r+7: row r of the group
             const float up = __shfl_down(tot, 8, kWave);  // SwiGLU: the up row of the output
             const int r = lane >> 3;
-            const int i = r / g.nm;
-            const bool lead = (lane & 7) == 0 && r % g.nm == 0 && i < ng;
+            const int i = r >> ns;
+            const bool lead = (lane & 7) == 0 && (r & ns) == 0 && i < ng;
             const int o = R.r0 + o0 + i;
             float y = tot;
             if (P.epi == EP_RESID) {
@@ -711,7 +717,7 @@ __device__ __forceinline__ void gdn_input(const Env& e, CPhase& P, int step, int
 __device__ __forceinline__ void gdn_body(const Env& e, CPhase& P, int step, int p, const Ctl& c, const uint8_t* cur,
                                          const float* xs, float* red) {
     const DecodeArgs& a = *e.a;
-    __builtin_amdgcn_s_waitcnt(kWaitAll);  // the state column (issued two region phases ago) is in
+    wait_all();  // the state column (issued two region phases ago) is in
     const int H = P.heads, lane = e.lane;
     const uint32_t tag = tag_of(a, step, p);
     uint64_t* out = P.out + (size_t)(step & 1) * P.out_stride;
@@ -872,7 +878,7 @@ __device__ __forceinline__ void attn_phase(const Env& e, CPhase& P, int step, in
             acc[gi][d] = 0.0f;
         }
     }
-    __builtin_amdgcn_s_waitcnt(kWaitVm0);  // prefetched K/V rows
+    wait_vm_n<0>();  // prefetched K/V rows
     for (int u = 0;; u++) {
         const int pp = p0 + 2 * (e.wave + kNW * u);
         if (pp >= p1) break;  // wave-uniform
@@ -906,8 +912,7 @@ __device__ __forceinline__ void attn_phase(const Env& e, CPhase& P, int step, in
                 float s = 0.0f;
 #pragma unroll
                 for (int d = 0; d < 8; d++) s = fmaf(qr[gi][d], kf[d], s);
-#pragma unroll
-                for (int mk = 16; mk >= 1; mk >>= 1) s += __shfl_xor(s, mk, kWave);  // 32-lane sum
+                s = half_sum_dpp(s, lane);  // the position's 32 lanes
                 if (valid) {
                     const float mn = fmaxf(m[gi], s);
                     const float corr = expf(m[gi] - mn), pw = expf(s - mn);
@@ -940,22 +945,29 @@ __device__ __forceinline__ void attn_phase(const Env& e, CPhase& P, int step, in
         }
     }
     bar();
-    // merge the 8 waves; threads 0..255 = dims
-    if (threadIdx.x < kHeadDim) {
-        const int t = threadIdx.x;
-        for (int gi = 0; gi < G; gi++) {
-            float mn = -INFINITY;
-            for (int w = 0; w < kNW; w++) mn = fmaxf(mn, ((const float*)(e.regs + w * kWaveLds + rh * kHalf))[gi * 258]);
-            float ls = 0.0f, ac = 0.0f;
+    // merge the 8 waves: thread = (head gi, dims d0, d0 + 1)
+    {
+        const int gi = threadIdx.x >> 7, d0 = 2 * (threadIdx.x & 127);
+        if (gi < G) {
+            float mw[kNW], mn = -INFINITY;
+#pragma unroll
+            for (int w = 0; w < kNW; w++) {
+                mw[w] = ((const float*)(e.regs + w * kWaveLds + rh * kHalf))[gi * 258];
+                mn = fmaxf(mn, mw[w]);
+            }
+            float ls = 0.0f, a0 = 0.0f, a1 = 0.0f;
+#pragma unroll
             for (int w = 0; w < kNW; w++) {
                 const float* pw = (const float*)(e.regs + w * kWaveLds + rh * kHalf) + gi * 258;
-                const float cw = pw[0] == -INFINITY ? 0.0f : expf(pw[0] - mn);
+                const float cw = mw[w] == -INFINITY ? 0.0f : expf(mw[w] - mn);
                 ls += pw[1] * cw;
-                ac += pw[2 + t] * cw;
+                a0 += pw[2 + d0] * cw;
+                a1 += pw[3 + d0] * cw;
             }
             const uint32_t base = (uint32_t)(((g * S + sp) * G + gi) * 258);
-            put(out, base + 2 + t, ac, tag);
-            if (t == 0) {
+            put(out, base + 2 + d0, a0, tag);
+            put(out, base + 3 + d0, a1, tag);
+            if (d0 == 0) {
                 put(out, base, mn, tag);
                 put(out, base + 1, ls, tag);
             }
@@ -966,6 +978,7 @@ __device__ __forceinline__ void attn_phase(const Env& e, CPhase& P, int step, in
 }
 
 // Combine of the attention partials: workgroup = (q head h, 64 dims c); times sigmoid(gate).
+static_assert(66 * kMaxSplits + 64 + 64 * kNW + kNW <= kXs, "the combine's staging must fit in xs");
 __device__ __forceinline__ void comb_phase(const Env& e, CPhase& P, int step, int p, const Ctl& c) {
     const DecodeArgs& a = *e.a;
     const int nq = P.heads, nkv = P.kv_heads, G = nq / nkv, S = P.splits;
@@ -1002,20 +1015,33 @@ __device__ __forceinline__ void comb_phase(const Env& e, CPhase& P, int step, in
     bar();
     if (*e.bail) return;
     mark(e, step, p, 2);
-    if (threadIdx.x < 64) {
-        const int d = threadIdx.x;
+    {
+        // wave sg takes splits sg, sg + 8, ...; lane = dim. Their sums meet in xs after the gate.
+        const int d = threadIdx.x & 63, sg = threadIdx.x >> 6;
         float mn = -INFINITY;
         for (int s = 0; s < S; s++) mn = fmaxf(mn, xs[2 * s]);
         float ls = 0.0f, ac = 0.0f;
-        for (int s = 0; s < S; s++) {
+        for (int s = sg; s < S; s += kNW) {
             const float ms = xs[2 * s];
             if (ms == -INFINITY) continue;
             const float cw = expf(ms - mn);
             ls += xs[2 * s + 1] * cw;
             ac += xs[2 * S + 64 * s + d] * cw;
         }
-        const float gate = xs[2 * S + 64 * S + d];
-        put(out, (uint32_t)(h * kHeadDim + 64 * cq + d), ac / ls / (1.0f + expf(-gate)), tag);
+        float* rd = xs + 2 * S + 64 * S + 64;  // [kNW][64] sums of acc, then [kNW] sums of l
+        rd[64 * sg + d] = ac;
+        if (d == 0) rd[64 * kNW + sg] = ls;
+        bar();
+        if (threadIdx.x < 64) {
+            float at = 0.0f, lt = 0.0f;
+#pragma unroll
+            for (int w = 0; w < kNW; w++) {
+                at += rd[64 * w + d];
+                lt += rd[64 * kNW + w];
+            }
+            const float gate = xs[2 * S + 64 * S + d];
+            put(out, (uint32_t)(h * kHeadDim + 64 * cq + d), at / lt / (1.0f + expf(-gate)), tag);
+        }
     }
     bar();
     mark(e, step, p, 3);
@@ -1078,15 +1104,9 @@ __device__ __forceinline__ void decode_program(const DecodeArgs& a) {
 
     uint32_t token = a.feed ? a.tok[0] : a.ids[0];
     int half = 0;  // half of the next region phase (region phases alternate between the halves)
-    {
-        // the first two region phases
-        int ps = 0, pp = 0;
-        bool more = uses_region(prog[0]) || next_region_phase(a, prog, 0, 0, ps, pp);
-        for (int k = 0; k < 2 && more; k++) {
-            prefetch(e, prog[pp], ps, region(k));
-            more = next_region_phase(a, prog, ps, pp, ps, pp);
-        }
-    }
+    // the first two region phases of the window
+    prefetch(e, prog[a.reg0], 0, region(0));
+    prefetch(e, prog[a.reg1], 0, region(1));
     for (int step = 0; step < a.n_steps; step++) {
         const uint32_t pos = a.pos0 + (uint32_t)step;
         const bool head = head_at(a, step);
@@ -1129,7 +1149,7 @@ __device__ __forceinline__ void decode_program(const DecodeArgs& a) {
             switch (P.kind) {
                 case PH_GEMV: {
                     const float inv = gemv_input(e, P, step, p, c);
-                    if (bail) { __builtin_amdgcn_s_waitcnt(kWaitAll); return; }
+                    if (bail) { wait_all(); return; }
                     trace_in(e, inst);
                     if (head_fast(P)) head_phase(e, P, ws, inv);
                     else gemv_body(e, P, step, p, ws, inv, region(half), xs);
@@ -1139,7 +1159,7 @@ __device__ __forceinline__ void decode_program(const DecodeArgs& a) {
                     mark(e, step, p, 0);
                     if (e.wg < P.heads * 16) gdn_input(e, P, step, p, e.wg, c);
                     mark(e, step, p, 1);
-                    if (bail) { __builtin_amdgcn_s_waitcnt(kWaitAll); return; }
+                    if (bail) { wait_all(); return; }
                     trace_in(e, inst);
                     gdn_body(e, P, step, p, c, region(half), xs, red);
                     mark(e, step, p, 2);
@@ -1153,16 +1173,19 @@ __device__ __forceinline__ void decode_program(const DecodeArgs& a) {
                     comb_phase(e, P, step, p, c);
                     break;
             }
-            if (bail) { __builtin_amdgcn_s_waitcnt(kWaitAll); return; }
+            if (bail) { wait_all(); return; }
             if (uses_region(P)) {
                 // this phase's LDS reads are done: send the data of the region phase two ahead
                 // into its half (the next region phase's data is in the other half)
                 int ns = 0, np = 0;
-                if (next_region_phase(a, prog, step, p, ns, np) && next_region_phase(a, prog, ns, np, ns, np))
-                    prefetch(e, prog[np], ns, region(rh));
+                if (region_after(a, P, step, p, 2, ns, np)) prefetch(e, prog[np], ns, region(rh));
                 mark(e, step, p, 7);
                 half ^= 1;
             }
+            // Every wave is done with xs and red before any wave stages the next phase's input
+            // there: a wave can receive that input (published by other workgroups) while a slower
+            // wave of its workgroup still reads this phase's.
+            bar();
             trace_done(e, inst);
         }
         if (head && a.argmax) {
@@ -1203,7 +1226,7 @@ __device__ __forceinline__ void decode_program(const DecodeArgs& a) {
             bar();
             if (e.lane == 0) { red[e.wave] = b; redi[e.wave] = bi; }
             bar();
-            if (bail) { __builtin_amdgcn_s_waitcnt(kWaitAll); return; }
+            if (bail) { wait_all(); return; }
             float bb = red[0];
             uint32_t bbi = redi[0];
             for (int w = 1; w < kNW; w++)
@@ -1223,7 +1246,7 @@ __device__ __forceinline__ void decode_program(const DecodeArgs& a) {
         }
         if (step + 1 < a.n_steps && !a.feed) token = a.ids[step + 1];
     }
-    __builtin_amdgcn_s_waitcnt(kWaitAll);
+    wait_all();
     if (a.trace && e.wg == 0 && threadIdx.x == 0) a.trace[1] = __builtin_amdgcn_s_memrealtime();
 }
 
@@ -1261,6 +1284,23 @@ void finalize_phase(Phase& P, int grid) {
     }
     if ((P.kind == PH_ATTN || P.kind == PH_COMB) && P.kv_heads > 0) P.splits = std::min(grid / P.kv_heads, kMaxSplits);
     P.region = (P.kind == PH_GEMV && !P.fast_head) || P.kind == PH_GDN || P.kind == PH_ATTN;
+}
+
+bool finalize_program(Phase* prog, int nph, DecodeArgs& a) {
+    a.reg0 = a.reg1 = a.head_reg = -1;
+    for (int p = 0; p < nph; p++) {
+        if (!prog[p].region) continue;
+        if (prog[p].is_head) a.head_reg = p;
+        else if (a.reg0 < 0) a.reg0 = p;
+        else if (a.reg1 < 0) a.reg1 = p;
+    }
+    for (int p = 0; p < nph; p++) {
+        int c = 0;
+        prog[p].nr[0] = prog[p].nr[1] = -1;
+        for (int q = p + 1; q < nph && c < 2; q++)
+            if (prog[q].region && !prog[q].is_head) prog[p].nr[c++] = q;
+    }
+    return a.reg1 >= 0 && (a.head_reg < 0 || a.head_reg == nph - 1);
 }
 
 hipError_t launch_decode(const DecodeArgs& a, int grid, hipStream_t st) {

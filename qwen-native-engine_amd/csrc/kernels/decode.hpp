@@ -26,7 +26,7 @@ enum { EP_STORE = 0, EP_CONV = 1, EP_RESID = 2, EP_SWIGLU = 3, EP_HEAD = 4 };
 constexpr int kDecodeThreads = 512;
 constexpr int kMaxPhases = 192;
 constexpr int kHeadDim = 256;  // attention head size the kernel is written for
-constexpr int kMaxSplits = 92;  // attention context splits per kv head (the combine stages 66 floats each)
+constexpr int kMaxSplits = 84;  // attention context splits per kv head (the combine stages 66 floats each, plus its reduction)
 
 // One phase. `variant` selects the compiled GEMV shape (matrix kind and K).
 struct Phase {
@@ -63,10 +63,9 @@ struct Phase {
     int gshift = 6;     // log2(group)
     int n4 = 0, n2 = 0, n1 = 0, nsteps = 0;  // x steps: 2048/1024/512-column slabs (q4) or 512 (f16)
     int splits = 0;     // attention: context splits per kv head
+    int nr[2] = {-1, -1};  // the next two region phases after this one in the same step (LM head excluded)
 };
 
-// Fills the derived fields of P for a launch of `grid` workgroups (kDecodeThreads / 64 waves each).
-void finalize_phase(Phase& P, int grid);
 
 struct DecodeArgs {
     const Phase* prog = nullptr;
@@ -95,6 +94,9 @@ struct DecodeArgs {
     int head = 0;    // 0: no LM head, 1: every step, 2: last step only
     int argmax = 0;  // greedy pick after the LM head
     uint32_t tag_base = 1;  // tag of phase p of step s = tag_base + s * nph + p
+    // region phases (those that read prefetched data): the first two of a step (LM head excluded)
+    // and the LM head when it is one (else -1); set by finalize_program
+    int reg0 = -1, reg1 = -1, head_reg = -1;
     unsigned* err = nullptr;  // [0] set on a polling timeout
     unsigned spin_limit = 1u << 20;
     // Optional device timeline (ticks of the constant-rate wall clock): trace[0] start, trace[1]
@@ -112,6 +114,11 @@ struct DecodeArgs {
     unsigned long long* sub = nullptr;
 };
 
+// Fills the derived fields of P for a launch of `grid` workgroups (kDecodeThreads / 64 waves each).
+void finalize_phase(Phase& P, int grid);
+// Fills the region-phase links of a finalized program (Phase::nr, DecodeArgs::reg0 / reg1 / head_reg).
+// Returns false if a step has fewer than two region phases besides the LM head.
+bool finalize_program(Phase* prog, int nph, DecodeArgs& a);
 // GEMV shapes compiled into the kernel: variant id of (matrix kind, K), or -1.
 int decode_gemv_variant(int kind, int k);
 hipError_t launch_decode(const DecodeArgs& a, int grid, hipStream_t st);

@@ -509,6 +509,8 @@ void Model::setup_engine() {
         }
     }
     for (Phase& P : prog) finalize_phase(P, grid);
+    DecodeArgs links;
+    if (!finalize_program(prog.data(), (int)prog.size(), links)) throw unsupported("too few region phases per step");
     nph_ = (int)prog.size();
     Phase* d_prog = (Phase*)dalloc(prog.size() * sizeof(Phase));
     QNE_HIP(hipMemcpy(d_prog, prog.data(), prog.size() * sizeof(Phase), hipMemcpyHostToDevice));
@@ -519,6 +521,7 @@ void Model::setup_engine() {
     engine_args_ = a;
     a->prog = d_prog;
     a->nph = nph_;
+    a->reg0 = links.reg0; a->reg1 = links.reg1; a->head_reg = links.head_reg;
     a->emb_w = embed_.w; a->emb_sz = embed_.sz; a->emb_kind = embed_.kind; a->emb_group = embed_.group;
     a->hidden = c.hidden; a->vocab = c.vocab; a->eps = c.eps;
     a->rope_dim = c.rope_dim; a->inv_freq = inv_freq_;
