@@ -264,41 +264,86 @@ struct XC {
     float sum;  // q4: sum of the step's values (the zero-point term)
 };
 
-// The lane's values of step j from xs. GDN inputs are scaled per head by the 1/rms computed from
-// the published partial sums of squares at xs[H*128 + h*16 + cb].
-__device__ __forceinline__ void load_step(const float* xs, const Step& t, int j, bool gdn, int H, XC& X, int lane) {
-    auto rn = [&](int c0) {
-        if (!gdn) return 1.0f;
-        const int h = c0 / kDK;
-        float s = 0.0f;
-#pragma unroll
-        for (int b = 0; b < 16; b++) s += xs[H * kDK + h * 16 + b];
-        return 1.0f / sqrtf(s / (float)kDK + 1e-6f);
-    };
-    X.sum = 0.0f;
-    int base, nch, cpl;  // slab base, chunks of 4 per lane, values per lane
+// Inverse of xs_slot for a position d < K of the chunk-major staging.
+__device__ __forceinline__ int xs_value(const Step& t, int d) {
+    int base, sh;
     if (t.kind == 1) {
-        if (j < t.n4) { base = 2048 * j; nch = 8; cpl = 32; }
-        else if (j < t.n4 + t.n2) { base = 2048 * t.n4; nch = 4; cpl = 16; }
-        else { base = 2048 * t.n4 + 1024 * t.n2; nch = 2; cpl = 8; }
+        if (d < 2048 * t.n4) { base = d & ~2047; sh = 5; }
+        else if (d < 2048 * t.n4 + 1024 * t.n2) { base = 2048 * t.n4; sh = 4; }
+        else { base = 2048 * t.n4 + 1024 * t.n2; sh = 3; }
+    } else {
+        base = d & ~511;
+        sh = 3;
+    }
+    const int w = d - base, i = ((w >> 8) << 2) + (w & 3), l = (w >> 2) & 63;
+    return base + (l << sh) + i;
+}
+
+// Slab of step j: base, chunks of 4 values per lane.
+__device__ __forceinline__ void step_slab(const Step& t, int j, int& base, int& nch) {
+    if (t.kind == 1) {
+        if (j < t.n4) { base = 2048 * j; nch = 8; }
+        else if (j < t.n4 + t.n2) { base = 2048 * t.n4; nch = 4; }
+        else { base = 2048 * t.n4 + 1024 * t.n2; nch = 2; }
     } else {
         base = 512 * j;
         nch = 2;
-        cpl = 8;
     }
-    const float r = rn(base + cpl * lane);
+}
+
+// Finishes the staged input of an LDS-region GEMV, once per workgroup so the waves do not each
+// redo it per step: the GDN output norm (per head, 1/rms from the published partial sums of
+// squares, kernels/src/shaders.rs:514) is applied in place, then the sum of every lane slice of
+// every step (the q4 zero-point term) goes to xsum[j * 64 + lane]. Ends with a barrier.
+__device__ __forceinline__ void stage_post(float* xs, CPhase& P, const Step& t, float* xsum, float* rnh) {
+    if (P.xnorm == XN_GDN) {
+        const int H = P.heads;
+        if ((int)threadIdx.x < H) {
+            float s = 0.0f;
+#pragma unroll
+            for (int b = 0; b < 16; b++) s += xs[H * kDK + threadIdx.x * 16 + b];
+            rnh[threadIdx.x] = 1.0f / sqrtf(s / (float)kDK + 1e-6f);
+        }
+        bar();
+        for (int d = threadIdx.x; d < t.K; d += kT) xs[d] *= rnh[xs_value(t, d) / kDK];
+        bar();
+    }
+    if (t.kind == 1) {
+        for (int q = threadIdx.x; q < t.nsteps * 64; q += kT) {
+            const int j = q >> 6, l = q & 63;
+            int base, nch;
+            step_slab(t, j, base, nch);
+            float sm = 0.0f;
+            for (int c = 0; c < nch; c++) {
+                const float4 f = *(const float4*)(xs + base + 256 * c + 4 * l);
+                sm += (f.x + f.y) + (f.z + f.w);
+            }
+            xsum[q] = sm;
+        }
+        bar();
+    }
+}
+
+// The lane's values of step j from xs, and (q4) their sum.
+__device__ __forceinline__ void load_step(const float* xs, const float* xsum, const Step& t, int j, XC& X, int lane) {
+    int base, nch;
+    step_slab(t, j, base, nch);
 #pragma unroll
     for (int c = 0; c < 8; c++) {
         if (c < nch) {
             const float4 f = *(const float4*)(xs + base + 256 * c + 4 * lane);
-            X.x[4 * c] = f.x * r; X.x[4 * c + 1] = f.y * r; X.x[4 * c + 2] = f.z * r; X.x[4 * c + 3] = f.w * r;
-            X.sum += X.x[4 * c] + X.x[4 * c + 1] + X.x[4 * c + 2] + X.x[4 * c + 3];
+            X.x[4 * c] = f.x; X.x[4 * c + 1] = f.y; X.x[4 * c + 2] = f.z; X.x[4 * c + 3] = f.w;
         }
     }
+    X.sum = t.kind == 1 ? xsum[j * 64 + lane] : 0.0f;
 }
 
+// Nibble c of w times x[c], c = 0..7. The even and odd nibbles are masked into bytes once, and the
+// empty asm keeps the compiler from folding the mask back into a bit-field extract per nibble: each
+// value then costs one v_cvt_f32_ubyteN and one FMA.
 __device__ __forceinline__ float dot8(uint32_t w, const float* x) {
-    const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
+    uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
+    asm("" : "+v"(lo), "+v"(hi));
     float p = (float)(lo & 0xFFu) * x[0];
     float q = (float)(hi & 0xFFu) * x[1];
     p = fmaf((float)((lo >> 8) & 0xFFu), x[2], p);
@@ -310,33 +355,73 @@ __device__ __forceinline__ float dot8(uint32_t w, const float* x) {
     return p + q;
 }
 
-// The lane's share of step j of the dot product of one row held in LDS (weights at `row`, the
-// row's (scale, zero) pairs at row + rb; gs = log2 of the group size).
-__device__ __forceinline__ float step_dot(const Step& t, int j, int gs, int rb, const uint8_t* row, const XC& X, int lane) {
+// The lane's share, over every step of x, of the dot products of NR rows held in LDS at
+// cur + roff[r] (q4: the row's (scale, zero) pairs follow its nibbles at + rb; gs = log2 of the
+// group size). Each slab type has its own loop with the NR rows unrolled and no branch between
+// them, so a step's LDS reads for all rows issue together. X holds step 0 when nsteps is 1.
+template <int NR>
+__device__ __forceinline__ void rows_dot(const Step& t, int gs, int rb, const uint8_t* cur, const int (&roff)[8],
+                                         const float* xs, const float* xsum, XC& X, int lane, float (&acc)[8]) {
+    const bool reload = t.nsteps > 1;
     if (t.kind == 1) {
-        const uint8_t* szr = row + rb;
-        if (j < t.n4) {
-            const u32x4 w = *(const u32x4*)(row + 1024 * j + 16 * lane);
-            const uint32_t sz = *(const uint32_t*)(szr + 4 * ((2048 * j + 32 * lane) >> gs));
-            const float dq = dot8(w.x, &X.x[0]) + dot8(w.y, &X.x[8]) + dot8(w.z, &X.x[16]) + dot8(w.w, &X.x[24]);
-            return lo_h(sz) * (dq - hi_h(sz) * X.sum);
+        for (int j = 0; j < t.n4; j++) {
+            if (reload) load_step(xs, xsum, t, j, X, lane);
+            u32x4 w[NR];
+            uint32_t sz[NR];
+#pragma unroll
+            for (int r = 0; r < NR; r++) {
+                w[r] = *(const u32x4*)(cur + roff[r] + 1024 * j + 16 * lane);
+                sz[r] = *(const uint32_t*)(cur + roff[r] + rb + 4 * ((2048 * j + 32 * lane) >> gs));
+            }
+#pragma unroll
+            for (int r = 0; r < NR; r++) {
+                const float dq = dot8(w[r].x, &X.x[0]) + dot8(w[r].y, &X.x[8]) + dot8(w[r].z, &X.x[16]) + dot8(w[r].w, &X.x[24]);
+                acc[r] += lo_h(sz[r]) * (dq - hi_h(sz[r]) * X.sum);
+            }
         }
-        if (j < t.n4 + t.n2) {
-            const u32x2 w = *(const u32x2*)(row + 1024 * t.n4 + 8 * lane);
-            const uint32_t sz = *(const uint32_t*)(szr + 4 * ((2048 * t.n4 + 16 * lane) >> gs));
-            return lo_h(sz) * (dot8(w.x, &X.x[0]) + dot8(w.y, &X.x[8]) - hi_h(sz) * X.sum);
+        if (t.n2) {
+            const int j = t.n4;
+            if (reload) load_step(xs, xsum, t, j, X, lane);
+            u32x2 w[NR];
+            uint32_t sz[NR];
+#pragma unroll
+            for (int r = 0; r < NR; r++) {
+                w[r] = *(const u32x2*)(cur + roff[r] + 1024 * t.n4 + 8 * lane);
+                sz[r] = *(const uint32_t*)(cur + roff[r] + rb + 4 * ((2048 * t.n4 + 16 * lane) >> gs));
+            }
+#pragma unroll
+            for (int r = 0; r < NR; r++)
+                acc[r] += lo_h(sz[r]) * (dot8(w[r].x, &X.x[0]) + dot8(w[r].y, &X.x[8]) - hi_h(sz[r]) * X.sum);
         }
-        const uint32_t w = *(const uint32_t*)(row + 1024 * t.n4 + 512 * t.n2 + 4 * lane);
-        const uint32_t sz = *(const uint32_t*)(szr + 4 * ((2048 * t.n4 + 1024 * t.n2 + 8 * lane) >> gs));
-        return lo_h(sz) * (dot8(w, &X.x[0]) - hi_h(sz) * X.sum);
+        if (t.n1) {
+            const int j = t.n4 + t.n2;
+            if (reload) load_step(xs, xsum, t, j, X, lane);
+            uint32_t w[NR], sz[NR];
+#pragma unroll
+            for (int r = 0; r < NR; r++) {
+                w[r] = *(const uint32_t*)(cur + roff[r] + 1024 * t.n4 + 512 * t.n2 + 4 * lane);
+                sz[r] = *(const uint32_t*)(cur + roff[r] + rb + 4 * ((2048 * t.n4 + 1024 * t.n2 + 8 * lane) >> gs));
+            }
+#pragma unroll
+            for (int r = 0; r < NR; r++) acc[r] += lo_h(sz[r]) * (dot8(w[r], &X.x[0]) - hi_h(sz[r]) * X.sum);
+        }
+    } else {
+        for (int j = 0; j < t.nsteps; j++) {
+            if (reload) load_step(xs, xsum, t, j, X, lane);
+            u32x4 w[NR];
+#pragma unroll
+            for (int r = 0; r < NR; r++) w[r] = *(const u32x4*)(cur + roff[r] + 1024 * j + 16 * lane);
+#pragma unroll
+            for (int r = 0; r < NR; r++) {
+                const float* x = &X.x[0];
+                float a = lo_h(w[r].x) * x[0], b = hi_h(w[r].x) * x[1];
+                a = fmaf(lo_h(w[r].y), x[2], a); b = fmaf(hi_h(w[r].y), x[3], b);
+                a = fmaf(lo_h(w[r].z), x[4], a); b = fmaf(hi_h(w[r].z), x[5], b);
+                a = fmaf(lo_h(w[r].w), x[6], a); b = fmaf(hi_h(w[r].w), x[7], b);
+                acc[r] += a + b;
+            }
+        }
     }
-    const u32x4 w = *(const u32x4*)(row + 1024 * j + 16 * lane);
-    const float* x = &X.x[0];
-    float a = lo_h(w.x) * x[0], b = hi_h(w.x) * x[1];
-    a = fmaf(lo_h(w.y), x[2], a); b = fmaf(hi_h(w.y), x[3], b);
-    a = fmaf(lo_h(w.z), x[4], a); b = fmaf(hi_h(w.z), x[5], b);
-    a = fmaf(lo_h(w.w), x[6], a); b = fmaf(hi_h(w.w), x[7], b);
-    return a + b;
 }
 
 // Sums 8 per-lane partials across the wave: after the call, lanes 8r..8r+7 hold the total of
@@ -378,18 +463,16 @@ struct Env {
     uint8_t* regs;  // all waves' regions
     float* red;
     int* bail;
+    unsigned long long* tt;  // profiling: the running phase's sub-step timestamps (registers)
 };
 
 __device__ __forceinline__ uint32_t tag_of(const DecodeArgs& a, int step, int p) {
     return a.tag_base + (uint32_t)step * (uint32_t)a.nph + (uint32_t)p;
 }
 
-// Profiling only: timestamp k of the phase instance (step, p), taken by thread 0.
-__device__ __forceinline__ void mark(const Env& e, int step, int p, int k) {
-    const DecodeArgs& a = *e.a;
-    const int inst = step * a.nph + p;
-    if (a.sub && threadIdx.x == 0 && inst < a.trace_cap)
-        a.sub[8 * ((size_t)inst * e.nwg + e.wg) + k] = __builtin_amdgcn_s_memrealtime();
+// Profiling only: timestamp k (0..7) of the running phase, kept in registers until the phase ends.
+__device__ __forceinline__ void mark(const Env& e, int k) {
+    if (e.a->sub) e.tt[k] = __builtin_amdgcn_s_memrealtime();
 }
 
 // Whether the LM head has a register-streaming path (else it goes through the LDS region).
@@ -430,6 +513,8 @@ __device__ __forceinline__ void prefetch(const Env& e, CPhase& P, int step, uint
         const GemvGeo g = geo(P);
         const Rows R = part_p(P, e.gwm);
         const int cnt = min(R.n, g.cap);
+        asm volatile("" ::"s"(cnt), "s"(g.stride));
+        mark(e, 6);
         dma_rows(P, g, R.r0, cnt, 0, nxt, lane);
         if (P.epi == EP_CONV && cnt > 0) {
             // conv state [ch][4] and weights [ch][4] of the prefetched rows, 16 bytes each
@@ -442,13 +527,18 @@ __device__ __forceinline__ void prefetch(const Env& e, CPhase& P, int step, uint
         }
     } else if (P.kind == PH_GDN) {
         const int it = e.wg;
+        const float* rec = P.rec;
+        asm volatile("" ::"s"(rec));
+        mark(e, 6);
         if (it < P.heads * 16) {
             const int h = it / 16, t = (it % 16) * 8 + e.wave;
             // state column t of head h: S[h][t][0..127] (value-major), 512 bytes
-            dma_bytes((const uint8_t*)(P.rec + ((size_t)h * kDK + t) * kDK), 512, nxt, lane);
+            dma_bytes((const uint8_t*)(rec + ((size_t)h * kDK + t) * kDK), 512, nxt, lane);
         }
     } else if (P.kind == PH_ATTN) {
         const int nkv = P.kv_heads, S = P.splits;
+        asm volatile("" ::"s"(nkv), "s"(S));
+        mark(e, 6);
         if (e.wg < nkv * S) {
             const int g = e.wg / S, sp = e.wg % S;
             const uint32_t pos = a.pos0 + (uint32_t)step, len = pos + 1;
@@ -580,21 +670,17 @@ __device__ __forceinline__ void head_phase(const Env& e, CPhase& P, WaveState& w
 // every step of x, the step's slice is read from LDS once and applied to the whole group, then the
 // group is reduced together. The caller then sends the data of the region phase two ahead into `cur`.
 __device__ __forceinline__ void gemv_body(const Env& e, CPhase& P, int step, int p, WaveState& ws, float inv,
-                                          uint8_t* cur, const float* xs) {
+                                          uint8_t* cur, const float* xs, const float* xsum) {
     const DecodeArgs& a = *e.a;
     const int lane = e.lane;
-    unsigned long long tt[6];
-    tt[0] = __builtin_amdgcn_s_memrealtime();
+    mark(e, 0);
     wait_all();  // this phase's rows (issued two region phases ago) are in
     const GemvGeo g = geo(P);
     const Rows R = part_p(P, e.gwm);
-    tt[1] = tt[2] = tt[3] = tt[0];
     if (R.n > 0) {
         const uint32_t tag = tag_of(a, step, p);
         uint64_t* out = P.out ? P.out + (size_t)(step & 1) * P.out_stride : nullptr;
         const Step t = make_step(P);
-        const bool gdn = P.xnorm == XN_GDN;
-        const int H = gdn ? P.heads : 0;
         const int gmax = 8 / g.nm;  // outputs per group
         const int pre = min(R.n, g.cap);  // outputs prefetched
         const bool stream = R.n > g.cap;
@@ -602,15 +688,14 @@ __device__ __forceinline__ void gemv_body(const Env& e, CPhase& P, int step, int
         const uint8_t* cvs = cur + pre * g.nm * g.stride;  // EP_CONV: conv state / weights of the prefetched rows
         int issued = pre;
         XC X;
-        if (t.nsteps == 1) load_step(xs, t, 0, gdn, H, X, lane);
+        if (t.nsteps == 1) load_step(xs, xsum, t, 0, X, lane);
         asm volatile("" ::"v"(X.x[0]), "v"(X.x[31]));
-        tt[1] = __builtin_amdgcn_s_memrealtime();
-        tt[2] = tt[1];
+        mark(e, 1);
         const int ns = g.nm - 1;  // log2(rows per output): 0 or 1 (SwiGLU)
         for (int o0 = 0; o0 < R.n; o0 += go) {
             const int ng = min(go, R.n - o0), nr = ng << ns;
             if (o0 + ng > pre) wait_vm((issued - o0 - ng) * g.per);  // refilled group
-            // LDS offsets of the group's rows (row r = row m of output i)
+            // LDS offsets of the group's rows (row r = row m of output i); padding rows repeat row 0
             int roff[8];
 #pragma unroll
             for (int r = 0; r < 8; r++) {
@@ -618,18 +703,20 @@ __device__ __forceinline__ void gemv_body(const Env& e, CPhase& P, int step, int
                 if (stream) slot = slot < g.cap ? slot : slot % g.cap;
                 roff[r] = ((slot << ns) + (r & ns)) * g.stride;
             }
+#pragma unroll
+            for (int r = 1; r < 8; r++)
+                if (r >= nr) roff[r] = roff[0];
             float acc[8];
 #pragma unroll
             for (int r = 0; r < 8; r++) acc[r] = 0.0f;
-            for (int j = 0; j < t.nsteps; j++) {
-                if (t.nsteps > 1) load_step(xs, t, j, gdn, H, X, lane);
-#pragma unroll
-                for (int r = 0; r < 8; r++)
-                    if (r < nr) acc[r] += step_dot(t, j, P.gshift, g.rb, cur + roff[r], X, lane);
-            }
+            if (nr == 1) rows_dot<1>(t, P.gshift, g.rb, cur, roff, xs, xsum, X, lane, acc);
+            else if (nr == 2) rows_dot<2>(t, P.gshift, g.rb, cur, roff, xs, xsum, X, lane, acc);
+            else if (nr <= 4) rows_dot<4>(t, P.gshift, g.rb, cur, roff, xs, xsum, X, lane, acc);
+            else if (nr <= 6) rows_dot<6>(t, P.gshift, g.rb, cur, roff, xs, xsum, X, lane, acc);
+            else rows_dot<8>(t, P.gshift, g.rb, cur, roff, xs, xsum, X, lane, acc);
             if (o0 == 0) {
                 asm volatile("" ::"v"(acc[0]), "v"(acc[1]), "v"(acc[7]));
-                tt[2] = __builtin_amdgcn_s_memrealtime();
+                mark(e, 2);
             }
             // refill the group's slots with the outputs cap further on
             for (int i = 0; i < ng && issued < R.n; i++, issued++) dma_rows(P, g, R.r0 + issued, 1, issued % g.cap, cur, lane);
@@ -677,11 +764,7 @@ __device__ __forceinline__ void gemv_body(const Env& e, CPhase& P, int step, int
                 }
             }
         }
-        tt[3] = __builtin_amdgcn_s_memrealtime();
-    }
-    if (a.sub && e.wave == 0 && lane == 0 && step * a.nph + p < a.trace_cap) {
-        unsigned long long* sb = a.sub + 8 * ((size_t)(step * a.nph + p) * e.nwg + e.wg);
-        for (int k = 0; k < 4; k++) sb[k] = tt[k];
+        mark(e, 3);
     }
 }
 
@@ -800,7 +883,7 @@ __device__ __forceinline__ void attn_phase(const Env& e, CPhase& P, int step, in
     const DecodeArgs& a = *e.a;
     const int nq = P.heads, nkv = P.kv_heads, G = nq / nkv, S = P.splits, lane = e.lane;
     if (e.wg >= nkv * S) return;
-    mark(e, step, p, 0);
+    mark(e, 0);
     const int g = e.wg / S, sp = e.wg % S;
     const uint32_t pos = a.pos0 + (uint32_t)step, len = pos + 1;
     const int p0 = split_at(sp, len, S), p1 = split_at(sp + 1, len, S);
@@ -821,7 +904,7 @@ __device__ __forceinline__ void attn_phase(const Env& e, CPhase& P, int step, in
                c);
     bar();
     if (*e.bail) return;
-    mark(e, step, p, 1);
+    mark(e, 1);
     float* qs = xs + 1536;  // [G][256], normed, rotated, pre-scaled by 1/sqrt(256)
     float* kc = xs + 2560;  // current key and value, f16-rounded
     float* vc = xs + 2816;
@@ -864,7 +947,7 @@ __device__ __forceinline__ void attn_phase(const Env& e, CPhase& P, int step, in
         }
     }
     bar();
-    mark(e, step, p, 2);
+    mark(e, 2);
     // wave: positions p0 + 2*(wave + 8u) + half; 32 lanes per position, 8 dims per lane
     const int half = lane / 32, li = lane % 32;
     float qr[4][8], acc[4][8], m[4], l[4];
@@ -924,7 +1007,7 @@ __device__ __forceinline__ void attn_phase(const Env& e, CPhase& P, int step, in
             }
         }
     }
-    mark(e, step, p, 3);
+    mark(e, 3);
     // merge the two position halves of the wave, then write the wave's partial into its region
     float* wp = (float*)cur;  // [G][258]: m, l, acc[256]
 #pragma unroll
@@ -974,7 +1057,7 @@ __device__ __forceinline__ void attn_phase(const Env& e, CPhase& P, int step, in
         }
     }
     bar();  // the regions are free again
-    mark(e, step, p, 4);
+    mark(e, 4);
 }
 
 // Combine of the attention partials: workgroup = (q head h, 64 dims c); times sigmoid(gate).
@@ -983,7 +1066,7 @@ __device__ __forceinline__ void comb_phase(const Env& e, CPhase& P, int step, in
     const DecodeArgs& a = *e.a;
     const int nq = P.heads, nkv = P.kv_heads, G = nq / nkv, S = P.splits;
     if (e.wg >= nq * 4) return;
-    mark(e, step, p, 0);
+    mark(e, 0);
     const int h = e.wg / 4, cq = e.wg % 4, g = h / G, gi = h % G;
     const uint32_t tin = tag_of(a, step, p - P.in_rel), tin2 = tag_of(a, step, p - P.in2_rel), tag = tag_of(a, step, p);
     const uint64_t* in = P.in + (size_t)(step & 1) * P.in_stride;
@@ -1004,7 +1087,7 @@ __device__ __forceinline__ void comb_phase(const Env& e, CPhase& P, int step, in
                    xs[d + 1] = v1;
                },
                c);
-    mark(e, step, p, 1);
+    mark(e, 1);
     const int ga = nq * kHeadDim + h * kHeadDim + 64 * cq;
     poll_pairs(in2, P.in2_cap, 32, tin2, [&](int q) { return ga + 2 * q; },
                [&](int q, float v0, float v1) {
@@ -1014,7 +1097,7 @@ __device__ __forceinline__ void comb_phase(const Env& e, CPhase& P, int step, in
                c);
     bar();
     if (*e.bail) return;
-    mark(e, step, p, 2);
+    mark(e, 2);
     {
         // wave sg takes splits sg, sg + 8, ...; lane = dim. Their sums meet in xs after the gate.
         const int d = threadIdx.x & 63, sg = threadIdx.x >> 6;
@@ -1044,7 +1127,7 @@ __device__ __forceinline__ void comb_phase(const Env& e, CPhase& P, int step, in
         }
     }
     bar();
-    mark(e, step, p, 3);
+    mark(e, 3);
 }
 
 __device__ __forceinline__ float embed_val(const DecodeArgs& a, uint32_t tok, int c) {
@@ -1077,12 +1160,16 @@ __device__ __forceinline__ void decode_program(const DecodeArgs& a) {
     __shared__ float red[2 * kNW];
     __shared__ uint32_t redi[kNW];
     __shared__ float rope[2 * 64];  // cos, sin of the step's RoPE angles
+    __shared__ float xsum[8 * 64];  // sums of the staged input's lane slices, per step
+    __shared__ float rnh[64];       // GDN output norm: 1/rms per head
     __shared__ int bail;
     Env e;
     e.a = &a;
     e.wg = blockIdx.x;
     e.nwg = gridDim.x;
-    e.wave = threadIdx.x / kWave;
+    // the same in every lane of a wave: readfirstlane lets the compiler keep it (and the row
+    // ranges derived from it) in scalar registers, with scalar loop control
+    e.wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     e.lane = threadIdx.x % kWave;
     e.gwm = e.wave * e.nwg + e.wg;
     e.nw = e.nwg * kNW;
@@ -1090,6 +1177,8 @@ __device__ __forceinline__ void decode_program(const DecodeArgs& a) {
     e.regs = regs;
     e.red = red;
     e.bail = &bail;
+    unsigned long long tts[8];
+    e.tt = tts;
     Ctl c{a.err, a.spin_limit, &bail};
     CPhase* prog = (CPhase*)a.prog;
     if (threadIdx.x == 0) bail = 0;
@@ -1146,23 +1235,31 @@ __device__ __forceinline__ void decode_program(const DecodeArgs& a) {
             if (P.is_head && !head) continue;
             const int inst = step * a.nph + p;
             const int rh = half;
+            if (a.sub) {
+#pragma unroll
+                for (int k = 0; k < 8; k++) tts[k] = 0;
+            }
             switch (P.kind) {
                 case PH_GEMV: {
                     const float inv = gemv_input(e, P, step, p, c);
                     if (bail) { wait_all(); return; }
                     trace_in(e, inst);
-                    if (head_fast(P)) head_phase(e, P, ws, inv);
-                    else gemv_body(e, P, step, p, ws, inv, region(half), xs);
+                    if (head_fast(P)) {
+                        head_phase(e, P, ws, inv);
+                    } else {
+                        stage_post(xs, P, make_step(P), xsum, rnh);
+                        gemv_body(e, P, step, p, ws, inv, region(half), xs, xsum);
+                    }
                     break;
                 }
                 case PH_GDN:
-                    mark(e, step, p, 0);
+                    mark(e, 0);
                     if (e.wg < P.heads * 16) gdn_input(e, P, step, p, e.wg, c);
-                    mark(e, step, p, 1);
+                    mark(e, 1);
                     if (bail) { wait_all(); return; }
                     trace_in(e, inst);
                     gdn_body(e, P, step, p, c, region(half), xs, red);
-                    mark(e, step, p, 2);
+                    mark(e, 2);
                     break;
                 case PH_ATTN:
                     trace_in(e, inst);
@@ -1178,9 +1275,15 @@ __device__ __forceinline__ void decode_program(const DecodeArgs& a) {
                 // this phase's LDS reads are done: send the data of the region phase two ahead
                 // into its half (the next region phase's data is in the other half)
                 int ns = 0, np = 0;
-                if (region_after(a, P, step, p, 2, ns, np)) prefetch(e, prog[np], ns, region(rh));
-                mark(e, step, p, 7);
+                const bool more = region_after(a, P, step, p, 2, ns, np);
+                mark(e, 5);
+                if (more) prefetch(e, prog[np], ns, region(rh));
+                mark(e, 7);
                 half ^= 1;
+            }
+            if (a.sub && threadIdx.x == 0 && inst < a.trace_cap) {
+#pragma unroll
+                for (int k = 0; k < 8; k++) a.sub[8 * ((size_t)inst * e.nwg + e.wg) + k] = tts[k];
             }
             // Every wave is done with xs and red before any wave stages the next phase's input
             // there: a wave can receive that input (published by other workgroups) while a slower

@@ -106,11 +106,12 @@ struct DecodeArgs {
     unsigned long long* trace = nullptr;
     int trace_cap = 0;
     // Optional finer timeline (profiling): for phase instance i and workgroup w, sub[8 (i * grid + w) + k]
-    // holds timestamps of the phase's sub-steps, k = 0 at entry and 7 after the prefetch issue of a
-    // region phase. GEMV (wave 0, stored at the end): 1 x slice loaded, 2 first group's rows done,
-    // 3 all rows published. GDN: 1 input staged, 2 state update done. Attention partials: 1 input
-    // staged, 2 q/k normed and rotated, 3 context loop done, 4 partials published. Combine:
-    // 1 partials staged, 2 gate staged, 3 published. Slots that stay 0 were not reached.
+    // holds timestamps of the phase's sub-steps (kept in registers, stored when the phase ends);
+    // 0 = not reached. k = 0 entry. GEMV: 1 x slice loaded, 2 first group's rows done, 3 all rows
+    // published. GDN: 1 input staged, 2 state update done. Attention partials: 1 input staged,
+    // 2 q/k normed and rotated, 3 context loop done, 4 partials published. Combine: 1 partials
+    // staged, 2 gate staged, 3 published. Region phases: 5 successor found, 6 its descriptor read,
+    // 7 its DMA issued.
     unsigned long long* sub = nullptr;
 };
 

@@ -901,9 +901,9 @@ std::string Model::profile_token_json() {
     }
     subs += "}";
     return std::string(head) +
-           "\"sub_step_names\":{\"gemv\":[\"x load\",\"first group\",\"other groups\",\"prefetch issue\"],"
-           "\"gdn\":[\"input\",\"state update\",\"prefetch issue\"],"
-           "\"attention\":[\"input\",\"q/k prep\",\"context loop\",\"merge + publish\",\"prefetch issue\"],"
+           "\"sub_step_names\":{\"gemv\":[\"x load\",\"first group\",\"other groups\",\"successor\",\"descriptor\",\"dma issue\"],"
+           "\"gdn\":[\"input\",\"state update\",\"successor\",\"descriptor\",\"dma issue\"],"
+           "\"attention\":[\"input\",\"q/k prep\",\"context loop\",\"merge + publish\",\"successor\",\"descriptor\",\"dma issue\"],"
            "\"combine\":[\"partials\",\"gate\",\"combine + publish\"]}," +
            "\"sub_steps_median_ms\":" + subs + ",\"labels\":" + obj(span_l) + ",\"compute_median_ms\":" + obj(comp_l) +
            ",\"handover_median_ms\":" + obj(exch_l) +

@@ -59,6 +59,24 @@ def test_decode_window_returns_every_id(pair):
     assert w1 == w8 and len(w8) == 20
 
 
+def test_decode_is_bitwise_repeatable(pair):
+    """Every reduction runs in a fixed order, so two runs from the same state agree bit for bit: a
+    race on shared staging buffers or on the hand-over between phases shows up here."""
+    name, m, om, _, _ = pair
+    ids = prompt(m.vocab, 33, 5)
+    runs = []
+    for _ in range(2):
+        m.reset()
+        m.prefill_batched(ids)
+        first = m.logits()
+        out = m.decode(24, 8, [])
+        tok, pos = m.last_token()
+        runs.append((first, out, m.step(tok, pos)))
+    assert np.array_equal(runs[0][0], runs[1][0])
+    assert runs[0][1] == runs[1][1]
+    assert np.array_equal(runs[0][2], runs[1][2])
+
+
 def test_decode_stops_at_stop_token(pair):
     name, m, om, _, _ = pair
     ids = prompt(m.vocab, 7, 3)
