@@ -177,11 +177,27 @@ __device__ __forceinline__ Rows part_p(CPhase& P, int gw) {
 
 // Weights and recurrent state are streamed once per token, so they are loaded non-temporal: the
 // L2 then keeps the small data every phase re-reads (program, norms, block table, conv weights).
+// One LDS DMA of 16 bytes per active lane (global_load_lds_dwordx4: lane l lands at dst + 16 l),
+// written as asm so that the compiler does not see an LDS write: it then does not make the LDS reads
+// of the running phase wait for the next phase's transfer. Readers of dst wait for it explicitly
+// (wait_all / wait_vm). m0 carries the LDS address; its previous value is restored.
+template <bool NT>
+__device__ __forceinline__ void lds_dma16(const void* src, void* dst) {
+    const uint32_t lds = __builtin_amdgcn_readfirstlane((uint32_t)(size_t)(lds_ptr_t)dst);
+    uint32_t saved;
+    if (NT)
+        asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off nt\n\ts_mov_b32 m0, %0"
+                     : "=&s"(saved) : "v"(src), "s"(lds) : "memory");
+    else
+        asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off\n\ts_mov_b32 m0, %0"
+                     : "=&s"(saved) : "v"(src), "s"(lds) : "memory");
+}
+
+// `bytes` (a multiple of 16) from src to dst in 1 KiB wave transfers.
 __device__ __forceinline__ void dma_bytes(const uint8_t* src, int bytes, uint8_t* dst, int lane) {
     for (int u = 0; u * 1024 < bytes; u++) {
         const int off = u * 1024 + lane * 16;
-        if (off < bytes)
-            __builtin_amdgcn_global_load_lds((const void*)(src + off), (lds_ptr_t)(dst + u * 1024), 16, 0, kNT);
+        if (off < bytes) lds_dma16<true>(src + off, dst + u * 1024);
     }
 }
 
@@ -204,17 +220,25 @@ __device__ __forceinline__ GemvGeo geo(CPhase& P) {
 }
 
 // DMA of outputs [o0, o0 + cnt) (row pairs for SwiGLU) into region slots starting at `slot`.
+// LDS layout of a GEMV phase in a half: the nibble (or f16) rows [nm][cap][rb], then the q4
+// (scale, zero) rows [nm][cap][szb], then (in-projection with the causal conv) the conv states
+// [cap][16 B] and conv weights [cap][16 B]. Row m of the output in slot s:
+__device__ __forceinline__ int lds_w(const GemvGeo& g, int s, int m) { return (m * g.cap + s) * g.rb; }
+__device__ __forceinline__ int lds_sz(const GemvGeo& g, int s, int m) {
+    return g.nm * g.cap * g.rb + (m * g.cap + s) * g.szb;
+}
+__device__ __forceinline__ int lds_conv(const GemvGeo& g) { return g.nm * g.cap * g.stride; }
+
+// DMA of outputs [o0, o0 + cnt) into slots [slot, slot + cnt). Consecutive outputs are consecutive
+// rows of each of the nm matrices, so each block is one contiguous transfer.
 __device__ __forceinline__ void dma_rows(CPhase& P, const GemvGeo& g, int o0, int cnt, int slot, uint8_t* __restrict__ reg,
                                          int lane) {
     const uint8_t* w = (const uint8_t*)P.w;
     const uint8_t* sz = (const uint8_t*)P.sz;
-    for (int i = 0; i < cnt; i++) {
-        for (int m = 0; m < g.nm; m++) {
-            const size_t row = (size_t)(o0 + i) + (size_t)m * P.rows;
-            uint8_t* d = reg + ((slot + i) * g.nm + m) * g.stride;
-            dma_bytes(w + row * g.rb, g.rb, d, lane);
-            if (g.szb) dma_bytes(sz + row * g.szb, g.szb, d + g.rb, lane);
-        }
+    for (int m = 0; m < g.nm; m++) {
+        const size_t row = (size_t)o0 + (size_t)m * P.rows;
+        dma_bytes(w + row * g.rb, cnt * g.rb, reg + lds_w(g, slot, m), lane);
+        if (g.szb) dma_bytes(sz + row * g.szb, cnt * g.szb, reg + lds_sz(g, slot, m), lane);
     }
 }
 
@@ -356,12 +380,12 @@ __device__ __forceinline__ float dot8(uint32_t w, const float* x) {
 }
 
 // The lane's share, over every step of x, of the dot products of NR rows held in LDS at
-// cur + roff[r] (q4: the row's (scale, zero) pairs follow its nibbles at + rb; gs = log2 of the
-// group size). Each slab type has its own loop with the NR rows unrolled and no branch between
+// cur + roff[r] (q4: the row's (scale, zero) pairs at cur + soff[r]; gs = log2 of the group size). Each slab type has its own loop with the NR rows unrolled and no branch between
 // them, so a step's LDS reads for all rows issue together. X holds step 0 when nsteps is 1.
 template <int NR>
-__device__ __forceinline__ void rows_dot(const Step& t, int gs, int rb, const uint8_t* cur, const int (&roff)[8],
-                                         const float* xs, const float* xsum, XC& X, int lane, float (&acc)[8]) {
+__device__ __forceinline__ void rows_dot(const Step& t, int gs, const uint8_t* cur, const int (&roff)[8],
+                                         const int (&soff)[8], const float* xs, const float* xsum, XC& X, int lane,
+                                         float (&acc)[8]) {
     const bool reload = t.nsteps > 1;
     if (t.kind == 1) {
         for (int j = 0; j < t.n4; j++) {
@@ -371,7 +395,7 @@ __device__ __forceinline__ void rows_dot(const Step& t, int gs, int rb, const ui
 #pragma unroll
             for (int r = 0; r < NR; r++) {
                 w[r] = *(const u32x4*)(cur + roff[r] + 1024 * j + 16 * lane);
-                sz[r] = *(const uint32_t*)(cur + roff[r] + rb + 4 * ((2048 * j + 32 * lane) >> gs));
+                sz[r] = *(const uint32_t*)(cur + soff[r] + 4 * ((2048 * j + 32 * lane) >> gs));
             }
 #pragma unroll
             for (int r = 0; r < NR; r++) {
@@ -387,7 +411,7 @@ __device__ __forceinline__ void rows_dot(const Step& t, int gs, int rb, const ui
 #pragma unroll
             for (int r = 0; r < NR; r++) {
                 w[r] = *(const u32x2*)(cur + roff[r] + 1024 * t.n4 + 8 * lane);
-                sz[r] = *(const uint32_t*)(cur + roff[r] + rb + 4 * ((2048 * t.n4 + 16 * lane) >> gs));
+                sz[r] = *(const uint32_t*)(cur + soff[r] + 4 * ((2048 * t.n4 + 16 * lane) >> gs));
             }
 #pragma unroll
             for (int r = 0; r < NR; r++)
@@ -400,7 +424,7 @@ __device__ __forceinline__ void rows_dot(const Step& t, int gs, int rb, const ui
 #pragma unroll
             for (int r = 0; r < NR; r++) {
                 w[r] = *(const uint32_t*)(cur + roff[r] + 1024 * t.n4 + 512 * t.n2 + 4 * lane);
-                sz[r] = *(const uint32_t*)(cur + roff[r] + rb + 4 * ((2048 * t.n4 + 1024 * t.n2 + 8 * lane) >> gs));
+                sz[r] = *(const uint32_t*)(cur + soff[r] + 4 * ((2048 * t.n4 + 1024 * t.n2 + 8 * lane) >> gs));
             }
 #pragma unroll
             for (int r = 0; r < NR; r++) acc[r] += lo_h(sz[r]) * (dot8(w[r], &X.x[0]) - hi_h(sz[r]) * X.sum);
@@ -513,23 +537,19 @@ __device__ __forceinline__ void prefetch(const Env& e, CPhase& P, int step, uint
         const GemvGeo g = geo(P);
         const Rows R = part_p(P, e.gwm);
         const int cnt = min(R.n, g.cap);
-        asm volatile("" ::"s"(cnt), "s"(g.stride));
-        mark(e, 6);
         dma_rows(P, g, R.r0, cnt, 0, nxt, lane);
         if (P.epi == EP_CONV && cnt > 0) {
             // conv state [ch][4] and weights [ch][4] of the prefetched rows, 16 bytes each
-            uint8_t* cv = nxt + cnt * g.nm * g.stride;
+            uint8_t* cv = nxt + lds_conv(g);
             const int row = min(R.r0 + lane, P.conv_ch - 1);
             if (lane < cnt) {
-                __builtin_amdgcn_global_load_lds((const void*)(P.conv + (size_t)row * 4), (lds_ptr_t)cv, 16, 0, 0);
-                __builtin_amdgcn_global_load_lds((const void*)(P.conv_w + (size_t)row * 4), (lds_ptr_t)(cv + 16 * cnt), 16, 0, 0);
+                lds_dma16<false>(P.conv + (size_t)row * 4, cv);
+                lds_dma16<false>(P.conv_w + (size_t)row * 4, cv + 16 * g.cap);
             }
         }
     } else if (P.kind == PH_GDN) {
         const int it = e.wg;
         const float* rec = P.rec;
-        asm volatile("" ::"s"(rec));
-        mark(e, 6);
         if (it < P.heads * 16) {
             const int h = it / 16, t = (it % 16) * 8 + e.wave;
             // state column t of head h: S[h][t][0..127] (value-major), 512 bytes
@@ -537,8 +557,6 @@ __device__ __forceinline__ void prefetch(const Env& e, CPhase& P, int step, uint
         }
     } else if (P.kind == PH_ATTN) {
         const int nkv = P.kv_heads, S = P.splits;
-        asm volatile("" ::"s"(nkv), "s"(S));
-        mark(e, 6);
         if (e.wg < nkv * S) {
             const int g = e.wg / S, sp = e.wg % S;
             const uint32_t pos = a.pos0 + (uint32_t)step, len = pos + 1;
@@ -555,8 +573,8 @@ __device__ __forceinline__ void prefetch(const Env& e, CPhase& P, int step, uint
                 const int pp = p0 + 2 * (e.wave + kNW * u) + half;
                 if (bid[u] >= 0) {
                     const size_t at = (((size_t)bid[u] * nkv + g) * kBlk + pp % kBlk) * kHeadDim + 8 * li;
-                    __builtin_amdgcn_global_load_lds((const void*)(P.kp + at), (lds_ptr_t)(nxt + u * 2048), 16, 0, 0);
-                    __builtin_amdgcn_global_load_lds((const void*)(P.vp + at), (lds_ptr_t)(nxt + u * 2048 + 1024), 16, 0, 0);
+                    lds_dma16<false>(P.kp + at, nxt + u * 2048);
+                    lds_dma16<false>(P.vp + at, nxt + u * 2048 + 1024);
                 }
             }
         }
@@ -685,7 +703,7 @@ __device__ __forceinline__ void gemv_body(const Env& e, CPhase& P, int step, int
         const int pre = min(R.n, g.cap);  // outputs prefetched
         const bool stream = R.n > g.cap;
         const int go = stream ? max(1, min(gmax, g.cap / 2)) : min(gmax, R.n);
-        const uint8_t* cvs = cur + pre * g.nm * g.stride;  // EP_CONV: conv state / weights of the prefetched rows
+        const uint8_t* cvs = cur + lds_conv(g);  // EP_CONV: conv state / weights of the prefetched rows
         int issued = pre;
         XC X;
         if (t.nsteps == 1) load_step(xs, xsum, t, 0, X, lane);
@@ -695,25 +713,31 @@ __device__ __forceinline__ void gemv_body(const Env& e, CPhase& P, int step, int
         for (int o0 = 0; o0 < R.n; o0 += go) {
             const int ng = min(go, R.n - o0), nr = ng << ns;
             if (o0 + ng > pre) wait_vm((issued - o0 - ng) * g.per);  // refilled group
-            // LDS offsets of the group's rows (row r = row m of output i); padding rows repeat row 0
-            int roff[8];
+            // LDS offsets of the group's rows and their (scale, zero) rows (row r = row m of output i);
+            // padding rows repeat row 0
+            int roff[8], soff[8];
 #pragma unroll
             for (int r = 0; r < 8; r++) {
                 int slot = o0 + (r >> ns);
                 if (stream) slot = slot < g.cap ? slot : slot % g.cap;
-                roff[r] = ((slot << ns) + (r & ns)) * g.stride;
+                roff[r] = lds_w(g, slot, r & ns);
+                soff[r] = lds_sz(g, slot, r & ns);
             }
 #pragma unroll
-            for (int r = 1; r < 8; r++)
-                if (r >= nr) roff[r] = roff[0];
+            for (int r = 1; r < 8; r++) {
+                if (r >= nr) {
+                    roff[r] = roff[0];
+                    soff[r] = soff[0];
+                }
+            }
             float acc[8];
 #pragma unroll
             for (int r = 0; r < 8; r++) acc[r] = 0.0f;
-            if (nr == 1) rows_dot<1>(t, P.gshift, g.rb, cur, roff, xs, xsum, X, lane, acc);
-            else if (nr == 2) rows_dot<2>(t, P.gshift, g.rb, cur, roff, xs, xsum, X, lane, acc);
-            else if (nr <= 4) rows_dot<4>(t, P.gshift, g.rb, cur, roff, xs, xsum, X, lane, acc);
-            else if (nr <= 6) rows_dot<6>(t, P.gshift, g.rb, cur, roff, xs, xsum, X, lane, acc);
-            else rows_dot<8>(t, P.gshift, g.rb, cur, roff, xs, xsum, X, lane, acc);
+            if (nr == 1) rows_dot<1>(t, P.gshift, cur, roff, soff, xs, xsum, X, lane, acc);
+            else if (nr == 2) rows_dot<2>(t, P.gshift, cur, roff, soff, xs, xsum, X, lane, acc);
+            else if (nr <= 4) rows_dot<4>(t, P.gshift, cur, roff, soff, xs, xsum, X, lane, acc);
+            else if (nr <= 6) rows_dot<6>(t, P.gshift, cur, roff, soff, xs, xsum, X, lane, acc);
+            else rows_dot<8>(t, P.gshift, cur, roff, soff, xs, xsum, X, lane, acc);
             if (o0 == 0) {
                 asm volatile("" ::"v"(acc[0]), "v"(acc[1]), "v"(acc[7]));
                 mark(e, 2);
@@ -746,7 +770,7 @@ __device__ __forceinline__ void gemv_body(const Env& e, CPhase& P, int step, int
                     float4 st, cw;
                     if (k < pre) {
                         st = *(const float4*)(cvs + 16 * k);
-                        cw = *(const float4*)(cvs + 16 * pre + 16 * k);
+                        cw = *(const float4*)(cvs + 16 * g.cap + 16 * k);
                     } else {
                         st = *(const float4*)(P.conv + (size_t)o * 4);
                         cw = *(const float4*)(P.conv_w + (size_t)o * 4);
@@ -961,7 +985,7 @@ __device__ __forceinline__ void attn_phase(const Env& e, CPhase& P, int step, in
             acc[gi][d] = 0.0f;
         }
     }
-    wait_vm_n<0>();  // prefetched K/V rows
+    wait_all();  // prefetched K/V rows
     for (int u = 0;; u++) {
         const int pp = p0 + 2 * (e.wave + kNW * u);
         if (pp >= p1) break;  // wave-uniform
@@ -1193,7 +1217,7 @@ __device__ __forceinline__ void decode_program(const DecodeArgs& a) {
 
     uint32_t token = a.feed ? a.tok[0] : a.ids[0];
     int half = 0;  // half of the next region phase (region phases alternate between the halves)
-    // the first two region phases of the window
+    // the window's first two region phases (each region phase sends the one two ahead)
     prefetch(e, prog[a.reg0], 0, region(0));
     prefetch(e, prog[a.reg1], 0, region(1));
     for (int step = 0; step < a.n_steps; step++) {
@@ -1248,7 +1272,7 @@ __device__ __forceinline__ void decode_program(const DecodeArgs& a) {
                         head_phase(e, P, ws, inv);
                     } else {
                         stage_post(xs, P, make_step(P), xsum, rnh);
-                        gemv_body(e, P, step, p, ws, inv, region(half), xs, xsum);
+                        gemv_body(e, P, step, p, ws, inv, region(rh), xs, xsum);
                     }
                     break;
                 }
@@ -1258,12 +1282,12 @@ __device__ __forceinline__ void decode_program(const DecodeArgs& a) {
                     mark(e, 1);
                     if (bail) { wait_all(); return; }
                     trace_in(e, inst);
-                    gdn_body(e, P, step, p, c, region(half), xs, red);
+                    gdn_body(e, P, step, p, c, region(rh), xs, red);
                     mark(e, 2);
                     break;
                 case PH_ATTN:
                     trace_in(e, inst);
-                    attn_phase(e, P, step, p, c, half, rope);
+                    attn_phase(e, P, step, p, c, rh, rope);
                     break;
                 default:
                     trace_in(e, inst);
@@ -1275,9 +1299,7 @@ __device__ __forceinline__ void decode_program(const DecodeArgs& a) {
                 // this phase's LDS reads are done: send the data of the region phase two ahead
                 // into its half (the next region phase's data is in the other half)
                 int ns = 0, np = 0;
-                const bool more = region_after(a, P, step, p, 2, ns, np);
-                mark(e, 5);
-                if (more) prefetch(e, prog[np], ns, region(rh));
+                if (region_after(a, P, step, p, 2, ns, np)) prefetch(e, prog[np], ns, region(rh));
                 mark(e, 7);
                 half ^= 1;
             }

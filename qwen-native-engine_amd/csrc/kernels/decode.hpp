@@ -107,11 +107,11 @@ struct DecodeArgs {
     int trace_cap = 0;
     // Optional finer timeline (profiling): for phase instance i and workgroup w, sub[8 (i * grid + w) + k]
     // holds timestamps of the phase's sub-steps (kept in registers, stored when the phase ends);
-    // 0 = not reached. k = 0 entry. GEMV: 1 x slice loaded, 2 first group's rows done, 3 all rows
-    // published. GDN: 1 input staged, 2 state update done. Attention partials: 1 input staged,
-    // 2 q/k normed and rotated, 3 context loop done, 4 partials published. Combine: 1 partials
-    // staged, 2 gate staged, 3 published. Region phases: 5 successor found, 6 its descriptor read,
-    // 7 its DMA issued.
+    // 0 = not reached. k = 0 entry. GEMV (entry = input staged): 1 x slice loaded, 2 first group's
+    // rows done, 3 all rows published. GDN: 1 input staged, 2 state update published. Attention
+    // partials: 1 input staged, 2 q/k normed and rotated, 3 context loop done, 4 partials
+    // published. Combine: 1 partials staged, 2 gate staged, 3 published. Region phases: 7 the DMA
+    // of the region phase two ahead issued.
     unsigned long long* sub = nullptr;
 };
 

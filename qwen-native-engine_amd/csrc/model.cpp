@@ -512,6 +512,8 @@ void Model::setup_engine() {
     DecodeArgs links;
     if (!finalize_program(prog.data(), (int)prog.size(), links)) throw unsupported("too few region phases per step");
     nph_ = (int)prog.size();
+    phase_kind_.clear();
+    for (const Phase& P : prog) phase_kind_.push_back(P.kind);
     Phase* d_prog = (Phase*)dalloc(prog.size() * sizeof(Phase));
     QNE_HIP(hipMemcpy(d_prog, prog.data(), prog.size() * sizeof(Phase), hipMemcpyHostToDevice));
     am_ = (uint64_t*)dalloc((size_t)4 * grid * 8);
@@ -822,6 +824,10 @@ std::string Model::profile_token_json() {
         return v[v.size() / 2];
     };
     std::map<std::string, double> span_l, comp_l, exch_l;
+    // critical chain: per phase, when each workgroup had its input staged and when it had
+    // published, relative to the previous phase's last publish (sub-step slots per kind)
+    std::string chain = "[";
+    unsigned long long pub_prev = 0;
     std::map<std::string, std::vector<double>> sub_l;
     std::string phases = "[";
     unsigned long long prev = tr[0];
@@ -865,6 +871,29 @@ std::string Model::profile_token_json() {
                 for (size_t k2 = 0; k2 < parts.size(); k2++) v[k2] += med(parts[k2]);
             }
         }
+        {
+            const int kind = phase_kind_[b];  // 0 GEMV, 1 GDN, 2 attention, 3 combine
+            const int in_slot = kind == 0 ? 0 : kind == 3 ? 2 : 1, pub_slot = kind == 0 ? 3 : kind == 1 ? 2 : kind == 2 ? 4 : 3;
+            std::vector<double> tin, tpub;
+            unsigned long long pmax = 0;
+            for (int w = 0; w < grid; w++) {
+                const unsigned long long* q = sub.data() + 8 * ((size_t)b * grid + w);
+                if (q[in_slot] == 0 || q[pub_slot] == 0) continue;
+                pmax = std::max(pmax, q[pub_slot]);
+                if (pub_prev) {
+                    tin.push_back((double)((long long)q[in_slot] - (long long)pub_prev) * tick_ms);
+                    tpub.push_back((double)((long long)q[pub_slot] - (long long)pub_prev) * tick_ms);
+                }
+            }
+            if (!tin.empty()) {
+                char buf[224];
+                std::snprintf(buf, sizeof buf, "%s[\"%s\",%.5f,%.5f,%.5f,%.5f]", chain.size() > 1 ? "," : "", label.c_str(),
+                              med(tin), *std::max_element(tin.begin(), tin.end()), med(tpub),
+                              *std::max_element(tpub.begin(), tpub.end()));
+                chain += buf;
+            }
+            if (pmax) pub_prev = pmax;
+        }
         const double span = ms(prev, dmax), cm = med(comp), em = med(exch);
         const double cx = *std::max_element(comp.begin(), comp.end()), ex = *std::max_element(exch.begin(), exch.end());
         span_l[label] += span;
@@ -901,14 +930,16 @@ std::string Model::profile_token_json() {
     }
     subs += "}";
     return std::string(head) +
-           "\"sub_step_names\":{\"gemv\":[\"x load\",\"first group\",\"other groups\",\"successor\",\"descriptor\",\"dma issue\"],"
-           "\"gdn\":[\"input\",\"state update\",\"successor\",\"descriptor\",\"dma issue\"],"
-           "\"attention\":[\"input\",\"q/k prep\",\"context loop\",\"merge + publish\",\"successor\",\"descriptor\",\"dma issue\"],"
+           "\"sub_step_names\":{\"gemv\":[\"x load\",\"first group\",\"other groups\",\"dma issue (two ahead)\"],"
+           "\"gdn\":[\"input\",\"state update\",\"dma issue (two ahead)\"],"
+           "\"attention\":[\"input\",\"q/k prep\",\"context loop\",\"merge + publish\",\"dma issue (two ahead)\"],"
            "\"combine\":[\"partials\",\"gate\",\"combine + publish\"]}," +
            "\"sub_steps_median_ms\":" + subs + ",\"labels\":" + obj(span_l) + ",\"compute_median_ms\":" + obj(comp_l) +
            ",\"handover_median_ms\":" + obj(exch_l) +
            ",\"phase_columns\":[\"label\",\"span\",\"compute_median\",\"compute_max\",\"handover_median\",\"handover_max\"]" +
-           ",\"phases\":" + phases + "}";
+           ",\"phases\":" + phases +
+           ",\"chain_columns\":[\"label\",\"input_median\",\"input_max\",\"published_median\",\"published_max\"]" +
+           ",\"chain\":" + chain + "]}";
 }
 
 }  // namespace qne

@@ -137,6 +137,7 @@ class Model {
     size_t exch_bytes_ = 0;
     uint64_t* am_ = nullptr;       // argmax exchange
     int nph_ = 0;                  // phases per token
+    std::vector<int> phase_kind_;  // PhaseKind of each phase (profile labels)
     uint32_t tag_base_ = 1;
     unsigned* host_err_ = nullptr;  // pinned
     double last_decode_ms_ = 0.0;
