@@ -99,6 +99,121 @@ def profiled_traffic(steps: int):
     return vals["traffic_bytes_per_launch"]
 
 
+def _events_ms(fn, warmup: int, iters: int):
+    """Device time per call of fn(stream) from HIP events recorded on the stream it launches on."""
+    import torch
+    st = torch.cuda.Stream()
+    h = st.cuda_stream
+    for _ in range(warmup):
+        fn(h)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(st)
+    for _ in range(iters):
+        fn(h)
+    e1.record(st)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / iters
+
+
+def bench_paged_attention(args) -> dict:
+    """Paged-KV GQA decode: 16 q / 4 kv heads of 256, f16 K/V N(0, 1) in 16-token blocks behind a
+    randomly permuted block table, `--batch` sequences with contexts uniform in [256, 4096], each
+    call appending one token per sequence. Algorithmic bytes per call: K and V of every attended
+    position (4096 B), the block-table entries, q, the new k/v and the output."""
+    import torch
+    import qne
+    B, nq, nkv, hd, blk, maxb = args.batch, 16, 4, 256, 16, 256
+    rng = np.random.default_rng(args.seed)
+    ctx = rng.integers(256, 4096, size=B).astype(np.int32)
+    pool = B * maxb
+    dev = "cuda"
+    bt = torch.from_numpy(rng.permutation(pool).astype(np.int32).reshape(B, maxb)).to(dev)
+    kp = torch.randn(pool, nkv, blk, hd, dtype=torch.float16, device=dev)
+    vp = torch.randn(pool, nkv, blk, hd, dtype=torch.float16, device=dev)
+    q = torch.randn(B, nq, hd, device=dev)
+    kn, vn = torch.randn(B, nkv, hd, device=dev), torch.randn(B, nkv, hd, device=dev)
+    dctx = torch.from_numpy(ctx).to(dev)
+    out = torch.empty(B, nq, hd, device=dev)
+
+    def call(stream):
+        qne.paged_attn_decode(q.data_ptr(), kn.data_ptr(), vn.data_ptr(), kp.data_ptr(), vp.data_ptr(), bt.data_ptr(),
+                              maxb, dctx.data_ptr(), out.data_ptr(), B, nq, nkv, stream)
+
+    ms = _events_ms(call, args.warmup, args.steps)
+    pos = (ctx.astype(np.int64) + 1)
+    nbytes = int(pos.sum()) * nkv * hd * 2 * 2 + int(((pos + blk - 1) // blk).sum()) * 4 + B * (2 * nq + 2 * nkv) * hd * 4
+    gbs = nbytes / (ms / 1e3) / 1e9
+    return {"metric": "paged attention decode GB/s (16q/4kv x 256, 16-token blocks)", "value": round(gbs, 1),
+            "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4),
+            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+            "config": {"workload": f"{B} sequences, contexts uniform in [256, 4096] (mean {float(ctx.mean()):.0f}), "
+                                   f"one appended token each", "batch": B},
+            "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                         "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None,
+                         "kernel": "k_kv_append + k_attn_partial + k_attn_combine", "bytes_per_step": nbytes},
+            "cpu_baseline": None}
+
+
+def bench_gdn(args) -> dict:
+    """Gated delta rule, 16 heads, dk = dv = 128, f32 state; q, k L2-normalised N(0, 1), v N(0, 1),
+    beta = sigmoid(N(0, 1)), decay g = exp(-softplus(N(0, 1))). (a) one recurrent step at batch 1, 8
+    and 64: 133 128 B per (sequence, head) (state read + written, q, k, v, o). (b) 2048 tokens in one
+    call at batch 4: 2048 B per (token, head) of q, k, v, o plus the state once per sequence."""
+    import torch
+    import torch.nn.functional as F
+    import qne
+    H, dk = 16, 128
+    dev = "cuda"
+    rng = np.random.default_rng(args.seed)
+
+    def inputs(shape):
+        t = lambda *s: torch.from_numpy(rng.normal(size=s).astype(np.float32)).to(dev)
+        q, k = F.normalize(t(*shape, dk), dim=-1), F.normalize(t(*shape, dk), dim=-1)
+        v = t(*shape, dk)
+        beta = torch.sigmoid(t(*shape))
+        g = torch.exp(-F.softplus(t(*shape)))
+        return q, k, v, beta, g
+
+    steps = {}
+    for B in (1, 8, 64):
+        q, k, v, beta, g = inputs((B, H))
+        # successive calls rotate over states totalling at least 512 MiB (above the 256 MB
+        # last-level cache), so every call reads its state from HBM
+        nst = max(2, min(512, (512 << 20) // (B * H * dk * dk * 4)))
+        S = torch.zeros(nst, B, H, dk, dk, device=dev)
+        o = torch.empty(B, H, dk, device=dev)
+        turn = [0]
+
+        def step_call(st):
+            Si = S[turn[0] % nst]
+            turn[0] += 1
+            qne.gdn_step(q.data_ptr(), k.data_ptr(), v.data_ptr(), beta.data_ptr(), g.data_ptr(), Si.data_ptr(),
+                         o.data_ptr(), B, H, st)
+
+        ms = _events_ms(step_call, args.warmup, args.steps)
+        nb = B * H * 133128
+        steps[B] = {"ms": round(ms, 4), "GB/s": round(nb / (ms / 1e3) / 1e9, 1)}
+    B, T = 4, 2048
+    q, k, v, beta, g = inputs((B, T, H))
+    S = torch.zeros(B, H, dk, dk, device=dev)
+    o = torch.empty(B, T, H, dk, device=dev)
+    ms = _events_ms(lambda st: qne.gdn_prefill_chunked(q.data_ptr(), k.data_ptr(), v.data_ptr(), beta.data_ptr(),
+                                                       g.data_ptr(), S.data_ptr(), o.data_ptr(), B, T, H, st),
+                    1, max(1, args.steps // 20))
+    nb = B * T * H * 2048 + B * H * dk * dk * 4 * 2
+    pre = {"ms": round(ms, 3), "GB/s": round(nb / (ms / 1e3) / 1e9, 1), "tokens_per_s": round(B * T / (ms / 1e3))}
+    gbs = steps[64]["GB/s"]
+    return {"metric": "gated delta rule GB/s (16 heads x 128 x 128 state), step at batch 64", "value": gbs,
+            "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": steps[64]["ms"],
+            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+            "config": {"workload": "recurrent step at batch 1/8/64; 2048-token prefill at batch 4", "batch": 64},
+            "roofline": {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                         "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None, "kernel": "k_delta_rule",
+                         "bytes_per_step": 64 * H * 133128},
+            "detail": {"step": steps, "prefill_b4_t2048": pre}, "cpu_baseline": None}
+
+
 def copy_calibration(mib: int) -> None:
     """A plain device-to-device copy of a known size: under a hardware-counter profiler its
     FETCH_SIZE / WRITE_SIZE readings per dispatch, divided into the bytes it must move, give the
@@ -122,7 +237,9 @@ def main():
                     help="untimed warmup steps, run as one window (default: as many as --steps, so that "
                          "every decode window a profile sees has the timed length)")
     ap.add_argument("--ctx", type=int, default=4000)
-    ap.add_argument("--config", default="2b")
+    ap.add_argument("--config", default="2b",
+                    help="2b (the decode benchmark), 0.8b, or the kernel microbenches attn / gdn")
+    ap.add_argument("--batch", type=int, default=64, help="sequences (--config attn)")
     ap.add_argument("--cpu-tokens", type=int, default=4)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--seed", type=int, default=0)
@@ -134,6 +251,10 @@ def main():
         args.warmup = args.steps
     if args.copy_calibration:
         copy_calibration(args.copy_calibration)
+        return
+    if args.config in ("attn", "gdn"):
+        sys.path[:0] = [str(ROOT / "qwen-native-engine_amd")]
+        print(json.dumps(bench_paged_attention(args) if args.config == "attn" else bench_gdn(args)))
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this engine runs batch-1 decode on one GPU; --gpus above 1 is not supported "

@@ -124,7 +124,10 @@ int qne_gdn_prefill_chunked(const float* q, const float* k, const float* v, cons
 /* Paged KV decode for `batch` sequences (kernels/src/shaders.rs:522-633 generalised): appends one
  * token's k,v (f16) per sequence at position ctx[b], then attends q over positions 0..ctx[b].
  * Pools are [num_blocks][nkv][16][hd] f16; block_table [batch][max_blocks] (int32);
- * q/out [batch][nq][hd] f32, k_new/v_new [batch][nkv][hd] f32. hd = 256. scale = 1/sqrt(hd). */
+ * q/out [batch][nq][hd] f32, k_new/v_new [batch][nkv][hd] f32. hd = 256. scale = 1/sqrt(hd).
+ * On the null stream the call returns when the result is ready; on another stream it is enqueued
+ * there. The partials' scratch is kept per device (allocated on first use, grown when a call needs
+ * more): calls that overlap on one device must not be issued. */
 int qne_paged_attn_decode(const float* q, const float* k_new, const float* v_new, void* k_pool,
                           void* v_pool, const int32_t* block_table, int max_blocks,
                           const int32_t* ctx, float* out, int batch, int nq, int nkv,

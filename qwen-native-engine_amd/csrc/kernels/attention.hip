@@ -5,8 +5,9 @@
 //  - the cache is paged: pools [block][kv_head][16][256] f16, a block table maps logical blocks;
 //  - split-context ("flash decoding") partials: workgroup (split, kv_head, seq) streams a slice
 //    of the context once for all query heads that share the kv head (GQA reuse);
-//  - a wave covers 4 positions per step, 16 lanes per position, 16 dims (32 bytes of K and of V)
-//    per lane; scores are 16-lane reductions; softmax is online (running max / sum);
+//  - a wave covers 2 positions per step, 32 lanes per position, 8 dims (16 bytes of K and of V)
+//    per lane, with the next step's rows in flight; scores are half-wave DPP sums; softmax is
+//    online (running max / sum) in base 2;
 //  - a combine kernel merges the splits (and applies the sigmoid output gate of the model).
 // The current token's k and v are appended (rounded to f16) before the partials run, so the
 // current position is read back exactly as every later step will read it.
@@ -77,8 +78,12 @@ __global__ __launch_bounds__(kAttnThreads) void k_kv_append(const float* __restr
     v_pool[at] = f2h(v_new[src]);
 }
 
-// Split-context partials. Grid (splits, nkv, batch). Sequence b attends positions 0..len-1 with
-// len = lens[b] + 1 (lens = tok + 1 for the model, ctx for the raw form).
+// Split-context partials. Grid (splits, nkv, batch), 4 waves. Sequence b attends positions
+// 0..len-1 with len = lens[b] + 1 (lens = tok + 1 for the model, ctx for the raw form). A wave takes
+// two positions per step (one per 32-lane half; a lane holds 8 dims, 16 bytes of K and of V) and
+// loads the next step's rows while it computes the current ones. Scores are half-wave DPP sums.
+// The softmax runs in base 2: q is pre-scaled by log2(e) / sqrt(256), so each weight is one
+// exp2, and the partial maxima and sums are in that base (the combine uses the same base).
 template <int G>
 __global__ __launch_bounds__(kAttnThreads) void k_attn_partial(const float* __restrict__ q, const uint16_t* __restrict__ k_pool,
                                                                const uint16_t* __restrict__ v_pool,
@@ -86,91 +91,86 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_partial(const float* __re
                                                                const int32_t* __restrict__ lens, int nkv,
                                                                float* __restrict__ part_ml, float* __restrict__ part_acc) {
     __shared__ float s_ml[4][G][2];
-    __shared__ float s_acc[4][G][kHD];
+    __shared__ __attribute__((aligned(16))) float s_acc[4][G][kHD];
     const int split = blockIdx.x, g = blockIdx.y, b = blockIdx.z, splits = gridDim.x;
-    const int t = threadIdx.x, lane = t % kWave, w = t / kWave, pg = lane / 16, li = lane % 16;
+    const int t = threadIdx.x, lane = t % kWave, w = t / kWave, half = lane >> 5, li = lane & 31;
     const int len = max(1, min(lens[b] + 1, max_blocks * kBlock));  // never past the block table
     int per = (len + splits - 1) / splits;
     per = (per + kBlock - 1) / kBlock * kBlock;
     const int p0 = split * per, p1 = min(len, p0 + per);
     const int32_t* bt = block_table + (size_t)b * max_blocks;
     const int nq = nkv * G;
+    constexpr float kScale = 1.4426950408889634f * 0.0625f;  // log2(e) / sqrt(256)
 
-    float qr[G][16], acc[G][16], m[G], l[G];
+    float qr[G][8], acc[G][8], m[G], l[G];
 #pragma unroll
     for (int gi = 0; gi < G; gi++) {
-        const float* qs = q + ((size_t)b * nq + g * G + gi) * kHD + 16 * li;
+        const float* qs = q + ((size_t)b * nq + g * G + gi) * kHD + 8 * li;
+        const float4 a0 = *(const float4*)qs, a1 = *(const float4*)(qs + 4);
+        qr[gi][0] = a0.x * kScale; qr[gi][1] = a0.y * kScale; qr[gi][2] = a0.z * kScale; qr[gi][3] = a0.w * kScale;
+        qr[gi][4] = a1.x * kScale; qr[gi][5] = a1.y * kScale; qr[gi][6] = a1.z * kScale; qr[gi][7] = a1.w * kScale;
 #pragma unroll
-        for (int d = 0; d < 16; d += 4) {
-            float4 v = *(const float4*)(qs + d);
-            qr[gi][d] = v.x * 0.0625f; qr[gi][d + 1] = v.y * 0.0625f;  // 1/sqrt(256), exact
-            qr[gi][d + 2] = v.z * 0.0625f; qr[gi][d + 3] = v.w * 0.0625f;
-        }
-#pragma unroll
-        for (int d = 0; d < 16; d++) acc[gi][d] = 0.0f;
+        for (int d = 0; d < 8; d++) acc[gi][d] = 0.0f;
         m[gi] = -INFINITY;
         l[gi] = 0.0f;
     }
-    for (int p = p0 + 4 * w + pg; p < p1; p += 16) {
-        const size_t at = kv_index(bt, p, nkv, g) + 16 * li;
-        const u32x4* kp = (const u32x4*)(k_pool + at);
-        const u32x4* vp = (const u32x4*)(v_pool + at);
-        const u32x4 k0 = __builtin_nontemporal_load(kp), k1 = __builtin_nontemporal_load(kp + 1);
-        const u32x4 v0 = __builtin_nontemporal_load(vp), v1 = __builtin_nontemporal_load(vp + 1);
-        const uint32_t kw[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
-        const uint32_t vw[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
-        float kf[16], vf[16];
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-            kf[2 * i] = lo_h(kw[i]); kf[2 * i + 1] = hi_h(kw[i]);
-            vf[2 * i] = lo_h(vw[i]); vf[2 * i + 1] = hi_h(vw[i]);
+    auto load = [&](int p, u32x4& kw, u32x4& vw) {
+        if (p < p1) {
+            const size_t at = kv_index(bt, p, nkv, g) + 8 * li;
+            kw = __builtin_nontemporal_load((const u32x4*)(k_pool + at));
+            vw = __builtin_nontemporal_load((const u32x4*)(v_pool + at));
+        } else {
+            kw = u32x4{0u, 0u, 0u, 0u};
+            vw = kw;
         }
+    };
+    u32x4 kc, vc, kn, vn;
+    load(p0 + 2 * w + half, kc, vc);
+    for (int base = p0 + 2 * w; base < p1; base += 8) {  // wave-uniform
+        const int pc = base + half;
+        const bool valid = pc < p1;
+        load(pc + 8, kn, vn);
+        float kf[8], vf[8];
+        kf[0] = lo_h(kc.x); kf[1] = hi_h(kc.x); kf[2] = lo_h(kc.y); kf[3] = hi_h(kc.y);
+        kf[4] = lo_h(kc.z); kf[5] = hi_h(kc.z); kf[6] = lo_h(kc.w); kf[7] = hi_h(kc.w);
+        vf[0] = lo_h(vc.x); vf[1] = hi_h(vc.x); vf[2] = lo_h(vc.y); vf[3] = hi_h(vc.y);
+        vf[4] = lo_h(vc.z); vf[5] = hi_h(vc.z); vf[6] = lo_h(vc.w); vf[7] = hi_h(vc.w);
 #pragma unroll
         for (int gi = 0; gi < G; gi++) {
             float s = 0.0f;
 #pragma unroll
-            for (int d = 0; d < 16; d++) s = fmaf(qr[gi][d], kf[d], s);
-            s = group16_sum(s);
-            float pw;
-            if (s > m[gi]) {
-                const float corr = expf(m[gi] - s);
-                m[gi] = s;
-                l[gi] *= corr;
+            for (int d = 0; d < 8; d++) s = fmaf(qr[gi][d], kf[d], s);
+            s = half_sum_dpp(s, lane);
+            if (valid) {
+                const float mn = fmaxf(m[gi], s);
+                const float corr = exp2f(m[gi] - mn), pw = exp2f(s - mn);
+                m[gi] = mn;
+                l[gi] = fmaf(l[gi], corr, pw);
 #pragma unroll
-                for (int d = 0; d < 16; d++) acc[gi][d] *= corr;
-                pw = 1.0f;
-            } else {
-                pw = expf(s - m[gi]);
+                for (int d = 0; d < 8; d++) acc[gi][d] = fmaf(pw, vf[d], acc[gi][d] * corr);
             }
-            l[gi] += pw;
-#pragma unroll
-            for (int d = 0; d < 16; d++) acc[gi][d] = fmaf(pw, vf[d], acc[gi][d]);
         }
+        kc = kn;
+        vc = vn;
     }
-    // merge the 4 position groups of the wave (lanes li, li+16, li+32, li+48)
+    // merge the two halves of the wave, then the 4 waves through LDS
 #pragma unroll
     for (int gi = 0; gi < G; gi++) {
+        const float mo = lane_xor32(m[gi], lane), lo = lane_xor32(l[gi], lane);
+        const float mn = fmaxf(m[gi], mo);
+        const float ca = mn == -INFINITY ? 0.0f : exp2f(m[gi] - mn), cb = mn == -INFINITY ? 0.0f : exp2f(mo - mn);
 #pragma unroll
-        for (int mask = 16; mask <= 32; mask <<= 1) {
-            const float mo = __shfl_xor(m[gi], mask, kWave), lo = __shfl_xor(l[gi], mask, kWave);
-            const float mn = fmaxf(m[gi], mo);
-            const float ca = mn == -INFINITY ? 0.0f : expf(m[gi] - mn), cb = mn == -INFINITY ? 0.0f : expf(mo - mn);
-#pragma unroll
-            for (int d = 0; d < 16; d++) {
-                const float ao = __shfl_xor(acc[gi][d], mask, kWave);
-                acc[gi][d] = acc[gi][d] * ca + ao * cb;
-            }
-            l[gi] = l[gi] * ca + lo * cb;
-            m[gi] = mn;
-        }
-        if (pg == 0) {
-#pragma unroll
-            for (int d = 0; d < 16; d++) s_acc[w][gi][16 * li + d] = acc[gi][d];
+        for (int d = 0; d < 8; d++) acc[gi][d] = acc[gi][d] * ca + lane_xor32(acc[gi][d], lane) * cb;
+        l[gi] = l[gi] * ca + lo * cb;
+        m[gi] = mn;
+        if (half == 0) {
+            *(float4*)&s_acc[w][gi][8 * li] = make_float4(acc[gi][0], acc[gi][1], acc[gi][2], acc[gi][3]);
+            *(float4*)&s_acc[w][gi][8 * li + 4] = make_float4(acc[gi][4], acc[gi][5], acc[gi][6], acc[gi][7]);
             if (li == 0) { s_ml[w][gi][0] = m[gi]; s_ml[w][gi][1] = l[gi]; }
         }
     }
     __syncthreads();
-    // merge the 4 waves: thread t owns dim t for every head of the group
+    // thread t owns dim t for every head of the group
     const size_t pbase = (((size_t)b * nkv + g) * splits + split) * G;
 #pragma unroll
     for (int gi = 0; gi < G; gi++) {
@@ -180,7 +180,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_partial(const float* __re
         float lsum = 0.0f, a = 0.0f;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            const float c = mn == -INFINITY ? 0.0f : expf(s_ml[i][gi][0] - mn);
+            const float c = mn == -INFINITY ? 0.0f : exp2f(s_ml[i][gi][0] - mn);
             lsum += s_ml[i][gi][1] * c;
             a += s_acc[i][gi][t] * c;
         }
@@ -202,7 +202,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_combine(const float* __re
         const size_t i = (((size_t)b * nkv + g) * splits + s) * G + gi;
         const float ms = part_ml[i * 2];
         if (ms == -INFINITY) continue;
-        const float c = expf(ms - mn);
+        const float c = exp2f(ms - mn);  // the partials' maxima are in base 2
         lsum += part_ml[i * 2 + 1] * c;
         a += part_acc[i * kHD + t] * c;
     }

@@ -168,3 +168,71 @@ def test_paged_attention_matches_dense(batch, nq, nkv):
         np.testing.assert_array_equal(kp[bt[b, p // blk], :, p % blk], kn[b].astype(np.float16))
         kp[bt[b, p // blk], :, p % blk] = kpool[bt[b, p // blk], :, p % blk]
     np.testing.assert_array_equal(kp, kpool)
+
+
+def test_paged_attention_config3_shape():
+    """Config-3 shape: 64 sequences, 16 q / 4 kv heads of 256, contexts uniform in [256, 4096], a
+    randomly permuted block table over the pool, one appended token per sequence; against the dense
+    unpaged oracle (f64)."""
+    rng = np.random.default_rng(303)
+    batch, nq, nkv, hd, blk, max_blocks = 64, 16, 4, 256, 16, 256
+    pool = batch * max_blocks
+    ctx = rng.integers(256, 4096, size=batch).astype(np.int32)
+    bt = rng.permutation(pool).astype(np.int32).reshape(batch, max_blocks)
+    kpool = rng.normal(size=(pool, nkv, blk, hd)).astype(np.float16)
+    vpool = rng.normal(size=(pool, nkv, blk, hd)).astype(np.float16)
+    q = rng.normal(size=(batch, nq, hd)).astype(np.float32)
+    kn = rng.normal(size=(batch, nkv, hd)).astype(np.float32)
+    vn = rng.normal(size=(batch, nkv, hd)).astype(np.float32)
+    want = np.empty((batch, nq, hd), np.float32)
+    for b in range(batch):
+        n = ctx[b] + 1
+        pos = np.arange(ctx[b])
+        kd = np.empty((nkv, n, hd), np.float16)
+        vd = np.empty((nkv, n, hd), np.float16)
+        kd[:, :-1] = kpool[bt[b, pos // blk], :, pos % blk].transpose(1, 0, 2)
+        vd[:, :-1] = vpool[bt[b, pos // blk], :, pos % blk].transpose(1, 0, 2)
+        kd[:, -1] = kn[b].astype(np.float16)
+        vd[:, -1] = vn[b].astype(np.float16)
+        kd, vd = np.ascontiguousarray(kd), np.ascontiguousarray(vd)
+        O.lib("f64").oc_attn_dense(nq, nkv, hd, O.ptr(q[b]), O.ptr(kd.view(np.uint16)), O.ptr(vd.view(np.uint16)), n,
+                                   1 / 16, O.ptr(want[b]))
+    dk, dv = to_dev(kpool.view(np.uint16)), to_dev(vpool.view(np.uint16))
+    dq, dkn, dvn, dbt, dctx = to_dev(q), to_dev(kn), to_dev(vn), to_dev(bt), to_dev(ctx)
+    out = torch.empty((batch, nq, hd), dtype=torch.float32, device=dev)
+    Q.paged_attn_decode(dq.data_ptr(), dkn.data_ptr(), dvn.data_ptr(), dk.data_ptr(), dv.data_ptr(), dbt.data_ptr(),
+                        max_blocks, dctx.data_ptr(), out.data_ptr(), batch, nq, nkv)
+    torch.cuda.synchronize()
+    assert rel_err(out.cpu().numpy(), want) < 1e-5
+
+
+def test_gdn_step_config4_batch64():
+    test_gdn_step_matches_oracle(64)
+
+
+def test_gdn_prefill_config4_shape():
+    """Config-4(b) shape: 2048 tokens per sequence at batch 4, 16 heads, in one call; against the
+    sequential recurrence of the oracle (f64)."""
+    rng = np.random.default_rng(404)
+    B, T, H, dk = 4, 2048, 16, 128
+    q = rng.normal(size=(B, T, H, dk)).astype(np.float32)
+    k = rng.normal(size=(B, T, H, dk)).astype(np.float32)
+    q /= np.linalg.norm(q, axis=-1, keepdims=True)
+    k /= np.linalg.norm(k, axis=-1, keepdims=True)
+    v = rng.normal(size=(B, T, H, dk)).astype(np.float32)
+    beta = (1 / (1 + np.exp(-rng.normal(size=(B, T, H))))).astype(np.float32)
+    g = np.exp(-np.log1p(np.exp(rng.normal(size=(B, T, H))))).astype(np.float32)
+    S = rng.normal(0, 0.1, size=(B, H, dk, dk)).astype(np.float32)
+    want_S, want_o = S.copy(), np.empty_like(v)
+    L = O.lib("f64")
+    for b in range(B):
+        for t in range(T):
+            for h in range(H):
+                L.oc_delta_rule(dk, dk, O.ptr(q[b, t, h]), O.ptr(k[b, t, h]), O.ptr(v[b, t, h]), float(beta[b, t, h]),
+                                float(g[b, t, h]), O.ptr(want_S[b, h]), O.ptr(want_o[b, t, h]))
+    d = [to_dev(a) for a in (q, k, v, beta, g, S)]
+    out = torch.empty_like(d[2])
+    Q.gdn_prefill_chunked(*[t.data_ptr() for t in d], out.data_ptr(), B, T, H)
+    torch.cuda.synchronize()
+    assert rel_err(out.cpu().numpy(), want_o) < 1e-4
+    assert rel_err(d[5].cpu().numpy(), want_S) < 1e-4
