@@ -116,8 +116,10 @@ int qne_pack_sz_q4g(const uint16_t* scales, const uint16_t* zeros, size_t n, uin
  * out [dv] = S'^T q. q and k are used as given (already normalised). */
 int qne_gdn_step(const float* q, const float* k, const float* v, const float* beta, const float* g,
                  float* state, float* out, int batch, int heads, void* stream);
-/* The same recurrence over T tokens per sequence (batch.rs:166-255 semantics), computed in
- * chunks of 64 tokens: q,k [B][T][H][dk], v/out [B][T][H][dv], beta/g [B][T][H]. */
+/* The same recurrence over T tokens per sequence in one call (batch.rs:166-255 semantics: the
+ * state after the call is the state after T sequential steps): q,k [B][T][H][dk], v/out
+ * [B][T][H][dv], beta/g [B][T][H]. The state stays in registers across the T tokens, its value
+ * columns split over B * H * 32 independent waves. */
 int qne_gdn_prefill_chunked(const float* q, const float* k, const float* v, const float* beta,
                             const float* g, float* state, float* out, int batch, int tokens,
                             int heads, void* stream);

@@ -448,31 +448,6 @@ __device__ __forceinline__ void rows_dot(const Step& t, int gs, const uint8_t* c
     }
 }
 
-// Sums 8 per-lane partials across the wave: after the call, lanes 8r..8r+7 hold the total of
-// partial r. Halving steps over lane bits 5, 4, 3 (each lane keeps the half its bit selects and
-// adds its partner's copy of it, exchanged with permlane swaps and DPP), then a plain sum over
-// lane bits 2, 1, 0 with DPP.
-__device__ __forceinline__ float reduce8(float (&v)[8], int lane) {
-    float h4[4], h2[2];
-    const bool b5 = lane & 32, b4 = lane & 16, b3 = lane & 8;
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const float send = b5 ? v[i] : v[i + 4], keep = b5 ? v[i + 4] : v[i];
-        h4[i] = keep + lane_xor32(send, lane);
-    }
-#pragma unroll
-    for (int i = 0; i < 2; i++) {
-        const float send = b4 ? h4[i] : h4[i + 2], keep = b4 ? h4[i + 2] : h4[i];
-        h2[i] = keep + lane_xor16(send, lane);
-    }
-    const float send = b3 ? h2[0] : h2[1], keep = b3 ? h2[1] : h2[0];
-    float t = keep + QNE_DPP(send, kDppRor8);
-    t += QNE_DPP(t, kDppXor1);
-    t += QNE_DPP(t, kDppXor2);
-    t += QNE_DPP(t, kDppHalfMirror);
-    return t;
-}
-
 // Per-wave state carried across phases.
 struct WaveState {
     float hown[2];   // residual rows this wave owns (uniform across lanes)

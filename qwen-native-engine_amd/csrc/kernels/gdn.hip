@@ -155,36 +155,84 @@ __global__ __launch_bounds__(kGdnThreads) void k_delta_rule(const float* __restr
     if (qq == 0) out[bh * kDV + col] = o;
 }
 
-// The delta rule over `tokens` tokens of sequence blockIdx.y, head blockIdx.x, state in VGPRs
-// for the whole launch. Layouts: q,k [B][T][H][dk], v,out [B][T][H][dv], beta,g [B][T][H].
-__global__ __launch_bounds__(kGdnThreads) void k_delta_rule_seq(const float* __restrict__ q, const float* __restrict__ k,
-                                                                const float* __restrict__ v, const float* __restrict__ beta,
-                                                                const float* __restrict__ g, float* __restrict__ state,
-                                                                float* __restrict__ out, int T, int H) {
-    __shared__ DeltaShared sh;
-    const int h = blockIdx.x, b = blockIdx.y, t = threadIdx.x, lane = t % kWave, w = t / kWave;
-    const int col = t & (kDV - 1), qq = t >> 7;
-    float* S = state + ((size_t)b * H + h) * kDK * kDV;
-    float s[32];
-    load_tile(s, S, col, qq);
-    for (int n = 0; n < T; n++) {
+// Sum over the 16 lanes of a DPP row; every lane of the row receives the row's total.
+__device__ __forceinline__ float row16_sum(float v) {
+    v += QNE_DPP(v, kDppXor1);
+    v += QNE_DPP(v, kDppXor2);
+    v += QNE_DPP(v, kDppHalfMirror);
+    v += QNE_DPP(v, kDppMirror);
+    return v;
+}
+
+// The delta rule over T tokens with the value columns split across waves: a wave owns (sequence
+// b, head h, columns 4c..4c+3); row r of the wave (lanes 16r..16r+15) owns column 4c + r, and lane
+// i of the row keeps keys 8i..8i+7 of it in registers for the whole launch. A token costs 8 FMAs
+// each for the lane's shares of (S^T k)_col and (S^T q)_col and of k.q, three 16-lane DPP sums
+// (no cross-row traffic), and 8 state FMAs; the next tokens' inputs load while one runs. The
+// waves are independent (no LDS, no barrier), so B * H * 32 of them run at once.
+// Layouts: q,k [B][T][H][dk], v,out [B][T][H][dv], beta,g [B][T][H], state [B][H][dk][dv].
+__global__ __launch_bounds__(256) void k_delta_rule_cols(const float* __restrict__ q, const float* __restrict__ k,
+                                                         const float* __restrict__ v, const float* __restrict__ beta,
+                                                         const float* __restrict__ g, float* __restrict__ state,
+                                                         float* __restrict__ out, int T, int H, int waves) {
+    const int lane = threadIdx.x & (kWave - 1), r = lane >> 4, i = lane & 15;
+    const int gw = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    if (gw >= waves) return;
+    constexpr int kGroups = kDV / 4;
+    const int col = 4 * (gw % kGroups) + r, bh = gw / kGroups, h = bh % H, b = bh / H;
+    float* S = state + (size_t)bh * kDK * kDV + (size_t)(8 * i) * kDV + col;
+    float s[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) s[j] = S[(size_t)j * kDV];
+    struct In {
+        float4 k0, k1, q0, q1;
+        float v, beta, g;
+    };
+    auto load = [&](int n, In& x) {
         const size_t bth = ((size_t)b * T + n) * H + h;
-        __syncthreads();  // previous token's readers of sh are done
-        if (t < 128) sh.q[t] = q[bth * kDK + t];
-        else if (t < 256) sh.k[t - 128] = k[bth * kDK + t - 128];
-        else if (t < 384) sh.v[t - 256] = v[bth * kDV + t - 256];
-        if (t == 0) { sh.g = g[bth]; sh.beta = beta[bth]; }
-        __syncthreads();
-        if (w == 0) {
-            float p = sh.k[lane] * sh.q[lane] + sh.k[lane + 64] * sh.q[lane + 64];
-            p = wave_sum(p);
-            if (lane == 0) sh.kq = p;
+        const float4* kp = (const float4*)(k + bth * kDK + 8 * i);
+        const float4* qp = (const float4*)(q + bth * kDK + 8 * i);
+        x.k0 = kp[0]; x.k1 = kp[1];
+        x.q0 = qp[0]; x.q1 = qp[1];
+        x.v = v[bth * kDV + col];
+        x.beta = beta[bth];
+        x.g = g[bth];
+    };
+    // kAhead tokens' inputs in flight in a register ring used in place (no copies, which would
+    // make each token wait for the next one's loads); slot d is refilled after its token ran
+    constexpr int kAhead = 4;
+    In ring[kAhead];
+#pragma unroll
+    for (int d = 0; d < kAhead; d++)
+        if (d < T) load(d, ring[d]);
+    for (int n0 = 0; n0 < T; n0 += kAhead) {
+#pragma unroll
+        for (int d = 0; d < kAhead; d++) {
+            const int n = n0 + d;
+            if (n >= T) break;
+            In& cur = ring[d];
+            const float kk[8] = {cur.k0.x, cur.k0.y, cur.k0.z, cur.k0.w, cur.k1.x, cur.k1.y, cur.k1.z, cur.k1.w};
+            const float qq[8] = {cur.q0.x, cur.q0.y, cur.q0.z, cur.q0.w, cur.q1.x, cur.q1.y, cur.q1.z, cur.q1.w};
+            const float vv = cur.v, bb = cur.beta, gg = cur.g;
+            if (n + kAhead < T) load(n + kAhead, cur);
+            float sk = 0.0f, sq = 0.0f, kq = 0.0f;
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                sk = fmaf(s[j], kk[j], sk);
+                sq = fmaf(s[j], qq[j], sq);
+                kq = fmaf(kk[j], qq[j], kq);
+            }
+            sk = row16_sum(sk);
+            sq = row16_sum(sq);
+            kq = row16_sum(kq);
+            const float dv = bb * (vv - gg * sk);
+#pragma unroll
+            for (int j = 0; j < 8; j++) s[j] = fmaf(gg, s[j], kk[j] * dv);
+            if (i == 0) out[(((size_t)b * T + n) * H + h) * kDV + col] = fmaf(gg, sq, dv * kq);
         }
-        __syncthreads();
-        const float o = delta_token(s, sh, col, qq);
-        if (qq == 0) out[bth * kDV + col] = o;
     }
-    store_tile(s, S, col, qq);
+#pragma unroll
+    for (int j = 0; j < 8; j++) S[(size_t)j * kDV] = s[j];
 }
 
 void launch_gdn_decode(const float* proj, float* conv_state, const float* conv_w, float* state, float* out,
@@ -200,8 +248,9 @@ void launch_delta_rule(const float* q, const float* k, const float* v, const flo
 
 void launch_delta_rule_chunked(const float* q, const float* k, const float* v, const float* beta, const float* g,
                                float* state, float* out, int batch, int tokens, int heads, hipStream_t st) {
-    hipLaunchKernelGGL(k_delta_rule_seq, dim3(heads, batch), dim3(kGdnThreads), 0, st, q, k, v, beta, g, state, out,
-                       tokens, heads);
+    const int waves = batch * heads * (kDV / 4);
+    hipLaunchKernelGGL(k_delta_rule_cols, dim3((waves + 3) / 4), dim3(256), 0, st, q, k, v, beta, g, state, out, tokens,
+                       heads, waves);
 }
 
 }  // namespace qne
