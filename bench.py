@@ -214,6 +214,81 @@ def bench_gdn(args) -> dict:
             "detail": {"step": steps, "prefill_b4_t2048": pre}, "cpu_baseline": None}
 
 
+def bench_batch(args) -> dict:
+    """Batched continuous decode on the 2B-shaped int4 model: `--batch` sequences (64) with contexts
+    uniform in [256, 4096) on the paged KV cache, all advancing one greedy token per step (each
+    row's pick fed back on the device). KV contents and recurrent state are pseudo-random (a fill
+    kernel), so no prefill is needed. Algorithmic bytes per step: every weight once (the embedding:
+    one row per sequence), each sequence's K and V over its attended positions, GDN and conv state
+    read and written per sequence. MFMA work: every GEMM runs two f16 MFMA passes (x split into hi
+    and lo halves) over 64 rows."""
+    import qne
+    import weights as W
+    cfg = W.full_config("2b")
+    t = time.perf_counter()
+    index, buf = W.synth_model("2b", seed=args.seed, body="q4", head="f16", group=64)
+    mats = json.loads(index)["matrices"]
+    gen_s = time.perf_counter() - t
+    m = qne.Model.load(index, buf, options={"max_context": 4096, "engine": "graph"})
+    B = args.batch
+    rng = np.random.default_rng(args.seed)
+    ctx = rng.integers(256, 4096 - args.steps - args.warmup - 1, size=B).astype(np.uint32)
+    b = qne.Batch(m, B, 4096)
+    b.fill_synthetic(ctx, seed=args.seed)
+    if args.warmup:
+        b.decode(B, args.warmup)
+    _, pos0 = b.row_state(B)
+    t0 = time.perf_counter()
+    ids = b.decode(B, args.steps)
+    wall = time.perf_counter() - t0
+    dev_ms, dev_steps = b.last_decode_timing()
+    assert dev_steps == args.steps and ids.shape == (args.steps, B)
+    tok_s = B * args.steps / wall
+    # bytes per step: weights once; per sequence its KV (mean position over the window), GDN, conv
+    one = algorithmic_bytes_per_token(cfg, mats, 0.0)
+    embed_row = mats["embed"]["k"] * 2
+    mean_pos = float(pos0.astype(np.float64).mean()) + (args.steps - 1) / 2
+    kv_row = cfg["n_kv_heads"] * cfg["head_dim"] * 2 * 2
+    n_attn = sum(1 for i in range(cfg["layers"]) if (i + 1) % cfg["full_attention_every"] == 0)
+    kv = B * n_attn * kv_row * (mean_pos + 1)
+    weights = one["weights"] - embed_row + one["lm_head"] + B * embed_row
+    per_step = weights + kv + B * (one["gdn_state"] + one["conv_state"])
+    achieved = per_step / (dev_ms / args.steps / 1e3) / 1e9
+    macs = sum(mm["rows"] * mm["k"] for name, mm in mats.items() if name != "embed")
+    mfma_flops = 2 * 2 * 64 * macs  # hi and lo passes over 64 rows
+    mfma_tflops = mfma_flops / (dev_ms / args.steps / 1e3) / 1e12
+    result = {
+        "metric": "batched decode tok/s (64 sequences, 2B int4, ctx U[256,4096]) + % of HBM roofline",
+        "value": round(tok_s, 1), "unit": "tok/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(1e3 * wall / args.steps, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f32 activations, f16 MFMA (x as hi + lo f16), int4 weights", "data": "synthetic",
+        "config": {"workload": f"Qwen3.5-2B-shaped hybrid decoder, int4 g64 body, f16 embed/lm_head, {B} sequences "
+                               f"with contexts uniform in [256, 4096) (mean {float(pos0.mean()):.0f}), one greedy "
+                               f"token per sequence per step", "batch": B, "layers": cfg["layers"]},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None,
+                     "kernel": "batched decode step (HIP graph: GEMMs, GDN, attention)",
+                     "bytes_per_step": int(per_step), "device_ms_per_step": round(dev_ms / args.steps, 4)},
+        "mfma": {"flops_per_step": mfma_flops, "achieved_tflops_over_step": round(mfma_tflops, 1),
+                 "peak_tflops_f16": 2500.0, "frac_over_step": round(mfma_tflops / 2500.0, 4)},
+        "detail": {"bytes_per_step": {"weights": int(weights), "kv": int(kv),
+                                      "gdn_state": int(B * one["gdn_state"]), "conv_state": int(B * one["conv_state"])},
+                   "weights_gen_s": round(gen_s, 2), "adapter": m.adapter},
+    }
+    if not args.no_cpu_baseline:
+        mean_ctx = int(pos0.mean())
+        v, cores = cpu_baseline(index, buf, cfg, mean_ctx, 2)
+        result["cpu_baseline"] = {"value": round(v, 4), "unit": "tok/s", "cores": cores, "kind": "port",
+                                  "sample": f"2 greedy decode steps of one sequence of the same model at context "
+                                            f"{mean_ctx} (the batch's mean; KV cache and GDN state random), oracle C "
+                                            f"restatement, f32, OpenMP; the oracle decodes one sequence at a time"}
+    else:
+        result["cpu_baseline"] = None
+    b.close()
+    m.close()
+    return result
+
+
 def copy_calibration(mib: int) -> None:
     """A plain device-to-device copy of a known size: under a hardware-counter profiler its
     FETCH_SIZE / WRITE_SIZE readings per dispatch, divided into the bytes it must move, give the
@@ -238,8 +313,9 @@ def main():
                          "every decode window a profile sees has the timed length)")
     ap.add_argument("--ctx", type=int, default=4000)
     ap.add_argument("--config", default="2b",
-                    help="2b (the decode benchmark), 0.8b, or the kernel microbenches attn / gdn")
-    ap.add_argument("--batch", type=int, default=64, help="sequences (--config attn)")
+                    help="2b (the decode benchmark), 0.8b, batch (64-sequence batched decode), or the kernel "
+                         "microbenches attn / gdn")
+    ap.add_argument("--batch", type=int, default=64, help="sequences (--config attn / batch)")
     ap.add_argument("--cpu-tokens", type=int, default=4)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--seed", type=int, default=0)
@@ -255,6 +331,9 @@ def main():
     if args.config in ("attn", "gdn"):
         sys.path[:0] = [str(ROOT / "qwen-native-engine_amd")]
         print(json.dumps(bench_paged_attention(args) if args.config == "attn" else bench_gdn(args)))
+        return
+    if args.config == "batch":
+        print(json.dumps(bench_batch(args)))
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this engine runs batch-1 decode on one GPU; --gpus above 1 is not supported "

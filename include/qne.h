@@ -135,6 +135,46 @@ int qne_paged_attn_decode(const float* q, const float* k_new, const float* v_new
                           const int32_t* ctx, float* out, int batch, int nq, int nkv,
                           void* stream);
 
+/* The batched form of gemv for m (1..64) rows of x: y[r] = W x[r] for r < m, on f16 MFMA (x split
+ * into two f16 halves, so the products keep about 22 bits), with the same norm prologue and
+ * epilogues as qne_gemv. The reference's 16-token GEMM (kernels/src/batch.rs:12-99, Gpu::gemm
+ * lib.rs:341-347) with M up to 64. x rows at x + r * x_stride (x_stride >= k, a multiple of 4), y
+ * rows at y + r * y_stride. k must be a multiple of 64 and q4 groups a multiple of 64. On the null
+ * stream the call returns when the result is ready. The split partials' scratch is kept per device
+ * (grown when a call needs more): calls that overlap on one device must not be issued. */
+int qne_gemm(int kind, const void* w, const void* sz, int rows, int k, int group, const float* x,
+             int x_stride, int m, const float* norm, float eps, float* y, int y_stride, int epilogue,
+             void* stream);
+
+/* ---- batched continuous decode ----
+ * Up to 64 sequences ("rows") advance one token per step through one loaded model's weights, each
+ * row with its own paged KV cache and recurrent state. The reference decodes one sequence at a
+ * time (Model::step / decode, kernels/src/model.rs:372-449); a row here follows exactly that step.
+ * A batch holds the model's weights: free every batch before the model. */
+typedef struct qne_batch qne_batch;
+int qne_batch_create(qne_model* m, uint32_t max_rows, uint32_t max_context, qne_batch** out);
+int qne_batch_free(qne_batch* b);
+/* Row `row` takes over the model's current sequence (after qne_prefill / qne_decode): its KV cache,
+ * recurrent state and next (token, position) as qne_last_token reports them. */
+int qne_batch_admit(qne_batch* b, uint32_t row);
+/* Row `row` becomes an empty sequence at position 0 whose next token is `token`. */
+int qne_batch_reset_row(qne_batch* b, uint32_t row, uint32_t token);
+/* The next token and position of rows 0..n-1 (either pointer may be null). */
+int qne_batch_row_state(qne_batch* b, uint32_t n, uint32_t* tokens, uint32_t* pos);
+/* One step of rows 0..n-1. `tokens` (n entries, may be null) replaces the rows' next tokens first.
+ * `next` (n entries, may be null) receives each row's greedy pick; `logits` (may be null) the
+ * rows' logits, n * vocab floats. Each row's next token becomes its pick, its position advances. */
+int qne_batch_step(qne_batch* b, uint32_t n, const uint32_t* tokens, uint32_t* next, float* logits,
+                   size_t logits_cap);
+/* `steps` greedy steps of rows 0..n-1 chained on the device; out[s * n + r] = pick of row r at
+ * step s (out may be null). */
+int qne_batch_decode(qne_batch* b, uint32_t n, uint32_t steps, uint32_t* out, size_t cap);
+/* Benchmark set-up: rows 0..n-1 get pseudo-random KV contents and recurrent state, random next
+ * tokens and positions ctx[r]. */
+int qne_batch_fill_synthetic(qne_batch* b, uint32_t n, const uint32_t* ctx, uint64_t seed);
+/* Device time (ms) and step count of the last qne_batch_decode. */
+int qne_batch_last_decode_timing(qne_batch* b, double* ms, size_t* steps);
+
 /* ---- synthetic weights (seeded generator used by the benches and tests) ---- */
 /* value[i] = std * N(0,1) from SplitMix64 + Box-Muller on a counter keyed by (seed, stream). */
 int qne_synth_normal_f32(uint64_t seed, uint64_t stream, size_t n, float std, float* out);

@@ -10,6 +10,7 @@
 #include <vector>
 
 #include "../../include/qne.h"
+#include "batch.hpp"
 #include "error.hpp"
 #include "hip_util.hpp"
 #include "index.hpp"
@@ -18,6 +19,12 @@
 
 struct qne_model {
     qne::Model* m;
+    int batches;  // live qne_batch objects that use this model's weights
+};
+
+struct qne_batch {
+    qne::BatchDecoder* b;
+    qne_model* owner;
 };
 
 namespace {
@@ -55,17 +62,20 @@ void need(bool ok, const char* what) {
 
 void check_launch() { qne::hip_check(hipGetLastError(), "kernel launch"); }
 
-// Scratch of the paged-attention partials, kept per device and grown on demand (held until the
-// process ends), so that a call allocates only when it needs more than any call before it on that
-// device. Calls that overlap on one device share it.
-float* attn_workspace(size_t bytes) {
+// Scratch of the kernel-level entry points (slot 0: paged-attention partials, slot 1: GEMM split
+// partials), kept per device and grown on demand (held until the process ends), so that a call
+// allocates only when it needs more than any call before it on that device. Calls of one entry
+// point that overlap on one device share it.
+enum { kWsAttention = 0, kWsGemm = 1, kWsSlots = 2 };
+float* workspace(int slot, size_t bytes) {
     static std::mutex mu;
     static std::vector<std::pair<void*, size_t>> per_dev;
     int dev = 0;
     QNE_HIP(hipGetDevice(&dev));
     std::lock_guard<std::mutex> lock(mu);
-    if ((int)per_dev.size() <= dev) per_dev.resize(dev + 1, {nullptr, 0});
-    auto& w = per_dev[dev];
+    const size_t i = (size_t)dev * kWsSlots + slot;
+    if (per_dev.size() <= i) per_dev.resize(i + 1, {nullptr, 0});
+    auto& w = per_dev[i];
     if (w.second < bytes) {
         QNE_HIP(hipDeviceSynchronize());  // a smaller buffer may still be in use by an earlier call
         if (w.first) (void)hipFree(w.first);
@@ -93,13 +103,14 @@ int qne_model_load(const char* index_json, size_t index_len, const void* weights
         qne::ModelIndex ix = qne::parse_index(index_json, index_len, weights_len);
         qne::LoadOptions opt = qne::parse_options(options_json);
         qne::Model* m = new qne::Model(ix, (const uint8_t*)weights, weights_len, opt);
-        *out = new qne_model{m};
+        *out = new qne_model{m, 0};
     });
 }
 
 int qne_model_free(qne_model* m) {
     return guard([&] {
         if (!m) return;
+        need(m->batches == 0, "the model still has live batches (free them first)");
         delete m->m;
         delete m;
     });
@@ -274,12 +285,111 @@ int qne_paged_attn_decode(const float* q, const float* k_new, const float* v_new
         if (splits > max_blocks) splits = max_blocks;
         const size_t parts = (size_t)batch * nkv * splits * G;
         hipStream_t st = (hipStream_t)stream;
-        float* ws = attn_workspace(parts * 258 * 4);
+        float* ws = workspace(kWsAttention, parts * 258 * 4);
         qne::launch_paged_attn(q, k_new, v_new, (uint16_t*)k_pool, (uint16_t*)v_pool, block_table, max_blocks, ctx,
                                out, batch, nq, nkv, ws, ws + parts * 2, splits, st);
         check_launch();
         // the null stream keeps the call synchronous; on a caller's stream it is ordered like a kernel
         if (!stream) qne::hip_check(hipStreamSynchronize(st), "paged attention");
+    });
+}
+
+int qne_gemm(int kind, const void* w, const void* sz, int rows, int k, int group, const float* x, int x_stride, int m,
+             const float* norm, float eps, float* y, int y_stride, int epilogue, void* stream) {
+    return guard([&] {
+        need(kind == QNE_MAT_F16 || kind == QNE_MAT_Q4, "unknown matrix kind");
+        need(w && x && y && rows > 0, "null or empty argument");
+        need(kind == QNE_MAT_F16 || sz, "q4 needs sz");
+        need(epilogue >= QNE_EPI_STORE && epilogue <= QNE_EPI_SWIGLU, "unknown epilogue");
+        need(epilogue != QNE_EPI_SWIGLU || rows % 2 == 0, "SwiGlu needs an even row count");
+        need(qne::gemm_shape_ok(kind, rows, k, group, m), "unsupported shape (m 1..64, k a multiple of 64, q4 group a multiple of 64)");
+        const int n_out = epilogue == QNE_EPI_SWIGLU ? rows / 2 : rows;
+        need(x_stride >= k && x_stride % 4 == 0, "x_stride must be >= k and a multiple of 4");
+        need(y_stride >= n_out, "y_stride must be >= the output count");
+        qne::GemmArgs a;
+        a.x = x;
+        a.x_stride = x_stride;
+        a.m = m;
+        a.gain = norm;
+        a.eps = eps;
+        a.kind = kind;
+        a.W = w;
+        a.SZ = (const uint32_t*)sz;
+        a.N = rows;
+        a.K = k;
+        a.group = kind == QNE_MAT_Q4 ? group : 64;
+        a.splits = qne::gemm_splits(kind, rows, k, a.group);
+        a.epi = epilogue;
+        a.y = y;
+        a.y_stride = y_stride;
+        a.n_out = n_out;
+        const size_t part = (size_t)a.splits * 64 * rows, ssp = (size_t)a.splits * 64;
+        float* ws = workspace(kWsGemm, (part + ssp) * 4);
+        a.part = ws;
+        a.ss_part = ws + part;
+        hipStream_t st = (hipStream_t)stream;
+        qne::launch_gemm(a, st);
+        check_launch();
+        if (!stream) qne::hip_check(hipStreamSynchronize(st), "gemm");
+    });
+}
+
+namespace {
+qne::BatchDecoder& batch(qne_batch* b) {
+    if (!b || !b->b) throw qne::Error(QNE_EINVAL, "null batch handle");
+    return *b->b;
+}
+}  // namespace
+
+int qne_batch_create(qne_model* m, uint32_t max_rows, uint32_t max_context, qne_batch** out) {
+    return guard([&] {
+        need(out != nullptr, "null argument");
+        *out = nullptr;
+        qne::BatchDecoder* b = new qne::BatchDecoder(model(m), (int)max_rows, (int)max_context);
+        *out = new qne_batch{b, m};
+        m->batches++;
+    });
+}
+
+int qne_batch_free(qne_batch* b) {
+    return guard([&] {
+        if (!b) return;
+        delete b->b;
+        if (b->owner) b->owner->batches--;
+        delete b;
+    });
+}
+
+int qne_batch_admit(qne_batch* b, uint32_t row) { return guard([&] { batch(b).admit((int)row); }); }
+
+int qne_batch_reset_row(qne_batch* b, uint32_t row, uint32_t token) {
+    return guard([&] { batch(b).reset_row((int)row, token); });
+}
+
+int qne_batch_row_state(qne_batch* b, uint32_t n, uint32_t* tokens, uint32_t* pos) {
+    return guard([&] { batch(b).row_state((int)n, tokens, pos); });
+}
+
+int qne_batch_step(qne_batch* b, uint32_t n, const uint32_t* tokens, uint32_t* next, float* logits, size_t logits_cap) {
+    return guard([&] { batch(b).step((int)n, tokens, next, logits, logits_cap); });
+}
+
+int qne_batch_decode(qne_batch* b, uint32_t n, uint32_t steps, uint32_t* out, size_t cap) {
+    return guard([&] { batch(b).decode((int)n, (int)steps, out, cap); });
+}
+
+int qne_batch_fill_synthetic(qne_batch* b, uint32_t n, const uint32_t* ctx, uint64_t seed) {
+    return guard([&] {
+        need(ctx != nullptr, "null ctx");
+        batch(b).fill_synthetic((int)n, ctx, seed);
+    });
+}
+
+int qne_batch_last_decode_timing(qne_batch* b, double* ms, size_t* steps) {
+    return guard([&] {
+        need(ms && steps, "null argument");
+        *ms = batch(b).last_ms();
+        *steps = batch(b).last_steps();
     });
 }
 

@@ -1,0 +1,82 @@
+// Batched continuous decode: up to 64 sequences ("rows") advance one token per step through the
+// weights of a loaded Model, each row with its own paged KV cache and recurrent state.
+//
+// The reference decodes one sequence at a time (kernels/src/model.rs:372-449) and batches only the
+// 16-token prefill GEMM (kernels/src/batch.rs:12-99); this object applies that GEMM form across
+// sequences so the weights are read once per step for every row.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <map>
+#include <vector>
+
+#include "model.hpp"
+
+namespace qne {
+
+class BatchDecoder {
+  public:
+    BatchDecoder(Model& m, int max_rows, int max_context);
+    ~BatchDecoder();
+    BatchDecoder(const BatchDecoder&) = delete;
+    BatchDecoder& operator=(const BatchDecoder&) = delete;
+
+    int max_rows() const { return max_rows_; }
+    int max_context() const { return max_context_; }
+    // Row `row` takes over the model's current sequence: its KV cache and recurrent state, and its
+    // next (token, position) as reported by Model::last_token.
+    void admit(int row);
+    // Row `row` becomes an empty sequence (position 0, zero state) whose next token is `token`.
+    void reset_row(int row, uint32_t token);
+    // The next (token, position) of rows 0..n-1.
+    void row_state(int n, uint32_t* tokens, uint32_t* pos);
+    // One step of rows 0..n-1. With `tokens` set, those tokens replace the rows' next tokens first.
+    // Writes each row's greedy pick to `next` (n entries) and, when `logits` is set, the rows'
+    // logits (n * vocab floats). Every row's next token becomes its pick and its position advances.
+    void step(int n, const uint32_t* tokens, uint32_t* next, float* logits, size_t logits_cap);
+    // `steps` greedy steps of rows 0..n-1 chained on the device; out[s * n + r] = pick of row r at
+    // step s.
+    void decode(int n, int steps, uint32_t* out, size_t cap);
+    // Benchmark set-up: rows 0..n-1 get pseudo-random KV contents and recurrent state, random next
+    // tokens, and positions ctx[r].
+    void fill_synthetic(int n, const uint32_t* ctx, uint64_t seed);
+    double last_ms() const { return last_ms_; }
+    size_t last_steps() const { return last_steps_; }
+
+  private:
+    void release();
+    void* dalloc(size_t bytes);
+    void enqueue_step(int n);
+    hipGraphExec_t graph_for(int n);
+    void check_row(int row) const;
+    void sync();
+
+    Model& m_;
+    int max_rows_, max_context_, max_blocks_;
+    hipStream_t stream_ = nullptr;
+    std::vector<void*> allocations_;
+    std::map<int, hipGraphExec_t> graphs_;
+    hipEvent_t ev0_ = nullptr, ev1_ = nullptr;
+
+    // per layer: rows x state
+    std::vector<float*> conv_, rec_;
+    std::vector<uint16_t*> kpool_, vpool_;
+    size_t conv_floats_ = 0, rec_floats_ = 0, pool_block_elems_ = 0;
+    int32_t* block_table_ = nullptr;  // [max_rows][max_blocks]
+    std::vector<int32_t> bt_host_;
+
+    // activations [64][...]
+    int proj_w_ = 0, mixed_w_ = 0;
+    float *h_ = nullptr, *proj_ = nullptr, *mixed_ = nullptr, *act_ = nullptr, *logits_ = nullptr, *qbuf_ = nullptr;
+    float *part_ = nullptr, *ss_part_ = nullptr, *attn_ml_ = nullptr, *attn_acc_ = nullptr;
+    size_t attn_part_rows_ = 0;  // rows * splits the attention partials hold
+    uint32_t *tokens_ = nullptr, *picks_ = nullptr, *ids_ = nullptr;
+    int32_t* pos_ = nullptr;
+    uint32_t* host_u32_ = nullptr;  // pinned, 2 * 64 entries
+    double last_ms_ = 0.0;
+    size_t last_steps_ = 0;
+};
+
+}  // namespace qne

@@ -65,6 +65,27 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_prep(AttnModelArgs a) {
     }
 }
 
+// Batched model form, grid (nq + nkv, rows): row b reads its projection at proj + b * proj_stride,
+// sits at position pos[b] and appends into its own block table row.
+__global__ __launch_bounds__(kAttnThreads) void k_attn_prep_rows(AttnRowsArgs a) {
+    __shared__ float sh[kHD];
+    __shared__ float red[16];
+    const int t = threadIdx.x, hb = blockIdx.x, b = blockIdx.y;
+    const uint32_t pos = (uint32_t)a.pos[b];
+    const float* proj = a.proj + (size_t)b * a.proj_stride;
+    if (hb < a.nq) {
+        const float x = proj[hb * kHD + t];
+        a.qbuf[((size_t)b * a.nq + hb) * kHD + t] = norm_rope(x, a.norms, a.inv_freq, a.rope_dim, pos, sh, red);
+    } else {
+        const int g = hb - a.nq;
+        const float* kp = proj + 2 * a.nq * kHD;
+        const float kr = norm_rope(kp[g * kHD + t], a.norms + kHD, a.inv_freq, a.rope_dim, pos, sh, red);
+        const size_t at = kv_index(a.block_table + (size_t)b * a.max_blocks, (int)pos, a.nkv, g) + t;
+        a.k_pool[at] = f2h(kr);
+        a.v_pool[at] = f2h(kp[a.nkv * kHD + g * kHD + t]);
+    }
+}
+
 // Raw form: append k_new / v_new of sequence blockIdx.y, kv head blockIdx.x at ctx[b].
 __global__ __launch_bounds__(kAttnThreads) void k_kv_append(const float* __restrict__ k_new, const float* __restrict__ v_new,
                                                             uint16_t* __restrict__ k_pool, uint16_t* __restrict__ v_pool,
@@ -193,7 +214,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_partial(const float* __re
 // sigmoid(gate) (shaders.rs:626-629).
 __global__ __launch_bounds__(kAttnThreads) void k_attn_combine(const float* __restrict__ part_ml, const float* __restrict__ part_acc,
                                                                int nkv, int G, int splits, const float* __restrict__ gate,
-                                                               float* __restrict__ out) {
+                                                               int gate_stride, float* __restrict__ out) {
     const int h = blockIdx.x, b = blockIdx.y, t = threadIdx.x, g = h / G, gi = h % G, nq = nkv * G;
     float mn = -INFINITY;
     for (int s = 0; s < splits; s++) mn = fmaxf(mn, part_ml[((((size_t)b * nkv + g) * splits + s) * G + gi) * 2]);
@@ -207,7 +228,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_combine(const float* __re
         a += part_acc[i * kHD + t] * c;
     }
     float o = a / lsum;
-    if (gate) o = o / (1.0f + expf(-gate[h * kHD + t]));
+    if (gate) o = o / (1.0f + expf(-gate[(size_t)b * gate_stride + h * kHD + t]));
     out[((size_t)b * nq + h) * kHD + t] = o;
 }
 
@@ -234,7 +255,16 @@ void launch_attention_model(const AttnModelArgs& a, hipStream_t st) {
     partial_by_g(G, a.qbuf, a.k_pool, a.v_pool, a.block_table, a.max_blocks, (const int32_t*)(a.tok + 1), a.nkv,
                  a.part_ml, a.part_acc, a.splits, 1, st);
     hipLaunchKernelGGL(k_attn_combine, dim3(a.nq, 1), dim3(kAttnThreads), 0, st, a.part_ml, a.part_acc, a.nkv, G,
-                       a.splits, a.proj + a.nq * kHD, a.out);
+                       a.splits, a.proj + a.nq * kHD, 0, a.out);
+}
+
+void launch_attention_rows(const AttnRowsArgs& a, hipStream_t st) {
+    hipLaunchKernelGGL(k_attn_prep_rows, dim3(a.nq + a.nkv, a.rows), dim3(kAttnThreads), 0, st, a);
+    const int G = a.nq / a.nkv;
+    partial_by_g(G, a.qbuf, a.k_pool, a.v_pool, a.block_table, a.max_blocks, a.pos, a.nkv, a.part_ml, a.part_acc,
+                 a.splits, a.rows, st);
+    hipLaunchKernelGGL(k_attn_combine, dim3(a.nq, a.rows), dim3(kAttnThreads), 0, st, a.part_ml, a.part_acc, a.nkv, G,
+                       a.splits, a.proj + a.nq * kHD, (int)a.proj_stride, a.out);
 }
 
 void launch_paged_attn(const float* q, const float* k_new, const float* v_new, uint16_t* k_pool, uint16_t* v_pool,
@@ -245,7 +275,7 @@ void launch_paged_attn(const float* q, const float* k_new, const float* v_new, u
     const int G = nq / nkv;
     partial_by_g(G, q, k_pool, v_pool, block_table, max_blocks, ctx, nkv, part_ml, part_acc, splits, batch, st);
     hipLaunchKernelGGL(k_attn_combine, dim3(nq, batch), dim3(kAttnThreads), 0, st, part_ml, part_acc, nkv, G, splits,
-                       (const float*)nullptr, out);
+                       (const float*)nullptr, 0, out);
 }
 
 }  // namespace qne

@@ -75,9 +75,15 @@ __device__ __forceinline__ void store_tile_t(const float (&s)[32], float* S, int
 // proj = [q(H*dk) k(H*dk) v(H*dv) z(H*dv) a(H) b(H)], prm = [dt_bias(H) A_neg_exp(H) norm_w(dv)].
 __global__ __launch_bounds__(kGdnThreads) void k_gdn_decode(const float* __restrict__ proj, float* __restrict__ conv_state,
                                                             const float* __restrict__ conv_w, float* __restrict__ state,
-                                                            float* __restrict__ out, const float* __restrict__ prm, int H) {
+                                                            float* __restrict__ out, const float* __restrict__ prm, int H,
+                                                            GdnRowStrides rs) {
     __shared__ DeltaShared sh;
     const int h = blockIdx.x, t = threadIdx.x, lane = t % kWave, w = t / kWave;
+    // row blockIdx.y of a batch: its own projection, conv and recurrent state, output
+    proj += (size_t)blockIdx.y * rs.proj;
+    conv_state += (size_t)blockIdx.y * rs.conv;
+    state += (size_t)blockIdx.y * rs.state;
+    out += (size_t)blockIdx.y * rs.out;
     const int col = t & (kDV - 1), qq = t >> 7;
     float* S = state + (size_t)h * kDK * kDV;
     float s[32];
@@ -238,7 +244,13 @@ __global__ __launch_bounds__(256) void k_delta_rule_cols(const float* __restrict
 void launch_gdn_decode(const float* proj, float* conv_state, const float* conv_w, float* state, float* out,
                        const float* prm, int heads, hipStream_t st) {
     hipLaunchKernelGGL(k_gdn_decode, dim3(heads), dim3(kGdnThreads), 0, st, proj, conv_state, conv_w, state, out, prm,
-                       heads);
+                       heads, GdnRowStrides{});
+}
+
+void launch_gdn_decode_rows(const float* proj, float* conv_state, const float* conv_w, float* state, float* out,
+                            const float* prm, int heads, int rows, const GdnRowStrides& rs, hipStream_t st) {
+    hipLaunchKernelGGL(k_gdn_decode, dim3(heads, rows), dim3(kGdnThreads), 0, st, proj, conv_state, conv_w, state, out,
+                       prm, heads, rs);
 }
 
 void launch_delta_rule(const float* q, const float* k, const float* v, const float* beta, const float* g, float* state,

@@ -31,6 +31,9 @@ bool launch_gemv(int kind, const void* W, const uint32_t* SZ, int rows, int k, i
 // tok[0] = ids[i], tok[1] = pos.
 void launch_set_tok(uint32_t* tok, const uint32_t* ids, int i, uint32_t pos, hipStream_t st);
 
+// Pseudo-random uniform [-amp, amp) fill of n f16 or f32 values (benchmark state).
+void launch_fill_uniform(void* p, size_t n, bool f16, uint64_t seed, float amp, hipStream_t st);
+
 // Embedding row tok[0] -> h (f32). kind 0: f16 [V][H]; kind 1: q4.
 void launch_embed(int kind, const void* W, const uint32_t* SZ, int group, int hidden, const uint32_t* tok,
                   float* h, hipStream_t st);
@@ -63,6 +66,65 @@ struct AttnModelArgs {
     int max_blocks;         // entries of block_table
 };
 void launch_attention_model(const AttnModelArgs& a, hipStream_t st);
+// Batched model form: row b (one sequence) has its projection at proj + b * proj_stride, position
+// pos[b] and block table row b; outputs [rows][nq * hd].
+struct AttnRowsArgs {
+    const float* proj;
+    size_t proj_stride;
+    const float* norms;
+    const float* inv_freq;
+    uint16_t* k_pool;
+    uint16_t* v_pool;
+    const int32_t* block_table;  // [rows][max_blocks]
+    const int32_t* pos;          // [rows]
+    float* qbuf;                 // [rows][nq][hd]
+    float* part_ml;              // [rows][nkv][splits][group][2]
+    float* part_acc;             // [rows][nkv][splits][group][hd]
+    float* out;                  // [rows][nq][hd]
+    int nq, nkv, rope_dim, splits, max_blocks, rows;
+};
+void launch_attention_rows(const AttnRowsArgs& a, hipStream_t st);
+
+// Per-row strides (in floats) of the batched GDN decode step.
+struct GdnRowStrides {
+    size_t proj = 0, conv = 0, state = 0, out = 0;
+};
+void launch_gdn_decode_rows(const float* proj, float* conv_state, const float* conv_w, float* state, float* out,
+                            const float* prm, int heads, int rows, const GdnRowStrides& rs, hipStream_t st);
+
+// y = x W^T for up to 64 rows of x (batched decode), on MFMA. Rows of x are f32 at x + r * x_stride;
+// with `gain` x is RMSNormed (gain, eps) first. Epilogues as the GEMV (store, residual add, SwiGLU
+// with n_out = N / 2). `part` / `ss_part` hold splits * 64 * N and splits * 64 floats.
+struct GemmArgs {
+    const float* x = nullptr;
+    int x_stride = 0;
+    int m = 0;
+    const float* gain = nullptr;
+    float eps = 1e-6f;
+    int kind = KIND_Q4;
+    const void* W = nullptr;
+    const uint32_t* SZ = nullptr;
+    int N = 0, K = 0, group = 64;
+    int splits = 1;
+    int gps = 0;         // set by launch_gemm
+    int direct = 0;      // set by launch_gemm: the GEMM applies the epilogue itself
+    float* part = nullptr;
+    float* ss_part = nullptr;
+    int epi = EPI_STORE;
+    float* y = nullptr;
+    int y_stride = 0;
+    int n_out = 0;
+};
+int gemm_splits(int kind, int N, int K, int group);
+bool gemm_shape_ok(int kind, int N, int K, int group, int m);
+void launch_gemm(GemmArgs a, hipStream_t st);
+// h[r] = embedding row tokens[r], r < m.
+void launch_embed_rows(int kind, const void* W, const uint32_t* SZ, int group, int hidden, const uint32_t* tokens, int m,
+                       float* h, hipStream_t st);
+// Greedy pick per row into out[r]; with `tokens`, also tokens[r] = pick and pos[r] += 1.
+void launch_argmax_rows(const float* logits, int m, int V, uint32_t* out, uint32_t* tokens, int32_t* pos,
+                        hipStream_t st);
+
 // Raw paged decode for `batch` sequences: append k/v at ctx[b], attend over 0..ctx[b].
 void launch_paged_attn(const float* q, const float* k_new, const float* v_new, uint16_t* k_pool, uint16_t* v_pool,
                        const int32_t* block_table, int max_blocks, const int32_t* ctx, float* out, int batch, int nq,

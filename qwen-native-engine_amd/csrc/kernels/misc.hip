@@ -28,6 +28,26 @@ __global__ void k_set_tok(uint32_t* __restrict__ tok, const uint32_t* __restrict
     tok[1] = pos;
 }
 
+// Pseudo-random fill for benchmark state: value i is uniform in [-amp, amp) from a SplitMix64 hash
+// of (seed, i).
+__global__ void k_fill_uniform(void* __restrict__ p, size_t n, int f16, uint64_t seed, float amp) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
+        uint64_t z = seed + (i + 1) * 0x9E3779B97F4A7C15ull;
+        z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+        z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+        z ^= z >> 31;
+        const float v = ((float)(z >> 40) * (1.0f / 8388608.0f) - 1.0f) * amp;
+        if (f16) ((uint16_t*)p)[i] = f2h(v);
+        else ((float*)p)[i] = v;
+    }
+}
+
+void launch_fill_uniform(void* p, size_t n, bool f16, uint64_t seed, float amp, hipStream_t st) {
+    if (n == 0) return;
+    const size_t blocks = std::min<size_t>((n + 255) / 256, 8192);
+    hipLaunchKernelGGL(k_fill_uniform, dim3((unsigned)blocks), dim3(256), 0, st, p, n, f16 ? 1 : 0, seed, amp);
+}
+
 void launch_set_tok(uint32_t* tok, const uint32_t* ids, int i, uint32_t pos, hipStream_t st) {
     hipLaunchKernelGGL(k_set_tok, dim3(1), dim3(1), 0, st, tok, ids, i, pos);
 }

@@ -239,6 +239,7 @@ void Model::alloc_state() {
     }
     block_table_ = (int32_t*)dalloc(blocks * 4);
     QNE_HIP(hipMemcpy(block_table_, bt.data(), blocks * 4, hipMemcpyHostToDevice));
+    bt_host_ = bt;
 
     size_t proj = (size_t)std::max(c.attn_proj(), c.gdn_proj());
     size_t mixed = (size_t)std::max(c.attn_out(), c.gdn_out());

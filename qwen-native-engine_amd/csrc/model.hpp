@@ -83,6 +83,7 @@ class Model {
     uint32_t max_context() const { return (uint32_t)max_context_; }
 
   private:
+    friend class BatchDecoder;
     void release();
     void upload(const ModelIndex& ix, const uint8_t* weights);
     void alloc_state();
@@ -120,6 +121,7 @@ class Model {
     uint32_t *am_idx_ = nullptr, *tok_ = nullptr, *tok_backup_ = nullptr, *ids_ = nullptr, *out_ids_ = nullptr;
     unsigned* am_counter_ = nullptr;
     int32_t* block_table_ = nullptr;
+    std::vector<int32_t> bt_host_;  // host copy of block_table_
     int attn_splits_ = 1;
     uint32_t* host_tok_ = nullptr;  // pinned
     float* host_logits_ = nullptr;  // pinned

@@ -65,6 +65,16 @@ def load_library(path: str | os.PathLike | None = None):
         "qne_gdn_step": ([c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_i, c_i, c_p], c_i),
         "qne_gdn_prefill_chunked": ([c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_i, c_i, c_i, c_p], c_i),
         "qne_paged_attn_decode": ([c_p, c_p, c_p, c_p, c_p, c_p, c_i, c_p, c_p, c_i, c_i, c_i, c_p], c_i),
+        "qne_gemm": ([c_i, c_p, c_p, c_i, c_i, c_i, c_p, c_i, c_i, c_p, c_f, c_p, c_i, c_i, c_p], c_i),
+        "qne_batch_create": ([c_p, c_u32, c_u32, ctypes.POINTER(c_p)], c_i),
+        "qne_batch_free": ([c_p], c_i),
+        "qne_batch_admit": ([c_p, c_u32], c_i),
+        "qne_batch_reset_row": ([c_p, c_u32, c_u32], c_i),
+        "qne_batch_row_state": ([c_p, c_u32, c_p, c_p], c_i),
+        "qne_batch_step": ([c_p, c_u32, c_p, c_p, c_p, c_sz], c_i),
+        "qne_batch_decode": ([c_p, c_u32, c_u32, c_p, c_sz], c_i),
+        "qne_batch_fill_synthetic": ([c_p, c_u32, c_p, ctypes.c_uint64], c_i),
+        "qne_batch_last_decode_timing": ([c_p, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(c_sz)], c_i),
         "qne_synth_normal_f32": ([ctypes.c_uint64, ctypes.c_uint64, c_sz, c_f, c_p], c_i),
         "qne_synth_normal_f16": ([ctypes.c_uint64, ctypes.c_uint64, c_sz, c_f, c_p], c_i),
         "qne_quantize_q4g": ([c_p, c_sz, c_sz, c_sz, c_p, c_p, c_p], c_i),
@@ -219,7 +229,90 @@ class Model:
         return ms.value, n.value
 
 
+class Batch:
+    """Batched continuous decode over one model's weights: rows 0..n-1 each hold a sequence with its
+    own KV cache and recurrent state, and every step advances all of them by one token."""
+
+    def __init__(self, model: Model, max_rows: int, max_context: int):
+        self._lib = model._lib
+        self._model = model  # the weights must outlive the batch
+        h = ctypes.c_void_p()
+        _check(self._lib, self._lib.qne_batch_create(model._h, max_rows, max_context, ctypes.byref(h)))
+        self._h = h
+        self.max_rows = max_rows
+        self.vocab = model.vocab
+
+    def close(self):
+        if self._h:
+            self._lib.qne_batch_free(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()
+
+    def _c(self, rc):
+        _check(self._lib, rc)
+
+    def admit(self, row: int):
+        """Row `row` takes over the model's current sequence (state, next token and position)."""
+        self._c(self._lib.qne_batch_admit(self._h, row))
+
+    def reset_row(self, row: int, token: int):
+        self._c(self._lib.qne_batch_reset_row(self._h, row, token))
+
+    def row_state(self, n: int):
+        t = np.zeros(n, dtype=np.uint32)
+        p = np.zeros(n, dtype=np.uint32)
+        self._c(self._lib.qne_batch_row_state(self._h, n, t.ctypes.data_as(ctypes.c_void_p),
+                                               p.ctypes.data_as(ctypes.c_void_p)))
+        return t, p
+
+    def step(self, n: int, tokens=None, logits: bool = False):
+        """One step of rows 0..n-1; returns (greedy picks, logits [n][vocab] or None)."""
+        nxt = np.zeros(n, dtype=np.uint32)
+        tp = None
+        if tokens is not None:
+            ta, tp = _u32_array(tokens)
+            assert ta.size == n
+        lg = np.zeros((n, self.vocab), dtype=np.float32) if logits else None
+        self._c(self._lib.qne_batch_step(self._h, n, tp, nxt.ctypes.data_as(ctypes.c_void_p),
+                                         lg.ctypes.data_as(ctypes.c_void_p) if logits else None,
+                                         lg.size if logits else 0))
+        return nxt, lg
+
+    def decode(self, n: int, steps: int):
+        """`steps` greedy steps of rows 0..n-1 on the device; returns ids [steps][n]."""
+        out = np.zeros((max(steps, 1), n), dtype=np.uint32)
+        self._c(self._lib.qne_batch_decode(self._h, n, steps, out.ctypes.data_as(ctypes.c_void_p), out.size))
+        return out[:steps]
+
+    def fill_synthetic(self, ctx, seed: int = 0):
+        ca, cp = _u32_array(ctx)
+        self._c(self._lib.qne_batch_fill_synthetic(self._h, ca.size, cp, seed))
+
+    def last_decode_timing(self):
+        ms, n = ctypes.c_double(), ctypes.c_size_t()
+        self._c(self._lib.qne_batch_last_decode_timing(self._h, ctypes.byref(ms), ctypes.byref(n)))
+        return ms.value, n.value
+
+
 # ---- kernel-level entry points on device pointers (ints) ----
+
+def gemm(kind, w, sz, rows, k, group, x, x_stride, m, y, y_stride, epilogue=EPI_STORE, norm=0, eps=1e-6, stream=0):
+    lib = load_library()
+    _check(lib, lib.qne_gemm(kind, w, sz or None, rows, k, group, x, x_stride, m, norm or None, eps, y, y_stride,
+                             epilogue, stream or None))
+
+
 
 def gemv(kind, w, sz, rows, k, group, x, y, epilogue=EPI_STORE, norm=0, eps=1e-6, stream=0):
     lib = load_library()

@@ -1,0 +1,204 @@
+"""Batched decode through the C ABI on the GPU: the M <= 64 MFMA GEMM against the oracle's GEMV row
+by row, and whole batches of sequences against the oracle's single-sequence decode.
+
+The GEMM splits x into two f16 halves (hi + lo) so its products keep about 22 bits; it accumulates
+in f32, so it is held to the GEMV's bar (rel_err < 2e-5 against the f64 oracle). Batched decode is
+held to the model tests' bar: logits within 1e-3 of the oracle, identical greedy ids."""
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+import cpu_oracle as O
+import qne as Q
+import weights as W
+from test_gpu_kernels import f16_matrix, q4_matrix, rel_err, to_dev
+
+pytestmark = pytest.mark.gpu
+dev = torch.device("cuda:0")
+
+
+def oracle_rows(m, X, G, epi, y0, norm):
+    """Row by row with the oracle GEMV (and RMSNorm prologue): the reference's gemm semantics."""
+    out = y0.copy()
+    for r in range(X.shape[0]):
+        x = np.ascontiguousarray(X[r])
+        if norm:
+            xn = np.empty_like(x)
+            O.lib("f64").oc_rmsnorm(O.ptr(x), O.ptr(G), O.ptr(xn), x.size, 1e-6)
+            x = xn
+        O.lib("f64").oc_gemv(ctypes.byref(m), O.ptr(x), O.ptr(out[r]), {0: O.STORE, 1: O.ACCUMULATE, 2: O.SWIGLU}[epi])
+    return out
+
+
+def run_gemm(kind, group, rows, k, M, epi, norm, seed, x_pad=0, y_pad=0):
+    rng = np.random.default_rng(seed)
+    m, w, sz = q4_matrix(rows, k, group, rng) if kind == Q.MAT_Q4 else f16_matrix(rows, k, rng)
+    X = rng.normal(0, 1, size=(M, k + x_pad)).astype(np.float32)
+    G = rng.normal(1, 0.2, size=k).astype(np.float32)
+    n_out = rows // 2 if epi == Q.EPI_SWIGLU else rows
+    Y0 = rng.normal(size=(M, n_out + y_pad)).astype(np.float32)
+    want = Y0.copy()
+    want[:, :n_out] = oracle_rows(m, np.ascontiguousarray(X[:, :k]), G, epi, np.ascontiguousarray(Y0[:, :n_out]), norm)
+    dw, dx, dy, dg = to_dev(w), to_dev(X), to_dev(Y0), to_dev(G)
+    dsz = to_dev(sz) if sz is not None else None
+    Q.gemm(kind, dw.data_ptr(), dsz.data_ptr() if dsz is not None else 0, rows, k, group, dx.data_ptr(), k + x_pad, M,
+           dy.data_ptr(), n_out + y_pad, epi, norm=dg.data_ptr() if norm else 0)
+    torch.cuda.synchronize()
+    return dy.cpu().numpy(), want
+
+
+@pytest.mark.parametrize("k", [512, 2048, 6144])
+@pytest.mark.parametrize("kind,group", [(Q.MAT_Q4, 64), (Q.MAT_Q4, 128), (Q.MAT_F16, 0)])
+@pytest.mark.parametrize("epi", [Q.EPI_STORE, Q.EPI_ACCUMULATE, Q.EPI_SWIGLU])
+@pytest.mark.parametrize("norm", [False, True])
+@pytest.mark.parametrize("M", [1, 7, 64])
+def test_gemm_matches_oracle(k, kind, group, epi, norm, M):
+    rows = 2 * 150 if epi == Q.EPI_SWIGLU else 300  # ragged last tile of 128 rows
+    got, want = run_gemm(kind, group, rows, k, M, epi, norm, seed=k + 7 * epi + 3 * group + norm + 101 * M)
+    err = rel_err(got, want)
+    assert err < 2e-5, err
+
+
+@pytest.mark.parametrize("kind,group", [(Q.MAT_Q4, 64), (Q.MAT_F16, 0)])
+def test_gemm_one_split_direct_epilogue(kind, group):
+    """More than 512 tiles of 128 rows: one split, the GEMM applies 1 / rms and the epilogue itself
+    (the LM head's path)."""
+    got, want = run_gemm(kind, group, 66000, 512, 3, Q.EPI_ACCUMULATE, True, seed=5)
+    assert rel_err(got, want) < 2e-5
+
+
+def test_gemm_strided_rows_untouched_padding():
+    got, want = run_gemm(Q.MAT_Q4, 64, 260, 1024, 5, Q.EPI_STORE, True, seed=9, x_pad=12, y_pad=7)
+    assert rel_err(got, want) < 2e-5
+    assert np.array_equal(got[:, 260:], want[:, 260:])  # columns past the outputs keep their values
+
+
+def test_gemm_row_result_does_not_depend_on_other_rows():
+    """Each row's sum runs in the same order whatever the other rows hold: bitwise equal."""
+    rng = np.random.default_rng(3)
+    rows, k = 640, 2048
+    _, w, sz = q4_matrix(rows, k, 64, rng)
+    X = rng.normal(size=(64, k)).astype(np.float32)
+    dw, dsz = to_dev(w), to_dev(sz)
+    full = torch.zeros((64, rows), dtype=torch.float32, device=dev)
+    one = torch.zeros((1, rows), dtype=torch.float32, device=dev)
+    dx = to_dev(X)
+    Q.gemm(Q.MAT_Q4, dw.data_ptr(), dsz.data_ptr(), rows, k, 64, dx.data_ptr(), k, 64, full.data_ptr(), rows)
+    dx1 = to_dev(X[37:38])
+    Q.gemm(Q.MAT_Q4, dw.data_ptr(), dsz.data_ptr(), rows, k, 64, dx1.data_ptr(), k, 1, one.data_ptr(), rows)
+    torch.cuda.synchronize()
+    assert torch.equal(full[37], one[0])
+
+
+def test_gemm_rejects_bad_shapes():
+    for args in [(Q.MAT_F16, 0, 256, 1000, 4), (Q.MAT_Q4, 32, 256, 1024, 4), (Q.MAT_F16, 0, 256, 1024, 65),
+                 (Q.MAT_F16, 0, 256, 1024, 0)]:
+        kind, group, rows, k, M = args
+        with pytest.raises(Q.QneError) as e:
+            Q.gemm(kind, 1, 1, rows, k, group, 1, k, M, 1, rows)
+        assert e.value.code == Q.EINVAL
+
+
+# ---- whole batches ----
+
+@pytest.fixture(scope="module", params=[("tiny", "q4", "f16"), ("small", "q4", "f16"), ("tiny", "f16", "q4")],
+                ids=["tiny-q4body", "small-q4body", "tiny-f16body-q4head"])
+def pair(request):
+    name, body, head = request.param
+    index, buf = W.synth_model(name, seed=11, body=body, head=head, norm_jitter=0.1)
+    m = Q.Model.load(index, buf)
+    om = O.OracleModel(index, buf, "f64")
+    yield m, om
+    m.close()
+
+
+def prompts(vocab, lengths, seed):
+    rng = np.random.default_rng(seed)
+    return [rng.integers(0, vocab, size=n).astype(np.uint32) for n in lengths]
+
+
+def test_batch_continues_each_sequence_like_the_oracle(pair):
+    m, om = pair
+    lengths = [5, 17, 40, 1, 33]
+    ps = prompts(m.vocab, lengths, 21)
+    steps = 20
+    with Q.Batch(m, max_rows=8, max_context=512) as b:
+        for r, p in enumerate(ps):
+            m.reset()
+            m.prefill_batched(p)
+            b.admit(r)
+        tok, pos = b.row_state(len(ps))
+        assert list(pos) == lengths
+        picks, logits = b.step(len(ps), logits=True)
+        ids = b.decode(len(ps), steps - 1)
+    for r, p in enumerate(ps):
+        om.reset()
+        want_ids, want_logits = om.greedy(p, steps + 1)
+        assert tok[r] == want_ids[0]
+        assert np.max(np.abs(logits[r] - want_logits[1])) < 1e-3, r
+        got = [int(picks[r])] + [int(x) for x in ids[:, r]]
+        assert got == want_ids[1:], r
+
+
+def test_batch_teacher_forced_logits_and_empty_rows(pair):
+    """Rows started empty (reset_row) and fed given tokens: every step's logits against the
+    oracle's token-by-token run from position 0."""
+    m, om = pair
+    R, T = 3, 6
+    seqs = prompts(m.vocab, [T] * R, 8)
+    with Q.Batch(m, max_rows=R, max_context=64) as b:
+        for r in range(R):
+            b.reset_row(r, int(seqs[r][0]))
+        got = []
+        for t in range(T):
+            _, lg = b.step(R, tokens=[int(s[t]) for s in seqs], logits=True)
+            got.append(lg)
+    for r in range(R):
+        om.reset()
+        for t in range(T):
+            want = om.token(int(seqs[r][t]), t)
+            assert np.max(np.abs(got[t][r] - want)) < 1e-3, (r, t)
+
+
+def test_batch_is_bitwise_repeatable(pair):
+    m, _ = pair
+    ps = prompts(m.vocab, [9, 3, 27], 4)
+    runs = []
+    for _ in range(2):
+        with Q.Batch(m, max_rows=4, max_context=256) as b:
+            for r, p in enumerate(ps):
+                m.reset()
+                m.prefill_batched(p)
+                b.admit(r)
+            _, lg = b.step(3, logits=True)
+            runs.append((lg, b.decode(3, 12)))
+    assert np.array_equal(runs[0][0], runs[1][0])
+    assert np.array_equal(runs[0][1], runs[1][1])
+
+
+def test_batch_errors(pair):
+    m, _ = pair
+    with Q.Batch(m, max_rows=2, max_context=32) as b:
+        with pytest.raises(Q.QneError) as e:
+            b.admit(2)
+        assert e.value.code == Q.EINVAL
+        with pytest.raises(Q.QneError) as e:
+            b.step(3)
+        assert e.value.code == Q.EINVAL
+        b.reset_row(0, 1)
+        b.reset_row(1, 2)
+        with pytest.raises(Q.QneError) as e:
+            b.decode(2, 33)  # past the batch context
+        assert e.value.code == Q.ECONTEXT
+        with pytest.raises(Q.QneError) as e:
+            b.step(2, tokens=[1, m.vocab])
+        assert e.value.code == Q.EINVAL
+        m.reset()
+        m.prefill_batched(np.arange(40, dtype=np.uint32))
+        with pytest.raises(Q.QneError) as e:
+            b.admit(0)  # the model's sequence is longer than the batch context
+        assert e.value.code == Q.ECONTEXT
+    with pytest.raises(Q.QneError):
+        Q.Batch(m, max_rows=65, max_context=32)
