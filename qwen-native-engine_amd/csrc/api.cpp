@@ -323,10 +323,10 @@ int qne_gemm(int kind, const void* w, const void* sz, int rows, int k, int group
         a.y = y;
         a.y_stride = y_stride;
         a.n_out = n_out;
-        const size_t part = (size_t)a.splits * 64 * rows, ssp = (size_t)a.splits * 64;
-        float* ws = workspace(kWsGemm, (part + ssp) * 4);
+        const size_t part = (size_t)a.splits * 64 * rows;
+        float* ws = workspace(kWsGemm, part * 4 + qne::gemm_frag_bytes(k));
         a.part = ws;
-        a.ss_part = ws + part;
+        a.frag = (uint8_t*)(ws + part);
         hipStream_t st = (hipStream_t)stream;
         qne::launch_gemm(a, st);
         check_launch();

@@ -86,11 +86,11 @@ BatchDecoder::BatchDecoder(Model& m, int max_rows, int max_context) : m_(m), max
         act_ = (float*)dalloc((size_t)kRowsMax * c.intermediate * 4);
         logits_ = (float*)dalloc((size_t)kRowsMax * c.vocab * 4);
         qbuf_ = (float*)dalloc((size_t)kRowsMax * c.n_q_heads * c.head_dim * 4);
-        size_t part = 0, ssp = 0;
+        size_t part = 0, frag = 0;
         auto need_part = [&](const DevMat& W, bool swiglu) {
             const int s = gemm_splits(W.kind, W.rows, W.k, W.group);
             if (s > 1 || swiglu) part = std::max(part, (size_t)s * kRowsMax * W.rows);
-            ssp = std::max(ssp, (size_t)s * kRowsMax);
+            frag = std::max(frag, gemm_frag_bytes(W.k));
         };
         for (const DevLayer& L : m.layers_) {
             need_part(L.in, false);
@@ -100,7 +100,7 @@ BatchDecoder::BatchDecoder(Model& m, int max_rows, int max_context) : m_(m), max
         }
         need_part(m.lm_head_, false);
         part_ = (float*)dalloc(part * 4);
-        ss_part_ = (float*)dalloc(ssp * 4);
+        frag_ = (uint8_t*)dalloc(frag);
         for (int r = 1; r <= max_rows; r++)
             attn_part_rows_ = std::max(attn_part_rows_, (size_t)r * attn_splits_for(r, c.n_kv_heads, max_blocks_));
         const size_t G = (size_t)(c.n_q_heads / c.n_kv_heads);
@@ -159,7 +159,7 @@ void BatchDecoder::enqueue_step(int n) {
         a.group = W.group;
         a.splits = gemm_splits(W.kind, W.rows, W.k, W.group);
         a.part = part_;
-        a.ss_part = ss_part_;
+        a.frag = frag_;
         a.epi = epi;
         a.y = y;
         a.y_stride = y_stride;

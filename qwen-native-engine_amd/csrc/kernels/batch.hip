@@ -4,19 +4,21 @@
 // Reference: the 16-token prefill GEMM `gemm` (kernels/src/batch.rs:12-99, launched by `Gpu::gemm`,
 // lib.rs:341-347) and its embed / argmax companions (shaders.rs:405-434, 635-699), generalised to M
 // rows of one decode step each. Design for gfx950:
-//  - a workgroup (4 waves) computes a 64 x 128 tile of y = x W^T (64 rows of x, 32 W rows per
-//    wave) over a slice of K (split-K), with v_mfma_f32_32x32x16_f16;
-//  - x chunks of 64 columns are staged in LDS once per workgroup from the f32 activations: scaled
-//    by the RMSNorm gain when the matrix follows a norm (the row's 1 / rms is a scalar per row and
-//    is applied after the sum), then split into f16 halves hi = f16(x), lo = f16(x - hi), so that
-//    the two MFMAs over hi and lo reproduce f32 products to about 2^-22;
+//  - k_stage_x writes the (RMSNormed) f32 activations once per GEMM as f16 halves hi = f16(x),
+//    lo = f16(x - hi), already in v_mfma_f32_32x32x16_f16 operand order, plus each row's sum over
+//    every 64-column chunk: two MFMAs (hi, lo) reproduce f32 products to about 2^-22;
+//  - k_gemm: a workgroup (4 or 8 waves) computes a 64 x (32 waves) tile of y = x W^T over a slice
+//    of K (split-K). x chunks and W chunks stream into a ring of LDS slots by LDS DMA
+//    (global_load_lds) with explicit vmcnt waits, so the compiler inserts no waits that would drain
+//    the pipeline;
 //  - q4 weights are dequantised in registers as exact f16 integers (0x6400 | q is 1024 + q, minus
-//    1024 is exact); each quantisation group is summed into a fresh f32 tile and its scale and zero
-//    applied once: y += s (sum q x - z sum x), with the group sums of x taken from the staged
-//    values. f16 weights go to the MFMA as they are;
-//  - with one split the workgroup applies the epilogue itself; otherwise it writes partials and
+//    1024 is exact); every chunk's sum is scaled once: y += s (sum q x) - s z (sum x), with sum x
+//    from the staged chunk sums. f16 weights go to the MFMA as they are;
+//  - with one split the GEMM applies the epilogue itself; otherwise it writes partials and
 //    k_gemm_reduce sums them in split order (so the result does not depend on timing) and applies
-//    1 / rms and the epilogue (store, residual add, SwiGLU).
+//    the epilogue (store, residual add, SwiGLU).
+#include <algorithm>
+
 #include "common.hpp"
 #include "launch.hpp"
 
@@ -25,14 +27,37 @@ namespace qne {
 namespace {
 
 constexpr int kBM = 64;            // rows of x per GEMM (sequences)
-constexpr int kTileN = 128;        // W rows per workgroup, 32 per wave
-constexpr int kChunk = 64;         // columns of x per staged chunk
-constexpr int kXRow = kChunk + 8;  // f16 per LDS row of a chunk (16 bytes of padding)
-constexpr int kGemmThreads = 256;
+constexpr int kChunk = 64;         // columns per staged chunk
+constexpr int kFragBytes = 8192;   // one half (hi or lo) of a chunk: 4 k-steps x 2 row tiles x 64 lanes x 16 B
+constexpr int kChunkBytes = 2 * kFragBytes + kBM * 4;  // hi, lo, per-row chunk sums
 
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 typedef float float16_t __attribute__((ext_vector_type(16)));
+
+// One LDS DMA: each active lane copies 16 (dma16) or 4 (dma4) bytes from its own global address to
+// LDS at dst + lane * 16 (or * 4); dst is the same for the whole wave. Issued from asm so that the
+// compiler adds no wait of its own; completion is awaited with wait_vm. m0 carries the LDS address
+// and is restored.
+__device__ __forceinline__ void dma16(const void* src, void* dst) {
+    const uint32_t lds = __builtin_amdgcn_readfirstlane((uint32_t)(size_t)(lds_ptr_t)dst);
+    uint32_t saved;
+    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off\n\ts_mov_b32 m0, %0"
+                 : "=&s"(saved) : "v"(src), "s"(lds) : "memory");
+}
+__device__ __forceinline__ void dma4(const void* src, void* dst) {
+    const uint32_t lds = __builtin_amdgcn_readfirstlane((uint32_t)(size_t)(lds_ptr_t)dst);
+    uint32_t saved;
+    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %1, off\n\ts_mov_b32 m0, %0"
+                 : "=&s"(saved) : "v"(src), "s"(lds) : "memory");
+}
+// Until at most N of this wave's vector-memory operations are outstanding; the memory clobber keeps
+// the LDS reads of the landed data after it.
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
 
 // The 8 nibbles of a q4 word (nibble i at bits 4i, column 8j + i of word j) as exact f16 values.
 __device__ __forceinline__ half8_t nibbles8(uint32_t v) {
@@ -53,194 +78,213 @@ __device__ __forceinline__ uint32_t pack_h2(float a, float b) {
     return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)a) | ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)b) << 16);
 }
 
+// Operand layout of v_mfma_f32_32x32x16_f16 (lane l): A[l % 32][8 (l / 32) + i], B[8 (l / 32) + i][l % 32],
+// D register j = [8 (j / 4) + 4 (l / 32) + j % 4][l % 32]. The 16 k-slots of k-step s of a chunk are
+// chunk columns 32 (l / 32) + 8 s + i, the same for A and B, so a lane's q4 bytes of a chunk (16) are
+// contiguous. In a staged chunk, fragment (s, row tile mt) of a half is 64 lanes x 16 bytes.
+__device__ __forceinline__ int frag_offset(int s, int mt, int lane) { return ((s * 2 + mt) * 64 + lane) * 16; }
+
 }  // namespace
 
-// Grid (ceil(N / 128), splits); split s covers quantisation groups [s * gps, (s + 1) * gps) (for f16
-// weights a "group" is one 64-column chunk). Lane layout of v_mfma_f32_32x32x16_f16 (lane l):
-// A[l % 32][8 (l / 32) + i], B[8 (l / 32) + i][l % 32], D register j = [8 (j / 4) + 4 (l / 32) + j % 4][l % 32].
-// The 16 MFMA k-slots of step s of a chunk map to chunk columns 32 (l / 32) + 8 s + i, the same for
-// A and B, so a lane's W bytes of a chunk are contiguous (16 bytes of q4, 64 of f16).
-template <int KIND>
-__global__ __launch_bounds__(kGemmThreads, 2) void k_gemm(const GemmArgs a) {
-    __shared__ __attribute__((aligned(16))) uint16_t sx[2][kBM * kXRow];  // hi, lo of one chunk
-    __shared__ float ssum[kBM];                                          // group sums of x (q4)
-    __shared__ float sinv[kBM];                                          // 1 / rms per row
-    const int t = threadIdx.x, lane = t & 63, w = __builtin_amdgcn_readfirstlane(t >> 6);
+// Grid 64 (one workgroup per row of the 64-row operand; rows >= m are zero). Row r of x (f32 at
+// x + r * x_stride), times 1 / rms(row) * gain when gain is set (RMSNorm, shaders.rs:378-403), is
+// written as chunk c = k / 64 of `frag`: hi and lo fragments and the chunk's sum of hi + lo.
+__global__ __launch_bounds__(256) void k_stage_x(const float* __restrict__ x, int x_stride, int m, int K,
+                                                 const float* __restrict__ gain, float eps, uint8_t* __restrict__ frag) {
+    __shared__ float red[16];
+    const int r = blockIdx.x, t = threadIdx.x;
+    const bool live = r < m;
+    const float* row = x + (size_t)(live ? r : 0) * x_stride;
+    float inv = 1.0f;
+    if (gain) {
+        float ss = 0.0f;
+        if (live)
+            for (int k = 4 * t; k < K; k += 1024) {
+                const float4 v = *(const float4*)(row + k);
+                ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+            }
+        ss = block_sum(ss, red);
+        inv = 1.0f / sqrtf(ss / (float)K + eps);
+    }
+    const int mt = r >> 5, rl = r & 31;
+    // 8 columns per thread per pass; threads 8q .. 8q + 7 cover one chunk
+    for (int base = 0; base < K; base += 2048) {
+        const int k = base + 8 * t;
+        float part = 0.0f;
+        if (k < K) {
+            float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+            if (live) {
+                const float4 a = *(const float4*)(row + k), b = *(const float4*)(row + k + 4);
+                v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+                if (gain) {
+                    const float4 ga = *(const float4*)(gain + k), gb = *(const float4*)(gain + k + 4);
+                    const float g[8] = {ga.x, ga.y, ga.z, ga.w, gb.x, gb.y, gb.z, gb.w};
+#pragma unroll
+                    for (int e = 0; e < 8; e++) v[e] = v[e] * inv * g[e];
+                }
+            }
+            uint32_t ph[4], pl[4];
+#pragma unroll
+            for (int e = 0; e < 8; e += 2) {
+                const float h0 = (float)(_Float16)v[e], h1 = (float)(_Float16)v[e + 1];
+                const float l0 = (float)(_Float16)(v[e] - h0), l1 = (float)(_Float16)(v[e + 1] - h1);
+                ph[e / 2] = pack_h2(h0, h1);
+                pl[e / 2] = pack_h2(l0, l1);
+                part += (h0 + l0) + (h1 + l1);
+            }
+            const int c = k / kChunk, kk = k % kChunk, hf = kk / 32, s = (kk % 32) / 8;
+            uint8_t* dst = frag + (size_t)c * kChunkBytes + frag_offset(s, mt, 32 * hf + rl);
+            *(uint4*)dst = make_uint4(ph[0], ph[1], ph[2], ph[3]);
+            *(uint4*)(dst + kFragBytes) = make_uint4(pl[0], pl[1], pl[2], pl[3]);
+        }
+        part += __shfl_xor(part, 1, 64);
+        part += __shfl_xor(part, 2, 64);
+        part += __shfl_xor(part, 4, 64);
+        if (k < K && (t & 7) == 0) ((float*)(frag + (size_t)(k / kChunk) * kChunkBytes + 2 * kFragBytes))[r] = part;
+    }
+}
+
+// Grid (ceil(N / (32 WAVES)), splits); split s covers chunks [s * cps, (s + 1) * cps). Wave w owns
+// W rows 32 (WAVES blockIdx.x + w) .. + 31. The chunks stream through a ring of D LDS slots, each
+// holding one x chunk and every wave's W chunk; D - 1 chunks are in flight while one is computed.
+template <int KIND, int WAVES, int D>
+__global__ __launch_bounds__(64 * WAVES) void k_gemm(const GemmArgs a) {
+    constexpr int kWBytes = KIND == KIND_Q4 ? 1024 + 128 : 4096;  // one wave's W chunk (q4: + scale/zero words)
+    constexpr int kSlot = kChunkBytes + WAVES * kWBytes;
+    constexpr int kXPart = 2 * kFragBytes / WAVES;                 // x bytes each wave copies
+    constexpr int kPer = kXPart / 1024 + 1 + (KIND == KIND_Q4 ? 2 : 4);  // DMAs per wave per chunk
+    __shared__ __attribute__((aligned(16))) uint8_t ring[D][kSlot];
+    const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int hf = lane >> 5, l32 = lane & 31;
-    const int n = blockIdx.x * kTileN + 32 * w + l32;
-    const int nr = min(n, a.N - 1);  // rows past N compute on row N - 1 and are not stored
-    const int K = a.K;
+    const int n = (blockIdx.x * WAVES + w) * 32 + l32;
+    const int nr = min(n, a.N - 1);  // rows past N load row N - 1 and are not stored
+    const int K = a.K, nchunks = K / kChunk;
     const int cpg = KIND == KIND_Q4 ? a.group / kChunk : 1;
-    const int ngroups = K / (cpg * kChunk);
-    const int g0 = blockIdx.y * a.gps, g1 = min(ngroups, g0 + a.gps);
-    const int c0 = g0 * cpg, c1 = g1 * cpg;
+    const int ngroups = nchunks / cpg;
+    const int c0 = blockIdx.y * a.cps, c1 = min(nchunks, c0 + a.cps);
+    const int nch = max(0, c1 - c0);
 
-    // staging: thread t copies row sm, columns sk .. sk + 15 of each chunk
-    const int sm = t >> 2, sk = 16 * (t & 3);
-    const bool live = sm < a.m;
-    const float* xr = a.x + (size_t)(live ? sm : 0) * a.x_stride + sk;
-    const float* gr = a.gain ? a.gain + sk : nullptr;
-
-    const uint8_t* wq = (const uint8_t*)a.W + (size_t)nr * (K / 2) + 16 * hf;  // q4: 16 bytes per chunk
-    const uint16_t* wf = (const uint16_t*)a.W + (size_t)nr * K + 32 * hf;      // f16: 64 bytes per chunk
+    auto issue = [&](int j, int slot) {
+        uint8_t* base = ring[slot];
+        const uint8_t* src = a.frag + (size_t)(c0 + j) * kChunkBytes;
+#pragma unroll
+        for (int u = 0; u < kXPart / 1024; u++) dma16(src + kXPart * w + 1024 * u + 16 * lane, base + kXPart * w + 1024 * u);
+        constexpr int kSumLanes = kBM * 4 / 16 / WAVES;  // lanes copying the chunk sums (16 B each)
+        if (lane < kSumLanes) dma16(src + 2 * kFragBytes + 16 * (kSumLanes * w + lane), base + 2 * kFragBytes + 16 * kSumLanes * w);
+        uint8_t* dst = base + kChunkBytes + w * kWBytes;
+        const int c = c0 + j;
+        if (KIND == KIND_Q4) {
+            dma16((const uint8_t*)a.W + (size_t)nr * (K / 2) + c * 32 + 16 * hf, dst);
+            if (lane < 32) dma4(a.SZ + (size_t)nr * ngroups + c / cpg, dst + 1024);
+        } else {
+#pragma unroll
+            for (int s = 0; s < 4; s++) dma16((const uint16_t*)a.W + (size_t)nr * K + c * kChunk + 32 * hf + 8 * s, dst + 1024 * s);
+        }
+    };
+    // until chunk j has landed: `ahead` chunks were issued after it
+    auto wait_chunk = [&](int ahead) {
+        if (ahead <= 0) wait_vm<0>();
+        else if (ahead == 1) wait_vm<kPer>();
+        else if (ahead == 2) wait_vm<2 * kPer>();
+        else if (ahead == 3) wait_vm<3 * kPer>();
+        else if (ahead == 4) wait_vm<4 * kPer>();
+        else wait_vm<5 * kPer>();
+    };
+    static_assert(D - 2 <= 5 && 5 * kPer <= 63, "ring deeper than the waits cover");
 
     float16_t acc0, acc1, grp0, grp1;
 #pragma unroll
     for (int j = 0; j < 16; j++) acc0[j] = acc1[j] = grp0[j] = grp1[j] = 0.0f;
-    float ss = 0.0f, gsum = 0.0f;
 
-    constexpr int kWv = KIND == KIND_Q4 ? 1 : 4;
-    float4 xv[4];
-    uint4 wv[kWv];
-    auto load = [&](int c) {
-        const int k0 = c * kChunk;
-#pragma unroll
-        for (int i = 0; i < 4; i++) xv[i] = live ? *(const float4*)(xr + k0 + 4 * i) : make_float4(0.f, 0.f, 0.f, 0.f);
-        if (KIND == KIND_Q4) {
-            wv[0] = *(const uint4*)(wq + (size_t)k0 / 2);
-        } else {
-#pragma unroll
-            for (int i = 0; i < 4; i++) wv[i] = *(const uint4*)(wf + k0 + 8 * i);
-        }
-    };
-    if (c0 < c1) load(c0);
-    for (int c = c0; c < c1; c++) {
-        const int k0 = c * kChunk;
-        // x chunk -> hi / lo (times the gain), sums of squares of the raw x, group sums of hi + lo
-        uint32_t ph[8], pl[8];
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const float v[4] = {xv[i].x, xv[i].y, xv[i].z, xv[i].w};
-            float4 gv = make_float4(1.f, 1.f, 1.f, 1.f);
-            if (gr) gv = *(const float4*)(gr + k0 + 4 * i);
-            const float g[4] = {gv.x, gv.y, gv.z, gv.w};
-            float hi[4], lo[4];
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                ss = fmaf(v[e], v[e], ss);
-                const float xg = v[e] * g[e];
-                hi[e] = (float)(_Float16)xg;
-                lo[e] = (float)(_Float16)(xg - hi[e]);
-                gsum += hi[e] + lo[e];
-            }
-            ph[2 * i] = pack_h2(hi[0], hi[1]);
-            ph[2 * i + 1] = pack_h2(hi[2], hi[3]);
-            pl[2 * i] = pack_h2(lo[0], lo[1]);
-            pl[2 * i + 1] = pack_h2(lo[2], lo[3]);
-        }
-        uint4 wcur[kWv];
-#pragma unroll
-        for (int i = 0; i < kWv; i++) wcur[i] = wv[i];
-        const bool group_end = KIND == KIND_Q4 && (c + 1 - c0) % cpg == 0;
-        float gtot = 0.0f;
-        if (group_end) {
-            gtot = gsum + __shfl_xor(gsum, 1, 64);
-            gtot += __shfl_xor(gtot, 2, 64);
-            gsum = 0.0f;
-        }
-        __syncthreads();  // every wave is done with the previous chunk
-        uint4* dh = (uint4*)&sx[0][sm * kXRow + sk];
-        uint4* dl = (uint4*)&sx[1][sm * kXRow + sk];
-        dh[0] = make_uint4(ph[0], ph[1], ph[2], ph[3]);
-        dh[1] = make_uint4(ph[4], ph[5], ph[6], ph[7]);
-        dl[0] = make_uint4(pl[0], pl[1], pl[2], pl[3]);
-        dl[1] = make_uint4(pl[4], pl[5], pl[6], pl[7]);
-        if (group_end && (t & 3) == 0) ssum[sm] = gtot;
-        __syncthreads();
-        if (c + 1 < c1) load(c + 1);  // next chunk in flight during the MFMAs
+    for (int j = 0; j < min(D - 1, nch); j++) issue(j, j);
+    int slot = 0;           // slot of chunk j
+    int next_slot = D - 1;  // slot of chunk j + D - 1
+    for (int j = 0; j < nch; j++) {
+        wait_chunk(min(j + D - 2, nch - 1) - j);
+        __syncthreads();  // every wave's part of chunk j has landed; every wave is done with chunk j - 1
+        if (j + D - 1 < nch) issue(j + D - 1, next_slot);
+        const uint8_t* xs = ring[slot];
+        const uint8_t* ws = ring[slot] + kChunkBytes + w * kWBytes;
+        uint4 wq;
+        if (KIND == KIND_Q4) wq = *(const uint4*)(ws + 16 * lane);
 #pragma unroll
         for (int s = 0; s < 4; s++) {
             half8_t b;
-            if (KIND == KIND_Q4) {
-                const uint32_t word = s == 0 ? wcur[0].x : s == 1 ? wcur[0].y : s == 2 ? wcur[0].z : wcur[0].w;
-                b = nibbles8(word);
-            } else {
-                b = __builtin_bit_cast(half8_t, wcur[s]);
-            }
-            const int o = l32 * kXRow + 32 * hf + 8 * s;
-            const half8_t a0h = *(const half8_t*)&sx[0][o];
-            const half8_t a0l = *(const half8_t*)&sx[1][o];
-            const half8_t a1h = *(const half8_t*)&sx[0][o + 32 * kXRow];
-            const half8_t a1l = *(const half8_t*)&sx[1][o + 32 * kXRow];
+            if (KIND == KIND_Q4) b = nibbles8(s == 0 ? wq.x : s == 1 ? wq.y : s == 2 ? wq.z : wq.w);
+            else b = *(const half8_t*)(ws + 1024 * s + 16 * lane);
+            const half8_t a0h = *(const half8_t*)(xs + frag_offset(s, 0, lane));
+            const half8_t a1h = *(const half8_t*)(xs + frag_offset(s, 1, lane));
+            const half8_t a0l = *(const half8_t*)(xs + kFragBytes + frag_offset(s, 0, lane));
+            const half8_t a1l = *(const half8_t*)(xs + kFragBytes + frag_offset(s, 1, lane));
             grp0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0h, b, grp0, 0, 0, 0);
             grp1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1h, b, grp1, 0, 0, 0);
             grp0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0l, b, grp0, 0, 0, 0);
             grp1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1l, b, grp1, 0, 0, 0);
         }
-        if (group_end) {
-            const uint32_t szw = a.SZ[(size_t)nr * ngroups + (c / cpg)];
-            const float sc = lo_h(szw), z = hi_h(szw);
+        if (KIND == KIND_Q4) {
+            // y += s (sum q x) - s z (sum x) over the chunk (scale and zero of the chunk's group)
+            const uint32_t szw = *(const uint32_t*)(ws + 1024 + 4 * l32);
+            const float sc = lo_h(szw), sz = sc * hi_h(szw);
+            const float* xsum = (const float*)(xs + 2 * kFragBytes);
 #pragma unroll
-            for (int j = 0; j < 16; j++) {
-                const int m = 8 * (j / 4) + 4 * hf + (j % 4);
-                acc0[j] = fmaf(sc, grp0[j] - z * ssum[m], acc0[j]);
-                acc1[j] = fmaf(sc, grp1[j] - z * ssum[32 + m], acc1[j]);
-                grp0[j] = 0.0f;
-                grp1[j] = 0.0f;
+            for (int q = 0; q < 4; q++) {
+                const float4 s0 = *(const float4*)(xsum + 8 * q + 4 * hf);
+                const float4 s1 = *(const float4*)(xsum + 32 + 8 * q + 4 * hf);
+                const float v0[4] = {s0.x, s0.y, s0.z, s0.w}, v1[4] = {s1.x, s1.y, s1.z, s1.w};
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    acc0[4 * q + e] = fmaf(sc, grp0[4 * q + e], fmaf(-sz, v0[e], acc0[4 * q + e]));
+                    acc1[4 * q + e] = fmaf(sc, grp1[4 * q + e], fmaf(-sz, v1[e], acc1[4 * q + e]));
+                    grp0[4 * q + e] = 0.0f;
+                    grp1[4 * q + e] = 0.0f;
+                }
             }
         }
+        slot = slot + 1 == D ? 0 : slot + 1;
+        next_slot = next_slot + 1 == D ? 0 : next_slot + 1;
     }
     if (KIND != KIND_Q4) {
         acc0 = grp0;
         acc1 = grp1;
     }
-    // sums of squares of the rows over this split's columns
-    ss += __shfl_xor(ss, 1, 64);
-    ss += __shfl_xor(ss, 2, 64);
+    if (n >= a.N) return;
     if (!a.direct) {
-        if (blockIdx.x == 0 && (t & 3) == 0) a.ss_part[(size_t)blockIdx.y * kBM + sm] = ss;
-        if (n < a.N) {
-            float* pp = a.part + (size_t)blockIdx.y * kBM * a.N + n;
-#pragma unroll
-            for (int j = 0; j < 16; j++) {
-                const int m = 8 * (j / 4) + 4 * hf + (j % 4);
-                pp[(size_t)m * a.N] = acc0[j];
-                pp[(size_t)(32 + m) * a.N] = acc1[j];
-            }
-        }
-        return;
-    }
-    // direct (one split, no SwiGLU): 1 / rms and the epilogue here (store or residual add)
-    if ((t & 3) == 0) sinv[sm] = a.gain ? 1.0f / sqrtf(ss / (float)K + a.eps) : 1.0f;
-    __syncthreads();
-    if (n < a.N) {
+        float* pp = a.part + (size_t)blockIdx.y * kBM * a.N + n;
 #pragma unroll
         for (int j = 0; j < 16; j++) {
             const int m = 8 * (j / 4) + 4 * hf + (j % 4);
-            if (m < a.m) {
-                float* d = a.y + (size_t)m * a.y_stride + n;
-                const float v = acc0[j] * sinv[m];
-                *d = a.epi == EPI_ACCUMULATE ? *d + v : v;
-            }
-            if (32 + m < a.m) {
-                float* d = a.y + (size_t)(32 + m) * a.y_stride + n;
-                const float v = acc1[j] * sinv[32 + m];
-                *d = a.epi == EPI_ACCUMULATE ? *d + v : v;
-            }
+            pp[(size_t)m * a.N] = acc0[j];
+            pp[(size_t)(32 + m) * a.N] = acc1[j];
+        }
+        return;
+    }
+    // direct (one split, no SwiGLU): store or residual add
+#pragma unroll
+    for (int j = 0; j < 16; j++) {
+        const int m = 8 * (j / 4) + 4 * hf + (j % 4);
+        if (m < a.m) {
+            float* d = a.y + (size_t)m * a.y_stride + n;
+            *d = a.epi == EPI_ACCUMULATE ? *d + acc0[j] : acc0[j];
+        }
+        if (32 + m < a.m) {
+            float* d = a.y + (size_t)(32 + m) * a.y_stride + n;
+            *d = a.epi == EPI_ACCUMULATE ? *d + acc1[j] : acc1[j];
         }
     }
 }
 
-// y rows r < m, columns c < n_out, from the split partials summed in split order, times 1 / rms of
-// the row when the GEMM followed a norm: store, residual add, or SwiGLU silu(gate) * up with gate =
-// column c and up = column c + n_out (matrix rows [gate; up], shaders.rs gemv epilogues).
+// y rows r < m, columns c < n_out, from the split partials summed in split order: store, residual
+// add, or SwiGLU silu(gate) * up with gate = column c and up = column c + n_out (matrix rows
+// [gate; up], shaders.rs gemv epilogues).
 __global__ __launch_bounds__(256) void k_gemm_reduce(const GemmArgs a) {
     const int c = blockIdx.x * 256 + threadIdx.x, r = blockIdx.y;
     if (c >= a.n_out || r >= a.m) return;
-    float inv = 1.0f;
-    if (a.gain) {
-        float ss = 0.0f;
-        for (int s = 0; s < a.splits; s++) ss += a.ss_part[(size_t)s * kBM + r];
-        inv = 1.0f / sqrtf(ss / (float)a.K + a.eps);
-    }
     float g = 0.0f, u = 0.0f;
     for (int s = 0; s < a.splits; s++) {
         const float* p = a.part + ((size_t)s * kBM + r) * a.N;
         g += p[c];
         if (a.epi == EPI_SWIGLU) u += p[c + a.n_out];
     }
-    g *= inv;
-    u *= inv;
     float* d = a.y + (size_t)r * a.y_stride + c;
     if (a.epi == EPI_STORE) *d = g;
     else if (a.epi == EPI_ACCUMULATE) *d += g;
@@ -315,14 +359,20 @@ __global__ __launch_bounds__(512) void k_argmax_rows(const float* __restrict__ l
     }
 }
 
+// Workgroup width: 8 waves (256 W rows) for wide matrices, 4 (128 rows) otherwise.
+static int gemm_waves(int N) { return N > 4096 ? 8 : 4; }
+
 int gemm_splits(int kind, int N, int K, int group) {
-    const int tiles = (N + kTileN - 1) / kTileN;
-    const int units = kind == KIND_Q4 ? K / group : K / kChunk;
-    int splits = (512 + tiles - 1) / tiles;  // about 512 workgroups
-    if (splits > units) splits = units;
-    if (splits < 1) splits = 1;
-    const int per = (units + splits - 1) / splits;
-    return (units + per - 1) / per;  // no empty split
+    (void)kind;
+    (void)group;
+    const int tiles = (N + 32 * gemm_waves(N) - 1) / (32 * gemm_waves(N));
+    const int nch = K / kChunk;
+    // about one workgroup per CU, at least 2 chunks per split (the partials are 64 x N floats per split)
+    int splits = (256 + tiles / 2) / tiles;
+    splits = std::min(splits, std::max(1, nch / 2));
+    splits = std::max(1, splits);
+    const int per = (nch + splits - 1) / splits;
+    return (nch + per - 1) / per;  // no empty split
 }
 
 bool gemm_shape_ok(int kind, int N, int K, int group, int m) {
@@ -331,13 +381,23 @@ bool gemm_shape_ok(int kind, int N, int K, int group, int m) {
     return true;
 }
 
+size_t gemm_frag_bytes(int K) { return (size_t)(K / kChunk) * kChunkBytes; }
+
 void launch_gemm(GemmArgs a, hipStream_t st) {
-    const int units = a.kind == KIND_Q4 ? a.K / a.group : a.K / kChunk;
-    a.gps = (units + a.splits - 1) / a.splits;
+    const int nch = a.K / kChunk;
+    a.cps = (nch + a.splits - 1) / a.splits;
     a.direct = a.splits == 1 && a.epi != EPI_SWIGLU;
-    const dim3 grid((a.N + kTileN - 1) / kTileN, a.splits);
-    if (a.kind == KIND_Q4) hipLaunchKernelGGL((k_gemm<KIND_Q4>), grid, dim3(kGemmThreads), 0, st, a);
-    else hipLaunchKernelGGL((k_gemm<KIND_F16>), grid, dim3(kGemmThreads), 0, st, a);
+    if (a.x) hipLaunchKernelGGL(k_stage_x, dim3(kBM), dim3(256), 0, st, a.x, a.x_stride, a.m, a.K, a.gain, a.eps, a.frag);
+    const int waves = gemm_waves(a.N);
+    const dim3 grid((a.N + 32 * waves - 1) / (32 * waves), a.splits);
+    // ring depths: as many chunk slots as fit in 160 KiB of LDS
+    if (a.kind == KIND_Q4) {
+        if (waves == 8) hipLaunchKernelGGL((k_gemm<KIND_Q4, 8, 5>), grid, dim3(512), 0, st, a);
+        else hipLaunchKernelGGL((k_gemm<KIND_Q4, 4, 7>), grid, dim3(256), 0, st, a);
+    } else {
+        if (waves == 8) hipLaunchKernelGGL((k_gemm<KIND_F16, 8, 3>), grid, dim3(512), 0, st, a);
+        else hipLaunchKernelGGL((k_gemm<KIND_F16, 4, 4>), grid, dim3(256), 0, st, a);
+    }
     if (!a.direct) hipLaunchKernelGGL(k_gemm_reduce, dim3((a.n_out + 255) / 256, a.m), dim3(256), 0, st, a);
 }
 

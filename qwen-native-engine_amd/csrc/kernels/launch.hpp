@@ -93,28 +93,31 @@ void launch_gdn_decode_rows(const float* proj, float* conv_state, const float* c
                             const float* prm, int heads, int rows, const GdnRowStrides& rs, hipStream_t st);
 
 // y = x W^T for up to 64 rows of x (batched decode), on MFMA. Rows of x are f32 at x + r * x_stride;
-// with `gain` x is RMSNormed (gain, eps) first. Epilogues as the GEMV (store, residual add, SwiGLU
-// with n_out = N / 2). `part` / `ss_part` hold splits * 64 * N and splits * 64 floats.
+// with `gain` x is RMSNormed (gain, eps) first. The x operand is staged in `frag`
+// (gemm_frag_bytes(K)); with x null, `frag` already holds it. Epilogues as the GEMV (store, residual
+// add, SwiGLU with n_out = N / 2). `part` holds splits * 64 * N floats when the GEMM has more than
+// one split or SwiGLU.
 struct GemmArgs {
     const float* x = nullptr;
     int x_stride = 0;
     int m = 0;
     const float* gain = nullptr;
     float eps = 1e-6f;
+    uint8_t* frag = nullptr;
     int kind = KIND_Q4;
     const void* W = nullptr;
     const uint32_t* SZ = nullptr;
     int N = 0, K = 0, group = 64;
     int splits = 1;
-    int gps = 0;         // set by launch_gemm
-    int direct = 0;      // set by launch_gemm: the GEMM applies the epilogue itself
+    int cps = 0;     // set by launch_gemm: chunks per split
+    int direct = 0;  // set by launch_gemm: the GEMM applies the epilogue itself
     float* part = nullptr;
-    float* ss_part = nullptr;
     int epi = EPI_STORE;
     float* y = nullptr;
     int y_stride = 0;
     int n_out = 0;
 };
+size_t gemm_frag_bytes(int K);
 int gemm_splits(int kind, int N, int K, int group);
 bool gemm_shape_ok(int kind, int N, int K, int group, int m);
 void launch_gemm(GemmArgs a, hipStream_t st);
