@@ -59,21 +59,26 @@ __device__ __forceinline__ void wait_vm() {
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
-// The 8 nibbles of a q4 word (nibble i at bits 4i, column 8j + i of word j) as exact f16 values.
+// The 8 nibbles of a q4 word (nibble i at bits 4i: column 8j + i of word j) as exact f16 values, in
+// the order [q0, q4, q1, q5, q2, q6, q3, q7]: 0x6400 | q is the f16 1024 + q, and 0x6400 | (q << 4)
+// is 1024 + 16 q, so four and-or, one shift, two packed subtracts and two packed fmas (x / 16 - 64)
+// give all eight. The x operand of a q4 GEMM is staged in the same column order.
 __device__ __forceinline__ half8_t nibbles8(uint32_t v) {
-    const half2_t bias = {(_Float16)1024.0f, (_Float16)1024.0f};
-    half8_t r;
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const uint32_t nb = v >> (8 * i);
-        const uint32_t p = (nb & 0xFu) | ((nb & 0xF0u) << 12) | 0x64006400u;
-        const half2_t x = __builtin_bit_cast(half2_t, p) - bias;
-        r[2 * i] = x.x;
-        r[2 * i + 1] = x.y;
-    }
-    return r;
+    typedef uint32_t u32;
+    const u32 v2 = v >> 8;
+    const u32 t0 = (v & 0x000F000Fu) | 0x64006400u;
+    const u32 t1 = (v & 0x00F000F0u) | 0x64006400u;
+    const u32 t2 = (v2 & 0x000F000Fu) | 0x64006400u;
+    const u32 t3 = (v2 & 0x00F000F0u) | 0x64006400u;
+    const half2_t k1024 = {(_Float16)1024.0f, (_Float16)1024.0f};
+    const half2_t k16 = {(_Float16)0.0625f, (_Float16)0.0625f};
+    const half2_t k64 = {(_Float16)-64.0f, (_Float16)-64.0f};
+    const half2_t h0 = __builtin_bit_cast(half2_t, t0) - k1024;
+    const half2_t h1 = __builtin_elementwise_fma(__builtin_bit_cast(half2_t, t1), k16, k64);
+    const half2_t h2 = __builtin_bit_cast(half2_t, t2) - k1024;
+    const half2_t h3 = __builtin_elementwise_fma(__builtin_bit_cast(half2_t, t3), k16, k64);
+    return half8_t{h0.x, h0.y, h1.x, h1.y, h2.x, h2.y, h3.x, h3.y};
 }
-
 __device__ __forceinline__ uint32_t pack_h2(float a, float b) {
     return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)a) | ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)b) << 16);
 }
@@ -90,7 +95,8 @@ __device__ __forceinline__ int frag_offset(int s, int mt, int lane) { return ((s
 // x + r * x_stride), times 1 / rms(row) * gain when gain is set (RMSNorm, shaders.rs:378-403), is
 // written as chunk c = k / 64 of `frag`: hi and lo fragments and the chunk's sum of hi + lo.
 __global__ __launch_bounds__(256) void k_stage_x(const float* __restrict__ x, int x_stride, int m, int K,
-                                                 const float* __restrict__ gain, float eps, uint8_t* __restrict__ frag) {
+                                                 const float* __restrict__ gain, float eps, int q4order,
+                                                 uint8_t* __restrict__ frag) {
     __shared__ float red[16];
     const int r = blockIdx.x, t = threadIdx.x;
     const bool live = r < m;
@@ -122,6 +128,11 @@ __global__ __launch_bounds__(256) void k_stage_x(const float* __restrict__ x, in
 #pragma unroll
                     for (int e = 0; e < 8; e++) v[e] = v[e] * inv * g[e];
                 }
+            }
+            if (q4order) {  // the q4 GEMM's B operand order [0, 4, 1, 5, 2, 6, 3, 7]
+                const float o[8] = {v[0], v[4], v[1], v[5], v[2], v[6], v[3], v[7]};
+#pragma unroll
+                for (int e = 0; e < 8; e++) v[e] = o[e];
             }
             uint32_t ph[4], pl[4];
 #pragma unroll
@@ -216,8 +227,14 @@ __global__ __launch_bounds__(64 * WAVES) void k_gemm(const GemmArgs a) {
             const half8_t a1h = *(const half8_t*)(xs + frag_offset(s, 1, lane));
             const half8_t a0l = *(const half8_t*)(xs + kFragBytes + frag_offset(s, 0, lane));
             const half8_t a1l = *(const half8_t*)(xs + kFragBytes + frag_offset(s, 1, lane));
-            grp0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0h, b, grp0, 0, 0, 0);
-            grp1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1h, b, grp1, 0, 0, 0);
+            if (KIND == KIND_Q4 && s == 0) {  // a fresh tile per chunk: C = 0
+                const float16_t zero = {};
+                grp0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0h, b, zero, 0, 0, 0);
+                grp1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1h, b, zero, 0, 0, 0);
+            } else {
+                grp0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0h, b, grp0, 0, 0, 0);
+                grp1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1h, b, grp1, 0, 0, 0);
+            }
             grp0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0l, b, grp0, 0, 0, 0);
             grp1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1l, b, grp1, 0, 0, 0);
         }
@@ -235,8 +252,6 @@ __global__ __launch_bounds__(64 * WAVES) void k_gemm(const GemmArgs a) {
                 for (int e = 0; e < 4; e++) {
                     acc0[4 * q + e] = fmaf(sc, grp0[4 * q + e], fmaf(-sz, v0[e], acc0[4 * q + e]));
                     acc1[4 * q + e] = fmaf(sc, grp1[4 * q + e], fmaf(-sz, v1[e], acc1[4 * q + e]));
-                    grp0[4 * q + e] = 0.0f;
-                    grp1[4 * q + e] = 0.0f;
                 }
             }
         }
@@ -387,7 +402,9 @@ void launch_gemm(GemmArgs a, hipStream_t st) {
     const int nch = a.K / kChunk;
     a.cps = (nch + a.splits - 1) / a.splits;
     a.direct = a.splits == 1 && a.epi != EPI_SWIGLU;
-    if (a.x) hipLaunchKernelGGL(k_stage_x, dim3(kBM), dim3(256), 0, st, a.x, a.x_stride, a.m, a.K, a.gain, a.eps, a.frag);
+    if (a.x)
+        hipLaunchKernelGGL(k_stage_x, dim3(kBM), dim3(256), 0, st, a.x, a.x_stride, a.m, a.K, a.gain, a.eps,
+                           a.kind == KIND_Q4 ? 1 : 0, a.frag);
     const int waves = gemm_waves(a.N);
     const dim3 grid((a.N + 32 * waves - 1) / (32 * waves), a.splits);
     // ring depths: as many chunk slots as fit in 160 KiB of LDS
