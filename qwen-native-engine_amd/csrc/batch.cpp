@@ -100,7 +100,10 @@ BatchDecoder::BatchDecoder(Model& m, int max_rows, int max_context) : m_(m), max
         }
         need_part(m.lm_head_, false);
         part_ = (float*)dalloc(part * 4);
-        frag_ = (uint8_t*)dalloc(frag);
+        frag_a_ = (uint8_t*)dalloc(frag);
+        frag_b_ = (uint8_t*)dalloc(frag);
+        QNE_HIP(hipMemset(frag_a_, 0, frag));
+        QNE_HIP(hipMemset(frag_b_, 0, frag));
         for (int r = 1; r <= max_rows; r++)
             attn_part_rows_ = std::max(attn_part_rows_, (size_t)r * attn_splits_for(r, c.n_kv_heads, max_blocks_));
         const size_t G = (size_t)(c.n_q_heads / c.n_kv_heads);
@@ -140,16 +143,22 @@ void BatchDecoder::check_row(int row) const {
     if (row < 0 || row >= max_rows_) throw Error(QNE_EINVAL, "row out of range");
 }
 
-// One decode step of rows 0..n-1: model.rs:220-269 with every GEMV a GEMM over the rows.
+// One decode step of rows 0..n-1: model.rs:220-269 with every GEMV a GEMM over the rows. The x
+// operands alternate between two staging buffers: the kernel that produces an activation (the
+// embedding, the reduce of the previous GEMM) stages it for the GEMM that reads it; the RMSNorm
+// gains are folded in there and the 1 / rms factors applied by the consuming GEMM.
 void BatchDecoder::enqueue_step(int n) {
     const ModelConfig& c = m_.cfg_;
-    launch_embed_rows(m_.embed_.kind, m_.embed_.w, m_.embed_.sz, m_.embed_.group, c.hidden, tokens_, n, h_, stream_);
-    auto gemm = [&](const DevMat& W, const float* x, int x_stride, const float* gain, float* y, int y_stride, int epi) {
+    const auto order = [](const DevMat& W) { return W.kind == KIND_Q4 ? 1 : 0; };
+    const DevLayer& first = m_.layers_.front();
+    launch_embed_rows(m_.embed_.kind, m_.embed_.w, m_.embed_.sz, m_.embed_.group, c.hidden, tokens_, n, h_, frag_a_,
+                      first.input_norm, order(first.in), stream_);
+    auto gemm = [&](const DevMat& W, uint8_t* frag, int norm, float* y, int y_stride, int epi, uint8_t* frag_out,
+                    const float* gain_out, int order_out) {
         GemmArgs a;
-        a.x = x;
-        a.x_stride = x_stride;
         a.m = n;
-        a.gain = gain;
+        a.frag = frag;
+        a.norm = norm;
         a.eps = c.eps;
         a.kind = W.kind;
         a.W = W.w;
@@ -159,17 +168,21 @@ void BatchDecoder::enqueue_step(int n) {
         a.group = W.group;
         a.splits = gemm_splits(W.kind, W.rows, W.k, W.group);
         a.part = part_;
-        a.frag = frag_;
         a.epi = epi;
         a.y = y;
         a.y_stride = y_stride;
         a.n_out = epi == EPI_SWIGLU ? W.rows / 2 : W.rows;
+        a.frag_out = frag_out;
+        a.gain_out = gain_out;
+        a.order_out = order_out;
         launch_gemm(a, stream_);
     };
     const int splits = attn_splits_for(n, c.n_kv_heads, max_blocks_);
     for (size_t li = 0; li < m_.layers_.size(); li++) {
         const DevLayer& L = m_.layers_[li];
-        gemm(L.in, h_, c.hidden, L.input_norm, proj_, proj_w_, EPI_STORE);
+        const bool last = li + 1 == m_.layers_.size();
+        // in-projection of RMSNorm(h, input_norm), staged in frag_a
+        gemm(L.in, frag_a_, 1, proj_, proj_w_, EPI_STORE, nullptr, nullptr, 0);
         if (L.attn) {
             AttnRowsArgs a;
             a.proj = proj_;
@@ -200,11 +213,17 @@ void BatchDecoder::enqueue_step(int n) {
             launch_gdn_decode_rows(proj_, conv_[li], L.conv_w, rec_[li], mixed_, L.gdn_params, c.gdn_heads, n, rs,
                                    stream_);
         }
-        gemm(L.out, mixed_, L.out.k, nullptr, h_, c.hidden, EPI_ACCUMULATE);
-        gemm(L.gate_up, h_, c.hidden, L.post_norm, act_, c.intermediate, EPI_SWIGLU);
-        gemm(L.down, act_, c.intermediate, nullptr, h_, c.hidden, EPI_ACCUMULATE);
+        launch_stage_x(mixed_, L.out.k, n, L.out.k, nullptr, order(L.out), frag_b_, stream_);
+        // h += W_out mixed; stage RMSNorm(h, post_norm) for gate_up
+        gemm(L.out, frag_b_, 0, h_, c.hidden, EPI_ACCUMULATE, frag_a_, L.post_norm, order(L.gate_up));
+        // act = SwiGLU(W_gu RMSNorm(h)), staged for down
+        gemm(L.gate_up, frag_a_, 1, nullptr, 0, EPI_SWIGLU, frag_b_, nullptr, order(L.down));
+        // h += W_down act; stage RMSNorm(h, next gain) for the next layer or the LM head
+        const float* next_gain = last ? m_.final_norm_ : m_.layers_[li + 1].input_norm;
+        const int next_order = last ? order(m_.lm_head_) : order(m_.layers_[li + 1].in);
+        gemm(L.down, frag_b_, 0, h_, c.hidden, EPI_ACCUMULATE, frag_a_, next_gain, next_order);
     }
-    gemm(m_.lm_head_, h_, c.hidden, m_.final_norm_, logits_, c.vocab, EPI_STORE);
+    gemm(m_.lm_head_, frag_a_, 1, logits_, c.vocab, EPI_STORE, nullptr, nullptr, 0);
     launch_argmax_rows(logits_, n, c.vocab, picks_, tokens_, pos_, stream_);
 }
 

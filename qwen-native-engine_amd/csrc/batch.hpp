@@ -71,7 +71,7 @@ class BatchDecoder {
     int proj_w_ = 0, mixed_w_ = 0;
     float *h_ = nullptr, *proj_ = nullptr, *mixed_ = nullptr, *act_ = nullptr, *logits_ = nullptr, *qbuf_ = nullptr;
     float *part_ = nullptr, *attn_ml_ = nullptr, *attn_acc_ = nullptr;
-    uint8_t* frag_ = nullptr;  // the GEMM's staged x operand
+    uint8_t *frag_a_ = nullptr, *frag_b_ = nullptr;  // staged x operands of the GEMMs
     size_t attn_part_rows_ = 0;  // rows * splits the attention partials hold
     uint32_t *tokens_ = nullptr, *picks_ = nullptr, *ids_ = nullptr;
     int32_t* pos_ = nullptr;

@@ -4,9 +4,13 @@
 // Reference: the 16-token prefill GEMM `gemm` (kernels/src/batch.rs:12-99, launched by `Gpu::gemm`,
 // lib.rs:341-347) and its embed / argmax companions (shaders.rs:405-434, 635-699), generalised to M
 // rows of one decode step each. Design for gfx950:
-//  - k_stage_x writes the (RMSNormed) f32 activations once per GEMM as f16 halves hi = f16(x),
-//    lo = f16(x - hi), already in v_mfma_f32_32x32x16_f16 operand order, plus each row's sum over
-//    every 64-column chunk: two MFMAs (hi, lo) reproduce f32 products to about 2^-22;
+//  - the x operand (f32 activations, times the RMSNorm gain when the matrix follows a norm) is
+//    written once per GEMM as f16 halves hi = f16(x), lo = f16(x - hi), already in
+//    v_mfma_f32_32x32x16_f16 operand order, with each row's sums of hi + lo and of x^2 over every
+//    64-column chunk: two MFMAs (hi, lo) reproduce f32 products to about 2^-22. The kernels that
+//    produce an activation write it (the reduce kernels, the embedding); k_stage_x does it for the
+//    others. The norm's 1 / rms is a per-row scalar, applied to the GEMM's output from the sums of
+//    x^2;
 //  - k_gemm: a workgroup (4 or 8 waves) computes a 64 x (32 waves) tile of y = x W^T over a slice
 //    of K (split-K). x chunks and W chunks stream into a ring of LDS slots by LDS DMA
 //    (global_load_lds) with explicit vmcnt waits, so the compiler inserts no waits that would drain
@@ -29,7 +33,10 @@ namespace {
 constexpr int kBM = 64;            // rows of x per GEMM (sequences)
 constexpr int kChunk = 64;         // columns per staged chunk
 constexpr int kFragBytes = 8192;   // one half (hi or lo) of a chunk: 4 k-steps x 2 row tiles x 64 lanes x 16 B
-constexpr int kChunkBytes = 2 * kFragBytes + kBM * 4;  // hi, lo, per-row chunk sums
+constexpr int kXsumOff = 2 * kFragBytes;           // per-row sums of hi + lo over the chunk
+constexpr int kSsOff = kXsumOff + kBM * 4;           // per-row sums of x^2 (raw x) over the chunk
+constexpr int kChunkBytes = kSsOff + kBM * 4;        // a staged chunk in memory
+constexpr int kChunkLds = kSsOff;                    // the part of a chunk the GEMM copies to LDS
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
@@ -91,68 +98,46 @@ __device__ __forceinline__ int frag_offset(int s, int mt, int lane) { return ((s
 
 }  // namespace
 
-// Grid 64 (one workgroup per row of the 64-row operand; rows >= m are zero). Row r of x (f32 at
-// x + r * x_stride), times 1 / rms(row) * gain when gain is set (RMSNorm, shaders.rs:378-403), is
-// written as chunk c = k / 64 of `frag`: hi and lo fragments and the chunk's sum of hi + lo.
+// Writes one value of the x operand of a GEMM: row r, column c, value v (times gain g). The 64
+// lanes of the calling wave hold the 64 columns of one chunk of row r (all lanes call it), so the
+// chunk's sums of hi + lo and of v^2 are wave sums. q4order: the column order of the q4 GEMM's B
+// operand within each 8 columns, [0, 4, 1, 5, 2, 6, 3, 7] (nibbles8); else natural.
+__device__ __forceinline__ void emit_x(uint8_t* __restrict__ frag, int r, int c, float v, float g, int q4order, int lane) {
+    const float xg = v * g;
+    const float hi = (float)(_Float16)xg;
+    const float lo = (float)(_Float16)(xg - hi);
+    const int chunk = c / kChunk, kk = c % kChunk, hf = kk / 32, st = (kk % 32) / 8, i = kk % 8;
+    const int slot = q4order ? 2 * (i % 4) + i / 4 : i;
+    uint8_t* dst = frag + (size_t)chunk * kChunkBytes + frag_offset(st, r >> 5, 32 * hf + (r & 31)) + 2 * slot;
+    *(uint16_t*)dst = __builtin_bit_cast(uint16_t, (_Float16)hi);
+    *(uint16_t*)(dst + kFragBytes) = __builtin_bit_cast(uint16_t, (_Float16)lo);
+    const float xs = wave_sum_dpp(hi + lo), ss = wave_sum_dpp(v * v);
+    if (lane == 0) {
+        float* sums = (float*)(frag + (size_t)chunk * kChunkBytes);
+        sums[kXsumOff / 4 + r] = xs;
+        sums[kSsOff / 4 + r] = ss;
+    }
+}
+
+// 1 / rms of row r from the staged chunk sums of x^2 (the RMSNorm of the GEMM's input, applied to
+// its output: y = (1 / rms) W (x * gain)). Called by every thread of a 256-thread workgroup.
+__device__ __forceinline__ float row_inv_rms(const uint8_t* __restrict__ frag, int nchunks, int K, float eps, int r,
+                                             float* red) {
+    float ss = 0.0f;
+    for (int c = threadIdx.x; c < nchunks; c += 256) ss += ((const float*)(frag + (size_t)c * kChunkBytes))[kSsOff / 4 + r];
+    ss = block_sum(ss, red);
+    return 1.0f / sqrtf(ss / (float)K + eps);
+}
+
+// Grid (ceil(K / 256), 64): the x operand of a GEMM from f32 rows (x + r * x_stride; rows >= m are
+// zero), times `gain` when set; the row's RMSNorm factor is applied by the GEMM's epilogue.
 __global__ __launch_bounds__(256) void k_stage_x(const float* __restrict__ x, int x_stride, int m, int K,
-                                                 const float* __restrict__ gain, float eps, int q4order,
-                                                 uint8_t* __restrict__ frag) {
-    __shared__ float red[16];
-    const int r = blockIdx.x, t = threadIdx.x;
-    const bool live = r < m;
-    const float* row = x + (size_t)(live ? r : 0) * x_stride;
-    float inv = 1.0f;
-    if (gain) {
-        float ss = 0.0f;
-        if (live)
-            for (int k = 4 * t; k < K; k += 1024) {
-                const float4 v = *(const float4*)(row + k);
-                ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
-            }
-        ss = block_sum(ss, red);
-        inv = 1.0f / sqrtf(ss / (float)K + eps);
-    }
-    const int mt = r >> 5, rl = r & 31;
-    // 8 columns per thread per pass; threads 8q .. 8q + 7 cover one chunk
-    for (int base = 0; base < K; base += 2048) {
-        const int k = base + 8 * t;
-        float part = 0.0f;
-        if (k < K) {
-            float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-            if (live) {
-                const float4 a = *(const float4*)(row + k), b = *(const float4*)(row + k + 4);
-                v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
-                if (gain) {
-                    const float4 ga = *(const float4*)(gain + k), gb = *(const float4*)(gain + k + 4);
-                    const float g[8] = {ga.x, ga.y, ga.z, ga.w, gb.x, gb.y, gb.z, gb.w};
-#pragma unroll
-                    for (int e = 0; e < 8; e++) v[e] = v[e] * inv * g[e];
-                }
-            }
-            if (q4order) {  // the q4 GEMM's B operand order [0, 4, 1, 5, 2, 6, 3, 7]
-                const float o[8] = {v[0], v[4], v[1], v[5], v[2], v[6], v[3], v[7]};
-#pragma unroll
-                for (int e = 0; e < 8; e++) v[e] = o[e];
-            }
-            uint32_t ph[4], pl[4];
-#pragma unroll
-            for (int e = 0; e < 8; e += 2) {
-                const float h0 = (float)(_Float16)v[e], h1 = (float)(_Float16)v[e + 1];
-                const float l0 = (float)(_Float16)(v[e] - h0), l1 = (float)(_Float16)(v[e + 1] - h1);
-                ph[e / 2] = pack_h2(h0, h1);
-                pl[e / 2] = pack_h2(l0, l1);
-                part += (h0 + l0) + (h1 + l1);
-            }
-            const int c = k / kChunk, kk = k % kChunk, hf = kk / 32, s = (kk % 32) / 8;
-            uint8_t* dst = frag + (size_t)c * kChunkBytes + frag_offset(s, mt, 32 * hf + rl);
-            *(uint4*)dst = make_uint4(ph[0], ph[1], ph[2], ph[3]);
-            *(uint4*)(dst + kFragBytes) = make_uint4(pl[0], pl[1], pl[2], pl[3]);
-        }
-        part += __shfl_xor(part, 1, 64);
-        part += __shfl_xor(part, 2, 64);
-        part += __shfl_xor(part, 4, 64);
-        if (k < K && (t & 7) == 0) ((float*)(frag + (size_t)(k / kChunk) * kChunkBytes + 2 * kFragBytes))[r] = part;
-    }
+                                                 const float* __restrict__ gain, int q4order, uint8_t* __restrict__ frag) {
+    const int c = blockIdx.x * 256 + threadIdx.x, r = blockIdx.y;
+    if (blockIdx.x * 256 >= K) return;  // whole workgroup; K is a multiple of 64, so waves are whole chunks
+    if ((threadIdx.x & ~63) + blockIdx.x * 256 >= K) return;  // whole wave
+    const float v = r < m ? x[(size_t)r * x_stride + c] : 0.0f;
+    emit_x(frag, r, c, v, gain ? gain[c] : 1.0f, q4order, threadIdx.x & 63);
 }
 
 // Grid (ceil(N / (32 WAVES)), splits); split s covers chunks [s * cps, (s + 1) * cps). Wave w owns
@@ -161,7 +146,7 @@ __global__ __launch_bounds__(256) void k_stage_x(const float* __restrict__ x, in
 template <int KIND, int WAVES, int D>
 __global__ __launch_bounds__(64 * WAVES) void k_gemm(const GemmArgs a) {
     constexpr int kWBytes = KIND == KIND_Q4 ? 1024 + 128 : 4096;  // one wave's W chunk (q4: + scale/zero words)
-    constexpr int kSlot = kChunkBytes + WAVES * kWBytes;
+    constexpr int kSlot = kChunkLds + WAVES * kWBytes;
     constexpr int kXPart = 2 * kFragBytes / WAVES;                 // x bytes each wave copies
     constexpr int kPer = kXPart / 1024 + 1 + (KIND == KIND_Q4 ? 2 : 4);  // DMAs per wave per chunk
     __shared__ __attribute__((aligned(16))) uint8_t ring[D][kSlot];
@@ -181,8 +166,8 @@ __global__ __launch_bounds__(64 * WAVES) void k_gemm(const GemmArgs a) {
 #pragma unroll
         for (int u = 0; u < kXPart / 1024; u++) dma16(src + kXPart * w + 1024 * u + 16 * lane, base + kXPart * w + 1024 * u);
         constexpr int kSumLanes = kBM * 4 / 16 / WAVES;  // lanes copying the chunk sums (16 B each)
-        if (lane < kSumLanes) dma16(src + 2 * kFragBytes + 16 * (kSumLanes * w + lane), base + 2 * kFragBytes + 16 * kSumLanes * w);
-        uint8_t* dst = base + kChunkBytes + w * kWBytes;
+        if (lane < kSumLanes) dma16(src + kXsumOff + 16 * (kSumLanes * w + lane), base + kXsumOff + 16 * kSumLanes * w);
+        uint8_t* dst = base + kChunkLds + w * kWBytes;
         const int c = c0 + j;
         if (KIND == KIND_Q4) {
             dma16((const uint8_t*)a.W + (size_t)nr * (K / 2) + c * 32 + 16 * hf, dst);
@@ -215,7 +200,7 @@ __global__ __launch_bounds__(64 * WAVES) void k_gemm(const GemmArgs a) {
         __syncthreads();  // every wave's part of chunk j has landed; every wave is done with chunk j - 1
         if (j + D - 1 < nch) issue(j + D - 1, next_slot);
         const uint8_t* xs = ring[slot];
-        const uint8_t* ws = ring[slot] + kChunkBytes + w * kWBytes;
+        const uint8_t* ws = ring[slot] + kChunkLds + w * kWBytes;
         uint4 wq;
         if (KIND == KIND_Q4) wq = *(const uint4*)(ws + 16 * lane);
 #pragma unroll
@@ -242,7 +227,7 @@ __global__ __launch_bounds__(64 * WAVES) void k_gemm(const GemmArgs a) {
             // y += s (sum q x) - s z (sum x) over the chunk (scale and zero of the chunk's group)
             const uint32_t szw = *(const uint32_t*)(ws + 1024 + 4 * l32);
             const float sc = lo_h(szw), sz = sc * hi_h(szw);
-            const float* xsum = (const float*)(xs + 2 * kFragBytes);
+            const float* xsum = (const float*)(xs + kXsumOff);
 #pragma unroll
             for (int q = 0; q < 4; q++) {
                 const float4 s0 = *(const float4*)(xsum + 8 * q + 4 * hf);
@@ -262,8 +247,8 @@ __global__ __launch_bounds__(64 * WAVES) void k_gemm(const GemmArgs a) {
         acc0 = grp0;
         acc1 = grp1;
     }
-    if (n >= a.N) return;
     if (!a.direct) {
+        if (n >= a.N) return;
         float* pp = a.part + (size_t)blockIdx.y * kBM * a.N + n;
 #pragma unroll
         for (int j = 0; j < 16; j++) {
@@ -273,56 +258,86 @@ __global__ __launch_bounds__(64 * WAVES) void k_gemm(const GemmArgs a) {
         }
         return;
     }
-    // direct (one split, no SwiGLU): store or residual add
+    // direct (one split, no SwiGLU): 1 / rms of the rows (normed input), then store or residual add
+    float* sinv = (float*)ring[0];
+    __syncthreads();  // ring no longer read
+    if (a.norm) {
+        if (threadIdx.x < kBM) {
+            float ss = 0.0f;
+            for (int c = 0; c < nchunks; c++) ss += ((const float*)(a.frag + (size_t)c * kChunkBytes))[kSsOff / 4 + threadIdx.x];
+            sinv[threadIdx.x] = 1.0f / sqrtf(ss / (float)K + a.eps);
+        }
+    } else if (threadIdx.x < kBM) {
+        sinv[threadIdx.x] = 1.0f;
+    }
+    __syncthreads();
+    if (n >= a.N) return;
 #pragma unroll
     for (int j = 0; j < 16; j++) {
         const int m = 8 * (j / 4) + 4 * hf + (j % 4);
         if (m < a.m) {
             float* d = a.y + (size_t)m * a.y_stride + n;
-            *d = a.epi == EPI_ACCUMULATE ? *d + acc0[j] : acc0[j];
+            const float v = acc0[j] * sinv[m];
+            *d = a.epi == EPI_ACCUMULATE ? *d + v : v;
         }
         if (32 + m < a.m) {
             float* d = a.y + (size_t)(32 + m) * a.y_stride + n;
-            *d = a.epi == EPI_ACCUMULATE ? *d + acc1[j] : acc1[j];
+            const float v = acc1[j] * sinv[32 + m];
+            *d = a.epi == EPI_ACCUMULATE ? *d + v : v;
         }
     }
 }
 
-// y rows r < m, columns c < n_out, from the split partials summed in split order: store, residual
-// add, or SwiGLU silu(gate) * up with gate = column c and up = column c + n_out (matrix rows
-// [gate; up], shaders.rs gemv epilogues).
+// Grid (ceil(n_out / 256), m). Output row r, columns c < n_out, from the split partials summed in
+// split order, times 1 / rms of the row when the GEMM's input was normed: store, residual add, or
+// SwiGLU silu(gate) * up with gate = column c and up = column c + n_out (matrix rows [gate; up],
+// shaders.rs gemv epilogues). With frag_out, the result (times gain_out) is also written as the x
+// operand of the next GEMM (n_out is a multiple of 64, so every wave holds whole chunks).
 __global__ __launch_bounds__(256) void k_gemm_reduce(const GemmArgs a) {
+    __shared__ float red[16];
     const int c = blockIdx.x * 256 + threadIdx.x, r = blockIdx.y;
-    if (c >= a.n_out || r >= a.m) return;
-    float g = 0.0f, u = 0.0f;
-    for (int s = 0; s < a.splits; s++) {
-        const float* p = a.part + ((size_t)s * kBM + r) * a.N;
-        g += p[c];
-        if (a.epi == EPI_SWIGLU) u += p[c + a.n_out];
+    const float inv = a.norm ? row_inv_rms(a.frag, a.K / kChunk, a.K, a.eps, r, red) : 1.0f;
+    if ((threadIdx.x & ~63) + blockIdx.x * 256 >= a.n_out) return;  // whole waves past the outputs
+    const bool live = c < a.n_out;
+    float v = 0.0f;
+    if (live) {
+        float g = 0.0f, u = 0.0f;
+        for (int s = 0; s < a.splits; s++) {
+            const float* p = a.part + ((size_t)s * kBM + r) * a.N;
+            g += p[c];
+            if (a.epi == EPI_SWIGLU) u += p[c + a.n_out];
+        }
+        g *= inv;
+        u *= inv;
+        float* d = a.y ? a.y + (size_t)r * a.y_stride + c : nullptr;
+        if (a.epi == EPI_STORE) v = g;
+        else if (a.epi == EPI_ACCUMULATE) v = *d + g;
+        else v = silu(g) * u;
+        if (d) *d = v;
     }
-    float* d = a.y + (size_t)r * a.y_stride + c;
-    if (a.epi == EPI_STORE) *d = g;
-    else if (a.epi == EPI_ACCUMULATE) *d += g;
-    else *d = silu(g) * u;
+    if (a.frag_out) emit_x(a.frag_out, r, c, v, a.gain_out ? a.gain_out[live ? c : 0] : 1.0f, a.order_out, threadIdx.x & 63);
 }
 
 // h[r] = embedding row tokens[r] (f16 row, or q4 values (q - z) s), shaders.rs:405-434 per row.
+// Grid (ceil(hidden / 256), m). With frag, h * gain is also written as the x operand of the first
+// GEMM.
 __global__ __launch_bounds__(256) void k_embed_rows(int kind, const void* __restrict__ W, const uint32_t* __restrict__ SZ,
                                                     int group, int hidden, const uint32_t* __restrict__ tokens,
-                                                    float* __restrict__ h) {
-    const int r = blockIdx.y;
+                                                    float* __restrict__ h, uint8_t* __restrict__ frag,
+                                                    const float* __restrict__ gain, int q4order) {
+    const int r = blockIdx.y, c = blockIdx.x * 256 + threadIdx.x;
+    if ((threadIdx.x & ~63) + blockIdx.x * 256 >= hidden) return;  // whole waves
     const size_t tok = tokens[r];
-    for (int c = blockIdx.x * 256 + threadIdx.x; c < hidden; c += gridDim.x * 256) {
-        float v;
-        if (kind == KIND_F16) {
-            v = h2f(((const uint16_t*)W)[tok * hidden + c]);
-        } else {
-            const uint32_t word = ((const uint32_t*)W)[tok * (hidden / 8) + c / 8];
-            const uint32_t sz = SZ[tok * (hidden / group) + c / group];
-            v = ((float)((word >> (4 * (c % 8))) & 15u) - hi_h(sz)) * lo_h(sz);
-        }
-        h[(size_t)r * hidden + c] = v;
+    float v;
+    if (kind == KIND_F16) {
+        v = h2f(((const uint16_t*)W)[tok * hidden + c]);
+    } else {
+        const uint32_t word = ((const uint32_t*)W)[tok * (hidden / 8) + c / 8];
+        const uint32_t sz = SZ[tok * (hidden / group) + c / group];
+        v = ((float)((word >> (4 * (c % 8))) & 15u) - hi_h(sz)) * lo_h(sz);
     }
+    h[(size_t)r * hidden + c] = v;
+    if (frag) emit_x(frag, r, c, v, gain ? gain[c] : 1.0f, q4order, threadIdx.x & 63);
 }
 
 // Greedy pick of every logits row (argmax_partial / argmax_final, shaders.rs:635-699): the largest
@@ -398,13 +413,19 @@ bool gemm_shape_ok(int kind, int N, int K, int group, int m) {
 
 size_t gemm_frag_bytes(int K) { return (size_t)(K / kChunk) * kChunkBytes; }
 
+void launch_stage_x(const float* x, int x_stride, int m, int K, const float* gain, int q4order, uint8_t* frag,
+                    hipStream_t st) {
+    hipLaunchKernelGGL(k_stage_x, dim3((K + 255) / 256, kBM), dim3(256), 0, st, x, x_stride, m, K, gain, q4order, frag);
+}
+
 void launch_gemm(GemmArgs a, hipStream_t st) {
     const int nch = a.K / kChunk;
     a.cps = (nch + a.splits - 1) / a.splits;
-    a.direct = a.splits == 1 && a.epi != EPI_SWIGLU;
-    if (a.x)
-        hipLaunchKernelGGL(k_stage_x, dim3(kBM), dim3(256), 0, st, a.x, a.x_stride, a.m, a.K, a.gain, a.eps,
-                           a.kind == KIND_Q4 ? 1 : 0, a.frag);
+    a.direct = a.splits == 1 && a.epi != EPI_SWIGLU && !a.frag_out;
+    if (a.x) {  // stage the x operand here (RMSNorm gain folded in, 1 / rms deferred to the epilogue)
+        launch_stage_x(a.x, a.x_stride, a.m, a.K, a.gain, a.kind == KIND_Q4 ? 1 : 0, a.frag, st);
+        a.norm = a.gain ? 1 : 0;
+    }
     const int waves = gemm_waves(a.N);
     const dim3 grid((a.N + 32 * waves - 1) / (32 * waves), a.splits);
     // ring depths: as many chunk slots as fit in 160 KiB of LDS
@@ -419,8 +440,9 @@ void launch_gemm(GemmArgs a, hipStream_t st) {
 }
 
 void launch_embed_rows(int kind, const void* W, const uint32_t* SZ, int group, int hidden, const uint32_t* tokens, int m,
-                       float* h, hipStream_t st) {
-    hipLaunchKernelGGL(k_embed_rows, dim3((hidden + 255) / 256, m), dim3(256), 0, st, kind, W, SZ, group, hidden, tokens, h);
+                       float* h, uint8_t* frag, const float* gain, int q4order, hipStream_t st) {
+    hipLaunchKernelGGL(k_embed_rows, dim3((hidden + 255) / 256, m), dim3(256), 0, st, kind, W, SZ, group, hidden, tokens,
+                       h, frag, gain, q4order);
 }
 
 void launch_argmax_rows(const float* logits, int m, int V, uint32_t* out, uint32_t* tokens, int32_t* pos,

@@ -92,11 +92,13 @@ struct GdnRowStrides {
 void launch_gdn_decode_rows(const float* proj, float* conv_state, const float* conv_w, float* state, float* out,
                             const float* prm, int heads, int rows, const GdnRowStrides& rs, hipStream_t st);
 
-// y = x W^T for up to 64 rows of x (batched decode), on MFMA. Rows of x are f32 at x + r * x_stride;
-// with `gain` x is RMSNormed (gain, eps) first. The x operand is staged in `frag`
-// (gemm_frag_bytes(K)); with x null, `frag` already holds it. Epilogues as the GEMV (store, residual
-// add, SwiGLU with n_out = N / 2). `part` holds splits * 64 * N floats when the GEMM has more than
-// one split or SwiGLU.
+// y = x W^T for up to 64 rows of x (batched decode), on MFMA. The x operand is staged in `frag`
+// (gemm_frag_bytes(K)): with x set, launch_gemm stages rows x + r * x_stride (times `gain`, the
+// RMSNorm's 1 / rms then applied to the output: norm); with x null, `frag` already holds the
+// operand and `norm` says whether its rows carry a deferred RMSNorm. Epilogues as the GEMV (store,
+// residual add, SwiGLU with n_out = N / 2); y may be null when frag_out is set. With frag_out the
+// result (times gain_out, column order order_out) is also staged as the next GEMM's x operand.
+// `part` holds splits * 64 * N floats unless the GEMM applies the epilogue itself.
 struct GemmArgs {
     const float* x = nullptr;
     int x_stride = 0;
@@ -104,6 +106,7 @@ struct GemmArgs {
     const float* gain = nullptr;
     float eps = 1e-6f;
     uint8_t* frag = nullptr;
+    int norm = 0;
     int kind = KIND_Q4;
     const void* W = nullptr;
     const uint32_t* SZ = nullptr;
@@ -116,14 +119,20 @@ struct GemmArgs {
     float* y = nullptr;
     int y_stride = 0;
     int n_out = 0;
+    uint8_t* frag_out = nullptr;
+    const float* gain_out = nullptr;
+    int order_out = 0;  // 1: the column order of a q4 GEMM's operand
 };
 size_t gemm_frag_bytes(int K);
 int gemm_splits(int kind, int N, int K, int group);
 bool gemm_shape_ok(int kind, int N, int K, int group, int m);
 void launch_gemm(GemmArgs a, hipStream_t st);
-// h[r] = embedding row tokens[r], r < m.
+// The x operand of a GEMM from f32 rows (rows >= m zero), times gain when set.
+void launch_stage_x(const float* x, int x_stride, int m, int K, const float* gain, int q4order, uint8_t* frag,
+                    hipStream_t st);
+// h[r] = embedding row tokens[r], r < m; with frag, h * gain is also staged as a GEMM's x operand.
 void launch_embed_rows(int kind, const void* W, const uint32_t* SZ, int group, int hidden, const uint32_t* tokens, int m,
-                       float* h, hipStream_t st);
+                       float* h, uint8_t* frag, const float* gain, int q4order, hipStream_t st);
 // Greedy pick per row into out[r]; with `tokens`, also tokens[r] = pick and pos[r] += 1.
 void launch_argmax_rows(const float* logits, int m, int V, uint32_t* out, uint32_t* tokens, int32_t* pos,
                         hipStream_t st);
