@@ -51,6 +51,10 @@ int qne_prefill(qne_model* m, const uint32_t* ids, size_t n);
 /* Model::prefill_chunk -- model.rs:349 (prefill_batched / prefill_from are start = 0 /
  * finish_logits = 1 forms, model.rs:339-346). Continues the state at `start`. With
  * finish_logits, computes the logits after the last id and the greedy pick (last_token).
+ * Like the reference's batched prefill (batch.rs), it runs the prompt in passes of 64 tokens
+ * through the batched MFMA GEMM; the state equals qne_prefill's to f32 rounding, and does not
+ * depend on how the prompt is split into calls. Models whose shapes the batched kernels do not
+ * take run it token by token.
  * QNE_EINVAL if n == 0, QNE_ECONTEXT if start + n >= max_context. */
 int qne_prefill_chunk(qne_model* m, const uint32_t* ids, size_t n, uint32_t start, int finish_logits);
 /* Model::logits -- model.rs:374. Copies vocab floats; QNE_EINVAL if cap < vocab. */

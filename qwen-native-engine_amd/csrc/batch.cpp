@@ -23,6 +23,61 @@ int attn_splits_for(int rows, int nkv, int max_blocks) {
 }
 }  // namespace
 
+int operand_order(const DevMat& W) { return W.kind == KIND_Q4 ? 1 : 0; }
+
+void rows_gemm(const DevMat& W, int n, float eps, uint8_t* frag, int norm, float* part, float* y, int y_stride, int epi,
+               uint8_t* frag_out, const float* gain_out, int order_out, hipStream_t st) {
+    GemmArgs a;
+    a.m = n;
+    a.frag = frag;
+    a.norm = norm;
+    a.eps = eps;
+    a.kind = W.kind;
+    a.W = W.w;
+    a.SZ = W.sz;
+    a.N = W.rows;
+    a.K = W.k;
+    a.group = W.group;
+    a.splits = gemm_splits(W.kind, W.rows, W.k, W.group);
+    a.part = part;
+    a.epi = epi;
+    a.y = y;
+    a.y_stride = y_stride;
+    a.n_out = epi == EPI_SWIGLU ? W.rows / 2 : W.rows;
+    a.frag_out = frag_out;
+    a.gain_out = gain_out;
+    a.order_out = order_out;
+    launch_gemm(a, st);
+}
+
+void rows_shapes_check(const ModelConfig& c) {
+    const int G = c.n_kv_heads > 0 ? c.n_q_heads / c.n_kv_heads : 0;
+    if (c.gdn_dk != 128 || c.gdn_dv != 128 || c.head_dim != 256 || c.n_kv_heads <= 0 ||
+        c.n_q_heads % c.n_kv_heads != 0 || (G != 1 && G != 2 && G != 4) || c.hidden % 64 != 0 ||
+        c.intermediate % 64 != 0)
+        throw Error(QNE_EFORMAT, "unsupported shapes for the batched path (GDN 128 x 128, head_dim 256, "
+                                 "1, 2 or 4 query heads per kv head, hidden and intermediate multiples of 64)");
+}
+
+void rows_workspace(const std::vector<DevLayer>& layers, const DevMat& head, size_t* part_floats, size_t* frag_bytes) {
+    size_t part = 0, frag = 0;
+    // layer GEMMs write partials even with one split (their reduce stages the next operand); the
+    // LM head only when it has more than one
+    auto need = [&](const DevMat& W, bool layer) {
+        if (!gemm_shape_ok(W.kind, W.rows, W.k, W.group, 1) || W.k % 4 != 0)
+            throw Error(QNE_EFORMAT, "unsupported matrix shape for the batched GEMM (k must be a multiple of 64, "
+                                     "q4 groups a multiple of 64)");
+        const int s = gemm_splits(W.kind, W.rows, W.k, W.group);
+        if (layer || s > 1) part = std::max(part, (size_t)s * kRowsMax * W.rows);
+        frag = std::max(frag, gemm_frag_bytes(W.k));
+    };
+    for (const DevLayer& L : layers)
+        for (const DevMat* W : {&L.in, &L.out, &L.gate_up, &L.down}) need(*W, true);
+    need(head, false);
+    *part_floats = part;
+    *frag_bytes = frag;
+}
+
 void* BatchDecoder::dalloc(size_t bytes) {
     void* p = nullptr;
     QNE_HIP(hipMalloc(&p, bytes ? bytes : 16));
@@ -37,13 +92,9 @@ BatchDecoder::BatchDecoder(Model& m, int max_rows, int max_context) : m_(m), max
     if (max_context < 1 || max_context > m.max_context_)
         throw Error(QNE_ECONTEXT, "batch context must be 1.." + std::to_string(m.max_context_));
     const ModelConfig& c = m.cfg_;
-    for (const DevLayer& L : m.layers_)
-        for (const DevMat* W : {&L.in, &L.out, &L.gate_up, &L.down})
-            if (!gemm_shape_ok(W->kind, W->rows, W->k, W->group, 1) || W->k % 4 != 0)
-                throw Error(QNE_EFORMAT, "unsupported matrix shape for the batched GEMM (k must be a multiple of 64, "
-                                         "q4 groups a multiple of 64)");
-    if (!gemm_shape_ok(m.lm_head_.kind, m.lm_head_.rows, m.lm_head_.k, m.lm_head_.group, 1))
-        throw Error(QNE_EFORMAT, "unsupported LM head shape for the batched GEMM");
+    rows_shapes_check(c);
+    size_t part = 0, frag = 0;
+    rows_workspace(m.layers_, m.lm_head_, &part, &frag);
     QNE_HIP(hipSetDevice(m.device_));
     QNE_HIP(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking));
     QNE_HIP(hipEventCreate(&ev0_));
@@ -86,19 +137,6 @@ BatchDecoder::BatchDecoder(Model& m, int max_rows, int max_context) : m_(m), max
         act_ = (float*)dalloc((size_t)kRowsMax * c.intermediate * 4);
         logits_ = (float*)dalloc((size_t)kRowsMax * c.vocab * 4);
         qbuf_ = (float*)dalloc((size_t)kRowsMax * c.n_q_heads * c.head_dim * 4);
-        size_t part = 0, frag = 0;
-        auto need_part = [&](const DevMat& W, bool swiglu) {
-            const int s = gemm_splits(W.kind, W.rows, W.k, W.group);
-            if (s > 1 || swiglu) part = std::max(part, (size_t)s * kRowsMax * W.rows);
-            frag = std::max(frag, gemm_frag_bytes(W.k));
-        };
-        for (const DevLayer& L : m.layers_) {
-            need_part(L.in, false);
-            need_part(L.out, false);
-            need_part(L.gate_up, true);
-            need_part(L.down, false);
-        }
-        need_part(m.lm_head_, false);
         part_ = (float*)dalloc(part * 4);
         frag_a_ = (uint8_t*)dalloc(frag);
         frag_b_ = (uint8_t*)dalloc(frag);
@@ -149,33 +187,13 @@ void BatchDecoder::check_row(int row) const {
 // gains are folded in there and the 1 / rms factors applied by the consuming GEMM.
 void BatchDecoder::enqueue_step(int n) {
     const ModelConfig& c = m_.cfg_;
-    const auto order = [](const DevMat& W) { return W.kind == KIND_Q4 ? 1 : 0; };
+    const auto order = operand_order;
     const DevLayer& first = m_.layers_.front();
     launch_embed_rows(m_.embed_.kind, m_.embed_.w, m_.embed_.sz, m_.embed_.group, c.hidden, tokens_, n, h_, frag_a_,
                       first.input_norm, order(first.in), stream_);
     auto gemm = [&](const DevMat& W, uint8_t* frag, int norm, float* y, int y_stride, int epi, uint8_t* frag_out,
                     const float* gain_out, int order_out) {
-        GemmArgs a;
-        a.m = n;
-        a.frag = frag;
-        a.norm = norm;
-        a.eps = c.eps;
-        a.kind = W.kind;
-        a.W = W.w;
-        a.SZ = W.sz;
-        a.N = W.rows;
-        a.K = W.k;
-        a.group = W.group;
-        a.splits = gemm_splits(W.kind, W.rows, W.k, W.group);
-        a.part = part_;
-        a.epi = epi;
-        a.y = y;
-        a.y_stride = y_stride;
-        a.n_out = epi == EPI_SWIGLU ? W.rows / 2 : W.rows;
-        a.frag_out = frag_out;
-        a.gain_out = gain_out;
-        a.order_out = order_out;
-        launch_gemm(a, stream_);
+        rows_gemm(W, n, c.eps, frag, norm, part_, y, y_stride, epi, frag_out, gain_out, order_out, stream_);
     };
     const int splits = attn_splits_for(n, c.n_kv_heads, max_blocks_);
     for (size_t li = 0; li < m_.layers_.size(); li++) {
@@ -203,6 +221,7 @@ void BatchDecoder::enqueue_step(int n) {
             a.splits = splits;
             a.max_blocks = max_blocks_;
             a.rows = n;
+            a.bt_stride = max_blocks_;
             launch_attention_rows(a, stream_);
         } else {
             GdnRowStrides rs;

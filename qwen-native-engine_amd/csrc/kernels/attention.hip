@@ -66,7 +66,8 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_prep(AttnModelArgs a) {
 }
 
 // Batched model form, grid (nq + nkv, rows): row b reads its projection at proj + b * proj_stride,
-// sits at position pos[b] and appends into its own block table row.
+// sits at position pos[b] and appends through block table row block_table + b * bt_stride (rows of
+// one sequence share a row: bt_stride 0).
 __global__ __launch_bounds__(kAttnThreads) void k_attn_prep_rows(AttnRowsArgs a) {
     __shared__ float sh[kHD];
     __shared__ float red[16];
@@ -80,7 +81,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_prep_rows(AttnRowsArgs a)
         const int g = hb - a.nq;
         const float* kp = proj + 2 * a.nq * kHD;
         const float kr = norm_rope(kp[g * kHD + t], a.norms + kHD, a.inv_freq, a.rope_dim, pos, sh, red);
-        const size_t at = kv_index(a.block_table + (size_t)b * a.max_blocks, (int)pos, a.nkv, g) + t;
+        const size_t at = kv_index(a.block_table + (size_t)b * a.bt_stride, (int)pos, a.nkv, g) + t;
         a.k_pool[at] = f2h(kr);
         a.v_pool[at] = f2h(kp[a.nkv * kHD + g * kHD + t]);
     }
@@ -109,7 +110,7 @@ template <int G>
 __global__ __launch_bounds__(kAttnThreads) void k_attn_partial(const float* __restrict__ q, const uint16_t* __restrict__ k_pool,
                                                                const uint16_t* __restrict__ v_pool,
                                                                const int32_t* __restrict__ block_table, int max_blocks,
-                                                               const int32_t* __restrict__ lens, int nkv,
+                                                               int bt_stride, const int32_t* __restrict__ lens, int nkv,
                                                                float* __restrict__ part_ml, float* __restrict__ part_acc) {
     __shared__ float s_ml[4][G][2];
     __shared__ __attribute__((aligned(16))) float s_acc[4][G][kHD];
@@ -119,7 +120,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_partial(const float* __re
     int per = (len + splits - 1) / splits;
     per = (per + kBlock - 1) / kBlock * kBlock;
     const int p0 = split * per, p1 = min(len, p0 + per);
-    const int32_t* bt = block_table + (size_t)b * max_blocks;
+    const int32_t* bt = block_table + (size_t)b * bt_stride;
     const int nq = nkv * G;
     constexpr float kScale = 1.4426950408889634f * 0.0625f;  // log2(e) / sqrt(256)
 
@@ -234,17 +235,19 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_combine(const float* __re
 
 template <int G>
 static void launch_partial(const float* q, const uint16_t* kp, const uint16_t* vp, const int32_t* bt, int max_blocks,
-                           const int32_t* lens, int nkv, float* ml, float* acc, int splits, int batch, hipStream_t st) {
+                           int bt_stride, const int32_t* lens, int nkv, float* ml, float* acc, int splits, int batch,
+                           hipStream_t st) {
     hipLaunchKernelGGL((k_attn_partial<G>), dim3(splits, nkv, batch), dim3(kAttnThreads), 0, st, q, kp, vp, bt,
-                       max_blocks, lens, nkv, ml, acc);
+                       max_blocks, bt_stride, lens, nkv, ml, acc);
 }
 
 static void partial_by_g(int G, const float* q, const uint16_t* kp, const uint16_t* vp, const int32_t* bt, int max_blocks,
-                         const int32_t* lens, int nkv, float* ml, float* acc, int splits, int batch, hipStream_t st) {
+                         int bt_stride, const int32_t* lens, int nkv, float* ml, float* acc, int splits, int batch,
+                         hipStream_t st) {
     switch (G) {
-        case 1: launch_partial<1>(q, kp, vp, bt, max_blocks, lens, nkv, ml, acc, splits, batch, st); break;
-        case 2: launch_partial<2>(q, kp, vp, bt, max_blocks, lens, nkv, ml, acc, splits, batch, st); break;
-        default: launch_partial<4>(q, kp, vp, bt, max_blocks, lens, nkv, ml, acc, splits, batch, st); break;
+        case 1: launch_partial<1>(q, kp, vp, bt, max_blocks, bt_stride, lens, nkv, ml, acc, splits, batch, st); break;
+        case 2: launch_partial<2>(q, kp, vp, bt, max_blocks, bt_stride, lens, nkv, ml, acc, splits, batch, st); break;
+        default: launch_partial<4>(q, kp, vp, bt, max_blocks, bt_stride, lens, nkv, ml, acc, splits, batch, st); break;
     }
 }
 
@@ -252,8 +255,8 @@ void launch_attention_model(const AttnModelArgs& a, hipStream_t st) {
     hipLaunchKernelGGL(k_attn_prep, dim3(a.nq + a.nkv), dim3(kAttnThreads), 0, st, a);
     const int G = a.nq / a.nkv;
     // tok[1] is the position; the partial kernel attends lens[0] + 1 = pos + 1 positions.
-    partial_by_g(G, a.qbuf, a.k_pool, a.v_pool, a.block_table, a.max_blocks, (const int32_t*)(a.tok + 1), a.nkv,
-                 a.part_ml, a.part_acc, a.splits, 1, st);
+    partial_by_g(G, a.qbuf, a.k_pool, a.v_pool, a.block_table, a.max_blocks, a.max_blocks, (const int32_t*)(a.tok + 1),
+                 a.nkv, a.part_ml, a.part_acc, a.splits, 1, st);
     hipLaunchKernelGGL(k_attn_combine, dim3(a.nq, 1), dim3(kAttnThreads), 0, st, a.part_ml, a.part_acc, a.nkv, G,
                        a.splits, a.proj + a.nq * kHD, 0, a.out);
 }
@@ -261,8 +264,8 @@ void launch_attention_model(const AttnModelArgs& a, hipStream_t st) {
 void launch_attention_rows(const AttnRowsArgs& a, hipStream_t st) {
     hipLaunchKernelGGL(k_attn_prep_rows, dim3(a.nq + a.nkv, a.rows), dim3(kAttnThreads), 0, st, a);
     const int G = a.nq / a.nkv;
-    partial_by_g(G, a.qbuf, a.k_pool, a.v_pool, a.block_table, a.max_blocks, a.pos, a.nkv, a.part_ml, a.part_acc,
-                 a.splits, a.rows, st);
+    partial_by_g(G, a.qbuf, a.k_pool, a.v_pool, a.block_table, a.max_blocks, a.bt_stride, a.pos, a.nkv, a.part_ml,
+                 a.part_acc, a.splits, a.rows, st);
     hipLaunchKernelGGL(k_attn_combine, dim3(a.nq, a.rows), dim3(kAttnThreads), 0, st, a.part_ml, a.part_acc, a.nkv, G,
                        a.splits, a.proj + a.nq * kHD, (int)a.proj_stride, a.out);
 }
@@ -273,7 +276,7 @@ void launch_paged_attn(const float* q, const float* k_new, const float* v_new, u
     hipLaunchKernelGGL(k_kv_append, dim3(nkv, batch), dim3(kAttnThreads), 0, st, k_new, v_new, k_pool, v_pool,
                        block_table, max_blocks, ctx, nkv);
     const int G = nq / nkv;
-    partial_by_g(G, q, k_pool, v_pool, block_table, max_blocks, ctx, nkv, part_ml, part_acc, splits, batch, st);
+    partial_by_g(G, q, k_pool, v_pool, block_table, max_blocks, max_blocks, ctx, nkv, part_ml, part_acc, splits, batch, st);
     hipLaunchKernelGGL(k_attn_combine, dim3(nq, batch), dim3(kAttnThreads), 0, st, part_ml, part_acc, nkv, G, splits,
                        (const float*)nullptr, 0, out);
 }

@@ -176,20 +176,23 @@ __device__ __forceinline__ float row16_sum(float v) {
 // each for the lane's shares of (S^T k)_col and (S^T q)_col and of k.q, three 16-lane DPP sums
 // (no cross-row traffic), and 8 state FMAs; the next tokens' inputs load while one runs. The
 // waves are independent (no LDS, no barrier), so B * H * 32 of them run at once.
-// Layouts: q,k [B][T][H][dk], v,out [B][T][H][dv], beta,g [B][T][H], state [B][H][dk][dv].
+// Layouts: q,k [B][T][H][dk], v,out [B][T][H][dv], beta,g [B][T][H], state [B][H][dk][dv], or with
+// value_major the model's [B][H][dv][dk] (a lane's 8 keys then contiguous).
 __global__ __launch_bounds__(256) void k_delta_rule_cols(const float* __restrict__ q, const float* __restrict__ k,
                                                          const float* __restrict__ v, const float* __restrict__ beta,
                                                          const float* __restrict__ g, float* __restrict__ state,
-                                                         float* __restrict__ out, int T, int H, int waves) {
+                                                         float* __restrict__ out, int T, int H, int waves,
+                                                         int value_major) {
     const int lane = threadIdx.x & (kWave - 1), r = lane >> 4, i = lane & 15;
     const int gw = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     if (gw >= waves) return;
     constexpr int kGroups = kDV / 4;
     const int col = 4 * (gw % kGroups) + r, bh = gw / kGroups, h = bh % H, b = bh / H;
-    float* S = state + (size_t)bh * kDK * kDV + (size_t)(8 * i) * kDV + col;
+    const size_t jstride = value_major ? 1 : kDV;
+    float* S = state + (size_t)bh * kDK * kDV + (value_major ? (size_t)col * kDK + 8 * i : (size_t)(8 * i) * kDV + col);
     float s[8];
 #pragma unroll
-    for (int j = 0; j < 8; j++) s[j] = S[(size_t)j * kDV];
+    for (int j = 0; j < 8; j++) s[j] = S[j * jstride];
     struct In {
         float4 k0, k1, q0, q1;
         float v, beta, g;
@@ -238,7 +241,88 @@ __global__ __launch_bounds__(256) void k_delta_rule_cols(const float* __restrict
         }
     }
 #pragma unroll
-    for (int j = 0; j < 8; j++) S[(size_t)j * kDV] = s[j];
+    for (int j = 0; j < 8; j++) S[j * jstride] = s[j];
+}
+
+// Prefill of a chunk of T tokens of one sequence, before the recurrence. Grid (T, H), 384 threads
+// (the head's q, k, v channels). Token n's projection row is proj + n * proj_stride. Causal conv
+// + SiLU (shaders.rs:457-468) with the inputs of tokens n-3..n-1 taken from the chunk or, before
+// it, from conv_state (read only; k_gdn_chunk_post shifts it); L2 norms of q (times 128^-1/2) and
+// k; g = exp(A_neg_exp ln(1 + e^(a + dt_bias))), beta = sigmoid(b) (:489-496). Outputs in the
+// layouts of k_delta_rule_cols: q, k [T][H][dk], v [T][H][dv], g, beta [T][H].
+__global__ __launch_bounds__(384) void k_gdn_chunk_prep(const float* __restrict__ proj, int proj_stride,
+                                                        const float* __restrict__ conv_state,
+                                                        const float* __restrict__ conv_w, const float* __restrict__ prm,
+                                                        int H, float* __restrict__ qo, float* __restrict__ ko,
+                                                        float* __restrict__ vo, float* __restrict__ go,
+                                                        float* __restrict__ bo) {
+    __shared__ float red[8];
+    const int n = blockIdx.x, h = blockIdx.y, t = threadIdx.x, lane = t % kWave, w = t / kWave;
+    const int ch = t < 128 ? h * kDK + t : (t < 256 ? H * kDK + h * kDK + (t - 128) : 2 * H * kDK + h * kDV + (t - 256));
+    const float* st = conv_state + (size_t)ch * 4;
+    const float* cw = conv_w + (size_t)ch * 4;
+    auto input = [&](int m) { return m >= 0 ? proj[(size_t)m * proj_stride + ch] : st[3 + m]; };
+    const float y = input(n - 3) * cw[0] + input(n - 2) * cw[1] + input(n - 1) * cw[2] + input(n) * cw[3];
+    const float val = silu(y);
+    const float ss = wave_sum(val * val);
+    if (lane == 0) red[w] = ss;
+    __syncthreads();
+    const size_t nh = (size_t)n * H + h;
+    if (t < 128) qo[nh * kDK + t] = val * (1.0f / sqrtf(red[0] + red[1] + 1e-6f)) * 0.08838834764831845f;
+    else if (t < 256) ko[nh * kDK + t - 128] = val * (1.0f / sqrtf(red[2] + red[3] + 1e-6f));
+    else vo[nh * kDV + t - 256] = val;
+    if (t == 0) {
+        const float* row = proj + (size_t)n * proj_stride;
+        const int zoff = 2 * H * kDK + 2 * H * kDV;  // a[H] then b[H] follow z
+        const float a = row[zoff + h], b = row[zoff + H + h];
+        go[nh] = expf(prm[H + h] * logf(1.0f + expf(a + prm[h])));
+        bo[nh] = 1.0f / (1.0f + expf(-b));
+    }
+}
+
+// After the recurrence. Grid (T, H), 384 threads. Gated RMSNorm of token n's head output
+// (shaders.rs:514-516) into mixed + n * mixed_stride; the workgroups of the last token also shift
+// the conv state by the chunk (the inputs of the chunk's last three tokens).
+__global__ __launch_bounds__(384) void k_gdn_chunk_post(const float* __restrict__ proj, int proj_stride,
+                                                        float* __restrict__ conv_state, const float* __restrict__ prm,
+                                                        int H, int T, const float* __restrict__ o,
+                                                        float* __restrict__ mixed, int mixed_stride) {
+    __shared__ float red[8];
+    const int n = blockIdx.x, h = blockIdx.y, t = threadIdx.x, lane = t % kWave, w = t / kWave;
+    const float* row = proj + (size_t)n * proj_stride;
+    const float v = t < kDV ? o[((size_t)n * H + h) * kDV + t] : 0.0f;
+    const float ss = wave_sum(v * v);
+    if (lane == 0) red[w] = ss;
+    __syncthreads();
+    if (t < kDV) {
+        const float inv = 1.0f / sqrtf((red[0] + red[1]) / (float)kDV + 1e-6f);
+        const float z = row[2 * H * kDK + H * kDV + h * kDV + t];
+        mixed[(size_t)n * mixed_stride + h * kDV + t] = v * inv * silu(z) * prm[2 * H + t];
+    }
+    if (n == T - 1) {
+        const int ch = t < 128 ? h * kDK + t : (t < 256 ? H * kDK + h * kDK + (t - 128) : 2 * H * kDK + h * kDV + (t - 256));
+        float* st = conv_state + (size_t)ch * 4;
+        float in[3];
+#pragma unroll
+        for (int j = 0; j < 3; j++) {
+            const int m = T - 3 + j;
+            in[j] = m >= 0 ? proj[(size_t)m * proj_stride + ch] : st[3 + m];
+        }
+#pragma unroll
+        for (int j = 0; j < 3; j++) st[j] = in[j];
+    }
+}
+
+void launch_gdn_chunk(const float* proj, int proj_stride, float* conv_state, const float* conv_w, float* state,
+                      const float* prm, int heads, int tokens, float* q, float* k, float* v, float* g, float* beta,
+                      float* o, float* mixed, int mixed_stride, hipStream_t st) {
+    hipLaunchKernelGGL(k_gdn_chunk_prep, dim3(tokens, heads), dim3(384), 0, st, proj, proj_stride, conv_state, conv_w,
+                       prm, heads, q, k, v, g, beta);
+    const int waves = heads * (kDV / 4);
+    hipLaunchKernelGGL(k_delta_rule_cols, dim3((waves + 3) / 4), dim3(256), 0, st, q, k, v, beta, g, state, o, tokens,
+                       heads, waves, 1);
+    hipLaunchKernelGGL(k_gdn_chunk_post, dim3(tokens, heads), dim3(384), 0, st, proj, proj_stride, conv_state, prm,
+                       heads, tokens, o, mixed, mixed_stride);
 }
 
 void launch_gdn_decode(const float* proj, float* conv_state, const float* conv_w, float* state, float* out,
@@ -262,7 +346,7 @@ void launch_delta_rule_chunked(const float* q, const float* k, const float* v, c
                                float* state, float* out, int batch, int tokens, int heads, hipStream_t st) {
     const int waves = batch * heads * (kDV / 4);
     hipLaunchKernelGGL(k_delta_rule_cols, dim3((waves + 3) / 4), dim3(256), 0, st, q, k, v, beta, g, state, out, tokens,
-                       heads, waves);
+                       heads, waves, 0);
 }
 
 }  // namespace qne

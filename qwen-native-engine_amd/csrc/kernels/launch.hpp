@@ -82,6 +82,7 @@ struct AttnRowsArgs {
     float* part_acc;             // [rows][nkv][splits][group][hd]
     float* out;                  // [rows][nq][hd]
     int nq, nkv, rope_dim, splits, max_blocks, rows;
+    int bt_stride;               // entries between rows of block_table (0: one shared row)
 };
 void launch_attention_rows(const AttnRowsArgs& a, hipStream_t st);
 
@@ -89,6 +90,12 @@ void launch_attention_rows(const AttnRowsArgs& a, hipStream_t st);
 struct GdnRowStrides {
     size_t proj = 0, conv = 0, state = 0, out = 0;
 };
+// Prefill of `tokens` consecutive tokens of one sequence: conv + norms + gates, the recurrence on
+// the model's value-major state, the gated RMSNorm into mixed + n * mixed_stride, the conv state
+// shifted by the chunk. q, k, v, o: tokens * heads * 128 floats of scratch; g, beta: tokens * heads.
+void launch_gdn_chunk(const float* proj, int proj_stride, float* conv_state, const float* conv_w, float* state,
+                      const float* prm, int heads, int tokens, float* q, float* k, float* v, float* g, float* beta,
+                      float* o, float* mixed, int mixed_stride, hipStream_t st);
 void launch_gdn_decode_rows(const float* proj, float* conv_state, const float* conv_w, float* state, float* out,
                             const float* prm, int heads, int rows, const GdnRowStrides& rs, hipStream_t st);
 

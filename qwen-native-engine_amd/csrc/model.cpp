@@ -1,6 +1,7 @@
 // Model: load, state, per-token graph and the prefill / step / decode protocol of
 // kernels/src/model.rs, on HIP.
 #include "model.hpp"
+#include "prefill.hpp"
 
 #include <algorithm>
 #include <chrono>
@@ -108,6 +109,8 @@ Model::~Model() { release(); }
 void Model::release() {
     if (device_ >= 0) (void)hipSetDevice(device_);
     if (stream_) (void)hipStreamSynchronize(stream_);
+    delete chunk_;
+    chunk_ = nullptr;
     for (hipGraphExec_t g : {g_layers_, g_head_logits_, g_head_greedy_})
         if (g) (void)hipGraphExecDestroy(g);
     g_layers_ = g_head_logits_ = g_head_greedy_ = nullptr;
@@ -641,6 +644,22 @@ void Model::prefill_chunk(const uint32_t* ids, size_t n, uint32_t start, bool fi
     check_ids(ids, n, cfg_.vocab);
     std::memcpy(host_ids_, ids, n * 4);
     QNE_HIP(hipMemcpyAsync(ids_, host_ids_, n * 4, hipMemcpyHostToDevice, stream_));
+    // The reference runs this path through its batched GEMM (batch.rs); so does this one, 64
+    // tokens per pass, unless the shapes do not fit the batched GEMM.
+    if (!chunk_tried_) {
+        chunk_tried_ = true;
+        try {
+            chunk_ = new ChunkPrefill(*this);
+        } catch (const Error& e) {
+            if (e.code != QNE_EFORMAT) throw;
+            chunk_ = nullptr;
+        }
+    }
+    if (chunk_) {
+        chunk_->run(ids_, n, start, finish_logits);
+        sync();
+        return;
+    }
     if (persistent_) {
         // tok is only written by the greedy pick, so without finish_logits it stays as it was
         if (finish_logits) QNE_HIP(hipMemsetAsync(tok_ + 2, 0, 4, stream_));

@@ -52,6 +52,8 @@ struct EngineRun {
 
 LoadOptions parse_options(const char* json);
 
+class ChunkPrefill;
+
 class Model {
   public:
     Model(const ModelIndex& ix, const uint8_t* weights, uint64_t wlen, const LoadOptions& opt);
@@ -84,6 +86,7 @@ class Model {
 
   private:
     friend class BatchDecoder;
+    friend class ChunkPrefill;
     void release();
     void upload(const ModelIndex& ix, const uint8_t* weights);
     void alloc_state();
@@ -146,6 +149,9 @@ class Model {
     size_t last_decode_steps_ = 0;
     size_t dispatches_ = 0;
     size_t launches_ = 0;  // kernel launches counted while recording
+    // prefill_chunk on the batched GEMM (created on first use; null when the shapes do not fit it)
+    ChunkPrefill* chunk_ = nullptr;
+    bool chunk_tried_ = false;
 };
 
 }  // namespace qne

@@ -1,0 +1,51 @@
+// Chunked prefill on the batched GEMM: Model::prefill_chunk (kernels/src/model.rs:349-372) runs
+// the prompt 64 tokens per pass, as the reference's prefill_batched runs 16 (kernels/src/batch.rs).
+// A chunk's tokens are the rows of one pass through the layers: every projection is one MFMA GEMM
+// over the chunk, attention appends the chunk's K/V and each token attends positions up to its own
+// (causal by construction), and the GDN recurrence runs over the chunk's tokens in order on the
+// model's state. The LM head runs on the last token only.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <map>
+#include <vector>
+
+#include "model.hpp"
+
+namespace qne {
+
+class ChunkPrefill {
+  public:
+    static constexpr int kChunk = 64;
+    explicit ChunkPrefill(Model& m);
+    ~ChunkPrefill();
+    ChunkPrefill(const ChunkPrefill&) = delete;
+    ChunkPrefill& operator=(const ChunkPrefill&) = delete;
+
+    // Tokens ids_dev[0..n) (device) at positions start..start+n-1 on the model's state; with
+    // finish_logits, the LM head and greedy pick of the last one (tok = [pick, start + n]).
+    void run(const uint32_t* ids_dev, size_t n, uint32_t start, bool finish_logits);
+
+  private:
+    void release();
+    void* dalloc(size_t bytes);
+    void enqueue_chunk(int n);
+    hipGraphExec_t graph_for(int n);
+
+    Model& m_;
+    hipStream_t st_;
+    std::vector<void*> allocations_;
+    std::map<int, hipGraphExec_t> graphs_;
+    int proj_w_ = 0, mixed_w_ = 0, splits_ = 1;
+    uint32_t* ids_ = nullptr;  // the chunk's token ids
+    int32_t* pos_ = nullptr;   // the chunk's positions
+    int32_t* host_pos_ = nullptr;  // pinned
+    float *h_ = nullptr, *proj_ = nullptr, *mixed_ = nullptr, *qbuf_ = nullptr, *part_ = nullptr;
+    float *attn_ml_ = nullptr, *attn_acc_ = nullptr;
+    float *gq_ = nullptr, *gk_ = nullptr, *gv_ = nullptr, *go_ = nullptr, *gg_ = nullptr, *gb_ = nullptr;
+    uint8_t *frag_a_ = nullptr, *frag_b_ = nullptr;
+};
+
+}  // namespace qne
