@@ -149,6 +149,7 @@ BatchDecoder::BatchDecoder(Model& m, int max_rows, int max_context) : m_(m), max
         attn_acc_ = (float*)dalloc(attn_part_rows_ * c.n_kv_heads * G * c.head_dim * 4);
         tokens_ = (uint32_t*)dalloc(kRowsMax * 4);
         picks_ = (uint32_t*)dalloc(kRowsMax * 4);
+        am_scratch_ = dalloc(argmax_rows_scratch(kRowsMax));
         pos_ = (int32_t*)dalloc(kRowsMax * 4);
         QNE_HIP(hipMemset(tokens_, 0, kRowsMax * 4));
         QNE_HIP(hipMemset(pos_, 0, kRowsMax * 4));
@@ -243,7 +244,7 @@ void BatchDecoder::enqueue_step(int n) {
         gemm(L.down, frag_b_, 0, h_, c.hidden, EPI_ACCUMULATE, frag_a_, next_gain, next_order);
     }
     gemm(m_.lm_head_, frag_a_, 1, logits_, c.vocab, EPI_STORE, nullptr, nullptr, 0);
-    launch_argmax_rows(logits_, n, c.vocab, picks_, tokens_, pos_, stream_);
+    launch_argmax_rows(logits_, n, c.vocab, picks_, tokens_, pos_, am_scratch_, stream_);
 }
 
 hipGraphExec_t BatchDecoder::graph_for(int n) {

@@ -302,10 +302,22 @@ __global__ __launch_bounds__(256) void k_gemm_reduce(const GemmArgs a) {
     float v = 0.0f;
     if (live) {
         float g = 0.0f, u = 0.0f;
-        for (int s = 0; s < a.splits; s++) {
-            const float* p = a.part + ((size_t)s * kBM + r) * a.N;
-            g += p[c];
-            if (a.epi == EPI_SWIGLU) u += p[c + a.n_out];
+        const float* p = a.part + (size_t)r * a.N + c;
+        const size_t ss = (size_t)kBM * a.N;  // between splits
+        // loads of four splits in flight at a time; the sum stays in split order
+        int s = 0;
+        for (; s + 4 <= a.splits; s += 4) {
+            const float g0 = p[s * ss], g1 = p[(s + 1) * ss], g2 = p[(s + 2) * ss], g3 = p[(s + 3) * ss];
+            g = g + g0 + g1 + g2 + g3;
+            if (a.epi == EPI_SWIGLU) {
+                const float u0 = p[s * ss + a.n_out], u1 = p[(s + 1) * ss + a.n_out];
+                const float u2 = p[(s + 2) * ss + a.n_out], u3 = p[(s + 3) * ss + a.n_out];
+                u = u + u0 + u1 + u2 + u3;
+            }
+        }
+        for (; s < a.splits; s++) {
+            g += p[s * ss];
+            if (a.epi == EPI_SWIGLU) u += p[s * ss + a.n_out];
         }
         g *= inv;
         u *= inv;
@@ -341,17 +353,22 @@ __global__ __launch_bounds__(256) void k_embed_rows(int kind, const void* __rest
 }
 
 // Greedy pick of every logits row (argmax_partial / argmax_final, shaders.rs:635-699): the largest
-// value, ties to the lower index. With `tokens`, row r's pick becomes its next token and its
-// position advances (pos[r] += 1), so decode steps chain on the device.
-__global__ __launch_bounds__(512) void k_argmax_rows(const float* __restrict__ logits, int V, uint32_t* __restrict__ out,
-                                                     uint32_t* __restrict__ tokens, int32_t* __restrict__ pos) {
-    __shared__ float sv[8];
-    __shared__ uint32_t si[8];
-    const int r = blockIdx.x, t = threadIdx.x, lane = t & 63, w = t >> 6;
+// value, ties to the lower index (a NaN never wins). Pass 1, grid (kArgParts, m): the best of each
+// 1/kArgParts of a row. Pass 2, one wave per row: the best of the parts, in part order; with
+// `tokens`, row r's pick becomes its next token and its position advances (pos[r] += 1), so decode
+// steps chain on the device.
+constexpr int kArgParts = 32;
+
+__global__ __launch_bounds__(256) void k_argmax_part(const float* __restrict__ logits, int V, float* __restrict__ pv,
+                                                     uint32_t* __restrict__ pi) {
+    __shared__ float sv[4];
+    __shared__ uint32_t si[4];
+    const int part = blockIdx.x, r = blockIdx.y, t = threadIdx.x, lane = t & 63, w = t >> 6;
+    const int per = (V + kArgParts - 1) / kArgParts, c0 = part * per, c1 = min(V, c0 + per);
     const float* row = logits + (size_t)r * V;
     float best = -INFINITY;
     uint32_t bi = 0xFFFFFFFFu;
-    for (int c = t; c < V; c += 512) {
+    for (int c = c0 + t; c < c1; c += 256) {
         const float v = row[c];
         if (better(v, (uint32_t)c, best, bi)) {
             best = v;
@@ -375,12 +392,33 @@ __global__ __launch_bounds__(512) void k_argmax_rows(const float* __restrict__ l
     if (t == 0) {
         float b = sv[0];
         uint32_t bix = si[0];
-        for (int i = 1; i < 8; i++)
+        for (int i = 1; i < 4; i++)
             if (better(sv[i], si[i], b, bix)) {
                 b = sv[i];
                 bix = si[i];
             }
-        const uint32_t pick = bix == 0xFFFFFFFFu ? 0u : bix;  // all NaN: token 0
+        pv[r * kArgParts + part] = b;
+        pi[r * kArgParts + part] = bix;
+    }
+}
+
+__global__ __launch_bounds__(64) void k_argmax_final(const float* __restrict__ pv, const uint32_t* __restrict__ pi,
+                                                     uint32_t* __restrict__ out, uint32_t* __restrict__ tokens,
+                                                     int32_t* __restrict__ pos) {
+    const int r = blockIdx.x, lane = threadIdx.x;
+    float best = lane < kArgParts ? pv[r * kArgParts + lane] : -INFINITY;
+    uint32_t bi = lane < kArgParts ? pi[r * kArgParts + lane] : 0xFFFFFFFFu;
+#pragma unroll
+    for (int mk = 32; mk >= 1; mk >>= 1) {
+        const float ov = __shfl_xor(best, mk, 64);
+        const uint32_t oi = (uint32_t)__shfl_xor((int)bi, mk, 64);
+        if (better(ov, oi, best, bi)) {
+            best = ov;
+            bi = oi;
+        }
+    }
+    if (lane == 0) {
+        const uint32_t pick = bi == 0xFFFFFFFFu ? 0u : bi;  // all NaN: token 0
         if (out) out[r] = pick;
         if (tokens) {
             tokens[r] = pick;
@@ -397,9 +435,10 @@ int gemm_splits(int kind, int N, int K, int group) {
     (void)group;
     const int tiles = (N + 32 * gemm_waves(N) - 1) / (32 * gemm_waves(N));
     const int nch = K / kChunk;
-    // about one workgroup per CU, at least 2 chunks per split (the partials are 64 x N floats per split)
+    // about one workgroup per CU, at least 4 chunks per split (the partials are 64 x N floats per
+    // split, written and read back by the reduce)
     int splits = (256 + tiles / 2) / tiles;
-    splits = std::min(splits, std::max(1, nch / 2));
+    splits = std::min(splits, std::max(1, nch / 4));
     splits = std::max(1, splits);
     const int per = (nch + splits - 1) / splits;
     return (nch + per - 1) / per;  // no empty split
@@ -445,9 +484,14 @@ void launch_embed_rows(int kind, const void* W, const uint32_t* SZ, int group, i
                        h, frag, gain, q4order);
 }
 
-void launch_argmax_rows(const float* logits, int m, int V, uint32_t* out, uint32_t* tokens, int32_t* pos,
+size_t argmax_rows_scratch(int m) { return (size_t)m * kArgParts * 8; }
+
+void launch_argmax_rows(const float* logits, int m, int V, uint32_t* out, uint32_t* tokens, int32_t* pos, void* scratch,
                         hipStream_t st) {
-    hipLaunchKernelGGL(k_argmax_rows, dim3(m), dim3(512), 0, st, logits, V, out, tokens, pos);
+    float* pv = (float*)scratch;
+    uint32_t* pi = (uint32_t*)(pv + (size_t)m * kArgParts);
+    hipLaunchKernelGGL(k_argmax_part, dim3(kArgParts, m), dim3(256), 0, st, logits, V, pv, pi);
+    hipLaunchKernelGGL(k_argmax_final, dim3(m), dim3(64), 0, st, pv, pi, out, tokens, pos);
 }
 
 }  // namespace qne

@@ -961,6 +961,7 @@ __device__ __forceinline__ void attn_phase(const Env& e, CPhase& P, int step, in
         }
     }
     wait_all();  // prefetched K/V rows
+    mark(e, 3);
     for (int u = 0;; u++) {
         const int pp = p0 + 2 * (e.wave + kNW * u);
         if (pp >= p1) break;  // wave-uniform
@@ -1006,7 +1007,7 @@ __device__ __forceinline__ void attn_phase(const Env& e, CPhase& P, int step, in
             }
         }
     }
-    mark(e, 3);
+    mark(e, 4);
     // merge the two position halves of the wave, then write the wave's partial into its region
     float* wp = (float*)cur;  // [G][258]: m, l, acc[256]
 #pragma unroll
@@ -1056,7 +1057,7 @@ __device__ __forceinline__ void attn_phase(const Env& e, CPhase& P, int step, in
         }
     }
     bar();  // the regions are free again
-    mark(e, 4);
+    mark(e, 5);
 }
 
 // Combine of the attention partials: workgroup = (q head h, 64 dims c); times sigmoid(gate).

@@ -140,8 +140,10 @@ void launch_stage_x(const float* x, int x_stride, int m, int K, const float* gai
 // h[r] = embedding row tokens[r], r < m; with frag, h * gain is also staged as a GEMM's x operand.
 void launch_embed_rows(int kind, const void* W, const uint32_t* SZ, int group, int hidden, const uint32_t* tokens, int m,
                        float* h, uint8_t* frag, const float* gain, int q4order, hipStream_t st);
-// Greedy pick per row into out[r]; with `tokens`, also tokens[r] = pick and pos[r] += 1.
-void launch_argmax_rows(const float* logits, int m, int V, uint32_t* out, uint32_t* tokens, int32_t* pos,
+// Greedy pick per row into out[r]; with `tokens`, also tokens[r] = pick and pos[r] += 1. `scratch`
+// holds argmax_rows_scratch(m) bytes.
+size_t argmax_rows_scratch(int m);
+void launch_argmax_rows(const float* logits, int m, int V, uint32_t* out, uint32_t* tokens, int32_t* pos, void* scratch,
                         hipStream_t st);
 
 // Raw paged decode for `batch` sequences: append k/v at ctx[b], attend over 0..ctx[b].

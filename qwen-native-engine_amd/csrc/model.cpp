@@ -893,7 +893,7 @@ std::string Model::profile_token_json() {
         }
         {
             const int kind = phase_kind_[b];  // 0 GEMV, 1 GDN, 2 attention, 3 combine
-            const int in_slot = kind == 0 ? 0 : kind == 3 ? 2 : 1, pub_slot = kind == 0 ? 3 : kind == 1 ? 2 : kind == 2 ? 4 : 3;
+            const int in_slot = kind == 0 ? 0 : kind == 3 ? 2 : 1, pub_slot = kind == 0 ? 3 : kind == 1 ? 2 : kind == 2 ? 5 : 3;
             std::vector<double> tin, tpub;
             unsigned long long pmax = 0;
             for (int w = 0; w < grid; w++) {
@@ -952,7 +952,7 @@ std::string Model::profile_token_json() {
     return std::string(head) +
            "\"sub_step_names\":{\"gemv\":[\"x load\",\"first group\",\"other groups\",\"dma issue (two ahead)\"],"
            "\"gdn\":[\"input\",\"state update\",\"dma issue (two ahead)\"],"
-           "\"attention\":[\"input\",\"q/k prep\",\"context loop\",\"merge + publish\",\"dma issue (two ahead)\"],"
+           "\"attention\":[\"input\",\"q/k prep\",\"K/V landed\",\"context loop\",\"merge + publish\",\"dma issue (two ahead)\"],"
            "\"combine\":[\"partials\",\"gate\",\"combine + publish\"]}," +
            "\"sub_steps_median_ms\":" + subs + ",\"labels\":" + obj(span_l) + ",\"compute_median_ms\":" + obj(comp_l) +
            ",\"handover_median_ms\":" + obj(exch_l) +
