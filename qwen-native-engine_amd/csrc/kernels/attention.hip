@@ -163,14 +163,23 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_partial(const float* __re
 #pragma unroll
             for (int d = 0; d < 8; d++) s = fmaf(qr[gi][d], kf[d], s);
             s = half_sum_dpp(s, lane);
-            if (valid) {
+            s = valid ? s : -INFINITY;
+            // The running sum and accumulators are kept relative to m; m moves (and they are
+            // rescaled) only when a score exceeds it by more than 8 (a weight of 2^8 at most),
+            // which after the first positions is rare, so most positions cost one exp2 (the
+            // hardware v_exp_f32: weights below 2^-126 flush to 0).
+            if (__builtin_amdgcn_ballot_w64(s > m[gi] + 8.0f)) {  // wave-uniform branch
                 const float mn = fmaxf(m[gi], s);
-                const float corr = exp2f(m[gi] - mn), pw = exp2f(s - mn);
+                const float corr = mn == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m[gi] - mn);
                 m[gi] = mn;
-                l[gi] = fmaf(l[gi], corr, pw);
+                l[gi] *= corr;
 #pragma unroll
-                for (int d = 0; d < 8; d++) acc[gi][d] = fmaf(pw, vf[d], acc[gi][d] * corr);
+                for (int d = 0; d < 8; d++) acc[gi][d] *= corr;
             }
+            const float pw = s == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(s - m[gi]);  // an invalid position weighs 0
+            l[gi] += pw;
+#pragma unroll
+            for (int d = 0; d < 8; d++) acc[gi][d] = fmaf(pw, vf[d], acc[gi][d]);
         }
         kc = kn;
         vc = vn;
