@@ -427,18 +427,20 @@ __global__ __launch_bounds__(64) void k_argmax_final(const float* __restrict__ p
     }
 }
 
-// Workgroup width: 8 waves (256 W rows) for wide matrices, 4 (128 rows) otherwise.
-static int gemm_waves(int N) { return N > 4096 ? 8 : 4; }
+// Workgroup width: 8 waves (256 W rows) for q4 and wide f16 matrices, else 4 (128 rows). At the
+// 2B model's M = 64 shapes (W streamed from HBM), 8 waves with a 3-deep ring (two workgroups fit a
+// CU) beat 4 waves by 8-20 % including the reduce.
+static int gemm_waves(int kind, int N) { return kind == KIND_Q4 || N > 4096 ? 8 : 4; }
 
 int gemm_splits(int kind, int N, int K, int group) {
-    (void)kind;
     (void)group;
-    const int tiles = (N + 32 * gemm_waves(N) - 1) / (32 * gemm_waves(N));
+    const int waves = gemm_waves(kind, N);
+    const int tiles = (N + 32 * waves - 1) / (32 * waves);
     const int nch = K / kChunk;
-    // about one workgroup per CU, at least 4 chunks per split (the partials are 64 x N floats per
-    // split, written and read back by the reduce)
-    int splits = (256 + tiles / 2) / tiles;
-    splits = std::min(splits, std::max(1, nch / 4));
+    // as many splits as keep the grid within one workgroup per CU (a second one on a CU shares its
+    // chunk throughput), at least 2 chunks per split, at most 24 (the reduce reads every split's
+    // 64 x N partials)
+    int splits = std::min(256 / tiles, std::min(24, nch / 2));
     splits = std::max(1, splits);
     const int per = (nch + splits - 1) / splits;
     return (nch + per - 1) / per;  // no empty split
@@ -465,13 +467,13 @@ void launch_gemm(GemmArgs a, hipStream_t st) {
         launch_stage_x(a.x, a.x_stride, a.m, a.K, a.gain, a.kind == KIND_Q4 ? 1 : 0, a.frag, st);
         a.norm = a.gain ? 1 : 0;
     }
-    const int waves = gemm_waves(a.N);
+    const int waves = gemm_waves(a.kind, a.N);
     const dim3 grid((a.N + 32 * waves - 1) / (32 * waves), a.splits);
-    // ring depths: as many chunk slots as fit in 160 KiB of LDS
     if (a.kind == KIND_Q4) {
-        if (waves == 8) hipLaunchKernelGGL((k_gemm<KIND_Q4, 8, 5>), grid, dim3(512), 0, st, a);
-        else hipLaunchKernelGGL((k_gemm<KIND_Q4, 4, 7>), grid, dim3(256), 0, st, a);
+        // 3 chunk slots (77.6 KiB): deeper rings measured slower, and two workgroups fit a CU
+        hipLaunchKernelGGL((k_gemm<KIND_Q4, 8, 3>), grid, dim3(512), 0, st, a);
     } else {
+        // f16: as many chunk slots as fit in 160 KiB of LDS
         if (waves == 8) hipLaunchKernelGGL((k_gemm<KIND_F16, 8, 3>), grid, dim3(512), 0, st, a);
         else hipLaunchKernelGGL((k_gemm<KIND_F16, 4, 4>), grid, dim3(256), 0, st, a);
     }
