@@ -122,8 +122,10 @@ int qne_gdn_step(const float* q, const float* k, const float* v, const float* be
                  float* state, float* out, int batch, int heads, void* stream);
 /* The same recurrence over T tokens per sequence in one call (batch.rs:166-255 semantics: the
  * state after the call is the state after T sequential steps): q,k [B][T][H][dk], v/out
- * [B][T][H][dv], beta/g [B][T][H]. The state stays in registers across the T tokens, its value
- * columns split over B * H * 32 independent waves. */
+ * [B][T][H][dv], beta/g [B][T][H]. From T = 64 on it runs in the chunk-64 WY form on f32 MFMA
+ * (every chunk's intra-chunk solve at once, then the state chained over chunks); shorter calls run
+ * token by token with the state in registers. g must be in (0, 1]. The WY operands' scratch is kept
+ * per device (grown when a call needs more): calls that overlap on one device must not be issued. */
 int qne_gdn_prefill_chunked(const float* q, const float* k, const float* v, const float* beta,
                             const float* g, float* state, float* out, int batch, int tokens,
                             int heads, void* stream);

@@ -63,10 +63,10 @@ void need(bool ok, const char* what) {
 void check_launch() { qne::hip_check(hipGetLastError(), "kernel launch"); }
 
 // Scratch of the kernel-level entry points (slot 0: paged-attention partials, slot 1: GEMM split
-// partials), kept per device and grown on demand (held until the process ends), so that a call
+// partials, slot 2: the chunk operands of the WY delta rule), kept per device and grown on demand (held until the process ends), so that a call
 // allocates only when it needs more than any call before it on that device. Calls of one entry
 // point that overlap on one device share it.
-enum { kWsAttention = 0, kWsGemm = 1, kWsSlots = 2 };
+enum { kWsAttention = 0, kWsGemm = 1, kWsGdn = 2, kWsSlots = 3 };
 float* workspace(int slot, size_t bytes) {
     static std::mutex mu;
     static std::vector<std::pair<void*, size_t>> per_dev;
@@ -258,12 +258,21 @@ int qne_gdn_step(const float* q, const float* k, const float* v, const float* be
     });
 }
 
+// From this many tokens on, qne_gdn_prefill_chunked runs the chunk-64 WY form; shorter calls run
+// the token-by-token recurrence.
+constexpr int kWyMinTokens = 64;
+
 int qne_gdn_prefill_chunked(const float* q, const float* k, const float* v, const float* beta, const float* g,
                             float* state, float* out, int batch, int tokens, int heads, void* stream) {
     return guard([&] {
         need(q && k && v && beta && g && state && out, "null argument");
         need(batch > 0 && heads > 0 && tokens > 0 && batch <= 65535 && heads <= 65535, "bad sizes");
-        qne::launch_delta_rule_chunked(q, k, v, beta, g, state, out, batch, tokens, heads, (hipStream_t)stream);
+        if (tokens >= kWyMinTokens) {
+            float* ws = workspace(kWsGdn, qne::wy_workspace_bytes(batch, tokens, heads));
+            qne::launch_delta_rule_wy(q, k, v, beta, g, state, out, batch, tokens, heads, ws, (hipStream_t)stream);
+        } else {
+            qne::launch_delta_rule_chunked(q, k, v, beta, g, state, out, batch, tokens, heads, (hipStream_t)stream);
+        }
         check_launch();
     });
 }

@@ -25,10 +25,13 @@
 
 #include "common.hpp"
 #include "launch.hpp"
+#include "lds_dma.hpp"
 
 namespace qne {
 
 namespace {
+
+using namespace lds_dma;
 
 constexpr int kBM = 64;            // rows of x per GEMM (sequences)
 constexpr int kChunk = 64;         // columns per staged chunk
@@ -38,33 +41,9 @@ constexpr int kSsOff = kXsumOff + kBM * 4;           // per-row sums of x^2 (raw
 constexpr int kChunkBytes = kSsOff + kBM * 4;        // a staged chunk in memory
 constexpr int kChunkLds = kSsOff;                    // the part of a chunk the GEMM copies to LDS
 
-typedef __attribute__((address_space(3))) void* lds_ptr_t;
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 typedef float float16_t __attribute__((ext_vector_type(16)));
-
-// One LDS DMA: each active lane copies 16 (dma16) or 4 (dma4) bytes from its own global address to
-// LDS at dst + lane * 16 (or * 4); dst is the same for the whole wave. Issued from asm so that the
-// compiler adds no wait of its own; completion is awaited with wait_vm. m0 carries the LDS address
-// and is restored.
-__device__ __forceinline__ void dma16(const void* src, void* dst) {
-    const uint32_t lds = __builtin_amdgcn_readfirstlane((uint32_t)(size_t)(lds_ptr_t)dst);
-    uint32_t saved;
-    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off\n\ts_mov_b32 m0, %0"
-                 : "=&s"(saved) : "v"(src), "s"(lds) : "memory");
-}
-__device__ __forceinline__ void dma4(const void* src, void* dst) {
-    const uint32_t lds = __builtin_amdgcn_readfirstlane((uint32_t)(size_t)(lds_ptr_t)dst);
-    uint32_t saved;
-    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %1, off\n\ts_mov_b32 m0, %0"
-                 : "=&s"(saved) : "v"(src), "s"(lds) : "memory");
-}
-// Until at most N of this wave's vector-memory operations are outstanding; the memory clobber keeps
-// the LDS reads of the landed data after it.
-template <int N>
-__device__ __forceinline__ void wait_vm() {
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-}
 
 // The 8 nibbles of a q4 word (nibble i at bits 4i: column 8j + i of word j) as exact f16 values, in
 // the order [q0, q4, q1, q5, q2, q6, q3, q7]: 0x6400 | q is the f16 1024 + q, and 0x6400 | (q << 4)

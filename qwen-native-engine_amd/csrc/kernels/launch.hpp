@@ -44,9 +44,13 @@ void launch_gdn_decode(const float* proj, float* conv_state, const float* conv_w
 // The bare delta rule for batch x heads (q, k used as given).
 void launch_delta_rule(const float* q, const float* k, const float* v, const float* beta, const float* g,
                        float* state, float* out, int batch, int heads, hipStream_t st);
-// The delta rule over T tokens in chunks of 64.
+// The delta rule over T tokens, token by token (value columns split over waves).
 void launch_delta_rule_chunked(const float* q, const float* k, const float* v, const float* beta, const float* g,
                                float* state, float* out, int batch, int tokens, int heads, hipStream_t st);
+// The delta rule over T tokens in the chunk-64 WY form on MFMA; ws holds wy_workspace_bytes.
+size_t wy_workspace_bytes(int batch, int tokens, int heads);
+void launch_delta_rule_wy(const float* q, const float* k, const float* v, const float* beta, const float* g,
+                          float* state, float* out, int batch, int tokens, int heads, float* ws, hipStream_t st);
 
 // Attention decode, model form: q/k RMSNorm + RoPE, f16 append at tok[1], split-context partials,
 // combine with the sigmoid gate into `out`.

@@ -128,6 +128,80 @@ def test_gdn_multi_token_equals_sequential_oracle():
     assert rel_err(d[5].cpu().numpy(), want_S) < 1e-4
 
 
+def gdn_inputs(rng, B, T, H, mode="random"):
+    dk = 128
+    q = rng.normal(size=(B, T, H, dk)).astype(np.float32)
+    k = rng.normal(size=(B, T, H, dk)).astype(np.float32)
+    q /= np.linalg.norm(q, axis=-1, keepdims=True)
+    k /= np.linalg.norm(k, axis=-1, keepdims=True)
+    v = rng.normal(size=(B, T, H, dk)).astype(np.float32)
+    beta = (1 / (1 + np.exp(-rng.normal(size=(B, T, H))))).astype(np.float32)
+    g = np.exp(-np.log1p(np.exp(rng.normal(size=(B, T, H))))).astype(np.float32)
+    if mode == "same_k":  # one key repeated, beta = 1, no decay: the WY solve at its least damped
+        k[:] = k[:, :1]
+        beta[:] = 1.0
+        g[:] = 1.0
+    elif mode == "tiny_g":  # decays that underflow the chunk's cumulative product
+        g[:, ::7] = 1e-30
+    elif mode == "beta0":  # no writes: the state only decays
+        beta[:] = 0.0
+    S = rng.normal(0, 0.1, size=(B, H, dk, dk)).astype(np.float32)
+    return q, k, v, beta, g, S
+
+
+def oracle_gdn_tokens(q, k, v, beta, g, S):
+    B, T, H, dk = q.shape
+    want_S, want_o = S.copy(), np.empty_like(v)
+    L = O.lib("f64")
+    for b in range(B):
+        for t in range(T):
+            for h in range(H):
+                L.oc_delta_rule(dk, dk, O.ptr(q[b, t, h]), O.ptr(k[b, t, h]), O.ptr(v[b, t, h]), float(beta[b, t, h]),
+                                float(g[b, t, h]), O.ptr(want_S[b, h]), O.ptr(want_o[b, t, h]))
+    return want_o, want_S
+
+
+@pytest.mark.parametrize("B,T,H,mode", [(1, 48, 3, "random"), (1, 64, 2, "random"), (2, 65, 2, "random"),
+                                        (1, 200, 2, "tiny_g"), (1, 130, 1, "same_k"), (3, 129, 2, "beta0"),
+                                        (2, 300, 5, "random")])
+def test_gdn_multi_token_cases(B, T, H, mode):
+    """Token-by-token (T < 64) and chunk-64 WY form (T >= 64, ragged last chunks) against the
+    oracle's sequential recurrence (f64), including a repeated key with beta = 1 and g = 1,
+    decays that underflow, and beta = 0."""
+    rng = np.random.default_rng(T * 10 + H)
+    q, k, v, beta, g, S = gdn_inputs(rng, B, T, H, mode)
+    want_o, want_S = oracle_gdn_tokens(q, k, v, beta, g, S)
+    d = [to_dev(a) for a in (q, k, v, beta, g, S)]
+    out = torch.empty_like(d[2])
+    Q.gdn_prefill_chunked(*[t.data_ptr() for t in d], out.data_ptr(), B, T, H)
+    torch.cuda.synchronize()
+    assert rel_err(out.cpu().numpy(), want_o) < 1e-4
+    assert rel_err(d[5].cpu().numpy(), want_S) < 1e-4
+
+
+def test_gdn_chunked_split_calls_equal_one_call():
+    """The state carried between calls: 64 + 136 tokens in two calls (WY, WY) and 40 + 160 (token by
+    token, then WY) against one 200-token call, within the f32 tolerance of either form."""
+    rng = np.random.default_rng(77)
+    B, T, H = 2, 200, 2
+    q, k, v, beta, g, S = gdn_inputs(rng, B, T, H)
+    whole = [to_dev(a) for a in (q, k, v, beta, g, S)]
+    out = torch.empty_like(whole[2])
+    Q.gdn_prefill_chunked(*[t.data_ptr() for t in whole], out.data_ptr(), B, T, H)
+    for cut in (64, 40):
+        st = to_dev(S)
+        parts = []
+        for a, bnd in ((0, cut), (cut, T)):
+            sl = [to_dev(np.ascontiguousarray(x[:, a:bnd])) for x in (q, k, v, beta, g)]
+            o = torch.empty_like(sl[2])
+            Q.gdn_prefill_chunked(*[t.data_ptr() for t in sl], st.data_ptr(), o.data_ptr(), B, bnd - a, H)
+            parts.append(o)
+        torch.cuda.synchronize()
+        got = torch.cat(parts, dim=1).cpu().numpy()
+        assert rel_err(got, out.cpu().numpy()) < 1e-4, cut
+        assert rel_err(st.cpu().numpy(), whole[5].cpu().numpy()) < 1e-4, cut
+
+
 @pytest.mark.parametrize("batch,nq,nkv", [(1, 16, 4), (3, 8, 2), (5, 4, 4)])
 def test_paged_attention_matches_dense(batch, nq, nkv):
     rng = np.random.default_rng(batch * 100 + nq)
