@@ -25,6 +25,7 @@ ROOT = Path(__file__).resolve().parent
 sys.path[:0] = [str(ROOT / "qwen-native-engine_amd"), str(ROOT / "oracle")]
 
 PEAK_HBM_GBS = 8000.0  # MI355X HBM3E
+PEAK_F32_TFLOPS = 157.3  # MI355X dense f32 MFMA
 
 
 def algorithmic_bytes_per_token(cfg: dict, mats: dict, ctx: float) -> dict:
@@ -202,7 +203,17 @@ def bench_gdn(args) -> dict:
                                                        g.data_ptr(), S.data_ptr(), o.data_ptr(), B, T, H, st),
                     1, max(1, args.steps // 20))
     nb = B * T * H * 2048 + B * H * dk * dk * 4 * 2
-    pre = {"ms": round(ms, 3), "GB/s": round(nb / (ms / 1e3) / 1e9, 1), "tokens_per_s": round(B * T / (ms / 1e3))}
+    # flops: the sequential-equivalent convention (6 dk dv = 98 304 per token and head), and the MFMA
+    # flops the chunk-64 WY form issues (f32 16x16x4 tiles, triangular tiles skipped): per chunk and
+    # head 1344 in the prep kernel (K K^T, K Q^T, T off-diagonal blocks, U, W^T) and 8 x 424 in
+    # the chain (D, output, state), 2048 flops each
+    chunks = B * H * ((T + 63) // 64)
+    seq_flop = B * T * H * 98304
+    wy_flop = chunks * (1344 + 8 * 424) * 2048
+    pre = {"ms": round(ms, 3), "GB/s": round(nb / (ms / 1e3) / 1e9, 1), "tokens_per_s": round(B * T / (ms / 1e3)),
+           "form": "chunk-64 WY on f32 MFMA", "seq_equiv_tflops": round(seq_flop / (ms / 1e3) / 1e12, 2),
+           "mfma_tflops": round(wy_flop / (ms / 1e3) / 1e12, 2),
+           "mfma_frac_f32": round(wy_flop / (ms / 1e3) / 1e12 / PEAK_F32_TFLOPS, 4)}
     gbs = steps[64]["GB/s"]
     return {"metric": "gated delta rule GB/s (16 heads x 128 x 128 state), step at batch 64", "value": gbs,
             "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": steps[64]["ms"],
