@@ -225,6 +225,84 @@ def bench_gdn(args) -> dict:
             "detail": {"step": steps, "prefill_b4_t2048": pre}, "cpu_baseline": None}
 
 
+def bench_sample(args) -> dict:
+    """Sampled decode (src/sampling.rs Sampler: temperature 0.6, top-k 20, top-p 0.95, presence
+    penalty 1.5, the agent's defaults plus a penalty) on the 2B model after a ctx-token prefill:
+    the reference's path reads vocab x 4 B of logits back per token and samples on the host (here
+    the oracle's C restatement of its sampler, one thread); the device path leaves the logits in HBM
+    and runs the O(vocab) part of the sampler on the GPU (qne_step_device + qne_sample), reading
+    back only the k best (value, token) pairs. Both paths must produce the same tokens."""
+    import torch
+    import qne
+    import weights as W
+    from cpu_oracle import OracleSampler
+    # torch's HIP runtime (the event timer below) must be initialised before the library's
+    torch.zeros(1, device="cuda")
+    opts = dict(temperature=0.6, top_k=20, top_p=0.95, seed=42, presence_penalty=1.5)
+    cfg = W.full_config("2b")
+    index, buf = W.synth_model("2b", seed=args.seed, body="q4", head="f16", group=64)
+    m = qne.Model.load(index, buf, options={"max_context": 4096})
+    V = cfg["vocab"]
+    prompt = np.random.default_rng(args.seed).integers(0, V, size=args.ctx).astype(np.uint32)
+    steps = min(args.steps, 4096 - args.ctx - 1)
+    for s0 in range(0, args.ctx, 512):
+        m.prefill_chunk(prompt[s0: min(s0 + 512, args.ctx)], s0, s0 + 512 >= args.ctx)
+    m.snapshot()
+    first, _ = m.last_token()
+
+    def host_path():
+        m.restore()
+        o = OracleSampler(**opts)
+        toks, tok, pos = [], first, args.ctx
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            tok = o.sample(m.step(tok, pos))
+            toks.append(tok)
+            pos += 1
+        return toks, time.perf_counter() - t0
+
+    def device_path():
+        m.restore()
+        toks, tok, pos = [], first, args.ctx
+        with qne.Sampler(V, **opts) as smp:
+            ptr = m.logits_device()
+            t0 = time.perf_counter()
+            for _ in range(steps):
+                m.step_device(tok, pos)
+                tok = smp.sample(ptr)
+                toks.append(tok)
+                pos += 1
+            return toks, time.perf_counter() - t0
+
+    host_path()
+    device_path()  # warm
+    host_toks, host_s = host_path()
+    dev_toks, dev_s = device_path()
+    # the sampler kernel alone: HIP events around repeated calls on one stream over the model's logits
+    kernel = {}
+    for name, o in (("top_k_20", opts), ("top_k_1024", dict(opts, top_k=1024)), ("greedy", dict(temperature=0.0))):
+        with qne.Sampler(V, **o) as smp:
+            ptr = m.logits_device()
+            ms = _events_ms(lambda s_: smp.sample(ptr, stream=s_), 5, 50)
+        kernel[name] = round(ms * 1e3, 1)
+    m.close()
+    step_ms = dev_s / steps * 1e3
+    return {"metric": "sampled decode tok/s (2B int4, ctx %d, device sampler)" % args.ctx,
+            "value": round(steps / dev_s, 2), "unit": "tok/s", "n_gpus": 1, "steps": steps, "warmup": steps,
+            "ms_per_step": round(step_ms, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+            "dtype": "f32", "data": "synthetic",
+            "config": {"workload": "2B-shaped int4 decoder, one sequence, sampled with temperature 0.6, top-k 20, "
+                                   "top-p 0.95, presence penalty 1.5 after a %d-token prefill" % args.ctx},
+            "roofline": None,
+            "detail": {"identical_tokens": host_toks == dev_toks, "device_path_ms_per_token": round(step_ms, 4),
+                       "host_sampling_path_ms_per_token": round(host_s / steps * 1e3, 4),
+                       "readback_bytes_per_token": {"host_path": V * 4, "device_path": 16 + 20 * 8},
+                       "sampler_call_us": kernel},
+            "cpu_baseline": {"value": round(steps / host_s, 2), "unit": "tok/s", "cores": 1, "kind": "port",
+                             "sample": "the same decode with the logits read back and sampled by the oracle's C "
+                                       "restatement of src/sampling.rs on one host thread"}}
+
+
 def bench_batch(args) -> dict:
     """Batched continuous decode on the 2B-shaped int4 model: `--batch` sequences (64) with contexts
     uniform in [256, 4096) on the paged KV cache, all advancing one greedy token per step (each
@@ -324,8 +402,8 @@ def main():
                          "every decode window a profile sees has the timed length)")
     ap.add_argument("--ctx", type=int, default=4000)
     ap.add_argument("--config", default="2b",
-                    help="2b (the decode benchmark), 0.8b, batch (64-sequence batched decode), or the kernel "
-                         "microbenches attn / gdn")
+                    help="2b (the decode benchmark), 0.8b, batch (64-sequence batched decode), sample (sampled "
+                         "decode with the device sampler), or the kernel microbenches attn / gdn")
     ap.add_argument("--batch", type=int, default=64, help="sequences (--config attn / batch)")
     ap.add_argument("--cpu-tokens", type=int, default=4)
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -345,6 +423,10 @@ def main():
         return
     if args.config == "batch":
         print(json.dumps(bench_batch(args)))
+        return
+    if args.config == "sample":
+        sys.path[:0] = [str(ROOT / "qwen-native-engine_amd")]
+        print(json.dumps(bench_sample(args)))
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this engine runs batch-1 decode on one GPU; --gpus above 1 is not supported "

@@ -62,6 +62,12 @@ int qne_logits(qne_model* m, float* out, size_t cap);
 /* Model::step -- model.rs:380. Feeds `token` at `pos`, writes vocab logits; does not update the
  * greedy pick. QNE_ECONTEXT if pos >= max_context. */
 int qne_step(qne_model* m, uint32_t token, uint32_t pos, float* out, size_t cap);
+/* Model::step without the logits readback (the reference's step copies vocab floats to the host,
+ * model.rs:388-391): the logits stay on the device, at qne_logits_device, for qne_sample. */
+int qne_step_device(qne_model* m, uint32_t token, uint32_t pos);
+/* The device address of the model's vocab logits (valid until qne_model_free; rewritten by
+ * qne_step / qne_step_device / qne_prefill_chunk with finish_logits / qne_prefill). */
+int qne_logits_device(qne_model* m, const float** out);
 /* Model::snapshot / Model::restore -- model.rs:395, 406. restore: QNE_ENOSNAPSHOT before any
  * snapshot ("no snapshot taken"). */
 int qne_snapshot(qne_model* m);
@@ -151,6 +157,29 @@ int qne_paged_attn_decode(const float* q, const float* k_new, const float* v_new
 int qne_gemm(int kind, const void* w, const void* sz, int rows, int k, int group, const float* x,
              int x_stride, int m, const float* norm, float eps, float* y, int y_stride, int epilogue,
              void* stream);
+
+/* ---- token sampling on the device ----
+ * src/sampling.rs Sampler (the agent's temperature + top-k + top-p sampler with presence penalty
+ * and grammar mask) over logits in device memory: the O(vocab) part (checks, penalty, mask, greedy
+ * pick or the top-k candidates) runs on the GPU, and only the pick or the k best (value, token)
+ * pairs cross to the host, where the softmax weights, top-p prefix and xorshift draw run in the
+ * reference's f32 arithmetic. The same logits, options and seed give the reference's tokens
+ * (equal logits are taken in increasing token order; the reference leaves that order open). */
+typedef struct qne_sampler qne_sampler;
+/* Sampler::new (src/sampling.rs:42-46) for a vocabulary of `vocab` tokens, on the current device.
+ * temperature <= 0: greedy. top_k 0 is taken as 1 (as the reference does); QNE_EINVAL above 1024. */
+int qne_sampler_create(float temperature, uint32_t top_k, float top_p, uint64_t seed, float presence_penalty,
+                       uint32_t vocab, qne_sampler** out);
+int qne_sampler_free(qne_sampler* s);
+/* Sampler::try_sample (src/sampling.rs:58-79) over `vocab` logits at device address `logits`
+ * (e.g. qne_logits_device). `bias` is added to token `bias_token` first (the agent's tool-call
+ * bias, agent/src/session.rs:399-404; bias_token >= vocab for none). mask: host bitset (bit i%32
+ * of word i/32 allows token i; tokens >= mask_len are not allowed) or NULL. The presence penalty
+ * applies only without a mask; the picked token is remembered for it either way. QNE_EINVAL
+ * ("non-finite model logits" / "no finite token is allowed by the sampling mask") where the
+ * reference fails closed. Returns when the token is known. */
+int qne_sample(qne_sampler* s, const float* logits, const uint32_t* mask, uint32_t mask_len, uint32_t bias_token,
+               float bias, uint32_t* token, void* stream);
 
 /* ---- batched continuous decode ----
  * Up to 64 sequences ("rows") advance one token per step through one loaded model's weights, each

@@ -72,6 +72,11 @@ def lib(precision: str = "f64"):
             getattr(L, n).argtypes = [vp, ctypes.c_int]
             getattr(L, n).restype = vp
         L.oc_num_threads.restype = ctypes.c_int
+        L.oc_sampler_seed.argtypes = [ctypes.c_uint64]; L.oc_sampler_seed.restype = ctypes.c_uint64
+        L.oc_sampler_next_f32.argtypes = [ctypes.POINTER(ctypes.c_uint64)]; L.oc_sampler_next_f32.restype = ctypes.c_float
+        L.oc_sample.argtypes = [vp, ctypes.c_uint32, vp, ctypes.c_uint32, ctypes.c_float, ctypes.c_uint32, ctypes.c_float,
+                                ctypes.c_float, ctypes.POINTER(ctypes.c_uint64), vp, ctypes.POINTER(ctypes.c_uint32)]
+        L.oc_sample.restype = ctypes.c_int
         _libs[precision] = L
     return _libs[precision]
 
@@ -192,3 +197,41 @@ class OracleModel:
             all_logits.append(logits)
             pos += 1
         return ids, all_logits
+
+
+class OracleSampler:
+    """src/sampling.rs Sampler restated in the C oracle (oc_sample), f32 throughout: the checker of
+    the device sampler. sample() raises ValueError where the reference's try_sample fails closed."""
+
+    def __init__(self, temperature=0.6, top_k=20, top_p=0.95, seed=42, presence_penalty=0.0):
+        self.L = lib("f32")
+        self.state = ctypes.c_uint64(self.L.oc_sampler_seed(seed))
+        self.opts = (float(temperature), int(top_k), float(top_p), float(presence_penalty))
+        self.seen = np.zeros(0, np.uint8)
+
+    def sample(self, logits, mask=None, mask_len=0):
+        x = np.ascontiguousarray(np.asarray(logits, dtype=np.float32))
+        V = x.size
+        if self.seen.size < max(V, 1):
+            self.seen = np.concatenate([self.seen, np.zeros(max(V, 1) - self.seen.size, np.uint8)])
+        if mask is not None:
+            m = np.ascontiguousarray(np.asarray(mask, dtype=np.uint32))
+            mp = m.ctypes.data_as(ctypes.c_void_p)
+        else:
+            m, mp, mask_len = None, None, 0
+        t, k, p, pen = self.opts
+        tok = ctypes.c_uint32()
+        rc = self.L.oc_sample(x.ctypes.data_as(ctypes.c_void_p) if V else None, V, mp, mask_len, t, k, p, pen,
+                              ctypes.byref(self.state), self.seen.ctypes.data_as(ctypes.c_void_p), ctypes.byref(tok))
+        if rc:
+            raise ValueError("distribution rejected")
+        return tok.value
+
+
+def bitset(allowed, n):
+    """uint32 words with bit i%32 of word i/32 set for each allowed token i < n (SimpleVob layout)."""
+    w = np.zeros((n + 31) // 32 or 1, np.uint32)
+    for i in allowed:
+        if i < n:
+            w[i >> 5] |= np.uint32(1 << (i & 31))
+    return w

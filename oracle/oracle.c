@@ -313,6 +313,115 @@ void oc_attn_dense(int nq, int nkv, int hd, const float* q, const uint16_t* kc, 
 }
 
 /* ------------------------------------------------------------------------------------------ */
+/* Sampling: src/sampling.rs, in f32 whatever OC_REAL is. */
+
+uint64_t oc_sampler_seed(uint64_t seed) { return (seed * 0x9E3779B97F4A7C15ull) | 1ull; } /* :42-46 */
+
+float oc_sampler_next_f32(uint64_t* state) { /* :48-55 */
+    uint64_t x = *state;
+    x ^= x << 13;
+    x ^= x >> 7;
+    x ^= x << 17;
+    *state = x;
+    return (float)(x >> 40) / (float)(1ull << 24);
+}
+
+static int oc_allowed(const uint32_t* mask, uint32_t mask_len, uint32_t i) {
+    return !mask || (i < mask_len && ((mask[i >> 5] >> (i & 31)) & 1u));
+}
+
+/* f32::total_cmp as an unsigned key: larger key = later in the total order. */
+static uint32_t oc_total_key(float v) {
+    uint32_t u;
+    memcpy(&u, &v, 4);
+    return (u >> 31) ? ~u : (u | 0x80000000u);
+}
+
+typedef struct {
+    float v;
+    uint32_t i;
+} oc_cand;
+
+static int oc_cand_desc(const void* a, const void* b) {
+    const oc_cand* x = (const oc_cand*)a;
+    const oc_cand* y = (const oc_cand*)b;
+    uint32_t kx = oc_total_key(x->v), ky = oc_total_key(y->v);
+    if (kx != ky) return kx > ky ? -1 : 1;
+    return x->i < y->i ? -1 : (x->i > y->i ? 1 : 0);
+}
+
+int oc_sample(const float* logits, uint32_t V, const uint32_t* mask, uint32_t mask_len, float temperature,
+              uint32_t top_k, float top_p, float presence_penalty, uint64_t* state, uint8_t* seen,
+              uint32_t* token) {
+    /* try_sample: fail closed */
+    int finite = 0;
+    for (uint32_t i = 0; i < V; i++) {
+        if (!oc_allowed(mask, mask_len, i)) continue;
+        float l = logits[i];
+        if (isnan(l) || l == INFINITY) return 1;
+        finite |= isfinite(l);
+    }
+    if (!finite) return 1;
+    /* choose */
+    const float penalty = mask ? 0.0f : presence_penalty;
+    uint32_t pick = 0;
+    if (temperature <= 0.0f) {
+        float best = -INFINITY;
+        for (uint32_t i = 0; i < V; i++) {
+            float l = logits[i];
+            if (penalty != 0.0f && seen[i]) l = l - penalty;
+            if (l > best && oc_allowed(mask, mask_len, i)) {
+                best = l;
+                pick = i;
+            }
+        }
+    } else {
+        oc_cand* c = (oc_cand*)malloc(sizeof(oc_cand) * (V ? V : 1));
+        uint32_t n = 0;
+        for (uint32_t i = 0; i < V; i++) {
+            if (!oc_allowed(mask, mask_len, i)) continue;
+            float l = logits[i];
+            if (penalty != 0.0f && seen[i]) l = l - penalty;
+            c[n].v = l;
+            c[n].i = i;
+            n++;
+        }
+        if (n > 0) {
+            uint32_t k = top_k < 1 ? 1 : top_k;
+            if (k > n) k = n;
+            qsort(c, n, sizeof(oc_cand), oc_cand_desc);
+            const float t = temperature, top = c[0].v;
+            float* w = (float*)malloc(sizeof(float) * k);
+            float total = 0.0f;
+            for (uint32_t j = 0; j < k; j++) w[j] = expf((c[j].v - top) / t);
+            for (uint32_t j = 0; j < k; j++) total += w[j];
+            /* the smallest prefix reaching top_p of the mass */
+            float kept = 0.0f;
+            uint32_t m = 0;
+            for (uint32_t j = 0; j < k; j++) {
+                kept += w[j];
+                m++;
+                if (kept >= top_p * total) break;
+            }
+            float r = oc_sampler_next_f32(state) * kept;
+            pick = c[m - 1].i;
+            for (uint32_t j = 0; j < m; j++) {
+                r -= w[j];
+                if (r <= 0.0f) {
+                    pick = c[j].i;
+                    break;
+                }
+            }
+            free(w);
+        }
+        free(c);
+    }
+    if (presence_penalty != 0.0f) seen[pick] = 1;
+    *token = pick;
+    return 0;
+}
+
+/* ------------------------------------------------------------------------------------------ */
 /* Model: graph order of kernels/src/model.rs:220-269. Layer i is full attention iff
  * (i + 1) % full_attention_every == 0 (model.rs:230). */
 

@@ -82,6 +82,20 @@ void oc_delta_rule(int dk, int dv, const float* q, const float* k, const float* 
 void oc_attn_dense(int nq, int nkv, int hd, const float* q, const uint16_t* kc, const uint16_t* vc,
                    int len, float scale, float* out);
 
+/* ---- sampling (src/sampling.rs), always in f32 as the reference ---- */
+/* Sampler::new's state (src/sampling.rs:42-46) and one draw of its xorshift64 (:48-55). */
+uint64_t oc_sampler_seed(uint64_t seed);
+float oc_sampler_next_f32(uint64_t* state);
+/* Sampler::try_sample (:58-67) with sample (:69-79) and choose (:81-134) over one row of V logits.
+ * mask: NULL for none, else a bitset of mask_len tokens (bit i%32 of word i/32 allows token i);
+ * seen: V bytes, the tokens this sampler generated (set when presence_penalty != 0). Equal values
+ * are taken in increasing token order (the reference's unstable sorts leave that order open).
+ * Returns 0 with *token set, or 1 for a distribution try_sample rejects (a NaN or +inf logit among
+ * the allowed tokens, or no finite allowed logit). */
+int oc_sample(const float* logits, uint32_t V, const uint32_t* mask, uint32_t mask_len, float temperature,
+              uint32_t top_k, float top_p, float presence_penalty, uint64_t* state, uint8_t* seen,
+              uint32_t* token);
+
 /* ---- model ---- */
 size_t oc_state_size_floats(const oc_model* m);
 oc_state* oc_state_new(const oc_model* m);

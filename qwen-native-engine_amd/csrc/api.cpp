@@ -11,6 +11,7 @@
 
 #include "../../include/qne.h"
 #include "batch.hpp"
+#include "sample.hpp"
 #include "error.hpp"
 #include "hip_util.hpp"
 #include "index.hpp"
@@ -143,6 +144,17 @@ int qne_step(qne_model* m, uint32_t token, uint32_t pos, float* out, size_t cap)
     return guard([&] {
         need(out != nullptr, "null output");
         model(m).step(token, pos, out, cap);
+    });
+}
+
+int qne_step_device(qne_model* m, uint32_t token, uint32_t pos) {
+    return guard([&] { model(m).step_device(token, pos); });
+}
+
+int qne_logits_device(qne_model* m, const float** out) {
+    return guard([&] {
+        need(out != nullptr, "null output");
+        *out = model(m).device_logits();
     });
 }
 
@@ -340,6 +352,42 @@ int qne_gemm(int kind, const void* w, const void* sz, int rows, int k, int group
         qne::launch_gemm(a, st);
         check_launch();
         if (!stream) qne::hip_check(hipStreamSynchronize(st), "gemm");
+    });
+}
+
+struct qne_sampler {
+    qne::DeviceSampler* s;
+};
+
+int qne_sampler_create(float temperature, uint32_t top_k, float top_p, uint64_t seed, float presence_penalty,
+                       uint32_t vocab, qne_sampler** out) {
+    return guard([&] {
+        need(out != nullptr, "null argument");
+        *out = nullptr;
+        qne::SamplingOptions o;
+        o.temperature = temperature;
+        o.top_k = top_k;
+        o.top_p = top_p;
+        o.seed = seed;
+        o.presence_penalty = presence_penalty;
+        qne::DeviceSampler* d = new qne::DeviceSampler(o, vocab);
+        *out = new qne_sampler{d};
+    });
+}
+
+int qne_sampler_free(qne_sampler* s) {
+    return guard([&] {
+        if (!s) return;
+        delete s->s;
+        delete s;
+    });
+}
+
+int qne_sample(qne_sampler* s, const float* logits, const uint32_t* mask, uint32_t mask_len, uint32_t bias_token,
+               float bias, uint32_t* token, void* stream) {
+    return guard([&] {
+        need(s && s->s && logits && token, "null argument");
+        *token = s->s->sample(logits, mask, mask_len, bias_token, bias, (hipStream_t)stream);
     });
 }
 

@@ -134,6 +134,27 @@ struct GemmArgs {
     const float* gain_out = nullptr;
     int order_out = 0;  // 1: the column order of a q4 GEMM's operand
 };
+// One row of token sampling (the O(vocab) part of src/sampling.rs choose / try_sample).
+struct SampleArgs {
+    const float* logits = nullptr;  // vocab logits
+    uint32_t V = 0;
+    const uint32_t* seen = nullptr;  // bitset of generated tokens (presence penalty), or null
+    float penalty = 0.0f;            // subtracted from a generated token's logit (0: none)
+    const uint32_t* mask = nullptr;  // bitset of allowed tokens, or null (all allowed)
+    uint32_t mask_len = 0;           // tokens the mask covers; tokens past it are not allowed
+    uint32_t bias_token = 0xFFFFFFFFu;
+    float bias = 0.0f;               // added to bias_token's logit first
+    uint32_t k = 0;                  // 0: greedy; else top-k candidates (<= 1024)
+    float* out_v = nullptr;          // k values, sorted by total order descending, ties by token
+    uint32_t* out_i = nullptr;       // their tokens
+    uint32_t* info = nullptr;        // [0] candidates written, [1] flags (1: NaN or +inf allowed,
+                                     // 2: a finite token allowed), [2] the greedy pick
+};
+constexpr uint32_t kSampleMaxK = 1024;
+// Device scratch one sampling call needs (counters, sampled keys, candidates).
+size_t sample_scratch_bytes();
+void launch_sample(const SampleArgs& a, void* scratch, hipStream_t st);
+
 size_t gemm_frag_bytes(int K);
 int gemm_splits(int kind, int N, int K, int group);
 bool gemm_shape_ok(int kind, int N, int K, int group, int m);

@@ -692,6 +692,15 @@ void Model::step(uint32_t token, uint32_t pos, float* out, size_t cap) {
     if (pos >= (uint32_t)max_context_)
         throw Error(QNE_ECONTEXT, "context limit of " + std::to_string(max_context_) + " tokens reached");
     if (cap < (size_t)cfg_.vocab) throw Error(QNE_EINVAL, "logits buffer smaller than the vocabulary");
+    step_device(token, pos);
+    QNE_HIP(hipMemcpyAsync(host_logits_, logits_, (size_t)cfg_.vocab * 4, hipMemcpyDeviceToHost, stream_));
+    sync();
+    std::memcpy(out, host_logits_, (size_t)cfg_.vocab * 4);
+}
+
+void Model::step_device(uint32_t token, uint32_t pos) {
+    if (pos >= (uint32_t)max_context_)
+        throw Error(QNE_ECONTEXT, "context limit of " + std::to_string(max_context_) + " tokens reached");
     if (token >= (uint32_t)cfg_.vocab) throw Error(QNE_EINVAL, "token id outside the vocabulary");
     set_tok(token, pos);
     if (persistent_) {
@@ -702,9 +711,7 @@ void Model::step(uint32_t token, uint32_t pos, float* out, size_t cap) {
         run_layers_graph();
         run_head_graph(false);
     }
-    QNE_HIP(hipMemcpyAsync(host_logits_, logits_, (size_t)cfg_.vocab * 4, hipMemcpyDeviceToHost, stream_));
     sync();
-    std::memcpy(out, host_logits_, (size_t)cfg_.vocab * 4);
 }
 
 // model.rs:395-414: device copies of all recurrent, conv and KV state.

@@ -66,6 +66,9 @@ class Model {
     void prefill_chunk(const uint32_t* ids, size_t n, uint32_t start, bool finish_logits);
     void logits(float* out, size_t cap);
     void step(uint32_t token, uint32_t pos, float* out, size_t cap);
+    // step without the logits readback: they stay in device_logits() (for DeviceSampler).
+    void step_device(uint32_t token, uint32_t pos);
+    const float* device_logits() const { return logits_; }
     void snapshot();
     void restore();
     void last_token(uint32_t* token, uint32_t* next_pos);

@@ -78,6 +78,11 @@ def load_library(path: str | os.PathLike | None = None):
         "qne_synth_normal_f32": ([ctypes.c_uint64, ctypes.c_uint64, c_sz, c_f, c_p], c_i),
         "qne_synth_normal_f16": ([ctypes.c_uint64, ctypes.c_uint64, c_sz, c_f, c_p], c_i),
         "qne_quantize_q4g": ([c_p, c_sz, c_sz, c_sz, c_p, c_p, c_p], c_i),
+        "qne_step_device": ([c_p, c_u32, c_u32], c_i),
+        "qne_logits_device": ([c_p, ctypes.POINTER(c_p)], c_i),
+        "qne_sampler_create": ([c_f, c_u32, c_f, ctypes.c_uint64, c_f, c_u32, ctypes.POINTER(c_p)], c_i),
+        "qne_sampler_free": ([c_p], c_i),
+        "qne_sample": ([c_p, c_p, c_p, c_u32, c_u32, c_f, ctypes.POINTER(c_u32), c_p], c_i),
     }
     for name, (args, res) in sigs.items():
         f = getattr(lib, name)
@@ -182,6 +187,15 @@ class Model:
         self._c(self._lib.qne_step(self._h, token, pos, out.ctypes.data_as(ctypes.c_void_p), out.size))
         return out
 
+    def step_device(self, token: int, pos: int):
+        """step without the logits readback; they stay at logits_device() for a Sampler."""
+        self._c(self._lib.qne_step_device(self._h, token, pos))
+
+    def logits_device(self) -> int:
+        p = ctypes.c_void_p()
+        self._c(self._lib.qne_logits_device(self._h, ctypes.byref(p)))
+        return p.value
+
     def snapshot(self):
         self._c(self._lib.qne_snapshot(self._h))
 
@@ -227,6 +241,52 @@ class Model:
         ms, n = ctypes.c_double(), ctypes.c_size_t()
         self._c(self._lib.qne_last_decode_timing(self._h, ctypes.byref(ms), ctypes.byref(n)))
         return ms.value, n.value
+
+
+class Sampler:
+    """src/sampling.rs Sampler over device logits (temperature + top-k + top-p, presence penalty,
+    grammar mask): the O(vocab) part on the GPU, the draw on the host in the reference's f32
+    arithmetic."""
+
+    def __init__(self, vocab: int, temperature: float = 0.6, top_k: int = 20, top_p: float = 0.95, seed: int = 42,
+                 presence_penalty: float = 0.0, lib=None):
+        self._lib = lib or load_library()
+        h = ctypes.c_void_p()
+        _check(self._lib, self._lib.qne_sampler_create(temperature, top_k, top_p, seed, presence_penalty, vocab,
+                                                       ctypes.byref(h)))
+        self._h = h
+        self.vocab = vocab
+
+    def close(self):
+        if self._h:
+            self._lib.qne_sampler_free(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()
+
+    def sample(self, logits_ptr: int, mask=None, mask_len: int = 0, bias_token: int = 0xFFFFFFFF,
+               bias: float = 0.0, stream: int = 0) -> int:
+        """Sampler::try_sample over `vocab` logits at device address logits_ptr. mask: a uint32
+        bitset (bit i%32 of word i/32 allows token i) covering mask_len tokens, or None."""
+        t = ctypes.c_uint32()
+        if mask is not None:
+            m = np.ascontiguousarray(np.asarray(mask, dtype=np.uint32))
+            mp = m.ctypes.data_as(ctypes.c_void_p)
+        else:
+            m, mp, mask_len = None, None, 0
+        _check(self._lib, self._lib.qne_sample(self._h, logits_ptr, mp, mask_len, bias_token, bias, ctypes.byref(t),
+                                               stream))
+        return t.value
 
 
 class Batch:
