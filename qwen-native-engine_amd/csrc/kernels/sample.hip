@@ -9,9 +9,9 @@
 //  1. k_sample_part: per slice of the row -- the checks, the allowed count, the greedy best, and the
 //     keys of 32 evenly spaced tokens;
 //  2. k_sample_plan (one workgroup): merges the slices (flags, count, greedy pick: the lowest token
-//     among the equal maxima), then sorts the 4096 sampled keys (bitonic, LDS) into a threshold with,
-//     by a wide margin, at least k allowed tokens at or above it (all allowed tokens when there are at
-//     most 4096);
+//     among the equal maxima), then picks from the 4096 sampled keys (radix select, LDS histograms)
+//     a threshold with, by a wide margin, at least k allowed tokens at or above it (all allowed tokens
+//     when there are at most 4096);
 //  3. k_sample_collect: per slice, the tokens at or above the threshold into a candidate buffer
 //     (slots from a global counter: a few hundred to a few thousand candidates);
 //  4. k_sample_final (one workgroup): sorts the candidates by (key descending, token ascending), so
@@ -191,11 +191,13 @@ __device__ void select_bin(const uint32_t* hist, int nb, uint32_t need, uint32_t
 
 // Bitonic sort of slots [0, N) (N a power of two <= kCap) into key-descending, token-ascending
 // order by a 1024-thread block; every thread takes its share of the N/2 pairs of each stage.
+template <bool kVal>
 __device__ void bitonic(uint32_t* key, uint32_t* idx, float* val, int N) {
     for (int size = 2; size <= N; size <<= 1) {
-        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+        for (int ls = __builtin_ctz((unsigned)size) - 1; ls >= 0; ls--) {
+            const int stride = 1 << ls;
             for (int p = threadIdx.x; p < N / 2; p += kST) {
-                const int i = 2 * stride * (p / stride) + (p % stride), j = i + stride;
+                const int i = ((p >> ls) << (ls + 1)) | (p & (stride - 1)), j = i + stride;
                 const uint32_t ka = key[i], kb = key[j], ia = idx[i], ib = idx[j];
                 const bool a_first = ka > kb || (ka == kb && ia < ib);  // i before j in the final order
                 const bool up = (i & size) == 0;                         // this block sorts in the final order
@@ -204,9 +206,11 @@ __device__ void bitonic(uint32_t* key, uint32_t* idx, float* val, int N) {
                     key[j] = ka;
                     idx[i] = ib;
                     idx[j] = ia;
-                    const float vi = val[i];
-                    val[i] = val[j];
-                    val[j] = vi;
+                    if (kVal) {
+                        const float vi = val[i];
+                        val[i] = val[j];
+                        val[j] = vi;
+                    }
                 }
             }
             __syncthreads();
@@ -280,22 +284,49 @@ __global__ __launch_bounds__(kPT) void k_sample_part(const SampleArgs a, Scratch
     }
 }
 
-// 2. Merge the slices; the candidate threshold.
+// 2. Merge the slices; the candidate threshold (a radix select over the sampled keys).
 __global__ __launch_bounds__(kST) void k_sample_plan(const SampleArgs a, Scratch* ws) {
-    __shared__ uint32_t skey[kCap], sidx[kCap];
-    __shared__ float sval[kCap];
+    __shared__ uint32_t hist[2048];
     __shared__ uint32_t red[kSW + 1];
+    __shared__ uint32_t res[2];
+    __shared__ float wv[kSW];
+    __shared__ uint32_t wi[kSW], wf[kSW], wn[kSW];
     __shared__ uint32_t plan[3];
-    const int t = threadIdx.x;
+    const int t = threadIdx.x, lane = t & (kWave - 1), w = t / kWave;
+    // the slices' flags, counts and greedy candidates, reduced over the block
+    uint32_t f = 0, nn = 0, ib = 0xFFFFFFFFu;
+    float b = -INFINITY;
+    if (t < kParts) {
+        f = ws->flags[t];
+        nn = ws->n[t];
+        b = ws->bv[t];
+        ib = ws->bi[t];
+    }
+#pragma unroll
+    for (int o = kWave / 2; o > 0; o >>= 1) {
+        f |= __shfl_xor(f, o, kWave);
+        nn += __shfl_xor(nn, o, kWave);
+        const float ov = __shfl_xor(b, o, kWave);
+        const uint32_t oi = __shfl_xor(ib, o, kWave);
+        if (greedy_better(ov, oi, b, ib)) {
+            b = ov;
+            ib = oi;
+        }
+    }
+    if (lane == 0) {
+        wv[w] = b;
+        wi[w] = ib;
+        wf[w] = f;
+        wn[w] = nn;
+    }
+    __syncthreads();
     if (t == 0) {
-        uint32_t f = 0, nn = 0, ib = 0xFFFFFFFFu;
-        float b = -INFINITY;
-        for (int p = 0; p < kParts; p++) {
-            f |= ws->flags[p];
-            nn += ws->n[p];
-            if (greedy_better(ws->bv[p], ws->bi[p], b, ib)) {
-                b = ws->bv[p];
-                ib = ws->bi[p];
+        for (int j = 1; j < kSW; j++) {
+            f |= wf[j];
+            nn += wn[j];
+            if (greedy_better(wv[j], wi[j], b, ib)) {
+                b = wv[j];
+                ib = wi[j];
             }
         }
         a.info[0] = 0;
@@ -315,17 +346,16 @@ __global__ __launch_bounds__(kST) void k_sample_plan(const SampleArgs a, Scratch
     }
     uint32_t Ts = 0;  // all allowed tokens when they fit the candidate slots
     if (n > (uint32_t)kCap) {
-        for (int j = t; j < kCap; j += kST) {
-            skey[j] = ws->samples[j];
-            sidx[j] = (uint32_t)j;
-            sval[j] = 0.0f;
-        }
-        __syncthreads();
-        bitonic(skey, sidx, sval, kCap);
+        constexpr int kPer = kCap / kST;  // sampled keys per thread
+        uint32_t key[kPer];
         uint32_t cnt = 0;
-        for (int j = t; j < kCap; j += kST) cnt += skey[j] != 0u;
+#pragma unroll
+        for (int e = 0; e < kPer; e++) {
+            key[e] = ws->samples[kPer * t + e];
+            cnt += key[e] != 0u;
+        }
         uint32_t as;
-        (void)block_scan(cnt, red, &as);  // allowed tokens among the samples
+        (void)block_scan(cnt, red, &as);  // allowed tokens among the samples (key 0: not allowed)
         // about kp = k as / n of the allowed samples lie at or above the k-th largest key, with a
         // spread of ~sqrt(kp) in that rank: the j-th largest allowed sample, j = kp + 5 sqrt(kp) + 3,
         // leaves at least k allowed tokens above it all but ~1e-6 of the time (and about
@@ -333,8 +363,27 @@ __global__ __launch_bounds__(kST) void k_sample_plan(const SampleArgs a, Scratch
         // kernel falls back to the exact select.
         if (as > 0) {
             const float kp = (float)k * (float)as / (float)n;
-            const uint32_t j = min(as, max(1u, (uint32_t)ceilf(kp + 5.0f * sqrtf(kp) + 3.0f)));
-            Ts = skey[j - 1];
+            uint32_t need = min(as, max(1u, (uint32_t)ceilf(kp + 5.0f * sqrtf(kp) + 3.0f)));
+            uint32_t prefix = 0;
+#pragma unroll
+            for (int p = 0; p < 3; p++) {
+                const int sh = p == 0 ? 21 : (p == 1 ? 10 : 0), wd = p == 2 ? 10 : 11;
+                const int nb = 1 << wd, hi = sh + wd;
+                for (int bb = t; bb < nb; bb += kST) hist[bb] = 0;
+                __syncthreads();
+#pragma unroll
+                for (int e = 0; e < kPer; e++) {
+                    if (key[e] == 0u || (hi < 32 && (key[e] >> hi) != prefix)) continue;
+                    atomicAdd(&hist[(key[e] >> sh) & (nb - 1)], 1u);
+                }
+                __syncthreads();
+                int bin;
+                uint32_t above;
+                select_bin(hist, nb, need, red, res, &bin, &above);
+                prefix = (prefix << wd) | (uint32_t)bin;
+                need -= above;
+            }
+            Ts = prefix;
         }
     }
     if (t == 0) {
@@ -455,7 +504,7 @@ __global__ __launch_bounds__(kST) void k_sample_final(const SampleArgs a, Scratc
         }
     }
     __syncthreads();
-    bitonic(ckey, cidx, cval, N);
+    bitonic<true>(ckey, cidx, cval, N);
     if ((uint32_t)t < k) {
         a.out_v[t] = cval[t];
         a.out_i[t] = cidx[t];
