@@ -298,10 +298,11 @@ int qne_paged_attn_decode(const float* q, const float* k_new, const float* v_new
         const int G = nq / nkv;
         need(G == 1 || G == 2 || G == 4, "nq/nkv must be 1, 2 or 4");
         need(max_blocks > 0, "max_blocks must be positive");
-        // Split-context partials: about 4096 4-wave workgroups (16 per CU, four resident at a time),
-        // so that enough K/V rows are in flight (measured: 2.8 / 2.9 / 3.2 TB/s at 1024 / 2048 /
-        // 4096 for 64 sequences of mean context 2213).
-        int splits = (4096 + nkv * batch - 1) / (nkv * batch);
+        // Split-context partials: about 1024 4-wave workgroups (4 per CU). Each wave keeps a whole
+        // 16-position block (16 KB of K and V) in flight, so longer splits beat more workgroups
+        // (measured for 64 sequences of mean context 2213: 4.75 / 4.66 / 4.40 / 3.82 TB/s at
+        // 1024 / 2048 / 4096 / 8192 workgroups).
+        int splits = (1024 + nkv * batch - 1) / (nkv * batch);
         if (splits < 1) splits = 1;
         if (splits > max_blocks) splits = max_blocks;
         const size_t parts = (size_t)batch * nkv * splits * G;

@@ -5,8 +5,8 @@
 //  - the cache is paged: pools [block][kv_head][16][256] f16, a block table maps logical blocks;
 //  - split-context ("flash decoding") partials: workgroup (split, kv_head, seq) streams a slice
 //    of the context once for all query heads that share the kv head (GQA reuse);
-//  - a wave covers 2 positions per step, 32 lanes per position, 8 dims (16 bytes of K and of V)
-//    per lane, with the next step's rows in flight; scores are half-wave DPP sums; softmax is
+//  - a wave takes 16-position blocks with all of a block's K and V rows in flight at once; scores
+//    on the matrix cores (f16 MFMA, q as two f16 halves), values on the vector ALUs; softmax is
 //    online (running max / sum) in base 2;
 //  - a combine kernel merges the splits (and applies the sigmoid output gate of the model).
 // The current token's k and v are appended (rounded to f16) before the partials run, so the
@@ -100,22 +100,40 @@ __global__ __launch_bounds__(kAttnThreads) void k_kv_append(const float* __restr
     v_pool[at] = f2h(v_new[src]);
 }
 
+typedef _Float16 h4v __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ h4v as_h4(uint32_t a, uint32_t b) { return __builtin_bit_cast(h4v, u32x2{a, b}); }
+
 // Split-context partials. Grid (splits, nkv, batch), 4 waves. Sequence b attends positions
 // 0..len-1 with len = lens[b] + 1 (lens = tok + 1 for the model, ctx for the raw form). A wave takes
-// two positions per step (one per 32-lane half; a lane holds 8 dims, 16 bytes of K and of V) and
-// loads the next step's rows while it computes the current ones. Scores are half-wave DPP sums.
-// The softmax runs in base 2: q is pre-scaled by log2(e) / sqrt(256), so each weight is one
-// exp2, and the partial maxima and sums are in that base (the combine uses the same base).
+// blocks of 16 positions (the waves interleave blocks); per block:
+//  - scores on the matrix cores: S[position][column] = K[16 x 256] . Qc[256 x 16] with
+//    v_mfma_f32_16x16x16_f16, K as stored (f16) and the columns 2h, 2h + 1 holding query head h as
+//    two f16 halves, hi = f16(x) and lo = f16((x - hi) * 2^11), so q keeps ~22 bits and the
+//    products are exact in f32. Lane l loads 16 bytes of row l % 16 at byte 64 i + 16 (l / 16)
+//    (i = 0..7): the 16 rows of a block are one contiguous 8 KB, each load instruction covers 16
+//    whole 64-byte segments, and the k slots of the two MFMAs fed by one load are the dims it holds;
+//  - the hi and lo columns are added across the lane pair, the block's per-head maximum and weight
+//    sum are reduced over the 4 lane groups, and the weights go through LDS ([position][head]);
+//  - values on the vector ALUs: lane l accumulates dims 4l..4l+3 of every head, reading one
+//    512-byte row per position (all 16 rows are loaded with the K rows, before the scores).
+// Rows past the sequence end in its last block are read (they lie in the block) but weigh 0 and
+// their values are replaced by 0. The softmax runs in base 2: q is pre-scaled by
+// log2(e) / sqrt(256), so each weight is one exp2 (the combine uses the same base).
 template <int G>
 __global__ __launch_bounds__(kAttnThreads) void k_attn_partial(const float* __restrict__ q, const uint16_t* __restrict__ k_pool,
                                                                const uint16_t* __restrict__ v_pool,
                                                                const int32_t* __restrict__ block_table, int max_blocks,
                                                                int bt_stride, const int32_t* __restrict__ lens, int nkv,
                                                                float* __restrict__ part_ml, float* __restrict__ part_acc) {
+    __shared__ __attribute__((aligned(16))) uint16_t s_q[G][2][kHD];  // per head: hi, lo halves as f16
+    __shared__ __attribute__((aligned(16))) float s_p[4][16][4];      // per wave: weights [position][head]
     __shared__ float s_ml[4][G][2];
     __shared__ __attribute__((aligned(16))) float s_acc[4][G][kHD];
     const int split = blockIdx.x, g = blockIdx.y, b = blockIdx.z, splits = gridDim.x;
-    const int t = threadIdx.x, lane = t % kWave, w = t / kWave, half = lane >> 5, li = lane & 31;
+    const int t = threadIdx.x, lane = t % kWave, w = t / kWave;
     const int len = max(1, min(lens[b] + 1, max_blocks * kBlock));  // never past the block table
     int per = (len + splits - 1) / splits;
     per = (per + kBlock - 1) / kBlock * kBlock;
@@ -124,99 +142,124 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_partial(const float* __re
     const int nq = nkv * G;
     constexpr float kScale = 1.4426950408889634f * 0.0625f;  // log2(e) / sqrt(256)
 
-    float qr[G][8], acc[G][8], m[G], l[G];
 #pragma unroll
     for (int gi = 0; gi < G; gi++) {
-        const float* qs = q + ((size_t)b * nq + g * G + gi) * kHD + 8 * li;
-        const float4 a0 = *(const float4*)qs, a1 = *(const float4*)(qs + 4);
-        qr[gi][0] = a0.x * kScale; qr[gi][1] = a0.y * kScale; qr[gi][2] = a0.z * kScale; qr[gi][3] = a0.w * kScale;
-        qr[gi][4] = a1.x * kScale; qr[gi][5] = a1.y * kScale; qr[gi][6] = a1.z * kScale; qr[gi][7] = a1.w * kScale;
-#pragma unroll
-        for (int d = 0; d < 8; d++) acc[gi][d] = 0.0f;
-        m[gi] = -INFINITY;
-        l[gi] = 0.0f;
-    }
-    auto load = [&](int p, u32x4& kw, u32x4& vw) {
-        if (p < p1) {
-            const size_t at = kv_index(bt, p, nkv, g) + 8 * li;
-            kw = __builtin_nontemporal_load((const u32x4*)(k_pool + at));
-            vw = __builtin_nontemporal_load((const u32x4*)(v_pool + at));
-        } else {
-            kw = u32x4{0u, 0u, 0u, 0u};
-            vw = kw;
-        }
-    };
-    u32x4 kc, vc, kn, vn;
-    load(p0 + 2 * w + half, kc, vc);
-    for (int base = p0 + 2 * w; base < p1; base += 8) {  // wave-uniform
-        const int pc = base + half;
-        const bool valid = pc < p1;
-        load(pc + 8, kn, vn);
-        float kf[8], vf[8];
-        kf[0] = lo_h(kc.x); kf[1] = hi_h(kc.x); kf[2] = lo_h(kc.y); kf[3] = hi_h(kc.y);
-        kf[4] = lo_h(kc.z); kf[5] = hi_h(kc.z); kf[6] = lo_h(kc.w); kf[7] = hi_h(kc.w);
-        vf[0] = lo_h(vc.x); vf[1] = hi_h(vc.x); vf[2] = lo_h(vc.y); vf[3] = hi_h(vc.y);
-        vf[4] = lo_h(vc.z); vf[5] = hi_h(vc.z); vf[6] = lo_h(vc.w); vf[7] = hi_h(vc.w);
-#pragma unroll
-        for (int gi = 0; gi < G; gi++) {
-            float s = 0.0f;
-#pragma unroll
-            for (int d = 0; d < 8; d++) s = fmaf(qr[gi][d], kf[d], s);
-            s = half_sum_dpp(s, lane);
-            s = valid ? s : -INFINITY;
-            // The running sum and accumulators are kept relative to m; m moves (and they are
-            // rescaled) only when a score exceeds it by more than 8 (a weight of 2^8 at most),
-            // which after the first positions is rare, so most positions cost one exp2 (the
-            // hardware v_exp_f32: weights below 2^-126 flush to 0).
-            if (__builtin_amdgcn_ballot_w64(s > m[gi] + 8.0f)) {  // wave-uniform branch
-                const float mn = fmaxf(m[gi], s);
-                const float corr = mn == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m[gi] - mn);
-                m[gi] = mn;
-                l[gi] *= corr;
-#pragma unroll
-                for (int d = 0; d < 8; d++) acc[gi][d] *= corr;
-            }
-            const float pw = s == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(s - m[gi]);  // an invalid position weighs 0
-            l[gi] += pw;
-#pragma unroll
-            for (int d = 0; d < 8; d++) acc[gi][d] = fmaf(pw, vf[d], acc[gi][d]);
-        }
-        kc = kn;
-        vc = vn;
-    }
-    // merge the two halves of the wave, then the 4 waves through LDS
-#pragma unroll
-    for (int gi = 0; gi < G; gi++) {
-        const float mo = lane_xor32(m[gi], lane), lo = lane_xor32(l[gi], lane);
-        const float mn = fmaxf(m[gi], mo);
-        const float ca = mn == -INFINITY ? 0.0f : exp2f(m[gi] - mn), cb = mn == -INFINITY ? 0.0f : exp2f(mo - mn);
-#pragma unroll
-        for (int d = 0; d < 8; d++) acc[gi][d] = acc[gi][d] * ca + lane_xor32(acc[gi][d], lane) * cb;
-        l[gi] = l[gi] * ca + lo * cb;
-        m[gi] = mn;
-        if (half == 0) {
-            *(float4*)&s_acc[w][gi][8 * li] = make_float4(acc[gi][0], acc[gi][1], acc[gi][2], acc[gi][3]);
-            *(float4*)&s_acc[w][gi][8 * li + 4] = make_float4(acc[gi][4], acc[gi][5], acc[gi][6], acc[gi][7]);
-            if (li == 0) { s_ml[w][gi][0] = m[gi]; s_ml[w][gi][1] = l[gi]; }
-        }
+        const float x = q[((size_t)b * nq + g * G + gi) * kHD + t] * kScale;
+        const _Float16 hi = (_Float16)x;
+        s_q[gi][0][t] = __builtin_bit_cast(uint16_t, hi);
+        s_q[gi][1][t] = __builtin_bit_cast(uint16_t, (_Float16)((x - (float)hi) * 2048.0f));
     }
     __syncthreads();
-    // thread t owns dim t for every head of the group
+
+    const int c = lane & 15, kq = lane >> 4;  // row (position) / column of the MFMA tiles, k group
+    // B operands, read from LDS per block: column c (zero past 2G), k slots = the dims lane loads
+    const uint16_t* qcol = &s_q[(c >> 1) % G][c & 1][8 * kq];
+
+    float m = -INFINITY, l = 0.0f;  // lanes c = 2h: head h's running maximum and weight sum
+    float acc[G][4];
+#pragma unroll
+    for (int gi = 0; gi < G; gi++)
+#pragma unroll
+        for (int e = 0; e < 4; e++) acc[gi][e] = 0.0f;
+
+    int bnext = p0 + 16 * w < p1 ? bt[(p0 + 16 * w) / kBlock] : 0;  // block table entries run one block ahead
+    for (int pb = p0 + 16 * w; pb < p1; pb += 64) {                  // wave-uniform
+        const int bcur = bnext;
+        if (pb + 64 < p1) bnext = bt[(pb + 64) / kBlock];
+        const size_t blk = ((size_t)bcur * nkv + g) * kBlock * kHD;  // the block's 16 rows, contiguous
+        u32x4 kw[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) kw[i] = __builtin_nontemporal_load((const u32x4*)(k_pool + blk + c * kHD + 32 * i + 8 * kq));
+        u32x2 vw[16];
+#pragma unroll
+        for (int j = 0; j < 16; j++) vw[j] = __builtin_nontemporal_load((const u32x2*)(v_pool + blk + j * kHD + 4 * lane));
+        __builtin_amdgcn_sched_barrier(0);  // all 24 loads in flight before the first MFMA waits
+        f32x4 sc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            u32x4 qw = *(const u32x4*)(qcol + 32 * i);
+            if (c >= 2 * G) qw = u32x4{0u, 0u, 0u, 0u};
+            sc = __builtin_amdgcn_mfma_f32_16x16x16f16(as_h4(kw[i].x, kw[i].y), as_h4(qw.x, qw.y), sc, 0, 0, 0);
+            sc = __builtin_amdgcn_mfma_f32_16x16x16f16(as_h4(kw[i].z, kw[i].w), as_h4(qw.z, qw.w), sc, 0, 0, 0);
+        }
+        // lane (c, kq) reg r holds column c of position pb + 4 kq + r; even lanes take hi + lo
+        float s[4];
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const float v = sc[r] + QNE_DPP(sc[r], kDppXor1) * (1.0f / 2048.0f);
+            s[r] = pb + 4 * kq + r < p1 ? v : -INFINITY;
+        }
+        float bm = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
+        bm = fmaxf(bm, lane_xor16(bm, lane));
+        bm = fmaxf(bm, lane_xor32(bm, lane));
+        const float mn = fmaxf(m, bm);                      // finite: position pb is in range
+        const float corr = __builtin_amdgcn_exp2f(m - mn);  // 0 on the first block
+        float p[4], ps = 0.0f;
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            p[r] = __builtin_amdgcn_exp2f(s[r] - mn);  // 0 past the range
+            ps += p[r];
+        }
+        ps += lane_xor16(ps, lane);
+        ps += lane_xor32(ps, lane);
+        l = l * corr + ps;
+        m = mn;
+        if (c < 2 * G && (c & 1) == 0) {
+#pragma unroll
+            for (int r = 0; r < 4; r++) s_p[w][4 * kq + r][c >> 1] = p[r];
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+        for (int gi = 0; gi < G; gi++) {
+            const float cg = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, corr), 2 * gi));
+#pragma unroll
+            for (int e = 0; e < 4; e++) acc[gi][e] *= cg;
+        }
+        const int nj = p1 - pb;  // rows at or past nj weigh 0; their values may be anything
+#pragma unroll
+        for (int j = 0; j < 16; j++) {
+            const uint32_t x0 = j < nj ? vw[j].x : 0u, x1 = j < nj ? vw[j].y : 0u;
+            const float v0 = lo_h(x0), v1 = hi_h(x0), v2 = lo_h(x1), v3 = hi_h(x1);
+            const float4 pw = *(const float4*)s_p[w][j];
+            const float pj[4] = {pw.x, pw.y, pw.z, pw.w};
+#pragma unroll
+            for (int gi = 0; gi < G; gi++) {
+                acc[gi][0] = fmaf(pj[gi], v0, acc[gi][0]);
+                acc[gi][1] = fmaf(pj[gi], v1, acc[gi][1]);
+                acc[gi][2] = fmaf(pj[gi], v2, acc[gi][2]);
+                acc[gi][3] = fmaf(pj[gi], v3, acc[gi][3]);
+            }
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();  // s_p is rewritten by the next block
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+    // the wave's partial: (m, l) of head h from lane 2h, acc for dims 4 lane..4 lane + 3
+    if (lane < 2 * G && (lane & 1) == 0) {
+        s_ml[w][lane >> 1][0] = m;
+        s_ml[w][lane >> 1][1] = l;
+    }
+#pragma unroll
+    for (int gi = 0; gi < G; gi++) *(float4*)&s_acc[w][gi][4 * lane] = make_float4(acc[gi][0], acc[gi][1], acc[gi][2], acc[gi][3]);
+    __syncthreads();
+    // merge the 4 waves: thread t owns dim t for every head of the group
     const size_t pbase = (((size_t)b * nkv + g) * splits + split) * G;
 #pragma unroll
     for (int gi = 0; gi < G; gi++) {
-        float mn = -INFINITY;
+        float mx = -INFINITY;
 #pragma unroll
-        for (int i = 0; i < 4; i++) mn = fmaxf(mn, s_ml[i][gi][0]);
+        for (int i = 0; i < 4; i++) mx = fmaxf(mx, s_ml[i][gi][0]);
         float lsum = 0.0f, a = 0.0f;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            const float c = mn == -INFINITY ? 0.0f : exp2f(s_ml[i][gi][0] - mn);
-            lsum += s_ml[i][gi][1] * c;
-            a += s_acc[i][gi][t] * c;
+            const float cw = mx == -INFINITY ? 0.0f : exp2f(s_ml[i][gi][0] - mx);
+            lsum += s_ml[i][gi][1] * cw;
+            a += s_acc[i][gi][t] * cw;
         }
         part_acc[(pbase + gi) * kHD + t] = a;
-        if (t == 0) { part_ml[(pbase + gi) * 2] = mn; part_ml[(pbase + gi) * 2 + 1] = lsum; }
+        if (t == 0) { part_ml[(pbase + gi) * 2] = mx; part_ml[(pbase + gi) * 2 + 1] = lsum; }
     }
 }
 
@@ -228,12 +271,13 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_combine(const float* __re
     const int h = blockIdx.x, b = blockIdx.y, t = threadIdx.x, g = h / G, gi = h % G, nq = nkv * G;
     float mn = -INFINITY;
     for (int s = 0; s < splits; s++) mn = fmaxf(mn, part_ml[((((size_t)b * nkv + g) * splits + s) * G + gi) * 2]);
+    // every split wrote its partial (an empty one: maximum -inf, sum 0, acc 0), and split 0 holds
+    // position 0, so mn is finite and an empty split weighs exp2(-inf) = 0
     float lsum = 0.0f, a = 0.0f;
+#pragma unroll 8
     for (int s = 0; s < splits; s++) {
         const size_t i = (((size_t)b * nkv + g) * splits + s) * G + gi;
-        const float ms = part_ml[i * 2];
-        if (ms == -INFINITY) continue;
-        const float c = exp2f(ms - mn);  // the partials' maxima are in base 2
+        const float c = exp2f(part_ml[i * 2] - mn);  // the partials' maxima are in base 2
         lsum += part_ml[i * 2 + 1] * c;
         a += part_acc[i * kHD + t] * c;
     }
