@@ -61,13 +61,41 @@ __device__ __forceinline__ void store_tile(const float (&s)[32], float* S, int c
 // The model keeps each head's state value-major, S_T[t][j] = S[j][t]: the 128 keys of one value
 // column are contiguous, so a column (what one wave updates in the persistent decode kernel) is a
 // single 512-byte read.
-__device__ __forceinline__ void load_tile_t(float (&s)[32], const float* S, int col, int qq) {
+// The value-major tile goes through LDS: the 512 threads read and write it as 16-byte pieces in
+// address order (each wave instruction one contiguous KiB), and each thread takes its 32 values
+// from the staged copy. Rows are padded to 132 floats, so the 8 lanes of a 16-byte LDS access
+// (consecutive columns) fall on distinct banks.
+constexpr int kTileStride = kDK + 4;
+typedef float f4v __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ void load_tile_t_issue(f4v (&v)[8], const float* S) {
 #pragma unroll
-    for (int i = 0; i < 32; i++) s[i] = S[col * kDK + 32 * qq + i];
+    for (int r = 0; r < 8; r++) v[r] = __builtin_nontemporal_load((const f4v*)S + threadIdx.x + kGdnThreads * r);
 }
-__device__ __forceinline__ void store_tile_t(const float (&s)[32], float* S, int col, int qq) {
+__device__ __forceinline__ void stage_tile_t(const f4v (&v)[8], float* tile) {
 #pragma unroll
-    for (int i = 0; i < 32; i++) S[col * kDK + 32 * qq + i] = s[i];
+    for (int r = 0; r < 8; r++) {
+        const int f = threadIdx.x + kGdnThreads * r;  // 16-byte piece f: column f / 32, keys 4 (f % 32)..+3
+        *(f4v*)&tile[(f >> 5) * kTileStride + 4 * (f & 31)] = v[r];
+    }
+}
+__device__ __forceinline__ void read_tile_t(float (&s)[32], const float* tile, int col, int qq) {
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const float4 x = *(const float4*)&tile[col * kTileStride + 32 * qq + 4 * i];
+        s[4 * i] = x.x; s[4 * i + 1] = x.y; s[4 * i + 2] = x.z; s[4 * i + 3] = x.w;
+    }
+}
+__device__ __forceinline__ void write_tile_t(const float (&s)[32], float* tile, int col, int qq) {
+#pragma unroll
+    for (int i = 0; i < 8; i++)
+        *(float4*)&tile[col * kTileStride + 32 * qq + 4 * i] = make_float4(s[4 * i], s[4 * i + 1], s[4 * i + 2], s[4 * i + 3]);
+}
+__device__ __forceinline__ void store_tile_t(const float* tile, float* S) {
+#pragma unroll
+    for (int r = 0; r < 8; r++) {
+        const int f = threadIdx.x + kGdnThreads * r;
+        __builtin_nontemporal_store(*(const f4v*)&tile[(f >> 5) * kTileStride + 4 * (f & 31)], (f4v*)S + f);
+    }
 }
 
 // Model decode step for head blockIdx.x: conv + SiLU on the head's q, k, v channels, L2 norms,
@@ -78,6 +106,7 @@ __global__ __launch_bounds__(kGdnThreads) void k_gdn_decode(const float* __restr
                                                             float* __restrict__ out, const float* __restrict__ prm, int H,
                                                             GdnRowStrides rs) {
     __shared__ DeltaShared sh;
+    __shared__ __attribute__((aligned(16))) float tile[kDV * kTileStride];
     const int h = blockIdx.x, t = threadIdx.x, lane = t % kWave, w = t / kWave;
     // row blockIdx.y of a batch: its own projection, conv and recurrent state, output
     proj += (size_t)blockIdx.y * rs.proj;
@@ -87,7 +116,8 @@ __global__ __launch_bounds__(kGdnThreads) void k_gdn_decode(const float* __restr
     const int col = t & (kDV - 1), qq = t >> 7;
     float* S = state + (size_t)h * kDK * kDV;
     float s[32];
-    load_tile_t(s, S, col, qq);  // in flight while the conv runs
+    f4v tv[8];
+    load_tile_t_issue(tv, S);  // in flight while the conv runs
 
     float val = 0.0f;
     if (t < 384) {
@@ -100,6 +130,7 @@ __global__ __launch_bounds__(kGdnThreads) void k_gdn_decode(const float* __restr
         st[0] = s1; st[1] = s2; st[2] = x;
         val = silu(y);
     }
+    stage_tile_t(tv, tile);
     const float ss = wave_sum(val * val);
     if (lane == 0) sh.red[w] = ss;
     __syncthreads();
@@ -118,12 +149,14 @@ __global__ __launch_bounds__(kGdnThreads) void k_gdn_decode(const float* __restr
         p = wave_sum(p);
         if (lane == 0) sh.kq = p;
     }
-    __syncthreads();
+    __syncthreads();  // also orders the staged tile before the reads below
+    read_tile_t(s, tile, col, qq);
     const float o = delta_token(s, sh, col, qq);
-    store_tile_t(s, S, col, qq);
+    write_tile_t(s, tile, col, qq);  // only this thread's slots: no hazard with the reads above
     // gated RMSNorm over the head's dv outputs (quarter 0 = waves 0 and 1)
     const float oo = wave_sum(o * o);
     __syncthreads();
+    store_tile_t(tile, S);
     if (lane == 0) sh.red[w] = oo;
     __syncthreads();
     if (qq == 0) {
