@@ -156,6 +156,70 @@ def bench_paged_attention(args) -> dict:
             "cpu_baseline": None}
 
 
+def bench_gemv(args) -> dict:
+    """The standalone GEMV kernels (qne_gemv, the graph engine's per-matrix launches) on every
+    matrix shape of one 2B decode token at batch 1: int4 g64 layer matrices (GDN and attention
+    in-projections, out-projections, gate_up with the SwiGLU epilogue, down) and the f16 LM head.
+    Each shape rotates over enough copies of its weights (>= 1 GiB) that the 256 MB MALL cannot
+    serve them. Algorithmic bytes per call: nibbles + (scale, zero) pairs (or f16 rows), x and y.
+    The aggregate weighs each shape by its launches per token (21 GDN and 7 attention layers)."""
+    import torch
+    import qne
+    cfg = {"hidden": 2048, "inter": 6144, "vocab": 151936, "gdn": 2 * 16 * 128 * 2 + 2 * 16, "attn": 2 * 16 * 256 + 2 * 4 * 256}
+    h, g64 = cfg["hidden"], 64
+    shapes = [  # name, kind, rows, k, epilogue, launches per token
+        ("gdn_in", qne.MAT_Q4, cfg["gdn"], h, qne.EPI_STORE, 21),
+        ("attn_in", qne.MAT_Q4, cfg["attn"], h, qne.EPI_STORE, 7),
+        ("gdn_out", qne.MAT_Q4, h, 16 * 128, qne.EPI_ACCUMULATE, 21),
+        ("attn_out", qne.MAT_Q4, h, 16 * 256, qne.EPI_ACCUMULATE, 7),
+        ("gate_up", qne.MAT_Q4, 2 * cfg["inter"], h, qne.EPI_SWIGLU, 28),
+        ("down", qne.MAT_Q4, h, cfg["inter"], qne.EPI_ACCUMULATE, 28),
+        ("lm_head", qne.MAT_F16, cfg["vocab"], h, qne.EPI_STORE, 1),
+    ]
+    gen = torch.Generator(device="cuda").manual_seed(args.seed)
+    rows_out, tot_bytes, tot_ms = [], 0, 0.0
+    for name, kind, rows, k, epi, per_tok in shapes:
+        if kind == qne.MAT_Q4:
+            wbytes = rows * k // 2 + rows * (k // g64) * 4
+        else:
+            wbytes = rows * k * 2
+        copies = max(2, -(-(1 << 30) // wbytes))
+        if kind == qne.MAT_Q4:
+            w = torch.randint(-2**31, 2**31 - 1, (copies, rows, k // 8), dtype=torch.int32, device="cuda", generator=gen)
+            sz = (torch.rand(copies, rows, k // g64, 2, device="cuda", generator=gen) * 0.02).half()
+        else:
+            w = (torch.randn(copies, rows, k, device="cuda", generator=gen) * 0.02).half()
+            sz = None
+        x = torch.randn(k, device="cuda", generator=gen)
+        y = torch.zeros(rows // 2 if epi == qne.EPI_SWIGLU else rows, device="cuda")
+        i = [0]
+
+        def call(stream):
+            c = i[0] % copies
+            i[0] += 1
+            qne.gemv(kind, w[c].data_ptr(), sz[c].data_ptr() if sz is not None else 0, rows, k, g64, x.data_ptr(),
+                     y.data_ptr(), epi, stream=stream)
+
+        ms = _events_ms(call, max(args.warmup, copies), max(args.steps, 2 * copies))
+        nbytes = wbytes + k * 4 + y.numel() * 4 * (2 if epi == qne.EPI_ACCUMULATE else 1)
+        rows_out.append({"matrix": name, "rows": rows, "k": k, "dtype": "q4 g64" if kind == qne.MAT_Q4 else "f16",
+                         "us": round(ms * 1e3, 2), "GB/s": round(nbytes / (ms / 1e3) / 1e9, 1), "copies": copies})
+        tot_bytes += nbytes * per_tok
+        tot_ms += ms * per_tok
+        del w, sz
+        torch.cuda.empty_cache()
+    gbs = tot_bytes / (tot_ms / 1e3) / 1e9
+    return {"metric": "GEMV kernel GB/s (2B int4 decode matrices + f16 LM head, batch 1)", "value": round(gbs, 1),
+            "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+            "ms_per_step": round(tot_ms, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+            "dtype": "f32 accumulate, int4 / f16 weights", "data": "synthetic",
+            "config": {"workload": "one decode token's GEMVs as standalone launches (21 GDN + 7 attention layers)"},
+            "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                         "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None, "kernel": "k_gemv (qne_gemv)",
+                         "bytes_per_step": tot_bytes},
+            "detail": rows_out, "cpu_baseline": None}
+
+
 def bench_gdn(args) -> dict:
     """Gated delta rule, 16 heads, dk = dv = 128, f32 state; q, k L2-normalised N(0, 1), v N(0, 1),
     beta = sigmoid(N(0, 1)), decay g = exp(-softplus(N(0, 1))). (a) one recurrent step at batch 1, 8
@@ -403,7 +467,7 @@ def main():
     ap.add_argument("--ctx", type=int, default=4000)
     ap.add_argument("--config", default="2b",
                     help="2b (the decode benchmark), 0.8b, batch (64-sequence batched decode), sample (sampled "
-                         "decode with the device sampler), or the kernel microbenches attn / gdn")
+                         "decode with the device sampler), or the kernel microbenches attn / gdn / gemv")
     ap.add_argument("--batch", type=int, default=64, help="sequences (--config attn / batch)")
     ap.add_argument("--cpu-tokens", type=int, default=4)
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -417,9 +481,10 @@ def main():
     if args.copy_calibration:
         copy_calibration(args.copy_calibration)
         return
-    if args.config in ("attn", "gdn"):
+    if args.config in ("attn", "gdn", "gemv"):
         sys.path[:0] = [str(ROOT / "qwen-native-engine_amd")]
-        print(json.dumps(bench_paged_attention(args) if args.config == "attn" else bench_gdn(args)))
+        fn = {"attn": bench_paged_attention, "gdn": bench_gdn, "gemv": bench_gemv}[args.config]
+        print(json.dumps(fn(args)))
         return
     if args.config == "batch":
         print(json.dumps(bench_batch(args)))
