@@ -283,20 +283,26 @@ __global__ __launch_bounds__(256) void k_gemm_reduce(const GemmArgs a) {
         float g = 0.0f, u = 0.0f;
         const float* p = a.part + (size_t)r * a.N + c;
         const size_t ss = (size_t)kBM * a.N;  // between splits
-        // loads of four splits in flight at a time; the sum stays in split order
-        int s = 0;
-        for (; s + 4 <= a.splits; s += 4) {
-            const float g0 = p[s * ss], g1 = p[(s + 1) * ss], g2 = p[(s + 2) * ss], g3 = p[(s + 3) * ss];
-            g = g + g0 + g1 + g2 + g3;
-            if (a.epi == EPI_SWIGLU) {
-                const float u0 = p[s * ss + a.n_out], u1 = p[(s + 1) * ss + a.n_out];
-                const float u2 = p[(s + 2) * ss + a.n_out], u3 = p[(s + 3) * ss + a.n_out];
-                u = u + u0 + u1 + u2 + u3;
-            }
+        // every split's load in flight at once (up to kSplitsInFlight), then the sum in split order
+        constexpr int kSplitsInFlight = 24;
+        const bool swiglu = a.epi == EPI_SWIGLU;
+        float gv[kSplitsInFlight], uv[kSplitsInFlight];
+#pragma unroll
+        for (int s = 0; s < kSplitsInFlight; s++) {
+            gv[s] = s < a.splits ? p[s * ss] : 0.0f;
+            uv[s] = s < a.splits && swiglu ? p[s * ss + a.n_out] : 0.0f;
         }
-        for (; s < a.splits; s++) {
+        __builtin_amdgcn_sched_barrier(0);
+        g = gv[0];  // a.splits >= 1
+        u = uv[0];
+#pragma unroll
+        for (int s = 1; s < kSplitsInFlight; s++) {  // past a.splits the terms are +0: g and u unchanged
+            g += gv[s];
+            u += uv[s];
+        }
+        for (int s = kSplitsInFlight; s < a.splits; s++) {
             g += p[s * ss];
-            if (a.epi == EPI_SWIGLU) u += p[s * ss + a.n_out];
+            if (swiglu) u += p[s * ss + a.n_out];
         }
         g *= inv;
         u *= inv;
