@@ -34,10 +34,14 @@ const char* qne_last_error(void);
  * Parses and validates index.json (format_version 1 or 2) against the weights blob before any
  * device work, then copies the tensors to HBM (tensors with the same (offset, bytes) are uploaded
  * once, model.rs:185-194). The caller may free `weights` after the call returns.
- * `options_json` (nullable) replaces the reference's tile profile and flags; recognised keys:
- *   "max_context" (default 4096, the reference's MAX_CONTEXT), "device" (HIP ordinal, default 0).
- * A reference tile-profile object (ModelTiles, model.rs:90-98) is accepted and ignored: kernel
- * shapes here are chosen per matrix at load. `allow_f16` is accepted for signature parity. */
+ * `options_json` (nullable) carries the reference's `tiles` argument and this library's flags;
+ * recognised keys: "max_context" (default 4096, the reference's MAX_CONTEXT), "device" (HIP
+ * ordinal, default 0), "engine" ("persistent" or "graph"), "tiles" (a serialised ModelTiles,
+ * model.rs:90-98). A serialised ModelTiles may also be passed as the whole object. A tile profile
+ * is validated like ModelTiles::validate (model.rs:101-109, called at model.rs:174, after the index
+ * and before any device work): QNE_EINVAL "invalid kernel tile profile: Tile { ... }" for a tile the
+ * reference rejects, or for a missing field. A valid profile changes nothing else: kernel shapes
+ * here are chosen per matrix at load. `allow_f16` is accepted for signature parity. */
 int qne_model_load(const char* index_json, size_t index_len, const void* weights, size_t weights_len,
                    const char* options_json, int allow_f16, qne_model** out);
 /* drop(Model) */
@@ -74,13 +78,22 @@ int qne_snapshot(qne_model* m);
 int qne_restore(qne_model* m);
 /* Model::last_token -- model.rs:417: (greedy id, next position). */
 int qne_last_token(qne_model* m, uint32_t* token, uint32_t* next_pos);
-/* Model::decode -- model.rs:426. Greedy decode of up to n ids, `window` steps per submission.
- * out[0] is last_token(); each later id is fed back on the device. Unlike the reference, every id
- * of a window is returned (no u32::MAX placeholders). Stops after the first id found in `stop`;
- * with window > 1 the state may have advanced past it, as in the reference. *len = ids written.
- * QNE_ECONTEXT if next_pos + steps would exceed max_context. */
+/* Model::decode -- model.rs:426-449. Greedy decode: out[0] = last_token().0, then submissions of
+ * min(window, n - len) steps whose picks are fed back on the device. As in the reference, a
+ * one-step submission appends its pick and a longer one appends that many u32::MAX (0xFFFFFFFF)
+ * placeholders (model.rs:441-446); the loop continues while len < n and the LAST value appended is
+ * not in `stop` (model.rs:433), so a stop id inside a window is not seen. *len = values written.
+ * QNE_ECONTEXT ("context limit of ... tokens reached after ... generated tokens") if
+ * next_pos + steps would exceed max_context. */
 int qne_decode(qne_model* m, size_t n, uint32_t window, const uint32_t* stop, size_t nstop,
                uint32_t* out, size_t cap, size_t* len);
+/* No counterpart in the reference (its decode reads back only the last pick of a window,
+ * model.rs:439-446): the same loop with every step's pick appended on the device, so every id of
+ * every window is returned, ending after the first id found in `stop` (with window > 1 the state
+ * may have advanced past it, as in the reference). For callers that want a window's ids without a
+ * host round trip per token. Same errors as qne_decode. */
+int qne_decode_ids(qne_model* m, size_t n, uint32_t window, const uint32_t* stop, size_t nstop,
+                   uint32_t* out, size_t cap, size_t* len);
 /* Model::dispatches_per_token -- model.rs:309 (kernel launches per decode token). */
 int qne_dispatches_per_token(qne_model* m, size_t* out);
 /* Model.adapter -- model.rs:167: device name, written NUL-terminated into buf. */
@@ -192,6 +205,11 @@ int qne_batch_free(qne_batch* b);
 /* Row `row` takes over the model's current sequence (after qne_prefill / qne_decode): its KV cache,
  * recurrent state and next (token, position) as qne_last_token reports them. */
 int qne_batch_admit(qne_batch* b, uint32_t row);
+/* Row `row` of dst takes over row `src_row` of src (a batch over the same model, possibly dst
+ * itself): its KV cache, recurrent state and next (token, position). No counterpart in the
+ * reference (one sequence per Model); it moves a sequence between batches of different sizes, and
+ * a row's results do not depend on the batch it runs in (bit for bit). */
+int qne_batch_copy_row(qne_batch* dst, uint32_t row, qne_batch* src, uint32_t src_row);
 /* Row `row` becomes an empty sequence at position 0 whose next token is `token`. */
 int qne_batch_reset_row(qne_batch* b, uint32_t row, uint32_t token);
 /* The next token and position of rows 0..n-1 (either pointer may be null). */

@@ -174,6 +174,23 @@ class OracleModel:
     def reset(self):
         self.L.oc_reset(self.state)
 
+    def state_bytes(self) -> bytes:
+        """Every recurrent, conv and KV value of the state, concatenated (for bitwise comparisons)."""
+        c = self.cfg
+        attn = [(i + 1) % c["full_attention_every"] == 0 for i in range(c["layers"])]
+        n_gdn, n_attn = attn.count(False), attn.count(True)
+        rec = c["gdn_heads"] * c["gdn_dk"] * c["gdn_dv"] * 4
+        conv = (2 * c["gdn_heads"] * c["gdn_dk"] + c["gdn_heads"] * c["gdn_dv"]) * (c["conv_kernel"] - 1) * 4
+        kv = c["n_kv_heads"] * self.max_context * c["head_dim"] * 2
+        out = []
+        for i in range(n_gdn):
+            out.append(ctypes.string_at(self.L.oc_state_recurrent(self.state, i), rec))
+            out.append(ctypes.string_at(self.L.oc_state_conv(self.state, i), conv))
+        for i in range(n_attn):
+            out.append(ctypes.string_at(self.L.oc_state_kcache(self.state, i), kv))
+            out.append(ctypes.string_at(self.L.oc_state_vcache(self.state, i), kv))
+        return b"".join(out)
+
     def token(self, token: int, pos: int, want_logits: bool = True):
         out = np.empty(self.cfg["vocab"], dtype=np.float32) if want_logits else None
         self.L.oc_token(ctypes.byref(self.m), self.state, token, pos, ptr(out) if want_logits else None)

@@ -71,9 +71,8 @@ void oc_dequant_row(const oc_mat* m, int row, float* out) {
     const uint32_t* w = (const uint32_t*)m->w + (size_t)row * (k / 8);
     const uint16_t* s = (const uint16_t*)m->s;
     const int groups = k / m->group;
-    for (int c = 0; c < k; c++) {
-        uint32_t q = (w[c / 8] >> (4 * (c % 8))) & 15u;
-        int b = c / m->group;
+    /* the group's scale and zero are converted once and reused for its values */
+    for (int b = 0; b < groups; b++) {
         float scale = oc_f16_to_f32(s[(size_t)row * groups + b]);
         float zp;
         if (m->kind == OC_Q4G) {
@@ -82,7 +81,10 @@ void oc_dequant_row(const oc_mat* m, int row, float* out) {
             const uint8_t* z = (const uint8_t*)m->z + (size_t)row * ((groups + 1) / 2);
             zp = (float)((z[b / 2] >> (4 * (b % 2))) & 15u);
         }
-        out[c] = ((float)q - zp) * scale;
+        for (int c = b * m->group; c < (b + 1) * m->group; c++) {
+            uint32_t q = (w[c / 8] >> (4 * (c % 8))) & 15u;
+            out[c] = ((float)q - zp) * scale;
+        }
     }
 }
 
@@ -533,13 +535,107 @@ void oc_token(const oc_model* m, oc_state* s, uint32_t token, uint32_t pos, floa
     if (logits) head(m, s, logits);
 }
 
+/* oc_gemv for n tokens at once: y[t*ys + r] from x[t*xs ...] for t < n. Within one projection
+ * the tokens of a prompt are independent, so each matrix row is dequantised once per block of
+ * kTokBlock tokens and applied to all of them. Every (row, token) result is computed with the
+ * operations of oc_gemv (dot_row's sum in column order, the same epilogue expression), so the
+ * outputs are bitwise those of calling oc_gemv once per token. */
+enum { kTokBlock = 32 };
+
+static void dot_tokens(const oc_mat* m, int row, const float* xt, float* scratch, real* acc) {
+    oc_dequant_row(m, row, scratch);
+    for (int j = 0; j < kTokBlock; j++) acc[j] = 0;
+    for (int c = 0; c < m->k; c++) {
+        const real w = (real)scratch[c];
+        const float* xc = xt + (size_t)c * kTokBlock;
+        for (int j = 0; j < kTokBlock; j++) acc[j] += w * (real)xc[j];
+    }
+}
+
+static void gemv_tokens(const oc_mat* m, const float* x, size_t xs, float* y, size_t ys, int n, int epilogue) {
+    const int out_rows = epilogue == OC_SWIGLU ? m->rows / 2 : m->rows;
+    const int k = m->k;
+    float* xt = (float*)malloc(sizeof(float) * (size_t)k * kTokBlock);
+    for (int t0 = 0; t0 < n; t0 += kTokBlock) {
+        const int nt = n - t0 < kTokBlock ? n - t0 : kTokBlock;
+        for (int c = 0; c < k; c++)
+            for (int j = 0; j < kTokBlock; j++) xt[(size_t)c * kTokBlock + j] = j < nt ? x[(size_t)(t0 + j) * xs + c] : 0.0f;
+#pragma omp parallel
+        {
+            float* scratch = (float*)malloc(sizeof(float) * (size_t)k);
+            real a[kTokBlock], u[kTokBlock];
+#pragma omp for schedule(static)
+            for (int r = 0; r < out_rows; r++) {
+                dot_tokens(m, r, xt, scratch, a);
+                if (epilogue == OC_SWIGLU) dot_tokens(m, r + out_rows, xt, scratch, u);
+                for (int j = 0; j < nt; j++) {
+                    float* yr = y + (size_t)(t0 + j) * ys + r;
+                    if (epilogue == OC_STORE) *yr = (float)a[j];
+                    else if (epilogue == OC_ACCUMULATE) *yr = (float)((real)*yr + a[j]);
+                    else *yr = (float)(r_silu(a[j]) * u[j]);
+                }
+            }
+            free(scratch);
+        }
+    }
+    free(xt);
+}
+
+/* The layers for tokens ids[0..n) at positions start.., layer by layer: every projection runs over
+ * all n tokens at once (gemv_tokens), the mixers (conv + delta rule, attention) token by token in
+ * order. Each token sees exactly the operations of run_layers, so the state and the last token's
+ * residual stream (left in s->h) are bitwise those of n run_layers calls. */
+static void run_layers_tokens(const oc_model* m, oc_state* s, const uint32_t* ids, int n, uint32_t start) {
+    const oc_config* c = &m->c;
+    const size_t H = (size_t)c->hidden;
+    const size_t attn_proj = (size_t)2 * c->n_q_heads * c->head_dim + (size_t)2 * c->n_kv_heads * c->head_dim;
+    const size_t gdn_proj = (size_t)2 * c->gdn_heads * c->gdn_dk + (size_t)2 * c->gdn_heads * c->gdn_dv + 2 * (size_t)c->gdn_heads;
+    const size_t P = attn_proj > gdn_proj ? attn_proj : gdn_proj;
+    size_t MX = (size_t)c->n_q_heads * c->head_dim;
+    if ((size_t)c->gdn_heads * c->gdn_dv > MX) MX = (size_t)c->gdn_heads * c->gdn_dv;
+    const size_t I = (size_t)c->intermediate;
+    float* h = (float*)malloc(sizeof(float) * n * H);
+    float* xn = (float*)malloc(sizeof(float) * n * H);
+    float* proj = (float*)malloc(sizeof(float) * n * P);
+    float* mixed = (float*)malloc(sizeof(float) * n * MX);
+    float* act = (float*)malloc(sizeof(float) * n * I);
+    for (int t = 0; t < n; t++) oc_embed(&m->embed, ids[t], h + t * H);
+    int gi = 0, ai = 0;
+    for (int i = 0; i < c->layers; i++) {
+        const oc_layer* L = &m->layers[i];
+        for (int t = 0; t < n; t++) oc_rmsnorm(h + t * H, L->input_norm, xn + t * H, c->hidden, c->eps);
+        gemv_tokens(&L->mixer_in, xn, H, proj, P, n, OC_STORE);
+        if (is_attn(c, i)) {
+            for (int t = 0; t < n; t++)
+                oc_attention_step(c, proj + t * P, oc_state_kcache(s, ai), oc_state_vcache(s, ai), start + (uint32_t)t,
+                                  mixed + t * MX, L->attn_norms);
+            ai++;
+        } else {
+            for (int t = 0; t < n; t++)
+                oc_gdn_step(c, proj + t * P, oc_state_conv(s, gi), L->conv_w, oc_state_recurrent(s, gi), mixed + t * MX,
+                            L->gdn_params);
+            gi++;
+        }
+        gemv_tokens(&L->mixer_out, mixed, MX, h, H, n, OC_ACCUMULATE);
+        for (int t = 0; t < n; t++) oc_rmsnorm(h + t * H, L->post_norm, xn + t * H, c->hidden, c->eps);
+        gemv_tokens(&L->gate_up, xn, H, act, I, n, OC_SWIGLU);
+        gemv_tokens(&L->down, act, I, h, H, n, OC_ACCUMULATE);
+    }
+    memcpy(s->h, h + (size_t)(n - 1) * H, sizeof(float) * H);
+    free(h); free(xn); free(proj); free(mixed); free(act);
+}
+
 /* Model::prefill_chunk (model.rs:349-372): the tokens continue the state at `start`; with
  * finish_logits, the logits after the last one. It leaves the same state as feeding the tokens
- * one at a time (model.rs:337-338), which is how the oracle computes it. */
+ * one at a time (model.rs:337-338): the oracle runs them layer by layer in blocks of up to 512
+ * tokens with exactly the arithmetic of oc_token (run_layers_tokens). */
 void oc_prefill_chunk(const oc_model* m, oc_state* s, const uint32_t* ids, int n, uint32_t start,
                       int finish_logits, float* logits) {
-    for (int i = 0; i < n; i++) run_layers(m, s, ids[i], start + (uint32_t)i);
-    if (finish_logits && logits) head(m, s, logits);
+    for (int i = 0; i < n; i += 512) {
+        const int nb = n - i < 512 ? n - i : 512;
+        run_layers_tokens(m, s, ids + i, nb, start + (uint32_t)i);
+    }
+    if (n > 0 && finish_logits && logits) head(m, s, logits);
 }
 
 int oc_num_threads(void) {

@@ -177,6 +177,15 @@ int qne_decode(qne_model* m, size_t n, uint32_t window, const uint32_t* stop, si
     });
 }
 
+int qne_decode_ids(qne_model* m, size_t n, uint32_t window, const uint32_t* stop, size_t nstop, uint32_t* out,
+                   size_t cap, size_t* len) {
+    return guard([&] {
+        need(len != nullptr && (out || n == 0), "null output");
+        need(stop || nstop == 0, "null stop list");
+        *len = model(m).decode_ids(n, window, stop, nstop, out, cap);
+    });
+}
+
 int qne_dispatches_per_token(qne_model* m, size_t* out) {
     return guard([&] {
         need(out != nullptr, "null output");
@@ -419,6 +428,10 @@ int qne_batch_free(qne_batch* b) {
 }
 
 int qne_batch_admit(qne_batch* b, uint32_t row) { return guard([&] { batch(b).admit((int)row); }); }
+
+int qne_batch_copy_row(qne_batch* dst, uint32_t row, qne_batch* src, uint32_t src_row) {
+    return guard([&] { batch(dst).copy_row((int)row, batch(src), (int)src_row); });
+}
 
 int qne_batch_reset_row(qne_batch* b, uint32_t row, uint32_t token) {
     return guard([&] { batch(b).reset_row((int)row, token); });

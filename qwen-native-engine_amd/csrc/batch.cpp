@@ -16,12 +16,13 @@ namespace qne {
 namespace {
 constexpr int kRowsMax = 64;
 
-int attn_splits_for(int rows, int nkv, int max_blocks) {
-    // about 1024 workgroups of context per attention layer: a wave keeps a whole 16-position block
-    // in flight, so longer splits beat more workgroups (64 sequences: 15.9k / 15.9k / 15.7k tok/s
-    // at 1024 / 2048 / 4096)
-    const int per = nkv * rows;
-    return std::max(1, std::min(max_blocks, (1024 + per - 1) / per));
+int attn_splits_for(int max_blocks) {
+    // One context split per 512 positions of capacity, whatever the number of rows: a row's split
+    // boundaries (and so the order its attention partials are merged in) depend only on its own
+    // length, and a row's result is bitwise the same in a batch of any size. At 64 rows of 4096
+    // positions that is 2048 workgroups per layer (64 sequences measured 15.9k / 15.9k / 15.7k
+    // tok/s at 1024 / 2048 / 4096 workgroups: a wave keeps a whole 16-position block in flight).
+    return std::max(1, std::min(max_blocks, (max_blocks + 31) / 32));
 }
 }  // namespace
 
@@ -87,7 +88,10 @@ void* BatchDecoder::dalloc(size_t bytes) {
     return p;
 }
 
-void BatchDecoder::sync() { wait_stream(stream_); }
+void BatchDecoder::sync(double steps) {
+    // a batched step is about 8 dependent launches per layer plus the LM head
+    wait_stream(stream_, work_deadline_s(steps * (8.0 * (double)m_.layers_.size() + 4.0)));
+}
 
 BatchDecoder::BatchDecoder(Model& m, int max_rows, int max_context) : m_(m), max_rows_(max_rows), max_context_(max_context) {
     if (max_rows < 1 || max_rows > kRowsMax) throw Error(QNE_EINVAL, "rows must be 1..64");
@@ -144,8 +148,7 @@ BatchDecoder::BatchDecoder(Model& m, int max_rows, int max_context) : m_(m), max
         frag_b_ = (uint8_t*)dalloc(frag);
         QNE_HIP(hipMemset(frag_a_, 0, frag));
         QNE_HIP(hipMemset(frag_b_, 0, frag));
-        for (int r = 1; r <= max_rows; r++)
-            attn_part_rows_ = std::max(attn_part_rows_, (size_t)r * attn_splits_for(r, c.n_kv_heads, max_blocks_));
+        attn_part_rows_ = (size_t)max_rows * attn_splits_for(max_blocks_);
         const size_t G = (size_t)(c.n_q_heads / c.n_kv_heads);
         attn_ml_ = (float*)dalloc(attn_part_rows_ * c.n_kv_heads * G * 2 * 4);
         attn_acc_ = (float*)dalloc(attn_part_rows_ * c.n_kv_heads * G * c.head_dim * 4);
@@ -198,7 +201,7 @@ void BatchDecoder::enqueue_step(int n) {
                     const float* gain_out, int order_out) {
         rows_gemm(W, n, c.eps, frag, norm, part_, y, y_stride, epi, frag_out, gain_out, order_out, stream_);
     };
-    const int splits = attn_splits_for(n, c.n_kv_heads, max_blocks_);
+    const int splits = attn_splits_for(max_blocks_);
     for (size_t li = 0; li < m_.layers_.size(); li++) {
         const DevLayer& L = m_.layers_[li];
         const bool last = li + 1 == m_.layers_.size();
@@ -301,6 +304,43 @@ void BatchDecoder::admit(int row) {
     sync();
 }
 
+void BatchDecoder::copy_row(int row, BatchDecoder& src, int src_row) {
+    check_row(row);
+    src.check_row(src_row);
+    if (&src.m_ != &m_) throw Error(QNE_EINVAL, "the batches decode different models");
+    uint32_t token = 0, next = 0;
+    {
+        uint32_t t[kRowsMax], p[kRowsMax];
+        src.row_state(src_row + 1, t, p);
+        token = t[src_row];
+        next = p[src_row];
+    }
+    if ((int)next >= max_context_) throw Error(QNE_ECONTEXT, "the row's sequence does not fit the batch context");
+    if (&src == this && src_row == row) return;
+    const size_t nblk = (next + 15) / 16;
+    for (size_t li = 0; li < m_.layers_.size(); li++) {
+        if (m_.layers_[li].attn) {
+            const size_t bytes = pool_block_elems_ * 2;
+            for (size_t i = 0; i < nblk; i++) {
+                const size_t from = (size_t)src.bt_host_[(size_t)src_row * src.max_blocks_ + i] * pool_block_elems_;
+                const size_t to = (size_t)bt_host_[(size_t)row * max_blocks_ + i] * pool_block_elems_;
+                QNE_HIP(hipMemcpyAsync(kpool_[li] + to, src.kpool_[li] + from, bytes, hipMemcpyDeviceToDevice, stream_));
+                QNE_HIP(hipMemcpyAsync(vpool_[li] + to, src.vpool_[li] + from, bytes, hipMemcpyDeviceToDevice, stream_));
+            }
+        } else {
+            QNE_HIP(hipMemcpyAsync(conv_[li] + (size_t)row * conv_floats_, src.conv_[li] + (size_t)src_row * conv_floats_,
+                                   conv_floats_ * 4, hipMemcpyDeviceToDevice, stream_));
+            QNE_HIP(hipMemcpyAsync(rec_[li] + (size_t)row * rec_floats_, src.rec_[li] + (size_t)src_row * rec_floats_,
+                                   rec_floats_ * 4, hipMemcpyDeviceToDevice, stream_));
+        }
+    }
+    host_u32_[0] = token;
+    host_u32_[1] = next;
+    QNE_HIP(hipMemcpyAsync(tokens_ + row, host_u32_, 4, hipMemcpyHostToDevice, stream_));
+    QNE_HIP(hipMemcpyAsync(pos_ + row, host_u32_ + 1, 4, hipMemcpyHostToDevice, stream_));
+    sync();
+}
+
 void BatchDecoder::reset_row(int row, uint32_t token) {
     check_row(row);
     if (token >= (uint32_t)m_.cfg_.vocab) throw Error(QNE_EINVAL, "token id out of range");
@@ -365,7 +405,7 @@ void BatchDecoder::decode(int n, int steps, uint32_t* out, size_t cap) {
     }
     QNE_HIP(hipEventRecord(ev1_, stream_));
     if (ids) QNE_HIP(hipMemcpyAsync(out, ids, (size_t)n * steps * 4, hipMemcpyDeviceToHost, stream_));
-    sync();
+    sync((double)steps);
     float ms = 0.0f;
     QNE_HIP(hipEventElapsedTime(&ms, ev0_, ev1_));
     last_ms_ = ms;

@@ -41,6 +41,9 @@ class BatchDecoder {
     // Row `row` takes over the model's current sequence: its KV cache and recurrent state, and its
     // next (token, position) as reported by Model::last_token.
     void admit(int row);
+    // Row `row` takes over row `src_row` of `src` (a batch over the same model; `src` may be this
+    // batch): its KV cache, recurrent state, next token and position.
+    void copy_row(int row, BatchDecoder& src, int src_row);
     // Row `row` becomes an empty sequence (position 0, zero state) whose next token is `token`.
     void reset_row(int row, uint32_t token);
     // The next (token, position) of rows 0..n-1.
@@ -64,7 +67,7 @@ class BatchDecoder {
     void enqueue_step(int n);
     hipGraphExec_t graph_for(int n);
     void check_row(int row) const;
-    void sync();
+    void sync(double steps = 1.0);  // waits with a deadline for `steps` batched steps
 
     Model& m_;
     int max_rows_, max_context_, max_blocks_;

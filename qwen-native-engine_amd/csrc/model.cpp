@@ -8,6 +8,7 @@
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
+#include <initializer_list>
 #include <map>
 #include <thread>
 
@@ -29,7 +30,46 @@ void wait_stream(hipStream_t st, double timeout_s) {
         if (e != hipErrorNotReady) hip_check(e, "hipStreamQuery");
         if (++spins > 2000) std::this_thread::sleep_for(std::chrono::microseconds(50));
         if (std::chrono::duration<double>(clk::now() - start).count() > timeout_s)
-            throw Error(QNE_EDEVICE, "GPU wait failed: timed out after 30 s");
+            throw Error(QNE_EDEVICE, "GPU wait failed: timed out after " + std::to_string((long long)timeout_s) + " s");
+    }
+}
+
+// ModelTiles::validate (kernels/src/model.rs:101-109) on a serialised tile profile: each of the six
+// matrix kinds names a GEMV tile {f16, tpr, rpw, rpt, splits} (kernels/src/lib.rs:40-49), and a
+// profile the reference would reject is rejected with its message. The kernels here choose their
+// own shapes per matrix, so a valid profile changes nothing else.
+static void validate_tiles(const Json& t) {
+    static const char* kKinds[] = {"gdn_in", "attn_in", "out", "gate_up", "down", "lm_head"};
+    if (t.type != Json::Object) throw Error(QNE_EINVAL, "tiles: expected a ModelTiles object");
+    for (const char* kind : kKinds) {
+        if (!t.has(kind)) throw Error(QNE_EINVAL, std::string("tiles: missing field `") + kind + "`");
+        const Json& v = t.at(kind);
+        if (v.type != Json::Object) throw Error(QNE_EINVAL, std::string("tiles: ") + kind + " is not a Tile object");
+        if (!v.has("f16") || v.at("f16").type != Json::Bool)
+            throw Error(QNE_EINVAL, std::string("tiles: ") + kind + ": missing or non-boolean field `f16`");
+        const bool f16 = v.at("f16").b;
+        uint32_t f[4];
+        static const char* kFields[] = {"tpr", "rpw", "rpt", "splits"};
+        for (int i = 0; i < 4; i++) {
+            if (!v.has(kFields[i]))
+                throw Error(QNE_EINVAL, std::string("tiles: ") + kind + ": missing field `" + kFields[i] + "`");
+            const Json& x = v.at(kFields[i]);
+            if (x.type != Json::Number || x.num < 0 || x.num > 4294967295.0 || x.num != (double)(uint32_t)x.num)
+                throw Error(QNE_EINVAL, std::string("tiles: ") + kind + ": `" + kFields[i] + "` is not a u32");
+            f[i] = (uint32_t)x.num;
+        }
+        const uint32_t tpr = f[0], rpw = f[1], rpt = f[2], splits = f[3];
+        auto in = [](uint32_t v, std::initializer_list<uint32_t> set) {
+            for (uint32_t s : set)
+                if (v == s) return true;
+            return false;
+        };
+        const bool ok = in(tpr, {1, 2, 4, 8, 16, 32, 64}) && in(rpw, {2, 4, 8, 16, 32}) && in(rpt, {1, 2, 4, 8}) &&
+                        in(splits, {1, 2, 4, 8}) && (uint64_t)tpr * rpw <= 256 && (f16 || (rpt == 1 && splits == 1));
+        if (!ok)
+            throw Error(QNE_EINVAL, "invalid kernel tile profile: Tile { f16: " + std::string(f16 ? "true" : "false") +
+                                        ", tpr: " + std::to_string(tpr) + ", rpw: " + std::to_string(rpw) +
+                                        ", rpt: " + std::to_string(rpt) + ", splits: " + std::to_string(splits) + " }");
     }
 }
 
@@ -38,6 +78,12 @@ LoadOptions parse_options(const char* json) {
     if (!json || !*json) return o;
     Json j = Json::parse(json, std::strlen(json));
     if (j.type != Json::Object) throw Error(QNE_EINVAL, "options must be a JSON object");
+    // The reference's `tiles` argument: a serialised ModelTiles, either as the whole options object
+    // or under "tiles".
+    if (j.has("tiles")) validate_tiles(j.at("tiles"));
+    else if (j.has("gdn_in") || j.has("attn_in") || j.has("out") || j.has("gate_up") || j.has("down") ||
+             j.has("lm_head"))
+        validate_tiles(j);
     if (j.has("max_context")) {
         uint64_t v = j.at("max_context").u64("max_context");
         if (v < 16 || v > (1u << 22)) throw Error(QNE_EINVAL, "max_context must be 16..4194304");
@@ -565,6 +611,7 @@ void Model::run_engine(const EngineRun& r) {
     a.trace_cap = r.trace_cap;
     a.tag_base = tag_base_;
     tag_base_ += (uint32_t)tags;
+    pending_units_ += (double)tags;
     QNE_HIP(hipMemsetAsync(eng_bar_, 0, 8, stream_));
     QNE_HIP(launch_decode(a, engine_grid_, stream_));
     QNE_HIP(hipMemcpyAsync(host_err_, eng_bar_, 4, hipMemcpyDeviceToHost, stream_));
@@ -578,7 +625,9 @@ void Model::check_engine_error() {
 }
 
 void Model::sync() {
-    wait_stream(stream_);
+    const double units = pending_units_;
+    pending_units_ = 0.0;
+    wait_stream(stream_, work_deadline_s(units));
     check_engine_error();
 }
 
@@ -597,6 +646,7 @@ static void check_ids(const uint32_t* ids, size_t n, int vocab) {
 }
 
 void Model::run_layers_graph() {
+    pending_units_ += 6.0 * (double)layers_.size();
     if (use_graphs_) QNE_HIP(hipGraphLaunch(g_layers_, stream_));
     else enqueue_layers();
 }
@@ -734,9 +784,24 @@ void Model::last_token(uint32_t* token, uint32_t* next_pos) {
     *next_pos = host_tok_[5];
 }
 
-// model.rs:426-449, GPU-resident greedy loop. Each step's pick is also appended on the device,
-// so a window returns every id.
+// model.rs:426-449, GPU-resident greedy loop: out[0] = last_token().0, then windows of up to
+// `window` steps whose picks are fed back on the device. As in the reference, a window of one
+// step yields its pick and a longer window yields u32::MAX placeholders (model.rs:441-446), and
+// `stop` is checked against the last value pushed (model.rs:433), so it ends the loop only after a
+// one-step window or on the first id.
 size_t Model::decode(size_t n, uint32_t window, const uint32_t* stop, size_t nstop, uint32_t* out, size_t cap) {
+    return decode_loop(n, window, stop, nstop, out, cap, false);
+}
+
+// The same loop with every step's pick appended on the device, so every window returns real ids;
+// the loop ends after the first id found in `stop` (the state may have advanced past it inside a
+// window, as the reference's does).
+size_t Model::decode_ids(size_t n, uint32_t window, const uint32_t* stop, size_t nstop, uint32_t* out, size_t cap) {
+    return decode_loop(n, window, stop, nstop, out, cap, true);
+}
+
+size_t Model::decode_loop(size_t n, uint32_t window, const uint32_t* stop, size_t nstop, uint32_t* out, size_t cap,
+                          bool every_id) {
     if (window == 0) throw Error(QNE_EINVAL, "window must be >= 1");
     if (cap < 1 || (n > 0 && cap < n)) throw Error(QNE_EINVAL, "output buffer smaller than n");
     if (n == 0) return 0;
@@ -778,6 +843,12 @@ size_t Model::decode(size_t n, uint32_t window, const uint32_t* stop, size_t nst
         QNE_HIP(hipEventElapsedTime(&ms, ev_start_, ev_stop_));
         last_decode_ms_ += ms;
         last_decode_steps_ += steps;
+        if (!every_id) {
+            if (steps == 1) out[len++] = host_ids_[0];
+            else
+                for (uint32_t s = 0; s < steps; s++) out[len++] = 0xFFFFFFFFu;
+            continue;
+        }
         for (uint32_t s = 0; s < steps && len < n; s++) {
             out[len++] = host_ids_[s];
             if (is_stop(out[len - 1])) break;

@@ -72,7 +72,10 @@ class Model {
     void snapshot();
     void restore();
     void last_token(uint32_t* token, uint32_t* next_pos);
+    // Model::decode (model.rs:426-449): a window of more than one step yields u32::MAX placeholders.
     size_t decode(size_t n, uint32_t window, const uint32_t* stop, size_t nstop, uint32_t* out, size_t cap);
+    // The same loop returning every id of every window and stopping after the first stop id.
+    size_t decode_ids(size_t n, uint32_t window, const uint32_t* stop, size_t nstop, uint32_t* out, size_t cap);
     double profile_token();
     // One greedy decode token with the device timeline on; JSON of per-phase times (persistent
     // engine only).
@@ -103,6 +106,8 @@ class Model {
     void run_engine(const EngineRun& r);
     void check_engine_error();
     void sync();
+    size_t decode_loop(size_t n, uint32_t window, const uint32_t* stop, size_t nstop, uint32_t* out, size_t cap,
+                       bool every_id);
     void* dalloc(size_t bytes);
 
     ModelConfig cfg_;
@@ -152,6 +157,7 @@ class Model {
     size_t last_decode_steps_ = 0;
     size_t dispatches_ = 0;
     size_t launches_ = 0;  // kernel launches counted while recording
+    double pending_units_ = 0.0;  // dependent device steps enqueued since the last sync (its deadline)
     // prefill_chunk on the batched GEMM (created on first use; null when the shapes do not fit it)
     ChunkPrefill* chunk_ = nullptr;
     bool chunk_tried_ = false;

@@ -31,11 +31,12 @@ class QneError(RuntimeError):
 
 
 def load_library(path: str | os.PathLike | None = None):
-    """Loads libqne.so (built by `make -C qwen-native-engine_amd`)."""
+    """Loads libqne.so (built by `make -C qwen-native-engine_amd`), or the build named by the
+    QNE_LIBRARY environment variable (the sanitizer build, for instance)."""
     global _lib
     if _lib is not None and path is None:
         return _lib
-    p = Path(path) if path else LIB_PATH
+    p = Path(path) if path else Path(os.environ.get("QNE_LIBRARY") or LIB_PATH)
     if not p.exists():
         raise QneError(EDEVICE, f"{p} is not built; run make -C {HERE}")
     lib = ctypes.CDLL(str(p))
@@ -53,6 +54,7 @@ def load_library(path: str | os.PathLike | None = None):
         "qne_restore": ([c_p], c_i),
         "qne_last_token": ([c_p, ctypes.POINTER(c_u32), ctypes.POINTER(c_u32)], c_i),
         "qne_decode": ([c_p, c_sz, c_u32, c_p, c_sz, c_p, c_sz, ctypes.POINTER(c_sz)], c_i),
+        "qne_decode_ids": ([c_p, c_sz, c_u32, c_p, c_sz, c_p, c_sz, ctypes.POINTER(c_sz)], c_i),
         "qne_dispatches_per_token": ([c_p, ctypes.POINTER(c_sz)], c_i),
         "qne_adapter": ([c_p, ctypes.c_char_p, c_sz], c_i),
         "qne_vocab": ([c_p, ctypes.POINTER(c_u32)], c_i),
@@ -70,6 +72,7 @@ def load_library(path: str | os.PathLike | None = None):
         "qne_batch_free": ([c_p], c_i),
         "qne_batch_admit": ([c_p, c_u32], c_i),
         "qne_batch_reset_row": ([c_p, c_u32, c_u32], c_i),
+        "qne_batch_copy_row": ([c_p, c_u32, c_p, c_u32], c_i),
         "qne_batch_row_state": ([c_p, c_u32, c_p, c_p], c_i),
         "qne_batch_step": ([c_p, c_u32, c_p, c_p, c_p, c_sz], c_i),
         "qne_batch_decode": ([c_p, c_u32, c_u32, c_p, c_sz], c_i),
@@ -208,11 +211,19 @@ class Model:
         return t.value, p.value
 
     def decode(self, n: int, window: int = 1, stop=()):
+        """Model::decode (model.rs:426-449): a window of more than one step yields u32::MAX
+        placeholders, and `stop` is checked against the last value pushed."""
+        return self._decode(self._lib.qne_decode, n, window, stop)
+
+    def decode_ids(self, n: int, window: int = 1, stop=()):
+        """The same greedy loop returning every id of every window, ending after the first stop id."""
+        return self._decode(self._lib.qne_decode_ids, n, window, stop)
+
+    def _decode(self, fn, n, window, stop):
         out = np.zeros(max(n, 1), dtype=np.uint32)
         st, sp = _u32_array(list(stop) if len(stop) else [0])
         ln = ctypes.c_size_t()
-        self._c(self._lib.qne_decode(self._h, n, window, sp, len(stop), out.ctypes.data_as(ctypes.c_void_p),
-                                     out.size, ctypes.byref(ln)))
+        self._c(fn(self._h, n, window, sp, len(stop), out.ctypes.data_as(ctypes.c_void_p), out.size, ctypes.byref(ln)))
         return [int(x) for x in out[:ln.value]]
 
     def dispatches_per_token(self) -> int:
@@ -325,6 +336,10 @@ class Batch:
     def admit(self, row: int):
         """Row `row` takes over the model's current sequence (state, next token and position)."""
         self._c(self._lib.qne_batch_admit(self._h, row))
+
+    def copy_row(self, row: int, src: "Batch", src_row: int):
+        """Row `row` takes over row `src_row` of `src` (a batch over the same model)."""
+        self._c(self._lib.qne_batch_copy_row(self._h, row, src._h, src_row))
 
     def reset_row(self, row: int, token: int):
         self._c(self._lib.qne_batch_reset_row(self._h, row, token))

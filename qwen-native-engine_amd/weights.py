@@ -92,39 +92,50 @@ def vector_shapes(cfg: dict) -> dict:
 
 
 class Writer:
-    """Streams tensors into weights.bin: 256-byte alignment, identical content stored once
-    (convert_weights.py:35-59)."""
+    """Appends tensors to a weights.bin file and builds its index.json "tensors" map.
+
+    Format rules (the reference's scripts/convert_weights.py defines them for format 1 and this
+    module keeps them): every tensor starts on a 256-byte boundary, and a tensor whose raw bytes,
+    kind and shape equal a tensor written earlier is not stored twice; its index entry names the
+    earlier copy's range (a tied LM head, repeated norm gains)."""
 
     def __init__(self, path):
-        self.file = open(path, "wb")
-        self.offset = 0
-        self.index = {}
-        self.content = {}
+        self._out = open(path, "wb")
+        self._size = 0            # bytes written so far
+        self._stored = {}         # content key -> index entry of the stored copy
+        self.index = {}           # tensor name -> {"offset", "bytes", "kind", "shape"}
+
+    def _align(self):
+        gap = -self._size % ALIGN
+        if gap:
+            self._out.write(bytes(gap))
+            self._size += gap
 
     def add(self, name, array, kind):
-        data = np.ascontiguousarray(array).tobytes()
-        digest = (kind, tuple(np.shape(array)), hashlib.sha256(data).digest())
-        if digest in self.content:
-            self.index[name] = dict(self.content[digest])
-            return
-        pad = (-self.offset) % ALIGN
-        self.file.write(b"\0" * pad)
-        self.offset += pad
-        self.index[name] = {"offset": self.offset, "bytes": len(data), "kind": kind, "shape": list(np.shape(array))}
-        self.content[digest] = self.index[name]
-        self.file.write(data)
-        self.offset += len(data)
+        arr = np.ascontiguousarray(array)
+        raw = arr.tobytes()
+        key = (hashlib.sha256(raw).hexdigest(), kind, arr.shape)
+        entry = self._stored.get(key)
+        if entry is None:
+            self._align()
+            entry = {"offset": self._size, "bytes": arr.nbytes, "kind": kind, "shape": list(arr.shape)}
+            self._out.write(raw)
+            self._size += arr.nbytes
+            self._stored[key] = entry
+        self.index[name] = dict(entry)
 
     def close(self):
-        self.file.close()
+        self._out.close()
 
 
-def interleaved_heads_to_split(part, heads, head_dim):
-    """Rows [h0 q | h0 gate | h1 q | ...] -> [all q | all gates] (convert_weights.py:72-78)."""
-    q, s, z = part
-    order = [h * 2 * head_dim + i for h in range(heads) for i in range(head_dim)]
-    order += [h * 2 * head_dim + head_dim + i for h in range(heads) for i in range(head_dim)]
-    return q[order], s[order], z[order]
+def split_query_gate_rows(parts, heads, head_dim):
+    """The attention in-projection of a Qwen3.5 checkpoint holds, per query head, its head_dim query
+    rows followed by its head_dim gate rows; the engine (and the reference's format) wants every
+    query row first, then every gate row, head by head. `parts` are arrays over those rows (weights,
+    scales, zeros); each is returned in the engine's order."""
+    per_head = np.arange(heads * 2 * head_dim).reshape(heads, 2, head_dim)
+    order = np.concatenate([per_head[:, 0, :].reshape(-1), per_head[:, 1, :].reshape(-1)])
+    return tuple(np.asarray(p)[order] for p in parts)
 
 
 def fnv1a64(name: str) -> int:

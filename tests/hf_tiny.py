@@ -21,12 +21,28 @@ TINY = dict(vocab_size=4096, hidden_size=512, intermediate_size=1024, num_hidden
 
 
 def available() -> bool:
+    """Whether safetensors and transformers' qwen3_5 model are installed, found without importing
+    either (a GPU test process must not load torch, which carries its own HIP runtime)."""
+    import importlib.util
     try:
-        import safetensors.torch  # noqa: F401
-        from transformers.models.qwen3_5 import Qwen3_5ForCausalLM  # noqa: F401
+        st, tf = importlib.util.find_spec("safetensors"), importlib.util.find_spec("transformers")
     except Exception:
         return False
-    return True
+    if st is None or tf is None or importlib.util.find_spec("torch") is None or not tf.submodule_search_locations:
+        return False
+    return any((Path(d) / "models" / "qwen3_5" / "modeling_qwen3_5.py").exists() for d in tf.submodule_search_locations)
+
+
+def build_in_subprocess(seed: int, directory, ids) -> tuple[Path, np.ndarray]:
+    """build + save + logits(ids) in a child process (for the GPU tests, which keep torch out of
+    their own process): returns the checkpoint directory and transformers' logits."""
+    import subprocess
+    import sys
+    d = Path(directory)
+    ids = np.asarray(ids, dtype=np.int64)
+    np.save(d / "ids.npy", ids)
+    subprocess.run([sys.executable, str(Path(__file__).resolve()), str(seed), str(d)], check=True)
+    return d / "hf", np.load(d / "logits.npy")
 
 
 def build(seed: int = 0, tied: bool = False):
@@ -93,3 +109,11 @@ def logits(m, ids) -> np.ndarray:
     with torch.no_grad():
         out = m(torch.as_tensor(np.asarray(ids, dtype=np.int64))[None]).logits[0]
     return out.float().numpy()
+
+
+if __name__ == "__main__":
+    import sys
+    seed, out = int(sys.argv[1]), Path(sys.argv[2])
+    model = build(seed=seed)
+    save(model, out / "hf")
+    np.save(out / "logits.npy", logits(model, np.load(out / "ids.npy")))

@@ -124,3 +124,108 @@ def test_valid_model_reaches_device_initialisation(tiny):
         Q.load_library().qne_model_free(h)
     else:
         assert rc == Q.EDEVICE, msg
+
+
+# ---- ModelTiles::validate (kernels/src/model.rs:101-109), checked at load after the index ----
+
+GOLDEN = ROOT / "tests" / "golden"
+
+
+def reference_profile(name):
+    """The reference's own tile-profile files (kernels/profiles/*.json), kept as test data."""
+    return json.loads((GOLDEN / name).read_text())
+
+
+def tile(f16, tpr, rpw, rpt, splits):
+    return dict(f16=f16, tpr=tpr, rpw=rpw, rpt=rpt, splits=splits)
+
+
+def fast_tiles():
+    """ModelTiles::fast() (model.rs:137-141)."""
+    f32 = tile(False, 16, 4, 1, 1)
+    return dict(gdn_in=tile(True, 16, 4, 4, 1), attn_in=tile(True, 4, 32, 4, 1), out=f32,
+                gate_up=tile(True, 4, 16, 4, 1), down=f32, lm_head=tile(True, 4, 32, 4, 1))
+
+
+def f32_tiles():
+    """ModelTiles::f32() (model.rs:111-114)."""
+    t = tile(False, 16, 4, 1, 1)
+    return {k: dict(t) for k in ("gdn_in", "attn_in", "out", "gate_up", "down", "lm_head")}
+
+
+def passes_tile_check(rc, msg):
+    # a profile the reference accepts gets past validation; on a machine without a GPU the load
+    # then stops at the device (and with one it loads)
+    return rc in (Q.OK, Q.EDEVICE) and "tile" not in msg
+
+
+@pytest.mark.parametrize("as_key", [True, False])
+def test_reference_tile_profiles_validate(tiny, as_key):
+    """model.rs:457-461: fast(), f32() and the shipped 2B profile are valid."""
+    index, buf = tiny
+    for profile in (fast_tiles(), f32_tiles(), reference_profile("tiles_uhd630_2b.json"),
+                    reference_profile("tiles_uhd630_0.8b.json")):
+        rc, msg, h = load_rc(index, buf, {"tiles": profile} if as_key else profile)
+        assert passes_tile_check(rc, msg), msg
+        if rc == Q.OK:
+            Q.load_library().qne_model_free(h)
+
+
+@pytest.mark.parametrize("kind,field,value", [("down", "splits", 0), ("lm_head", "tpr", 0)])
+def test_invalid_tile_profiles_are_rejected(tiny, kind, field, value):
+    """model.rs:462-465: the 2B profile with down.splits = 0, or with lm_head.tpr = 0, is invalid."""
+    index, buf = tiny
+    bad = reference_profile("tiles_uhd630_2b.json")
+    bad[kind][field] = value
+    rc, msg, _ = load_rc(index, buf, {"tiles": bad})
+    assert rc == Q.EINVAL and msg.startswith("invalid kernel tile profile: Tile {"), msg
+    t = bad[kind]
+    assert msg == ("invalid kernel tile profile: Tile { f16: %s, tpr: %d, rpw: %d, rpt: %d, splits: %d }"
+                   % ("true" if t["f16"] else "false", t["tpr"], t["rpw"], t["rpt"], t["splits"]))
+
+
+@pytest.mark.parametrize("t,ok", [
+    (tile(True, 64, 4, 8, 8), True),     # tpr * rpw = 256 is the largest allowed
+    (tile(True, 64, 8, 1, 1), False),    # 512 threads per row group
+    (tile(True, 3, 4, 1, 1), False),     # tpr not a power of two
+    (tile(True, 4, 64, 1, 1), False),    # rpw above 32
+    (tile(True, 4, 1, 1, 1), False),     # rpw below 2
+    (tile(True, 4, 4, 16, 1), False),    # rpt above 8
+    (tile(True, 4, 4, 1, 16), False),    # splits above 8
+    (tile(False, 4, 4, 2, 1), False),    # f32 tiles take rpt = 1 ...
+    (tile(False, 4, 4, 1, 2), False),    # ... and splits = 1
+    (tile(False, 1, 2, 1, 1), True),
+])
+def test_tile_rules(tiny, t, ok):
+    index, buf = tiny
+    prof = f32_tiles()
+    prof["gate_up"] = t
+    rc, msg, h = load_rc(index, buf, {"tiles": prof})
+    if ok:
+        assert passes_tile_check(rc, msg), msg
+        if rc == Q.OK:
+            Q.load_library().qne_model_free(h)
+    else:
+        assert rc == Q.EINVAL and "invalid kernel tile profile" in msg, msg
+
+
+def test_tile_profile_with_a_missing_field_is_rejected(tiny):
+    index, buf = tiny
+    prof = f32_tiles()
+    del prof["down"]
+    rc, msg, _ = load_rc(index, buf, {"tiles": prof})
+    assert rc == Q.EINVAL and "down" in msg
+    prof = f32_tiles()
+    del prof["out"]["rpw"]
+    rc, msg, _ = load_rc(index, buf, {"tiles": prof})
+    assert rc == Q.EINVAL and "rpw" in msg
+
+
+def test_index_errors_come_before_tile_errors(tiny):
+    """model.rs:172-174: index.validate runs before tiles.validate."""
+    index, buf = tiny
+    bad_index = mutate(index, lambda ix: ix["tensors"]["final_norm"].update(offset=len(buf)))
+    prof = f32_tiles()
+    prof["down"]["splits"] = 0
+    rc, msg, _ = load_rc(bad_index, buf, {"tiles": prof})
+    assert rc == Q.EFORMAT and "tile" not in msg

@@ -28,7 +28,7 @@ def test_shared_weights_and_alignment(tmp_path):
 
 def test_query_and_gate_head_order():
     data = np.arange(8).reshape(8, 1)
-    result = W.interleaved_heads_to_split((data, data, data), 2, 2)
+    result = W.split_query_gate_rows((data, data, data), 2, 2)
     assert result[0].ravel().tolist() == [0, 1, 4, 5, 2, 3, 6, 7]
 
 

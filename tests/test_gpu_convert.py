@@ -15,10 +15,15 @@ pytestmark = [pytest.mark.gpu,
               pytest.mark.skipif(not hf_tiny.available(), reason="transformers qwen3_5 / safetensors not importable")]
 
 
+IDS = np.random.default_rng(5).integers(0, hf_tiny.TINY["vocab_size"], size=24)
+
+
 @pytest.fixture(scope="module")
 def checkpoint(tmp_path_factory):
-    m = hf_tiny.build(seed=3)
-    return m, hf_tiny.save(m, tmp_path_factory.mktemp("hf"))
+    """The seeded tiny transformers model, saved, and its logits at every position of IDS; made in a
+    child process so that this GPU test process never loads torch."""
+    src, want = hf_tiny.build_in_subprocess(3, tmp_path_factory.mktemp("hf"), IDS)
+    return want, src
 
 
 def load(d):
@@ -27,11 +32,10 @@ def load(d):
 
 @pytest.mark.parametrize("engine", ["persistent", "graph"])
 def test_engine_on_converted_checkpoint_matches_transformers(checkpoint, tmp_path, engine):
-    hf, src = checkpoint
+    want, src = checkpoint
     C.convert(src, tmp_path / "f16", body="f16", head="f16")
     index, buf = load(tmp_path / "f16")
-    ids = np.random.default_rng(5).integers(0, hf_tiny.TINY["vocab_size"], size=24)
-    want = hf_tiny.logits(hf, ids)
+    ids = IDS
     m = Q.Model.load(index, buf, options={"engine": engine})
     try:
         got = np.stack([m.step(int(t), p) for p, t in enumerate(ids)])
@@ -53,7 +57,7 @@ def test_int4_converted_checkpoint_greedy_matches_oracle(checkpoint, tmp_path):
     try:
         m.prefill_batched(ids)
         first = m.logits()
-        out = m.decode(32, 8, [])
+        out = m.decode_ids(32, 8, [])
     finally:
         m.close()
     assert float(np.abs(first - want_logits[0]).max()) <= 1e-3

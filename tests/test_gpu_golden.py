@@ -48,7 +48,7 @@ def test_greedy_ids_and_logits_match_oracle_fixture(golden, engine):
         err = float(np.max(np.abs(got[g["logit_idx"][0]] - g["logit_val"][0])))
         worst = max(worst, err)
         assert m.last_token() == (ids[0], P)
-        out = m.decode(len(ids), 32, [])
+        out = m.decode_ids(len(ids), 32, [])
         assert out == ids, f"{name}/{engine}: first divergence at step {next(i for i, (a, b) in enumerate(zip(out, ids)) if a != b)}"
         # step(): the logits after each fed id, sampled at the logged steps; every argmax is the next id
         m.reset()
@@ -64,3 +64,41 @@ def test_greedy_ids_and_logits_match_oracle_fixture(golden, engine):
         print(f"{name}/{engine}: 128 greedy ids identical; max |dlogit| over sampled logits {worst:.2e}; "
               f"smallest top-2 margin {float(np.min(g['margin'])):.4f}")
         assert worst <= LOGIT_TOL
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name,window", [("c2_long", 16), ("small_long", 8)])
+def test_long_context_decode_matches_oracle_fixture(name, window):
+    """The decode benchmark's own positions: the 2B int4 model after a 4000-id prompt, greedy decode
+    over positions 4000..4094 through the persistent decode kernel (prefill_chunk in 512-id calls,
+    then decode windows of 16), ids identical to the oracle's and the sampled logits within 1e-2.
+    small_long: the 8-layer model with an 8192-position cache after a 5500-id prompt, where an
+    attention split holds more positions than the kernel prefetches into LDS (its direct-load
+    path)."""
+    g = fixture(name)
+    case = json.loads(str(g["case"]))
+    index, buf = synth(case)
+    prompt, ids = g["prompt"], g["ids"].tolist()
+    P = len(prompt)
+    with Q.Model.load(index, buf, options={"max_context": case.get("max_context", 4096)}) as m:
+        for s in range(0, P, 512):
+            m.prefill_chunk(prompt[s:s + 512], s, s + 512 >= P)
+        got = m.logits()
+        worst = float(np.max(np.abs(got[g["logit_idx"][0]] - g["logit_val"][0])))
+        assert m.last_token() == (ids[0], P)
+        m.snapshot()
+        out = m.decode_ids(len(ids), window, [])
+        assert out == ids, f"{name}: first divergence at step {next(i for i, (a, b) in enumerate(zip(out, ids)) if a != b)}"
+        # the logits after the logged fed ids, through step() from the same prompt state
+        m.restore()
+        logged = {int(s): i for i, s in enumerate(g["steps"])}
+        last = max(logged)
+        for i in range(last):
+            v = m.step(ids[i], P + i)
+            assert int(np.argmax(v)) == ids[i + 1], f"{name}: step {i + 1}"
+            if i + 1 in logged:
+                j = logged[i + 1]
+                worst = max(worst, float(np.max(np.abs(v[g["logit_idx"][j]] - g["logit_val"][j]))))
+    print(f"{name}: {len(ids)} greedy ids identical; max |dlogit| {worst:.2e}; smallest top-2 margin "
+          f"{float(np.min(g['margin'])):.4f}")
+    assert worst <= LOGIT_TOL

@@ -7,13 +7,11 @@ import ctypes
 
 import numpy as np
 import pytest
-import torch
-
 import cpu_oracle as O
+import devmem as D
 import qne as Q
 
 pytestmark = pytest.mark.gpu
-dev = torch.device("cuda:0")
 
 
 def rel_err(got, want):
@@ -23,8 +21,7 @@ def rel_err(got, want):
     return np.max(np.abs(got - want)) / max(1e-6, np.max(np.abs(want)))
 
 
-def to_dev(a):
-    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+to_dev = D.to_dev
 
 
 def q4_matrix(rows, k, group, rng):
@@ -66,8 +63,8 @@ def test_gemv_matches_oracle(k, kind, group, epi, norm):
     dsz = to_dev(sz) if sz is not None else None
     Q.gemv(kind, dw.data_ptr(), dsz.data_ptr() if dsz is not None else 0, rows, k, group, dx.data_ptr(), dy.data_ptr(),
            epi, norm=dg.data_ptr() if norm else 0)
-    torch.cuda.synchronize()
-    err = rel_err(dy.cpu().numpy(), want)
+    D.sync()
+    err = rel_err(dy.numpy(), want)
     assert err < 2e-5, err
 
 
@@ -95,11 +92,11 @@ def test_gdn_step_matches_oracle(batch):
             O.lib("f64").oc_delta_rule(dk, dv, O.ptr(q[b, h]), O.ptr(k[b, h]), O.ptr(v[b, h]), float(beta[b, h]),
                                        float(g[b, h]), O.ptr(want_S[b, h]), O.ptr(want_o[b, h]))
     d = [to_dev(a) for a in (q, k, v, beta, g, S)]
-    out = torch.empty((batch, H, dv), dtype=torch.float32, device=dev)
+    out = D.empty((batch, H, dv), np.float32)
     Q.gdn_step(*[t.data_ptr() for t in d], out.data_ptr(), batch, H)
-    torch.cuda.synchronize()
-    assert rel_err(out.cpu().numpy(), want_o) < 1e-5
-    assert rel_err(d[5].cpu().numpy(), want_S) < 1e-5
+    D.sync()
+    assert rel_err(out.numpy(), want_o) < 1e-5
+    assert rel_err(d[5].numpy(), want_S) < 1e-5
 
 
 def test_gdn_multi_token_equals_sequential_oracle():
@@ -121,11 +118,11 @@ def test_gdn_multi_token_equals_sequential_oracle():
                                            float(beta[b, t, h]), float(g[b, t, h]), O.ptr(want_S[b, h]),
                                            O.ptr(want_o[b, t, h]))
     d = [to_dev(a) for a in (q, k, v, beta, g, S)]
-    out = torch.empty_like(d[2])
+    out = D.empty_like(d[2])
     Q.gdn_prefill_chunked(*[t.data_ptr() for t in d], out.data_ptr(), B, T, H)
-    torch.cuda.synchronize()
-    assert rel_err(out.cpu().numpy(), want_o) < 1e-4
-    assert rel_err(d[5].cpu().numpy(), want_S) < 1e-4
+    D.sync()
+    assert rel_err(out.numpy(), want_o) < 1e-4
+    assert rel_err(d[5].numpy(), want_S) < 1e-4
 
 
 def gdn_inputs(rng, B, T, H, mode="random"):
@@ -172,11 +169,11 @@ def test_gdn_multi_token_cases(B, T, H, mode):
     q, k, v, beta, g, S = gdn_inputs(rng, B, T, H, mode)
     want_o, want_S = oracle_gdn_tokens(q, k, v, beta, g, S)
     d = [to_dev(a) for a in (q, k, v, beta, g, S)]
-    out = torch.empty_like(d[2])
+    out = D.empty_like(d[2])
     Q.gdn_prefill_chunked(*[t.data_ptr() for t in d], out.data_ptr(), B, T, H)
-    torch.cuda.synchronize()
-    assert rel_err(out.cpu().numpy(), want_o) < 1e-4
-    assert rel_err(d[5].cpu().numpy(), want_S) < 1e-4
+    D.sync()
+    assert rel_err(out.numpy(), want_o) < 1e-4
+    assert rel_err(d[5].numpy(), want_S) < 1e-4
 
 
 def test_gdn_chunked_split_calls_equal_one_call():
@@ -186,20 +183,20 @@ def test_gdn_chunked_split_calls_equal_one_call():
     B, T, H = 2, 200, 2
     q, k, v, beta, g, S = gdn_inputs(rng, B, T, H)
     whole = [to_dev(a) for a in (q, k, v, beta, g, S)]
-    out = torch.empty_like(whole[2])
+    out = D.empty_like(whole[2])
     Q.gdn_prefill_chunked(*[t.data_ptr() for t in whole], out.data_ptr(), B, T, H)
     for cut in (64, 40):
         st = to_dev(S)
         parts = []
         for a, bnd in ((0, cut), (cut, T)):
             sl = [to_dev(np.ascontiguousarray(x[:, a:bnd])) for x in (q, k, v, beta, g)]
-            o = torch.empty_like(sl[2])
+            o = D.empty_like(sl[2])
             Q.gdn_prefill_chunked(*[t.data_ptr() for t in sl], st.data_ptr(), o.data_ptr(), B, bnd - a, H)
             parts.append(o)
-        torch.cuda.synchronize()
-        got = torch.cat(parts, dim=1).cpu().numpy()
-        assert rel_err(got, out.cpu().numpy()) < 1e-4, cut
-        assert rel_err(st.cpu().numpy(), whole[5].cpu().numpy()) < 1e-4, cut
+        D.sync()
+        got = np.concatenate([p.numpy() for p in parts], axis=1)
+        assert rel_err(got, out.numpy()) < 1e-4, cut
+        assert rel_err(st.numpy(), whole[5].numpy()) < 1e-4, cut
 
 
 @pytest.mark.parametrize("batch,nq,nkv", [(1, 16, 4), (3, 8, 2), (5, 4, 4)])
@@ -230,13 +227,13 @@ def test_paged_attention_matches_dense(batch, nq, nkv):
                                    1 / 16, O.ptr(want[b]))
     dk, dv = to_dev(kpool.view(np.uint16)), to_dev(vpool.view(np.uint16))
     dq, dkn, dvn, dbt, dctx = to_dev(q), to_dev(kn), to_dev(vn), to_dev(bt), to_dev(ctx)
-    out = torch.empty((batch, nq, hd), dtype=torch.float32, device=dev)
+    out = D.empty((batch, nq, hd), np.float32)
     Q.paged_attn_decode(dq.data_ptr(), dkn.data_ptr(), dvn.data_ptr(), dk.data_ptr(), dv.data_ptr(), dbt.data_ptr(),
                         max_blocks, dctx.data_ptr(), out.data_ptr(), batch, nq, nkv)
-    torch.cuda.synchronize()
-    assert rel_err(out.cpu().numpy(), want) < 1e-5
+    D.sync()
+    assert rel_err(out.numpy(), want) < 1e-5
     # the append wrote exactly the new token's f16 k/v and nothing else
-    kp = dk.cpu().numpy().view(np.float16)
+    kp = dk.numpy().view(np.float16)
     for b in range(batch):
         p = ctx[b]
         np.testing.assert_array_equal(kp[bt[b, p // blk], :, p % blk], kn[b].astype(np.float16))
@@ -273,11 +270,11 @@ def test_paged_attention_config3_shape():
                                    1 / 16, O.ptr(want[b]))
     dk, dv = to_dev(kpool.view(np.uint16)), to_dev(vpool.view(np.uint16))
     dq, dkn, dvn, dbt, dctx = to_dev(q), to_dev(kn), to_dev(vn), to_dev(bt), to_dev(ctx)
-    out = torch.empty((batch, nq, hd), dtype=torch.float32, device=dev)
+    out = D.empty((batch, nq, hd), np.float32)
     Q.paged_attn_decode(dq.data_ptr(), dkn.data_ptr(), dvn.data_ptr(), dk.data_ptr(), dv.data_ptr(), dbt.data_ptr(),
                         max_blocks, dctx.data_ptr(), out.data_ptr(), batch, nq, nkv)
-    torch.cuda.synchronize()
-    assert rel_err(out.cpu().numpy(), want) < 1e-5
+    D.sync()
+    assert rel_err(out.numpy(), want) < 1e-5
 
 
 def test_gdn_step_config4_batch64():
@@ -305,8 +302,8 @@ def test_gdn_prefill_config4_shape():
                 L.oc_delta_rule(dk, dk, O.ptr(q[b, t, h]), O.ptr(k[b, t, h]), O.ptr(v[b, t, h]), float(beta[b, t, h]),
                                 float(g[b, t, h]), O.ptr(want_S[b, h]), O.ptr(want_o[b, t, h]))
     d = [to_dev(a) for a in (q, k, v, beta, g, S)]
-    out = torch.empty_like(d[2])
+    out = D.empty_like(d[2])
     Q.gdn_prefill_chunked(*[t.data_ptr() for t in d], out.data_ptr(), B, T, H)
-    torch.cuda.synchronize()
-    assert rel_err(out.cpu().numpy(), want_o) < 1e-4
-    assert rel_err(d[5].cpu().numpy(), want_S) < 1e-4
+    D.sync()
+    assert rel_err(out.numpy(), want_o) < 1e-4
+    assert rel_err(d[5].numpy(), want_S) < 1e-4

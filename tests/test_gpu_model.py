@@ -47,6 +47,9 @@ def test_prefill_logits_and_greedy_decode(pair):
     assert out == want_ids
 
 
+MAX = 0xFFFFFFFF
+
+
 def test_decode_window_returns_every_id(pair):
     name, m, om, _, _ = pair
     ids = prompt(m.vocab, 9, 2)
@@ -55,8 +58,36 @@ def test_decode_window_returns_every_id(pair):
     w1 = m.decode(20, 1, [])
     m.reset()
     m.prefill_batched(ids)
-    w8 = m.decode(20, 8, [])
+    w8 = m.decode_ids(20, 8, [])
     assert w1 == w8 and len(w8) == 20
+
+
+def test_decode_windows_push_placeholders_like_the_reference(pair):
+    """Model::decode (model.rs:426-449): a window of s > 1 steps pushes s u32::MAX values, a one-step
+    window pushes its pick, and `stop` is only checked against the last value pushed."""
+    name, m, om, _, _ = pair
+    ids = prompt(m.vocab, 9, 2)
+    m.reset()
+    m.prefill_batched(ids)
+    w1 = m.decode(20, 1, [])
+    m.reset()
+    m.prefill_batched(ids)
+    # n = 20, window 8: [first], 8 placeholders, 8 placeholders, then a 3-step window
+    assert m.decode(20, 8, []) == [w1[0]] + [MAX] * 19
+    assert m.last_token() == (w1[19], len(ids) + 19)
+    m.reset()
+    m.prefill_batched(ids)
+    # n = 10, window 8: [first], 8 placeholders, then a one-step window that returns its pick
+    assert m.decode(10, 8, []) == [w1[0]] + [MAX] * 8 + [w1[9]]
+    m.reset()
+    m.prefill_batched(ids)
+    # a stop id inside a window is not seen (the window returns placeholders)
+    assert m.decode(20, 8, [w1[3]]) == [w1[0]] + [MAX] * 19
+    m.reset()
+    m.prefill_batched(ids)
+    # the first id is checked before any window runs
+    assert m.decode(20, 8, [w1[0]]) == [w1[0]]
+    assert m.last_token() == (w1[0], len(ids))
 
 
 def test_decode_is_bitwise_repeatable(pair):
@@ -69,7 +100,7 @@ def test_decode_is_bitwise_repeatable(pair):
         m.reset()
         m.prefill_batched(ids)
         first = m.logits()
-        out = m.decode(24, 8, [])
+        out = m.decode_ids(24, 8, [])
         tok, pos = m.last_token()
         runs.append((first, out, m.step(tok, pos)))
     assert np.array_equal(runs[0][0], runs[1][0])

@@ -4,14 +4,13 @@ temperature sampling, top-k up to 1024, top-p, presence penalty, grammar masks, 
 bias, equal logits (taken in increasing token order) and the fail-closed cases."""
 import numpy as np
 import pytest
-import torch
 
+import devmem as D
 import qne as Q
 import weights as W
 from cpu_oracle import OracleSampler, bitset
 
 pytestmark = pytest.mark.gpu
-dev = torch.device("cuda:0")
 
 
 def run_both(logits_rows, opts, masks=None, bias=None):
@@ -27,7 +26,7 @@ def run_both(logits_rows, opts, masks=None, bias=None):
             host = lg.copy()
             if bias and bt < V:
                 host[bt] = np.float32(host[bt] + np.float32(bv))
-            d = torch.from_numpy(np.ascontiguousarray(lg)).to(dev)
+            d = D.to_dev(np.ascontiguousarray(lg))
             got.append(s.sample(d.data_ptr(), m, ml, bt, bv))
             want.append(o.sample(host, m, ml))
     return got, want
@@ -101,22 +100,24 @@ def test_signed_zero_and_extreme_values_use_the_total_order():
 def test_fail_closed():
     V = 1000
     with Q.Sampler(V, temperature=0.7) as s:
-        lg = torch.zeros(V, device=dev)
-        lg[5] = float("nan")
+        host = np.zeros(V, np.float32)
+        host[5] = np.nan
+        lg = D.to_dev(host)
         with pytest.raises(Q.QneError) as e:
             s.sample(lg.data_ptr())
         assert e.value.code == Q.EINVAL and "non-finite" in str(e.value)
         allowed = [i for i in range(V) if i != 5]
         assert s.sample(lg.data_ptr(), bitset(allowed, V), V) != 5  # NaN outside the mask is ignored
-        lg[5] = float("inf")
+        host[5] = np.inf
+        lg.upload(host)
         with pytest.raises(Q.QneError):
             s.sample(lg.data_ptr())
-        lg.fill_(float("-inf"))
+        lg.upload(np.full(V, -np.inf, np.float32))
         with pytest.raises(Q.QneError) as e:
             s.sample(lg.data_ptr())
         assert "no finite token" in str(e.value)
         with pytest.raises(Q.QneError):
-            s.sample(torch.zeros(V, device=dev).data_ptr(), bitset([], V), V)
+            s.sample(D.zeros(V, np.float32).data_ptr(), bitset([], V), V)
     with pytest.raises(Q.QneError):
         Q.Sampler(V, top_k=1025)
 

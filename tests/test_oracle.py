@@ -361,3 +361,24 @@ def test_model_f32_oracle_tracks_f64(tiny_model):
     for pos, tok in enumerate([1, 2, 3, 4, 5]):
         la, lb = a.token(tok, pos), b.token(tok, pos)
         assert np.max(np.abs(la - lb)) < 1e-4
+
+
+@pytest.mark.parametrize("prec", ["f32", "f64"])
+@pytest.mark.parametrize("body", ["q4", "f16"])
+def test_layered_prefill_is_bitwise_token_by_token(prec, body):
+    """oc_prefill_chunk runs a prompt layer by layer (each projection over all tokens at once); every
+    token must see exactly oc_token's arithmetic, so the state and the logits after the prompt are
+    bitwise those of feeding the tokens one at a time (model.rs:337-338 asks for the same state).
+    70 tokens span two full 32-token blocks of the projections and a ragged one, and the prompt is
+    split into two calls so a non-zero start is covered."""
+    import weights as W
+    index, buf = W.synth_model("tiny", seed=9, body=body, head="f16", norm_jitter=0.1)
+    ids = np.random.default_rng(3).integers(0, 4096, size=70).astype(np.uint32)
+    a, b = O.OracleModel(index, buf, prec, max_context=128), O.OracleModel(index, buf, prec, max_context=128)
+    for pos, t in enumerate(ids[:-1]):
+        a.token(int(t), pos, want_logits=False)
+    want = a.token(int(ids[-1]), len(ids) - 1)
+    b.prefill_chunk(ids[:45], 0, False)
+    got = b.prefill_chunk(ids[45:], 45, True)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    assert a.state_bytes() == b.state_bytes()
