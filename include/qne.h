@@ -160,6 +160,19 @@ int qne_paged_attn_decode(const float* q, const float* k_new, const float* v_new
                           const int32_t* ctx, float* out, int batch, int nq, int nkv,
                           void* stream);
 
+/* No counterpart in the reference. For callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc): qne_paged_attn_decode with
+ * the same arguments, kernels and results, whose split partials live in a fixed device array of
+ * 8 MiB (8388608 bytes) per GPU, held by each GPU the library runs on until the process ends. The
+ * call allocates nothing. QNE_EINVAL, before any device work, if batch * nkv * splits * (nq/nkv)
+ * * 1032 bytes exceed that (splits = min(max_blocks, ceil(1024 / (nkv * batch)))): up to 64
+ * sequences of 16 q / 4 kv heads always fit. Every call on one GPU shares that GPU's array, so
+ * calls that overlap on one GPU (from several threads or streams) race and must not be issued. */
+int qne_paged_attn_decode_noalloc(const float* q, const float* k_new, const float* v_new, void* k_pool,
+                                  void* v_pool, const int32_t* block_table, int max_blocks,
+                                  const int32_t* ctx, float* out, int batch, int nq, int nkv,
+                                  void* stream);
+
 /* The batched form of gemv for m (1..64) rows of x: y[r] = W x[r] for r < m, on f16 MFMA (x split
  * into two f16 halves, so the products keep about 22 bits), with the same norm prologue and
  * epilogues as qne_gemv. The reference's 16-token GEMM (kernels/src/batch.rs:12-99, Gpu::gemm

@@ -325,6 +325,34 @@ int qne_paged_attn_decode(const float* q, const float* k_new, const float* v_new
     });
 }
 
+int qne_paged_attn_decode_noalloc(const float* q, const float* k_new, const float* v_new, void* k_pool, void* v_pool,
+                                  const int32_t* block_table, int max_blocks, const int32_t* ctx, float* out, int batch,
+                                  int nq, int nkv, void* stream) {
+    return guard([&] {
+        need(q && k_new && v_new && k_pool && v_pool && block_table && ctx && out, "null argument");
+        need(batch > 0 && batch <= 65535 && nkv > 0 && nq % nkv == 0, "bad batch or heads");
+        const int G = nq / nkv;
+        need(G == 1 || G == 2 || G == 4, "nq/nkv must be 1, 2 or 4");
+        need(max_blocks > 0, "max_blocks must be positive");
+        // the same split count as qne_paged_attn_decode, so both give the same results
+        int splits = (1024 + nkv * batch - 1) / (nkv * batch);
+        if (splits < 1) splits = 1;
+        if (splits > max_blocks) splits = max_blocks;
+        const size_t parts = (size_t)batch * nkv * splits * G;
+        const size_t bytes = parts * 258 * 4;
+        if (bytes > qne::kNoAllocScratchBytes)
+            throw qne::Error(QNE_EINVAL, "qne_paged_attn_decode_noalloc: this call needs " + std::to_string(bytes) +
+                                             " bytes of split partials; its fixed scratch holds " +
+                                             std::to_string(qne::kNoAllocScratchBytes) + " (use qne_paged_attn_decode)");
+        float* ws = qne::noalloc_scratch();
+        hipStream_t st = (hipStream_t)stream;
+        qne::launch_paged_attn(q, k_new, v_new, (uint16_t*)k_pool, (uint16_t*)v_pool, block_table, max_blocks, ctx,
+                               out, batch, nq, nkv, ws, ws + parts * 2, splits, st);
+        check_launch();
+        if (!stream) qne::hip_check(hipStreamSynchronize(st), "paged attention");
+    });
+}
+
 int qne_gemm(int kind, const void* w, const void* sz, int rows, int k, int group, const float* x, int x_stride, int m,
              const float* norm, float eps, float* y, int y_stride, int epilogue, void* stream) {
     return guard([&] {

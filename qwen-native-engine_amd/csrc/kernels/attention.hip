@@ -11,12 +11,40 @@
 //  - a combine kernel merges the splits (and applies the sigmoid output gate of the model).
 // The current token's k and v are appended (rounded to f16) before the partials run, so the
 // current position is read back exactly as every later step will read it.
+#include <mutex>
+#include <string>
+
+#include "../error.hpp"
 #include "common.hpp"
 #include "launch.hpp"
 
 namespace qne {
 
 constexpr int kHD = 256, kBlock = 16, kAttnThreads = 256;
+
+// The split partials of qne_paged_attn_decode_noalloc ((maximum, sum) pairs, then 256-float
+// accumulators) live here instead of in memory the library allocates. Each GPU holds its own copy
+// for the life of the process. In host code `scratch` names a host-side stand-in, never the
+// device memory: host code uses the address noalloc_scratch() looked up.
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+float* noalloc_scratch() {
+    static std::mutex mu;
+    static void* per_device[256] = {};
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) throw Error(QNE_EDEVICE, std::string("HIP error in hipGetDevice: ") + hipGetErrorString(e));
+    if (dev < 0 || dev >= 256) throw Error(QNE_EDEVICE, "device ordinal out of range");
+    std::lock_guard<std::mutex> lock(mu);
+    if (!per_device[dev]) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p)
+            throw Error(QNE_EDEVICE, std::string("HIP error in hipGetSymbolAddress(scratch): ") + hipGetErrorString(e));
+        per_device[dev] = p;
+    }
+    return (float*)per_device[dev];
+}
 
 __device__ __forceinline__ size_t kv_index(const int32_t* bt, int pos, int nkv, int g) {
     const int blk = bt[pos / kBlock];

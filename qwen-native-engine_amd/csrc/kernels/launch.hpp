@@ -171,6 +171,13 @@ size_t argmax_rows_scratch(int m);
 void launch_argmax_rows(const float* logits, int m, int V, uint32_t* out, uint32_t* tokens, int32_t* pos, void* scratch,
                         hipStream_t st);
 
+// Scratch of the no-allocation paged decode entry point: a file-scope device array of
+// kNoAllocScratchBytes in attention.hip. noalloc_scratch() returns its address on the current
+// device, looked up (hipGetSymbolAddress) on the first call made with that device current and kept
+// per device; it allocates nothing.
+constexpr size_t kNoAllocScratchBytes = (size_t)8 << 20;
+float* noalloc_scratch();
+
 // Raw paged decode for `batch` sequences: append k/v at ctx[b], attend over 0..ctx[b].
 void launch_paged_attn(const float* q, const float* k_new, const float* v_new, uint16_t* k_pool, uint16_t* v_pool,
                        const int32_t* block_table, int max_blocks, const int32_t* ctx, float* out, int batch, int nq,

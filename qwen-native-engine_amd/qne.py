@@ -67,6 +67,7 @@ def load_library(path: str | os.PathLike | None = None):
         "qne_gdn_step": ([c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_i, c_i, c_p], c_i),
         "qne_gdn_prefill_chunked": ([c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_i, c_i, c_i, c_p], c_i),
         "qne_paged_attn_decode": ([c_p, c_p, c_p, c_p, c_p, c_p, c_i, c_p, c_p, c_i, c_i, c_i, c_p], c_i),
+        "qne_paged_attn_decode_noalloc": ([c_p, c_p, c_p, c_p, c_p, c_p, c_i, c_p, c_p, c_i, c_i, c_i, c_p], c_i),
         "qne_gemm": ([c_i, c_p, c_p, c_i, c_i, c_i, c_p, c_i, c_i, c_p, c_f, c_p, c_i, c_i, c_p], c_i),
         "qne_batch_create": ([c_p, c_u32, c_u32, ctypes.POINTER(c_p)], c_i),
         "qne_batch_free": ([c_p], c_i),
@@ -408,3 +409,11 @@ def paged_attn_decode(q, k_new, v_new, k_pool, v_pool, block_table, max_blocks, 
     lib = load_library()
     _check(lib, lib.qne_paged_attn_decode(q, k_new, v_new, k_pool, v_pool, block_table, max_blocks, ctx, out, batch,
                                           nq, nkv, stream or None))
+
+
+def paged_attn_decode_noalloc(q, k_new, v_new, k_pool, v_pool, block_table, max_blocks, ctx, out, batch, nq, nkv,
+                              stream=0):
+    """paged_attn_decode with its split partials in the library's fixed per-GPU array (no allocation)."""
+    lib = load_library()
+    _check(lib, lib.qne_paged_attn_decode_noalloc(q, k_new, v_new, k_pool, v_pool, block_table, max_blocks, ctx, out,
+                                                  batch, nq, nkv, stream or None))
