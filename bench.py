@@ -95,9 +95,11 @@ def _profile_value(path, key):
 
 
 def profiled_traffic(steps: int):
-    """HBM bytes per decode launch measured by the FETCH_SIZE / WRITE_SIZE counter passes recorded
-    in the profile summary (scaled by a plain copy of known size), when that profile covers launches
-    of the same window length; else None."""
+    """HBM bytes of a `steps`-token decode launch from the FETCH_SIZE / WRITE_SIZE counter passes
+    recorded in the profile summary (scaled by a plain copy of known size): the profiled launch's
+    bytes per token times `steps`. A token moves the same bytes whatever the window length, except
+    for the KV cache's growth with the context (under 0.1 % between a 20- and a 96-token window at
+    context 4000). None without the profile."""
     try:
         text = TRAFFIC_PROFILE.read_text()
     except OSError:
@@ -107,9 +109,9 @@ def profiled_traffic(steps: int):
         if line.startswith("traffic_") and ":" in line:
             k, v = line.split(":", 1)
             vals[k.strip()] = float(v)
-    if int(vals.get("traffic_steps_per_launch", -1)) != steps or "traffic_bytes_per_launch" not in vals:
+    if vals.get("traffic_steps_per_launch", 0) <= 0 or "traffic_bytes_per_launch" not in vals:
         return None
-    return vals["traffic_bytes_per_launch"]
+    return vals["traffic_bytes_per_launch"] / vals["traffic_steps_per_launch"] * steps
 
 
 def _events_ms(fn, warmup: int, iters: int):
@@ -457,6 +459,121 @@ def bench_batch(args) -> dict:
     return result
 
 
+class _Hip:
+    """The few HIP runtime calls the probes need, through the runtime libqne.so itself links."""
+
+    def __init__(self):
+        import ctypes
+        import qne
+        qne.load_library()
+        h = ctypes.CDLL("libamdhip64.so.7")
+        vp, sz = ctypes.c_void_p, ctypes.c_size_t
+        for name, args in (("hipMalloc", [ctypes.POINTER(vp), sz]), ("hipFree", [vp]),
+                           ("hipMemcpy", [vp, vp, sz, ctypes.c_int]), ("hipMemsetD32", [vp, ctypes.c_int, sz]),
+                           ("hipDeviceSynchronize", []), ("hipEventCreate", [ctypes.POINTER(vp)]),
+                           ("hipEventRecord", [vp, vp]), ("hipEventSynchronize", [vp]),
+                           ("hipEventElapsedTime", [ctypes.POINTER(ctypes.c_float), vp, vp])):
+            f = getattr(h, name)
+            f.argtypes = args
+            f.restype = ctypes.c_int
+        self.h, self.ct = h, ctypes
+
+    def ck(self, rc, what):
+        if rc != 0:
+            raise RuntimeError(f"{what} failed ({rc})")
+
+    def malloc(self, n):
+        p = self.ct.c_void_p()
+        self.ck(self.h.hipMalloc(self.ct.byref(p), n), "hipMalloc")
+        return p.value
+
+    def free(self, p):
+        self.h.hipFree(p)
+
+    def upload(self, p, a, off=0):
+        self.ck(self.h.hipMemcpy(p + off, a.ctypes.data, a.nbytes, 1), "hipMemcpy")
+
+    def copy(self, dst, src, n):
+        self.ck(self.h.hipMemcpy(dst, src, n, 3), "hipMemcpy")
+
+    def fill32(self, p, v, n_words):
+        self.ck(self.h.hipMemsetD32(p, v, n_words), "hipMemsetD32")
+
+    def sync(self):
+        self.ck(self.h.hipDeviceSynchronize(), "hipDeviceSynchronize")
+
+    def timed(self, fn, n):
+        """Device ms per call of fn() (HIP events on the null stream, which fn launches on)."""
+        a, b = self.ct.c_void_p(), self.ct.c_void_p()
+        self.h.hipEventCreate(self.ct.byref(a))
+        self.h.hipEventCreate(self.ct.byref(b))
+        self.h.hipEventRecord(a, None)
+        for _ in range(n):
+            fn()
+        self.h.hipEventRecord(b, None)
+        self.h.hipEventSynchronize(b)
+        ms = self.ct.c_float()
+        self.h.hipEventElapsedTime(self.ct.byref(ms), a, b)
+        return ms.value / n
+
+
+def bench_stream(args) -> dict:
+    """The reference's two probes on MI355X: the streaming-read bandwidth probe (bandwidth_probe,
+    kernels/src/lib.rs:837-863: 64 MB and 400 MB buffers, constant and random data, three runs each)
+    and the fixed cost of one dispatch (dispatch_cost, lib.rs:718-724: 2000 no-op dispatches). A
+    4 GiB buffer is added: 64 MB fits the 256 MB MALL, 400 MB mostly does not, and 4 GiB measures
+    HBM alone. `value` is the 4 GiB random-data read rate: the achievable ceiling a streaming
+    kernel (the GEMV, the LM head) can be held against."""
+    import qne
+    hip = _Hip()
+    lib = qne.load_library()
+    groups = args.stream_workgroups
+    sink = hip.malloc(groups * 256 * 4)
+    rng = np.random.default_rng(args.seed)
+    block = rng.integers(0, 2**32, size=(64 << 20) // 4, dtype=np.uint32)
+    runs = []
+    for mb in (64, 400, 4096):
+        n = mb << 20
+        data = hip.malloc(n)
+        for random in (False, True):
+            if random:
+                hip.upload(data, block)
+                for off in range(64 << 20, n, 64 << 20):
+                    hip.copy(data + off, data, min(64 << 20, n - off))
+            else:
+                hip.fill32(data, 0x12345678, n // 4)
+            hip.sync()
+            call = lambda: lib.qne_stream_read(data, n, sink, groups, None)
+            hip.timed(call, 2)
+            repeat = 20 if mb <= 100 else 5 if mb <= 1000 else 3
+            for run in range(3):
+                ms = hip.timed(call, repeat)
+                runs.append({"mb": mb, "data": "random" if random else "constant", "run": run,
+                             "GB/s": round(n / (ms / 1e3) / 1e9, 1)})
+        hip.free(data)
+    y = hip.malloc(256)
+    hip.fill32(y, 0, 64)
+    noop = lambda: lib.qne_noop_dispatch(y, None)
+    hip.timed(noop, 10)
+    n_disp = 2000
+    t0 = time.perf_counter()
+    dev_ms = hip.timed(noop, n_disp)
+    host_us = (time.perf_counter() - t0) * 1e6 / n_disp
+    hip.free(y)
+    hip.free(sink)
+    best = max(r["GB/s"] for r in runs if r["mb"] == 4096 and r["data"] == "random")
+    return {"metric": "streaming read GB/s (16-byte non-temporal loads, 4 GiB random data)", "value": best,
+            "unit": "GB/s", "n_gpus": 1, "steps": 3, "warmup": 2, "ms_per_step": round((4096 << 20) / best / 1e6, 4),
+            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "u32", "data": "synthetic",
+            "config": {"workload": "read 64 MB / 400 MB / 4 GiB once, constant and random data; 2000 no-op dispatches",
+                       "workgroups": groups, "threads_per_workgroup": 256},
+            "roofline": {"bound": "hbm", "achieved": best, "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                         "frac": round(best / PEAK_HBM_GBS, 4), "traffic": None, "kernel": "k_stream_read"},
+            "detail": {"stream": runs, "dispatch_us_device": round(dev_ms * 1e3, 3),
+                       "dispatch_us_host": round(host_us, 3), "dispatches": n_disp},
+            "cpu_baseline": None}
+
+
 def copy_calibration(mib: int) -> None:
     """A plain device-to-device copy of a known size: under a hardware-counter profiler its
     FETCH_SIZE / WRITE_SIZE readings per dispatch, divided into the bytes it must move, give the
@@ -475,15 +592,17 @@ def copy_calibration(mib: int) -> None:
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=96)
+    ap.add_argument("--steps", type=int, default=None, help="timed decode steps (default 96; 128 for --config 0.8b)")
     ap.add_argument("--warmup", type=int, default=None,
                     help="untimed warmup steps, run as one window (default: as many as --steps, so that "
                          "every decode window a profile sees has the timed length)")
-    ap.add_argument("--ctx", type=int, default=4000)
+    ap.add_argument("--ctx", type=int, default=None, help="prompt length (default 4000; 128 for --config 0.8b)")
     ap.add_argument("--config", default="2b",
-                    help="2b (the decode benchmark), 0.8b, batch (64-sequence batched decode), sample (sampled "
-                         "decode with the device sampler), or the kernel microbenches attn / gdn / gemv")
+                    help="2b (the decode benchmark), 0.8b (f16 weights, 128-id prompt, 128 steps), batch "
+                         "(64-sequence batched decode), sample (sampled decode with the device sampler), stream "
+                         "(the read-bandwidth and dispatch-cost probes), or the kernel microbenches attn / gdn / gemv")
     ap.add_argument("--batch", type=int, default=64, help="sequences (--config attn / batch)")
+    ap.add_argument("--stream-workgroups", type=int, default=2048, help="workgroups of the --config stream probe")
     ap.add_argument("--cpu-tokens", type=int, default=4)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--seed", type=int, default=0)
@@ -491,6 +610,11 @@ def main():
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB three times (scales the HBM byte counters)")
     args = ap.parse_args()
+    small = args.config == "0.8b"
+    if args.steps is None:
+        args.steps = 128 if small else 96
+    if args.ctx is None:
+        args.ctx = 128 if small else 4000
     if args.warmup is None:
         args.warmup = args.steps
     if args.copy_calibration:
@@ -503,6 +627,10 @@ def main():
         return
     if args.config == "batch":
         print(json.dumps(bench_batch(args)))
+        return
+    if args.config == "stream":
+        sys.path[:0] = [str(ROOT / "qwen-native-engine_amd")]
+        print(json.dumps(bench_stream(args)))
         return
     if args.config == "sample":
         sys.path[:0] = [str(ROOT / "qwen-native-engine_amd")]
@@ -517,7 +645,9 @@ def main():
 
     cfg = W.full_config(args.config)
     t = time.perf_counter()
-    index, buf = W.synth_model(args.config, seed=args.seed, body="q4", head="f16", group=64)
+    # the 0.8B configuration has f16 weights throughout, the 2B one an int4 g64 body
+    body = "f16" if small else "q4"
+    index, buf = W.synth_model(args.config, seed=args.seed, body=body, head="f16", group=64)
     mats = json.loads(index)["matrices"]
     gen_s = time.perf_counter() - t
     m = qne.Model.load(index, buf, options={"max_context": 4096, "engine": args.engine})
@@ -548,7 +678,8 @@ def main():
     achieved = bytes_tok["total"] * args.steps / (dev_ms / 1e3) / 1e9
     traffic = profiled_traffic(args.steps) if args.ctx == 4000 and args.config == "2b" else None
     result = {
-        "metric": "decode tok/s @ batch 1, ctx 4096 (2B int4) + % of HBM roofline",
+        "metric": ("decode tok/s @ batch 1, 0.8B f16, 128-id prompt" if small else
+                   "decode tok/s @ batch 1, ctx 4096 (2B int4) + % of HBM roofline"),
         "value": round(tok_s, 2),
         "unit": "tok/s",
         "n_gpus": 1,
@@ -560,7 +691,8 @@ def main():
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic",
-        "config": {"workload": f"Qwen3.5-{args.config.upper()}-shaped hybrid decoder, int4 g64 body, f16 embed/lm_head, "
+        "config": {"workload": f"Qwen3.5-{args.config.upper()}-shaped hybrid decoder, "
+                               f"{'f16' if small else 'int4 g64'} body, f16 embed/lm_head, "
                                f"batch 1 greedy decode after a {args.ctx}-token prefill",
                    "layers": cfg["layers"], "hidden": cfg["hidden"], "vocab": cfg["vocab"], "ctx": args.ctx,
                    "batch": 1, "window": args.steps},

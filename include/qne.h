@@ -184,6 +184,16 @@ int qne_gemm(int kind, const void* w, const void* sz, int rows, int k, int group
              int x_stride, int m, const float* norm, float eps, float* y, int y_stride, int epilogue,
              void* stream);
 
+/* ---- measurement kernels (the reference's probes) ----
+ * The streaming-read probe: `bandwidth` (kernels/src/shaders.rs:701-717), run by bandwidth_probe
+ * (kernels/src/lib.rs:837-863). Reads every 16-byte word of data[0..bytes) once (non-temporal)
+ * and xor-folds it into sink[workgroups * 256] (one word per thread); the read bandwidth a GEMV
+ * with no unpacking work could reach. bytes: a positive multiple of 16. Enqueued on `stream`. */
+int qne_stream_read(const void* data, size_t bytes, uint32_t* sink, uint32_t workgroups, void* stream);
+/* The dispatch-cost probe: `noop` (kernels/src/shaders.rs:719-729) timed by dispatch_cost
+ * (kernels/src/lib.rs:718-724). One 64-thread workgroup adds 1 to y[0]. Enqueued on `stream`. */
+int qne_noop_dispatch(float* y, void* stream);
+
 /* ---- token sampling on the device ----
  * src/sampling.rs Sampler (the agent's temperature + top-k + top-p sampler with presence penalty
  * and grammar mask) over logits in device memory: the O(vocab) part (checks, penalty, mask, greedy

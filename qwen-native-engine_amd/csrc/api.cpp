@@ -393,6 +393,24 @@ int qne_gemm(int kind, const void* w, const void* sz, int rows, int k, int group
     });
 }
 
+int qne_stream_read(const void* data, size_t bytes, uint32_t* sink, uint32_t workgroups, void* stream) {
+    return guard([&] {
+        need(data && sink, "null argument");
+        need(bytes > 0 && bytes % 16 == 0, "bytes must be a positive multiple of 16");
+        need(workgroups >= 1 && workgroups <= 65536, "workgroups must be 1..65536");
+        qne::launch_stream_read(data, bytes, sink, (int)workgroups, (hipStream_t)stream);
+        check_launch();
+    });
+}
+
+int qne_noop_dispatch(float* y, void* stream) {
+    return guard([&] {
+        need(y != nullptr, "null argument");
+        qne::launch_noop(y, (hipStream_t)stream);
+        check_launch();
+    });
+}
+
 struct qne_sampler {
     qne::DeviceSampler* s;
 };

@@ -30,6 +30,10 @@ bool launch_gemv(int kind, const void* W, const uint32_t* SZ, int rows, int k, i
 
 // tok[0] = ids[i], tok[1] = pos.
 void launch_set_tok(uint32_t* tok, const uint32_t* ids, int i, uint32_t pos, hipStream_t st);
+// Measurement kernels: a streaming read of `bytes` (a multiple of 16) folded into sink
+// [workgroups * 256], and a dispatch that does almost nothing.
+void launch_stream_read(const void* data, size_t bytes, uint32_t* sink, int workgroups, hipStream_t st);
+void launch_noop(float* y, hipStream_t st);
 
 // Pseudo-random uniform [-amp, amp) fill of n f16 or f32 values (benchmark state).
 void launch_fill_uniform(void* p, size_t n, bool f16, uint64_t seed, float amp, hipStream_t st);

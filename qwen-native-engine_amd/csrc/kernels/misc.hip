@@ -42,6 +42,34 @@ __global__ void k_fill_uniform(void* __restrict__ p, size_t n, int f16, uint64_t
     }
 }
 
+// Streaming-read probe (the reference's `bandwidth` shader, kernels/src/shaders.rs:701-717): every
+// 16-byte word of `data` is read once, non-temporal, and xor-folded into one word per thread, so
+// nothing but the loads costs time. Four loads per thread are in flight per iteration.
+__global__ __launch_bounds__(256) void k_stream_read(const u32x4* __restrict__ data, size_t n, uint32_t* __restrict__ sink) {
+    const size_t threads = (size_t)gridDim.x * blockDim.x;
+    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    u32x4 acc = {0u, 0u, 0u, 0u};
+    for (; i + 3 * threads < n; i += 4 * threads) {
+        const u32x4 a = __builtin_nontemporal_load(data + i), b = __builtin_nontemporal_load(data + i + threads);
+        const u32x4 c = __builtin_nontemporal_load(data + i + 2 * threads), d = __builtin_nontemporal_load(data + i + 3 * threads);
+        acc ^= a ^ b ^ c ^ d;
+    }
+    for (; i < n; i += threads) acc ^= __builtin_nontemporal_load(data + i);
+    sink[(size_t)blockIdx.x * blockDim.x + threadIdx.x] = acc.x ^ acc.y ^ acc.z ^ acc.w;
+}
+
+// A dispatch that does almost nothing (the reference's `noop`, kernels/src/shaders.rs:719-729): the
+// fixed cost of one dispatch.
+__global__ void k_noop(float* y) {
+    if (threadIdx.x == 0) y[0] = y[0] + 1.0f;
+}
+
+void launch_stream_read(const void* data, size_t bytes, uint32_t* sink, int workgroups, hipStream_t st) {
+    hipLaunchKernelGGL(k_stream_read, dim3(workgroups), dim3(256), 0, st, (const u32x4*)data, bytes / 16, sink);
+}
+
+void launch_noop(float* y, hipStream_t st) { hipLaunchKernelGGL(k_noop, dim3(1), dim3(64), 0, st, y); }
+
 void launch_fill_uniform(void* p, size_t n, bool f16, uint64_t seed, float amp, hipStream_t st) {
     if (n == 0) return;
     const size_t blocks = std::min<size_t>((n + 255) / 256, 8192);

@@ -15,6 +15,7 @@ import weights as W
 
 GOLDEN = Path(__file__).resolve().parent / "golden"
 LOGIT_TOL = 1e-2  # max |logit - oracle logit|
+TIE = 1e-3  # oracle top-2 margins below this are ties at the engine's precision (long-context fixtures)
 
 
 def fixture(name):
@@ -78,8 +79,13 @@ def test_long_context_decode_matches_oracle_fixture(name, window):
     g = fixture(name)
     case = json.loads(str(g["case"]))
     index, buf = synth(case)
-    prompt, ids = g["prompt"], g["ids"].tolist()
+    prompt, ids, margin = g["prompt"], g["ids"].tolist(), g["margin"]
     P = len(prompt)
+    # A pick whose top-2 logits are closer than TIE in the oracle's own f32 arithmetic is a tie at
+    # the engine's precision (its logits differ from the oracle's by ~1e-4): past the first such
+    # step a free-running decode may take the other branch. Free-running ids must be identical up
+    # to that step; every later step is checked teacher-forced (the oracle's ids fed through step()).
+    tie = next((s for s in range(len(ids)) if margin[s] < TIE), len(ids))
     with Q.Model.load(index, buf, options={"max_context": case.get("max_context", 4096)}) as m:
         for s in range(0, P, 512):
             m.prefill_chunk(prompt[s:s + 512], s, s + 512 >= P)
@@ -88,17 +94,18 @@ def test_long_context_decode_matches_oracle_fixture(name, window):
         assert m.last_token() == (ids[0], P)
         m.snapshot()
         out = m.decode_ids(len(ids), window, [])
-        assert out == ids, f"{name}: first divergence at step {next(i for i, (a, b) in enumerate(zip(out, ids)) if a != b)}"
-        # the logits after the logged fed ids, through step() from the same prompt state
+        assert out[:tie] == ids[:tie], \
+            f"{name}: first divergence at step {next(i for i, (a, b) in enumerate(zip(out, ids)) if a != b)}"
+        # teacher-forced: the logits after every fed id from the same prompt state
         m.restore()
         logged = {int(s): i for i, s in enumerate(g["steps"])}
-        last = max(logged)
-        for i in range(last):
+        for i in range(len(ids) - 1):
             v = m.step(ids[i], P + i)
-            assert int(np.argmax(v)) == ids[i + 1], f"{name}: step {i + 1}"
+            if margin[i + 1] >= TIE:
+                assert int(np.argmax(v)) == ids[i + 1], f"{name}: step {i + 1}"
             if i + 1 in logged:
                 j = logged[i + 1]
                 worst = max(worst, float(np.max(np.abs(v[g["logit_idx"][j]] - g["logit_val"][j]))))
-    print(f"{name}: {len(ids)} greedy ids identical; max |dlogit| {worst:.2e}; smallest top-2 margin "
-          f"{float(np.min(g['margin'])):.4f}")
+    print(f"{name}: free-running ids identical over {tie} steps (first oracle tie at {tie}), teacher-forced picks "
+          f"identical wherever the oracle margin >= {TIE}; max |dlogit| {worst:.2e}")
     assert worst <= LOGIT_TOL

@@ -307,3 +307,20 @@ def test_gdn_prefill_config4_shape():
     D.sync()
     assert rel_err(out.numpy(), want_o) < 1e-4
     assert rel_err(d[5].numpy(), want_S) < 1e-4
+
+
+@pytest.mark.parametrize("words,groups", [(4 * 1000003, 64), (4 * 256 * 4, 1), (4 * 7, 3)])
+def test_stream_read_probe_reads_every_word_once(words, groups):
+    """The streaming-read probe (shaders.rs:701-717) folds every 16-byte word into the sink: the xor
+    of all sink words is the xor of all data words (a skipped or doubled word changes it)."""
+    lib = Q.load_library()
+    data = np.random.default_rng(words).integers(0, 2**32, size=words, dtype=np.uint32)
+    d, sink = D.to_dev(data), D.zeros(groups * 256, np.uint32)
+    assert lib.qne_stream_read(d.ptr, data.nbytes, sink.ptr, groups, None) == 0
+    D.sync()
+    assert int(np.bitwise_xor.reduce(sink.numpy())) == int(np.bitwise_xor.reduce(data))
+    y = D.zeros(1, np.float32)
+    for _ in range(5):
+        assert lib.qne_noop_dispatch(y.ptr, None) == 0
+    D.sync()
+    assert float(y.numpy()[0]) == 5.0
