@@ -52,6 +52,9 @@ constexpr int kNT = 2;                 // cache policy: non-temporal (streamed o
 constexpr int kBlk = 16;               // KV block size (positions)
 constexpr int kDK = 128;               // GDN dk = dv
 constexpr int kAttnU = kHalf / 2048;   // prefetched K/V wave-loads (2 positions each) per wave
+// Attention scores are kept in base 2: q is pre-scaled by log2(e) / sqrt(256), so every softmax
+// weight is one hardware exp2 (v_exp_f32) instead of a range-reduced expf.
+constexpr float kScoreScale = 1.4426950408889634f * 0.0625f;
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 typedef __amdgpu_buffer_rsrc_t rsrc_t;
@@ -88,6 +91,8 @@ typedef const __attribute__((address_space(4))) Phase CPhase;
 typedef const __attribute__((address_space(4))) float cfloat;
 
 __device__ __forceinline__ void cbar() { asm volatile("" ::: "memory"); }
+// 2^x on the hardware unit (exp2(-inf) = 0).
+__device__ __forceinline__ float exp2_hw(float x) { return __builtin_amdgcn_exp2f(x); }
 // Workgroup barrier for LDS hand-offs only. Unlike __syncthreads it does not wait for the wave's
 // outstanding global loads (the prefetch of the next phase stays in flight).
 __device__ __forceinline__ void bar() {
@@ -904,7 +909,7 @@ __device__ __forceinline__ void attn_phase(const Env& e, CPhase& P, int step, in
     bar();
     if (*e.bail) return;
     mark(e, 1);
-    float* qs = xs + 1536;  // [G][256], normed, rotated, pre-scaled by 1/sqrt(256)
+    float* qs = xs + 1536;  // [G][256], normed, rotated, pre-scaled by log2(e) / sqrt(256)
     float* kc = xs + 2560;  // current key and value, f16-rounded
     float* vc = xs + 2816;
     if (e.wave < G) {
@@ -913,7 +918,7 @@ __device__ __forceinline__ void attn_phase(const Env& e, CPhase& P, int step, in
         v[0] = f.x; v[1] = f.y; v[2] = f.z; v[3] = f.w;
         norm_rope4(v, P.gain, a, rope, lane);
 #pragma unroll
-        for (int i = 0; i < 4; i++) qs[e.wave * kHeadDim + 4 * lane + i] = v[i] * 0.0625f;
+        for (int i = 0; i < 4; i++) qs[e.wave * kHeadDim + 4 * lane + i] = v[i] * kScoreScale;
     } else if (e.wave == G) {
         float v[4];
         const float4 f = *(const float4*)(xs + 1024 + 4 * lane);
@@ -998,7 +1003,7 @@ __device__ __forceinline__ void attn_phase(const Env& e, CPhase& P, int step, in
                 s = half_sum_dpp(s, lane);  // the position's 32 lanes
                 if (valid) {
                     const float mn = fmaxf(m[gi], s);
-                    const float corr = expf(m[gi] - mn), pw = expf(s - mn);
+                    const float corr = exp2_hw(m[gi] - mn), pw = exp2_hw(s - mn);
                     m[gi] = mn;
                     l[gi] = l[gi] * corr + pw;
 #pragma unroll
@@ -1015,7 +1020,7 @@ __device__ __forceinline__ void attn_phase(const Env& e, CPhase& P, int step, in
         if (gi < G) {
             const float mo = __shfl_xor(m[gi], 32, kWave), lo = __shfl_xor(l[gi], 32, kWave);
             const float mn = fmaxf(m[gi], mo);
-            const float ca = mn == -INFINITY ? 0.0f : expf(m[gi] - mn), cb = mn == -INFINITY ? 0.0f : expf(mo - mn);
+            const float ca = mn == -INFINITY ? 0.0f : exp2_hw(m[gi] - mn), cb = mn == -INFINITY ? 0.0f : exp2_hw(mo - mn);
 #pragma unroll
             for (int d = 0; d < 8; d++) acc[gi][d] = acc[gi][d] * ca + __shfl_xor(acc[gi][d], 32, kWave) * cb;
             l[gi] = l[gi] * ca + lo * cb;
@@ -1042,7 +1047,7 @@ __device__ __forceinline__ void attn_phase(const Env& e, CPhase& P, int step, in
 #pragma unroll
             for (int w = 0; w < kNW; w++) {
                 const float* pw = (const float*)(e.regs + w * kWaveLds + rh * kHalf) + gi * 258;
-                const float cw = mw[w] == -INFINITY ? 0.0f : expf(mw[w] - mn);
+                const float cw = mw[w] == -INFINITY ? 0.0f : exp2_hw(mw[w] - mn);
                 ls += pw[1] * cw;
                 a0 += pw[2 + d0] * cw;
                 a1 += pw[3 + d0] * cw;
@@ -1101,13 +1106,15 @@ __device__ __forceinline__ void comb_phase(const Env& e, CPhase& P, int step, in
     {
         // wave sg takes splits sg, sg + 8, ...; lane = dim. Their sums meet in xs after the gate.
         const int d = threadIdx.x & 63, sg = threadIdx.x >> 6;
-        float mn = -INFINITY;
-        for (int s = 0; s < S; s++) mn = fmaxf(mn, xs[2 * s]);
+        // every wave finds the maximum over the splits with its lanes (one split each), in parallel
+        float mm = -INFINITY;
+        for (int s = d; s < S; s += kWave) mm = fmaxf(mm, xs[2 * s]);
+        const float mn = wave_max(mm);
         float ls = 0.0f, ac = 0.0f;
         for (int s = sg; s < S; s += kNW) {
             const float ms = xs[2 * s];
             if (ms == -INFINITY) continue;
-            const float cw = expf(ms - mn);
+            const float cw = exp2_hw(ms - mn);  // the partials' maxima and sums are in base 2
             ls += xs[2 * s + 1] * cw;
             ac += xs[2 * S + 64 * s + d] * cw;
         }
