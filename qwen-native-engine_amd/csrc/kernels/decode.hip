@@ -257,6 +257,7 @@ __device__ __forceinline__ void dma_rows(CPhase& P, const GemvGeo& g, int o0, in
 //  - f16 rows: step j is the 512-column slab j (8 values, 16 bytes per lane).
 struct Step {
     int kind, K, n4, n2, n1, nsteps;
+    int gdn;  // the input is a GDN output: each lane's slice is scaled by its head's 1/rms
 };
 __device__ __forceinline__ Step make_step(CPhase& P) {
     Step t;
@@ -266,6 +267,7 @@ __device__ __forceinline__ Step make_step(CPhase& P) {
     t.n2 = P.n2;
     t.n1 = P.n1;
     t.nsteps = P.nsteps;
+    t.gdn = P.xnorm == XN_GDN;
     return t;
 }
 
@@ -290,7 +292,8 @@ __device__ __forceinline__ int xs_slot(const Step& t, int k) {
 
 struct XC {
     float x[32];
-    float sum;  // q4: sum of the step's values (the zero-point term)
+    float sum;    // q4: sum of the step's values (the zero-point term)
+    float scale;  // the slice's factor: 1, or its head's 1/rms for a GDN output
 };
 
 // Inverse of xs_slot for a position d < K of the chunk-major staging.
@@ -320,51 +323,31 @@ __device__ __forceinline__ void step_slab(const Step& t, int j, int& base, int& 
     }
 }
 
-// Finishes the staged input of an LDS-region GEMV, once per workgroup so the waves do not each
-// redo it per step: the GDN output norm (per head, 1/rms from the published partial sums of
-// squares, kernels/src/shaders.rs:514) is applied in place, then the sum of every lane slice of
-// every step (the q4 zero-point term) goes to xsum[j * 64 + lane]. Ends with a barrier.
-__device__ __forceinline__ void stage_post(float* xs, CPhase& P, const Step& t, float* xsum, float* rnh) {
-    if (P.xnorm == XN_GDN) {
-        const int H = P.heads;
-        if ((int)threadIdx.x < H) {
-            float s = 0.0f;
-#pragma unroll
-            for (int b = 0; b < 16; b++) s += xs[H * kDK + threadIdx.x * 16 + b];
-            rnh[threadIdx.x] = 1.0f / sqrtf(s / (float)kDK + 1e-6f);
-        }
-        bar();
-        for (int d = threadIdx.x; d < t.K; d += kT) xs[d] *= rnh[xs_value(t, d) / kDK];
-        bar();
-    }
-    if (t.kind == 1) {
-        for (int q = threadIdx.x; q < t.nsteps * 64; q += kT) {
-            const int j = q >> 6, l = q & 63;
-            int base, nch;
-            step_slab(t, j, base, nch);
-            float sm = 0.0f;
-            for (int c = 0; c < nch; c++) {
-                const float4 f = *(const float4*)(xs + base + 256 * c + 4 * l);
-                sm += (f.x + f.y) + (f.z + f.w);
-            }
-            xsum[q] = sm;
-        }
-        bar();
-    }
-}
-
 // The lane's values of step j from xs, and (q4) their sum.
-__device__ __forceinline__ void load_step(const float* xs, const float* xsum, const Step& t, int j, XC& X, int lane) {
+__device__ __forceinline__ void load_step(const float* xs, const Step& t, int j, XC& X, int lane) {
     int base, nch;
     step_slab(t, j, base, nch);
+    float sm = 0.0f;  // q4: the slice's sum (the zero-point term), chunk by chunk
 #pragma unroll
     for (int c = 0; c < 8; c++) {
         if (c < nch) {
             const float4 f = *(const float4*)(xs + base + 256 * c + 4 * lane);
             X.x[4 * c] = f.x; X.x[4 * c + 1] = f.y; X.x[4 * c + 2] = f.z; X.x[4 * c + 3] = f.w;
+            sm += (f.x + f.y) + (f.z + f.w);
         }
     }
-    X.sum = t.kind == 1 ? xsum[j * 64 + lane] : 0.0f;
+    X.sum = t.kind == 1 ? sm : 0.0f;
+    X.scale = 1.0f;
+    if (t.gdn) {
+        // GDN output norm (kernels/src/shaders.rs:514): the lane's slice lies in one 128-value head;
+        // its 1/rms comes from the head's 16 published partial sums of squares (staged past K)
+        const int h = (base + lane * 4 * nch) / kDK;
+        const float4* ps = (const float4*)(xs + t.K + 16 * h);
+        const float4 a = ps[0], b = ps[1], c = ps[2], d = ps[3];
+        const float ssum = (((a.x + a.y) + (a.z + a.w)) + ((b.x + b.y) + (b.z + b.w))) +
+                           (((c.x + c.y) + (c.z + c.w)) + ((d.x + d.y) + (d.z + d.w)));
+        X.scale = 1.0f / sqrtf(ssum / (float)kDK + 1e-6f);
+    }
 }
 
 // Nibble c of w times x[c], c = 0..7. The even and odd nibbles are masked into bytes once, and the
@@ -389,12 +372,12 @@ __device__ __forceinline__ float dot8(uint32_t w, const float* x) {
 // them, so a step's LDS reads for all rows issue together. X holds step 0 when nsteps is 1.
 template <int NR>
 __device__ __forceinline__ void rows_dot(const Step& t, int gs, const uint8_t* cur, const int (&roff)[8],
-                                         const int (&soff)[8], const float* xs, const float* xsum, XC& X, int lane,
+                                         const int (&soff)[8], const float* xs, XC& X, int lane,
                                          float (&acc)[8]) {
     const bool reload = t.nsteps > 1;
     if (t.kind == 1) {
         for (int j = 0; j < t.n4; j++) {
-            if (reload) load_step(xs, xsum, t, j, X, lane);
+            if (reload) load_step(xs, t, j, X, lane);
             u32x4 w[NR];
             uint32_t sz[NR];
 #pragma unroll
@@ -405,12 +388,12 @@ __device__ __forceinline__ void rows_dot(const Step& t, int gs, const uint8_t* c
 #pragma unroll
             for (int r = 0; r < NR; r++) {
                 const float dq = dot8(w[r].x, &X.x[0]) + dot8(w[r].y, &X.x[8]) + dot8(w[r].z, &X.x[16]) + dot8(w[r].w, &X.x[24]);
-                acc[r] += lo_h(sz[r]) * (dq - hi_h(sz[r]) * X.sum);
+                acc[r] += (X.scale * lo_h(sz[r])) * (dq - hi_h(sz[r]) * X.sum);
             }
         }
         if (t.n2) {
             const int j = t.n4;
-            if (reload) load_step(xs, xsum, t, j, X, lane);
+            if (reload) load_step(xs, t, j, X, lane);
             u32x2 w[NR];
             uint32_t sz[NR];
 #pragma unroll
@@ -420,11 +403,11 @@ __device__ __forceinline__ void rows_dot(const Step& t, int gs, const uint8_t* c
             }
 #pragma unroll
             for (int r = 0; r < NR; r++)
-                acc[r] += lo_h(sz[r]) * (dot8(w[r].x, &X.x[0]) + dot8(w[r].y, &X.x[8]) - hi_h(sz[r]) * X.sum);
+                acc[r] += (X.scale * lo_h(sz[r])) * (dot8(w[r].x, &X.x[0]) + dot8(w[r].y, &X.x[8]) - hi_h(sz[r]) * X.sum);
         }
         if (t.n1) {
             const int j = t.n4 + t.n2;
-            if (reload) load_step(xs, xsum, t, j, X, lane);
+            if (reload) load_step(xs, t, j, X, lane);
             uint32_t w[NR], sz[NR];
 #pragma unroll
             for (int r = 0; r < NR; r++) {
@@ -432,11 +415,11 @@ __device__ __forceinline__ void rows_dot(const Step& t, int gs, const uint8_t* c
                 sz[r] = *(const uint32_t*)(cur + soff[r] + 4 * ((2048 * t.n4 + 1024 * t.n2 + 8 * lane) >> gs));
             }
 #pragma unroll
-            for (int r = 0; r < NR; r++) acc[r] += lo_h(sz[r]) * (dot8(w[r], &X.x[0]) - hi_h(sz[r]) * X.sum);
+            for (int r = 0; r < NR; r++) acc[r] += (X.scale * lo_h(sz[r])) * (dot8(w[r], &X.x[0]) - hi_h(sz[r]) * X.sum);
         }
     } else {
         for (int j = 0; j < t.nsteps; j++) {
-            if (reload) load_step(xs, xsum, t, j, X, lane);
+            if (reload) load_step(xs, t, j, X, lane);
             u32x4 w[NR];
 #pragma unroll
             for (int r = 0; r < NR; r++) w[r] = *(const u32x4*)(cur + roff[r] + 1024 * j + 16 * lane);
@@ -447,7 +430,7 @@ __device__ __forceinline__ void rows_dot(const Step& t, int gs, const uint8_t* c
                 a = fmaf(lo_h(w[r].y), x[2], a); b = fmaf(hi_h(w[r].y), x[3], b);
                 a = fmaf(lo_h(w[r].z), x[4], a); b = fmaf(hi_h(w[r].z), x[5], b);
                 a = fmaf(lo_h(w[r].w), x[6], a); b = fmaf(hi_h(w[r].w), x[7], b);
-                acc[r] += a + b;
+                acc[r] += X.scale * (a + b);
             }
         }
     }
@@ -668,7 +651,7 @@ __device__ __forceinline__ void head_phase(const Env& e, CPhase& P, WaveState& w
 // every step of x, the step's slice is read from LDS once and applied to the whole group, then the
 // group is reduced together. The caller then sends the data of the region phase two ahead into `cur`.
 __device__ __forceinline__ void gemv_body(const Env& e, CPhase& P, int step, int p, WaveState& ws, float inv,
-                                          uint8_t* cur, const float* xs, const float* xsum) {
+                                          uint8_t* cur, const float* xs) {
     const DecodeArgs& a = *e.a;
     const int lane = e.lane;
     mark(e, 0);
@@ -686,7 +669,7 @@ __device__ __forceinline__ void gemv_body(const Env& e, CPhase& P, int step, int
         const uint8_t* cvs = cur + lds_conv(g);  // EP_CONV: conv state / weights of the prefetched rows
         int issued = pre;
         XC X;
-        if (t.nsteps == 1) load_step(xs, xsum, t, 0, X, lane);
+        if (t.nsteps == 1) load_step(xs, t, 0, X, lane);
         asm volatile("" ::"v"(X.x[0]), "v"(X.x[31]));
         mark(e, 1);
         const int ns = g.nm - 1;  // log2(rows per output): 0 or 1 (SwiGLU)
@@ -713,11 +696,11 @@ __device__ __forceinline__ void gemv_body(const Env& e, CPhase& P, int step, int
             float acc[8];
 #pragma unroll
             for (int r = 0; r < 8; r++) acc[r] = 0.0f;
-            if (nr == 1) rows_dot<1>(t, P.gshift, cur, roff, soff, xs, xsum, X, lane, acc);
-            else if (nr == 2) rows_dot<2>(t, P.gshift, cur, roff, soff, xs, xsum, X, lane, acc);
-            else if (nr <= 4) rows_dot<4>(t, P.gshift, cur, roff, soff, xs, xsum, X, lane, acc);
-            else if (nr <= 6) rows_dot<6>(t, P.gshift, cur, roff, soff, xs, xsum, X, lane, acc);
-            else rows_dot<8>(t, P.gshift, cur, roff, soff, xs, xsum, X, lane, acc);
+            if (nr == 1) rows_dot<1>(t, P.gshift, cur, roff, soff, xs, X, lane, acc);
+            else if (nr == 2) rows_dot<2>(t, P.gshift, cur, roff, soff, xs, X, lane, acc);
+            else if (nr <= 4) rows_dot<4>(t, P.gshift, cur, roff, soff, xs, X, lane, acc);
+            else if (nr <= 6) rows_dot<6>(t, P.gshift, cur, roff, soff, xs, X, lane, acc);
+            else rows_dot<8>(t, P.gshift, cur, roff, soff, xs, X, lane, acc);
             if (o0 == 0) {
                 asm volatile("" ::"v"(acc[0]), "v"(acc[1]), "v"(acc[7]));
                 mark(e, 2);
@@ -1167,8 +1150,6 @@ __device__ __forceinline__ void decode_program(const DecodeArgs& a) {
     __shared__ float red[2 * kNW];
     __shared__ uint32_t redi[kNW];
     __shared__ float rope[2 * 64];  // cos, sin of the step's RoPE angles
-    __shared__ float xsum[8 * 64];  // sums of the staged input's lane slices, per step
-    __shared__ float rnh[64];       // GDN output norm: 1/rms per head
     __shared__ int bail;
     Env e;
     e.a = &a;
@@ -1254,8 +1235,7 @@ __device__ __forceinline__ void decode_program(const DecodeArgs& a) {
                     if (head_fast(P)) {
                         head_phase(e, P, ws, inv);
                     } else {
-                        stage_post(xs, P, make_step(P), xsum, rnh);
-                        gemv_body(e, P, step, p, ws, inv, region(rh), xs, xsum);
+                        gemv_body(e, P, step, p, ws, inv, region(rh), xs);
                     }
                     break;
                 }
