@@ -33,6 +33,9 @@
 //    64 dims) with the sigmoid gate;
 //  - the LM head tracks a per-wave argmax; workgroups publish their best and every workgroup
 //    reduces all of them, so the next step needs no separate broadcast.
+#include <cstddef>
+#include <cstring>
+
 #include "common.hpp"
 #include "decode.hpp"
 #include "gemv.hpp"
@@ -88,6 +91,7 @@ __device__ __forceinline__ void wait_vm(int n) {
 // not change during a launch, so the compiler reads them with scalar loads, which do not wait
 // behind the wave's outstanding weight DMA (vector-memory completion is in order).
 typedef const __attribute__((address_space(4))) Phase CPhase;
+typedef const __attribute__((address_space(4))) PhaseBufs CBufs;
 typedef const __attribute__((address_space(4))) float cfloat;
 
 __device__ __forceinline__ void cbar() { asm volatile("" ::: "memory"); }
@@ -236,10 +240,10 @@ __device__ __forceinline__ int lds_conv(const GemvGeo& g) { return g.nm * g.cap 
 
 // DMA of outputs [o0, o0 + cnt) into slots [slot, slot + cnt). Consecutive outputs are consecutive
 // rows of each of the nm matrices, so each block is one contiguous transfer.
-__device__ __forceinline__ void dma_rows(CPhase& P, const GemvGeo& g, int o0, int cnt, int slot, uint8_t* __restrict__ reg,
-                                         int lane) {
-    const uint8_t* w = (const uint8_t*)P.w;
-    const uint8_t* sz = (const uint8_t*)P.sz;
+__device__ __forceinline__ void dma_rows(CPhase& P, CBufs& B, const GemvGeo& g, int o0, int cnt, int slot,
+                                         uint8_t* __restrict__ reg, int lane) {
+    const uint8_t* w = (const uint8_t*)B.w;
+    const uint8_t* sz = (const uint8_t*)B.sz;
     for (int m = 0; m < g.nm; m++) {
         const size_t row = (size_t)o0 + (size_t)m * P.rows;
         dma_bytes(w + row * g.rb, cnt * g.rb, reg + lds_w(g, slot, m), lane);
@@ -476,7 +480,7 @@ __device__ __forceinline__ bool region_after(const DecodeArgs& a, CPhase& P, int
     int c = 0;
     for (int i = 0; i < 2; i++) {
         if (P.nr[i] < 0) break;
-        if (++c == k) { ns = step; np = P.nr[i]; return true; }
+        if (++c == k) { ns = step; np = p + P.nr[i]; return true; }
     }
     if (a.head_reg >= 0 && p < a.head_reg && head_at(a, step) && ++c == k) { ns = step; np = a.head_reg; return true; }
     if (step + 1 < a.n_steps) {
@@ -493,26 +497,26 @@ __device__ __forceinline__ int split_at(int sp, uint32_t len, int S) { return (i
 // GEMV: the wave's first outputs (rows, then their scale/zero pairs; for the GDN in-projection the
 // conv state and conv weights of those rows after them). GDN: the wave's 512-byte state column.
 // Attention: the K/V rows of the wave's positions, through the block table.
-__device__ __forceinline__ void prefetch(const Env& e, CPhase& P, int step, uint8_t* __restrict__ nxt) {
+__device__ __forceinline__ void prefetch(const Env& e, CPhase& P, CBufs& B, int step, uint8_t* __restrict__ nxt) {
     const DecodeArgs& a = *e.a;
     const int lane = e.lane;
     if (P.kind == PH_GEMV) {
         const GemvGeo g = geo(P);
         const Rows R = part_p(P, e.gwm);
         const int cnt = min(R.n, g.cap);
-        dma_rows(P, g, R.r0, cnt, 0, nxt, lane);
+        dma_rows(P, B, g, R.r0, cnt, 0, nxt, lane);
         if (P.epi == EP_CONV && cnt > 0) {
             // conv state [ch][4] and weights [ch][4] of the prefetched rows, 16 bytes each
             uint8_t* cv = nxt + lds_conv(g);
             const int row = min(R.r0 + lane, P.conv_ch - 1);
             if (lane < cnt) {
-                lds_dma16<false>(P.conv + (size_t)row * 4, cv);
-                lds_dma16<false>(P.conv_w + (size_t)row * 4, cv + 16 * g.cap);
+                lds_dma16<false>(B.conv + (size_t)row * 4, cv);
+                lds_dma16<false>((const float*)B.aux + (size_t)row * 4, cv + 16 * g.cap);
             }
         }
     } else if (P.kind == PH_GDN) {
         const int it = e.wg;
-        const float* rec = P.rec;
+        const float* rec = (const float*)B.w;
         if (it < P.heads * 16) {
             const int h = it / 16, t = (it % 16) * 8 + e.wave;
             // state column t of head h: S[h][t][0..127] (value-major), 512 bytes
@@ -536,8 +540,8 @@ __device__ __forceinline__ void prefetch(const Env& e, CPhase& P, int step, uint
                 const int pp = p0 + 2 * (e.wave + kNW * u) + half;
                 if (bid[u] >= 0) {
                     const size_t at = (((size_t)bid[u] * nkv + g) * kBlk + pp % kBlk) * kHeadDim + 8 * li;
-                    lds_dma16<false>(P.kp + at, nxt + u * 2048);
-                    lds_dma16<false>(P.vp + at, nxt + u * 2048 + 1024);
+                    lds_dma16<false>((const uint16_t*)B.w + at, nxt + u * 2048);
+                    lds_dma16<false>((const uint16_t*)B.sz + at, nxt + u * 2048 + 1024);
                 }
             }
         }
@@ -547,11 +551,11 @@ __device__ __forceinline__ void prefetch(const Env& e, CPhase& P, int step, uint
 // ---- phases ----
 
 // Waits for the GEMV input vector and stages it in xs (times the RMSNorm gain); returns 1/rms (or 1).
-__device__ __forceinline__ float gemv_input(const Env& e, CPhase& P, int step, int p, const Ctl& c) {
+__device__ __forceinline__ float gemv_input(const Env& e, CPhase& P, CBufs& B, int step, int p, const Ctl& c) {
     const DecodeArgs& a = *e.a;
     if (P.xin == XI_EMBED) return e.red[2 * kNW - 1];  // staged with the embedding row
     const uint32_t tag = tag_of(a, step, p - P.in_rel);
-    const uint64_t* in = P.in + (size_t)(step & 1) * P.in_stride;
+    const uint64_t* in = B.in + (size_t)(step & 1) * P.in_stride;
     float ss = 0.0f;
     float* xs = e.xs;
     const bool norm = P.xnorm == XN_NORM;
@@ -564,7 +568,7 @@ __device__ __forceinline__ float gemv_input(const Env& e, CPhase& P, int step, i
 #pragma unroll
         for (int j = 0; j < kPoll; j++) {
             const int q = j * kT + (int)threadIdx.x;
-            gn[j] = 2 * q < P.in_n ? *(const float2*)(P.gain + 2 * q) : make_float2(1.0f, 1.0f);
+            gn[j] = 2 * q < P.in_n ? *(const float2*)(B.gain + 2 * q) : make_float2(1.0f, 1.0f);
         }
     }
     poll_pairs(in, P.in_cap, (P.in_n + 1) / 2, tag, [](int q) { return 2 * q; },
@@ -600,7 +604,7 @@ __device__ __forceinline__ float gemv_input(const Env& e, CPhase& P, int step, i
 // hidden). Two rows are computed while the next two load; the register file, not the LDS region,
 // holds the bytes in flight.
 template <int KIND, int K>
-__device__ __forceinline__ void head_rows(const Env& e, CPhase& P, WaveState& ws, float inv, const Rows& R,
+__device__ __forceinline__ void head_rows(const Env& e, CPhase& P, CBufs& B, WaveState& ws, float inv, const Rows& R,
                                           const float* __restrict__ xs) {
     const DecodeArgs& a = *e.a;
     const int lane = e.lane;
@@ -611,11 +615,11 @@ __device__ __forceinline__ void head_rows(const Env& e, CPhase& P, WaveState& ws
     constexpr int NB = 2;
     RowRaw<KIND, K> cur[NB], nxt[NB];
 #pragma unroll
-    for (int k = 0; k < NB; k++) load_row<KIND, K, 64>(cur[k], P.w, P.sz, R.r0 + min(k, R.n - 1), lane);
+    for (int k = 0; k < NB; k++) load_row<KIND, K, 64>(cur[k], B.w, (const uint32_t*)B.sz, R.r0 + min(k, R.n - 1), lane);
     for (int i = 0; i < R.n; i += NB) {
         if (i + NB < R.n) {
 #pragma unroll
-            for (int k = 0; k < NB; k++) load_row<KIND, K, 64>(nxt[k], P.w, P.sz, R.r0 + min(i + NB + k, R.n - 1), lane);
+            for (int k = 0; k < NB; k++) load_row<KIND, K, 64>(nxt[k], B.w, (const uint32_t*)B.sz, R.r0 + min(i + NB + k, R.n - 1), lane);
         }
 #pragma unroll
         for (int k = 0; k < NB; k++) {
@@ -631,17 +635,17 @@ __device__ __forceinline__ void head_rows(const Env& e, CPhase& P, WaveState& ws
     }
 }
 
-__device__ __forceinline__ void head_phase(const Env& e, CPhase& P, WaveState& ws, float inv) {
+__device__ __forceinline__ void head_phase(const Env& e, CPhase& P, CBufs& B, WaveState& ws, float inv) {
     const Rows R = part_p(P, e.gwm);
     if (R.n == 0) return;
     if (P.mkind == 0) {
-        if (P.k == 512) head_rows<KIND_F16, 512>(e, P, ws, inv, R, e.xs);
-        else if (P.k == 1024) head_rows<KIND_F16, 1024>(e, P, ws, inv, R, e.xs);
-        else head_rows<KIND_F16, 2048>(e, P, ws, inv, R, e.xs);
+        if (P.k == 512) head_rows<KIND_F16, 512>(e, P, B, ws, inv, R, e.xs);
+        else if (P.k == 1024) head_rows<KIND_F16, 1024>(e, P, B, ws, inv, R, e.xs);
+        else head_rows<KIND_F16, 2048>(e, P, B, ws, inv, R, e.xs);
     } else {
-        if (P.k == 512) head_rows<KIND_Q4, 512>(e, P, ws, inv, R, e.xs);
-        else if (P.k == 1024) head_rows<KIND_Q4, 1024>(e, P, ws, inv, R, e.xs);
-        else head_rows<KIND_Q4, 2048>(e, P, ws, inv, R, e.xs);
+        if (P.k == 512) head_rows<KIND_Q4, 512>(e, P, B, ws, inv, R, e.xs);
+        else if (P.k == 1024) head_rows<KIND_Q4, 1024>(e, P, B, ws, inv, R, e.xs);
+        else head_rows<KIND_Q4, 2048>(e, P, B, ws, inv, R, e.xs);
     }
 }
 
@@ -650,7 +654,7 @@ __device__ __forceinline__ void head_phase(const Env& e, CPhase& P, WaveState& w
 // refilled as groups finish). Outputs are computed in groups of up to 8 rows (8 / nm outputs): for
 // every step of x, the step's slice is read from LDS once and applied to the whole group, then the
 // group is reduced together. The caller then sends the data of the region phase two ahead into `cur`.
-__device__ __forceinline__ void gemv_body(const Env& e, CPhase& P, int step, int p, WaveState& ws, float inv,
+__device__ __forceinline__ void gemv_body(const Env& e, CPhase& P, CBufs& B, int step, int p, WaveState& ws, float inv,
                                           uint8_t* cur, const float* xs) {
     const DecodeArgs& a = *e.a;
     const int lane = e.lane;
@@ -660,7 +664,7 @@ __device__ __forceinline__ void gemv_body(const Env& e, CPhase& P, int step, int
     const Rows R = part_p(P, e.gwm);
     if (R.n > 0) {
         const uint32_t tag = tag_of(a, step, p);
-        uint64_t* out = P.out ? P.out + (size_t)(step & 1) * P.out_stride : nullptr;
+        uint64_t* out = B.out ? B.out + (size_t)(step & 1) * P.out_stride : nullptr;
         const Step t = make_step(P);
         const int gmax = 8 / g.nm;  // outputs per group
         const int pre = min(R.n, g.cap);  // outputs prefetched
@@ -706,7 +710,7 @@ __device__ __forceinline__ void gemv_body(const Env& e, CPhase& P, int step, int
                 mark(e, 2);
             }
             // refill the group's slots with the outputs cap further on
-            for (int i = 0; i < ng && issued < R.n; i++, issued++) dma_rows(P, g, R.r0 + issued, 1, issued % g.cap, cur, lane);
+            for (int i = 0; i < ng && issued < R.n; i++, issued++) dma_rows(P, B, g, R.r0 + issued, 1, issued % g.cap, cur, lane);
             const float tot = reduce8(acc, lane) * inv;   // lanes 8r..8r+7: row r of the group
             const float up = __shfl_down(tot, 8, kWave);  // SwiGLU: the up row of the output
             const int r = lane >> 3;
@@ -735,11 +739,11 @@ __device__ __forceinline__ void gemv_body(const Env& e, CPhase& P, int step, int
                         st = *(const float4*)(cvs + 16 * k);
                         cw = *(const float4*)(cvs + 16 * g.cap + 16 * k);
                     } else {
-                        st = *(const float4*)(P.conv + (size_t)o * 4);
-                        cw = *(const float4*)(P.conv_w + (size_t)o * 4);
+                        st = *(const float4*)(B.conv + (size_t)o * 4);
+                        cw = *(const float4*)((const float*)B.aux + (size_t)o * 4);
                     }
                     const float cv = st.x * cw.x + st.y * cw.y + st.z * cw.z + tot * cw.w;
-                    float* sp = P.conv + (size_t)o * 4;
+                    float* sp = B.conv + (size_t)o * 4;
                     sp[0] = st.y; sp[1] = st.z; sp[2] = tot;
                     y = silu(cv);
                 }
@@ -757,11 +761,11 @@ __device__ __forceinline__ void gemv_body(const Env& e, CPhase& P, int step, int
 
 // The inputs of GDN item `it` (head h, value columns 8cb..8cb+7): q_h, k_h (64 pairs each), v and
 // z of the 8 columns (4 pairs each), a_h and b_h; staged at xs[0..276).
-__device__ __forceinline__ void gdn_input(const Env& e, CPhase& P, int step, int p, int it, const Ctl& c) {
+__device__ __forceinline__ void gdn_input(const Env& e, CPhase& P, CBufs& B, int step, int p, int it, const Ctl& c) {
     const DecodeArgs& a = *e.a;
     const int H = P.heads, h = it / 16, cb = it % 16;
     const uint32_t tin = tag_of(a, step, p - P.in_rel);
-    const uint64_t* in = P.in + (size_t)(step & 1) * P.in_stride;
+    const uint64_t* in = B.in + (size_t)(step & 1) * P.in_stride;
     const int qa = h * kDK, ka = H * kDK + h * kDK, va = 2 * H * kDK + h * kDK + cb * 8;
     const int za = 3 * H * kDK + h * kDK + cb * 8, aa = 4 * H * kDK + h, ba = 4 * H * kDK + H + h;
     float* xs = e.xs;
@@ -784,17 +788,17 @@ __device__ __forceinline__ void gdn_input(const Env& e, CPhase& P, int step, int
 // Gated DeltaNet step (kernels/src/shaders.rs:436-520 after the conv): workgroup = (head, 8 value
 // columns), wave = one value column t, lane = keys 2l, 2l+1 of the value-major state column.
 // The first item's inputs are staged by gdn_input and its state column is in `cur`.
-__device__ __forceinline__ void gdn_body(const Env& e, CPhase& P, int step, int p, const Ctl& c, const uint8_t* cur,
+__device__ __forceinline__ void gdn_body(const Env& e, CPhase& P, CBufs& B, int step, int p, const Ctl& c, const uint8_t* cur,
                                          const float* xs, float* red) {
     const DecodeArgs& a = *e.a;
     wait_all();  // the state column (issued two region phases ago) is in
     const int H = P.heads, lane = e.lane;
     const uint32_t tag = tag_of(a, step, p);
-    uint64_t* out = P.out + (size_t)(step & 1) * P.out_stride;
-    cfloat* prm = (cfloat*)P.gain;
+    uint64_t* out = B.out + (size_t)(step & 1) * P.out_stride;
+    cfloat* prm = (cfloat*)B.gain;
     for (int it = e.wg; it < H * 16; it += e.nwg) {
         if (it != e.wg) {
-            gdn_input(e, P, step, p, it, c);
+            gdn_input(e, P, B, step, p, it, c);
             if (*e.bail) break;
         }
         const int h = it / 16, cb = it % 16;
@@ -804,7 +808,7 @@ __device__ __forceinline__ void gdn_body(const Env& e, CPhase& P, int step, int 
         const float2 k2 = *(const float2*)(xs + 128 + 2 * lane);
         const float v = xs[256 + e.wave], z = xs[264 + e.wave];
         const float av = xs[272 + (aa & 1)], bv = xs[274 + (ba & 1)];
-        float* Sg = P.rec + ((size_t)h * kDK + t) * kDK + 2 * lane;
+        float* Sg = (float*)B.w + ((size_t)h * kDK + t) * kDK + 2 * lane;
         const float2 s = it == e.wg ? *(const float2*)(cur + 8 * lane) : *(const float2*)Sg;
         const float nq = 1.0f / sqrtf(wave_sum_dpp(q2.x * q2.x + q2.y * q2.y) + 1e-6f) * rsqrtf((float)kDK);
         const float nk = 1.0f / sqrtf(wave_sum_dpp(k2.x * k2.x + k2.y * k2.y) + 1e-6f);
@@ -864,7 +868,7 @@ __device__ __forceinline__ void norm_rope4(float (&v)[4], const float* w, const 
 // (kv head g, split sp) over positions [p0, p1) of 0..pos; publishes (max, sum, acc[256]) per
 // q head of the group. The K/V rows prefetched into half `rh` are read from it and the waves'
 // partials merged through it.
-__device__ __forceinline__ void attn_phase(const Env& e, CPhase& P, int step, int p, const Ctl& c, int rh,
+__device__ __forceinline__ void attn_phase(const Env& e, CPhase& P, CBufs& B, int step, int p, const Ctl& c, int rh,
                                            const float* rope) {
     uint8_t* cur = e.regs + e.wave * kWaveLds + rh * kHalf;
     const DecodeArgs& a = *e.a;
@@ -875,8 +879,10 @@ __device__ __forceinline__ void attn_phase(const Env& e, CPhase& P, int step, in
     const uint32_t pos = a.pos0 + (uint32_t)step, len = pos + 1;
     const int p0 = split_at(sp, len, S), p1 = split_at(sp + 1, len, S);
     const uint32_t tin = tag_of(a, step, p - P.in_rel), tag = tag_of(a, step, p);
-    const uint64_t* in = P.in + (size_t)(step & 1) * P.in_stride;
-    uint64_t* out = P.out + (size_t)(step & 1) * P.out_stride;
+    const uint64_t* in = B.in + (size_t)(step & 1) * P.in_stride;
+    uint64_t* out = B.out + (size_t)(step & 1) * P.out_stride;
+    uint16_t* kp = (uint16_t*)B.w;
+    uint16_t* vp = (uint16_t*)B.sz;
     float* xs = e.xs;
     // q of the group's heads -> xs[0, G*256), k -> xs[1024, 1280), v -> xs[1280, 1536)
     const int qa = g * G * kHeadDim, ka = 2 * nq * kHeadDim + g * kHeadDim, va = ka + nkv * kHeadDim;
@@ -899,14 +905,14 @@ __device__ __forceinline__ void attn_phase(const Env& e, CPhase& P, int step, in
         float v[4];
         const float4 f = *(const float4*)(xs + e.wave * kHeadDim + 4 * lane);
         v[0] = f.x; v[1] = f.y; v[2] = f.z; v[3] = f.w;
-        norm_rope4(v, P.gain, a, rope, lane);
+        norm_rope4(v, B.gain, a, rope, lane);
 #pragma unroll
         for (int i = 0; i < 4; i++) qs[e.wave * kHeadDim + 4 * lane + i] = v[i] * kScoreScale;
     } else if (e.wave == G) {
         float v[4];
         const float4 f = *(const float4*)(xs + 1024 + 4 * lane);
         v[0] = f.x; v[1] = f.y; v[2] = f.z; v[3] = f.w;
-        norm_rope4(v, P.gain + kHeadDim, a, rope, lane);
+        norm_rope4(v, B.gain + kHeadDim, a, rope, lane);
         const float4 vv = *(const float4*)(xs + 1280 + 4 * lane);
         const float val[4] = {vv.x, vv.y, vv.z, vv.w};
         uint16_t kh[4], vh[4];
@@ -928,8 +934,8 @@ __device__ __forceinline__ void attn_phase(const Env& e, CPhase& P, int step, in
                 u32x4 kw, vw;
                 kw.x = k01; kw.y = k23; kw.z = nk01; kw.w = nk23;
                 vw.x = v01; vw.y = v23; vw.z = nv01; vw.w = nv23;
-                st16_agent(P.kp + at + 4 * lane, kw);
-                st16_agent(P.vp + at + 4 * lane, vw);
+                st16_agent(kp + at + 4 * lane, kw);
+                st16_agent(vp + at + 4 * lane, vw);
             }
         }
     }
@@ -966,8 +972,8 @@ __device__ __forceinline__ void attn_phase(const Env& e, CPhase& P, int step, in
                 vw = *(const u32x4*)(cur + u * 2048 + 1024 + 16 * lane);
             } else {
                 const size_t at = (((size_t)a.block_table[ps / kBlk] * nkv + g) * kBlk + ps % kBlk) * kHeadDim + 8 * li;
-                kw = *(const u32x4*)(P.kp + at);
-                vw = *(const u32x4*)(P.vp + at);
+                kw = *(const u32x4*)(kp + at);
+                vw = *(const u32x4*)(vp + at);
             }
             kf[0] = lo_h(kw.x); kf[1] = hi_h(kw.x); kf[2] = lo_h(kw.y); kf[3] = hi_h(kw.y);
             kf[4] = lo_h(kw.z); kf[5] = hi_h(kw.z); kf[6] = lo_h(kw.w); kf[7] = hi_h(kw.w);
@@ -1050,16 +1056,16 @@ __device__ __forceinline__ void attn_phase(const Env& e, CPhase& P, int step, in
 
 // Combine of the attention partials: workgroup = (q head h, 64 dims c); times sigmoid(gate).
 static_assert(66 * kMaxSplits + 64 + 64 * kNW + kNW <= kXs, "the combine's staging must fit in xs");
-__device__ __forceinline__ void comb_phase(const Env& e, CPhase& P, int step, int p, const Ctl& c) {
+__device__ __forceinline__ void comb_phase(const Env& e, CPhase& P, CBufs& B, int step, int p, const Ctl& c) {
     const DecodeArgs& a = *e.a;
     const int nq = P.heads, nkv = P.kv_heads, G = nq / nkv, S = P.splits;
     if (e.wg >= nq * 4) return;
     mark(e, 0);
     const int h = e.wg / 4, cq = e.wg % 4, g = h / G, gi = h % G;
     const uint32_t tin = tag_of(a, step, p - P.in_rel), tin2 = tag_of(a, step, p - P.in2_rel), tag = tag_of(a, step, p);
-    const uint64_t* in = P.in + (size_t)(step & 1) * P.in_stride;
-    const uint64_t* in2 = P.in2 + (size_t)(step & 1) * P.in2_stride;
-    uint64_t* out = P.out + (size_t)(step & 1) * P.out_stride;
+    const uint64_t* in = B.in + (size_t)(step & 1) * P.in_stride;
+    const uint64_t* in2 = (const uint64_t*)B.aux + (size_t)(step & 1) * P.in2_stride;
+    uint64_t* out = B.out + (size_t)(step & 1) * P.out_stride;
     float* xs = e.xs;
     // xs: ml[2S] then acc[S][64] then gate[64]
     poll_pairs(in, P.in_cap, S * 33, tin,
@@ -1168,7 +1174,8 @@ __device__ __forceinline__ void decode_program(const DecodeArgs& a) {
     unsigned long long tts[8];
     e.tt = tts;
     Ctl c{a.err, a.spin_limit, &bail};
-    CPhase* prog = (CPhase*)a.prog;
+    CBufs* prog = (CBufs*)a.prog;
+    CPhase* shapes = (CPhase*)a.shapes;
     if (threadIdx.x == 0) bail = 0;
     if (a.trace && e.wg == 0 && threadIdx.x == 0) a.trace[0] = __builtin_amdgcn_s_memrealtime();
     WaveState ws;
@@ -1182,15 +1189,15 @@ __device__ __forceinline__ void decode_program(const DecodeArgs& a) {
     uint32_t token = a.feed ? a.tok[0] : a.ids[0];
     int half = 0;  // half of the next region phase (region phases alternate between the halves)
     // the window's first two region phases (each region phase sends the one two ahead)
-    prefetch(e, prog[a.reg0], 0, region(0));
-    prefetch(e, prog[a.reg1], 0, region(1));
+    prefetch(e, shapes[prog[a.reg0].shape], prog[a.reg0], 0, region(0));
+    prefetch(e, shapes[prog[a.reg1].shape], prog[a.reg1], 0, region(1));
     for (int step = 0; step < a.n_steps; step++) {
         const uint32_t pos = a.pos0 + (uint32_t)step;
         const bool head = head_at(a, step);
         // embedding row (kernels/src/shaders.rs:405-434) times the first layer's input-norm gain,
         // in the layout the first in-projection reads; 1/rms in red[2 kNW - 1]
         {
-            CPhase& P0 = prog[0];
+            CPhase& P0 = shapes[prog[0].shape];
             const Step st0 = make_step(P0);
             if ((int)threadIdx.x < a.rope_dim / 2) {
                 float sn, cs;
@@ -1201,7 +1208,7 @@ __device__ __forceinline__ void decode_program(const DecodeArgs& a) {
             float ss = 0.0f;
             for (int cc = threadIdx.x; cc < a.hidden; cc += kT) {
                 const float v = embed_val(a, token, cc);
-                xs[xs_slot(st0, cc)] = v * P0.gain[cc];
+                xs[xs_slot(st0, cc)] = v * prog[0].gain[cc];
                 ss += v * v;
             }
             ss = wave_sum_dpp(ss);
@@ -1219,7 +1226,8 @@ __device__ __forceinline__ void decode_program(const DecodeArgs& a) {
         ws.best = -INFINITY;
         ws.best_i = 0xFFFFFFFFu;
         for (int p = 0; p < a.nph; p++) {
-            CPhase& P = prog[p];
+            CBufs& B = prog[p];
+            CPhase& P = shapes[B.shape];
             if (P.is_head && !head) continue;
             const int inst = step * a.nph + p;
             const int rh = half;
@@ -1229,32 +1237,32 @@ __device__ __forceinline__ void decode_program(const DecodeArgs& a) {
             }
             switch (P.kind) {
                 case PH_GEMV: {
-                    const float inv = gemv_input(e, P, step, p, c);
+                    const float inv = gemv_input(e, P, B, step, p, c);
                     if (bail) { wait_all(); return; }
                     trace_in(e, inst);
                     if (head_fast(P)) {
-                        head_phase(e, P, ws, inv);
+                        head_phase(e, P, B, ws, inv);
                     } else {
-                        gemv_body(e, P, step, p, ws, inv, region(rh), xs);
+                        gemv_body(e, P, B, step, p, ws, inv, region(rh), xs);
                     }
                     break;
                 }
                 case PH_GDN:
                     mark(e, 0);
-                    if (e.wg < P.heads * 16) gdn_input(e, P, step, p, e.wg, c);
+                    if (e.wg < P.heads * 16) gdn_input(e, P, B, step, p, e.wg, c);
                     mark(e, 1);
                     if (bail) { wait_all(); return; }
                     trace_in(e, inst);
-                    gdn_body(e, P, step, p, c, region(rh), xs, red);
+                    gdn_body(e, P, B, step, p, c, region(rh), xs, red);
                     mark(e, 2);
                     break;
                 case PH_ATTN:
                     trace_in(e, inst);
-                    attn_phase(e, P, step, p, c, rh, rope);
+                    attn_phase(e, P, B, step, p, c, rh, rope);
                     break;
                 default:
                     trace_in(e, inst);
-                    comb_phase(e, P, step, p, c);
+                    comb_phase(e, P, B, step, p, c);
                     break;
             }
             if (bail) { wait_all(); return; }
@@ -1262,7 +1270,7 @@ __device__ __forceinline__ void decode_program(const DecodeArgs& a) {
                 // this phase's LDS reads are done: send the data of the region phase two ahead
                 // into its half (the next region phase's data is in the other half)
                 int ns = 0, np = 0;
-                if (region_after(a, P, step, p, 2, ns, np)) prefetch(e, prog[np], ns, region(rh));
+                if (region_after(a, P, step, p, 2, ns, np)) prefetch(e, shapes[prog[np].shape], prog[np], ns, region(rh));
                 mark(e, 7);
                 half ^= 1;
             }
@@ -1386,9 +1394,45 @@ bool finalize_program(Phase* prog, int nph, DecodeArgs& a) {
         int c = 0;
         prog[p].nr[0] = prog[p].nr[1] = -1;
         for (int q = p + 1; q < nph && c < 2; q++)
-            if (prog[q].region && !prog[q].is_head) prog[p].nr[c++] = q;
+            if (prog[q].region && !prog[q].is_head) prog[p].nr[c++] = q - p;
     }
     return a.reg1 >= 0 && (a.head_reg < 0 || a.head_reg == nph - 1);
+}
+
+void split_program(const Phase* prog, int nph, std::vector<PhaseBufs>& bufs, std::vector<Phase>& shapes) {
+    // the shape is every field before the buffers (all 4-byte fields: no padding inside)
+    constexpr size_t kShapeBytes = offsetof(Phase, w);
+    static_assert(kShapeBytes % 4 == 0, "shape fields are 4-byte");
+    bufs.assign(nph, PhaseBufs());
+    shapes.clear();
+    for (int p = 0; p < nph; p++) {
+        const Phase& P = prog[p];
+        size_t s = 0;
+        while (s < shapes.size() && std::memcmp(&shapes[s], &P, kShapeBytes) != 0) s++;
+        if (s == shapes.size()) {
+            Phase sh;
+            std::memcpy((void*)&sh, (const void*)&P, kShapeBytes);
+            shapes.push_back(sh);
+        }
+        PhaseBufs& b = bufs[p];
+        b.shape = (uint32_t)s;
+        b.gain = P.gain;
+        b.in = P.in;
+        b.out = P.out;
+        if (P.kind == PH_GEMV) {
+            b.w = P.w;
+            b.sz = P.sz;
+            b.aux = P.conv_w;
+            b.conv = P.conv;
+        } else if (P.kind == PH_GDN) {
+            b.w = P.rec;
+        } else if (P.kind == PH_ATTN) {
+            b.w = P.kp;
+            b.sz = P.vp;
+        } else {
+            b.aux = P.in2;
+        }
+    }
 }
 
 hipError_t launch_decode(const DecodeArgs& a, int grid, hipStream_t st) {

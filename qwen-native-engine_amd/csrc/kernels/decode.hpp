@@ -11,6 +11,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <vector>
+
 namespace qne {
 
 enum PhaseKind { PH_GEMV = 0, PH_GDN = 1, PH_ATTN = 2, PH_COMB = 3 };
@@ -28,7 +30,10 @@ constexpr int kMaxPhases = 192;
 constexpr int kHeadDim = 256;  // attention head size the kernel is written for
 constexpr int kMaxSplits = 84;  // attention context splits per kv head (the combine stages 66 floats each, plus its reduction)
 
-// One phase. `variant` selects the compiled GEMV shape (matrix kind and K).
+// One phase. `variant` selects the compiled GEMV shape (matrix kind and K). The integer fields
+// come first: they are the phase's shape, which the kernel reads from a table of distinct shapes
+// (every layer of a kind shares one). The buffers at the end are the host's; the kernel reads them
+// from the phase's PhaseBufs record.
 struct Phase {
     int kind = 0, variant = -1;
     int mkind = 0, k = 0, group = 64, rows = 0;  // GEMV matrix; rows = outputs (SwiGLU: pairs)
@@ -40,17 +45,6 @@ struct Phase {
     int in_rel = 1;     // the input was published `in_rel` phases earlier in the same step
     int in2_rel = 0;    // second input (COMB: the gate in the in-projection output)
     int is_head = 0;    // phase runs only on steps that compute logits
-    const void* w = nullptr;
-    const uint32_t* sz = nullptr;
-    const float* gain = nullptr;    // XN_NORM gain; GDN: dt_bias, A_neg_exp, norm_w; ATTN: q_norm, k_norm
-    const float* conv_w = nullptr;  // EP_CONV [conv_ch][4]
-    float* conv = nullptr;          // EP_CONV state [conv_ch][4] (3 used)
-    float* rec = nullptr;           // GDN state [heads][dv][dk] (value-major)
-    uint16_t* kp = nullptr;         // attention pools [blocks][kv_heads][16][256]
-    uint16_t* vp = nullptr;
-    uint64_t* in = nullptr;         // input exchange buffer (step parity 0; parity 1 at + in_stride)
-    uint64_t* in2 = nullptr;
-    uint64_t* out = nullptr;        // output exchange buffer
     uint32_t in_stride = 0, in2_stride = 0, out_stride = 0;  // u64 entries
     uint32_t in_cap = 0, in2_cap = 0;  // entries readable from in / in2 (bounds of the polling loads)
     // Derived by finalize_phase from the fields above and the launch grid, so the kernel reads
@@ -63,12 +57,41 @@ struct Phase {
     int gshift = 6;     // log2(group)
     int n4 = 0, n2 = 0, n1 = 0, nsteps = 0;  // x steps: 2048/1024/512-column slabs (q4) or 512 (f16)
     int splits = 0;     // attention: context splits per kv head
-    int nr[2] = {-1, -1};  // the next two region phases after this one in the same step (LM head excluded)
+    int nr[2] = {-1, -1};  // the next two region phases after this one in the same step (LM head
+                           // excluded), as distances from this phase; -1: none
+    // buffers
+    const void* w = nullptr;
+    const uint32_t* sz = nullptr;
+    const float* gain = nullptr;    // XN_NORM gain; GDN: dt_bias, A_neg_exp, norm_w; ATTN: q_norm, k_norm
+    const float* conv_w = nullptr;  // EP_CONV [conv_ch][4]
+    float* conv = nullptr;          // EP_CONV state [conv_ch][4] (3 used)
+    float* rec = nullptr;           // GDN state [heads][dv][dk] (value-major)
+    uint16_t* kp = nullptr;         // attention pools [blocks][kv_heads][16][256]
+    uint16_t* vp = nullptr;
+    uint64_t* in = nullptr;         // input exchange buffer (step parity 0; parity 1 at + in_stride)
+    uint64_t* in2 = nullptr;
+    uint64_t* out = nullptr;        // output exchange buffer
 };
 
+// The kernel's per-phase record: the phase's buffers and the index of its shape, in one 64-byte
+// line. The program is read through the scalar data cache at every phase; with the shapes shared
+// between layers, a 2B-sized token's program (about 150 of these plus ~16 shapes) stays resident
+// there instead of missing to L2 on every phase. A slot holds what the phase's kind uses.
+struct PhaseBufs {
+    const void* w = nullptr;     // GEMV rows; GDN recurrent state; attention K pool
+    const void* sz = nullptr;    // GEMV q4 (scale, zero) rows; attention V pool
+    const float* gain = nullptr;
+    const void* aux = nullptr;   // EP_CONV conv weights; combine: the second input
+    float* conv = nullptr;       // EP_CONV conv state
+    uint64_t* in = nullptr;
+    uint64_t* out = nullptr;
+    uint32_t shape = 0, pad = 0;
+};
+static_assert(sizeof(PhaseBufs) == 64, "one scalar-cache line per phase");
 
 struct DecodeArgs {
-    const Phase* prog = nullptr;
+    const PhaseBufs* prog = nullptr;  // per phase
+    const Phase* shapes = nullptr;    // distinct shapes, indexed by PhaseBufs::shape
     int nph = 0;  // phases per token
     // embedding (read by every workgroup at the start of a step)
     const void* emb_w = nullptr;
@@ -120,6 +143,9 @@ void finalize_phase(Phase& P, int grid);
 // Fills the region-phase links of a finalized program (Phase::nr, DecodeArgs::reg0 / reg1 / head_reg).
 // Returns false if a step has fewer than two region phases besides the LM head.
 bool finalize_program(Phase* prog, int nph, DecodeArgs& a);
+// Splits a finalized program into the kernel's tables: one PhaseBufs per phase and the distinct
+// shapes (phases equal in every field before the buffers share one).
+void split_program(const Phase* prog, int nph, std::vector<PhaseBufs>& bufs, std::vector<Phase>& shapes);
 // GEMV shapes compiled into the kernel: variant id of (matrix kind, K), or -1.
 int decode_gemv_variant(int kind, int k);
 hipError_t launch_decode(const DecodeArgs& a, int grid, hipStream_t st);

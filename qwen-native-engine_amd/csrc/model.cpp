@@ -564,14 +564,20 @@ void Model::setup_engine() {
     nph_ = (int)prog.size();
     phase_kind_.clear();
     for (const Phase& P : prog) phase_kind_.push_back(P.kind);
-    Phase* d_prog = (Phase*)dalloc(prog.size() * sizeof(Phase));
-    QNE_HIP(hipMemcpy(d_prog, prog.data(), prog.size() * sizeof(Phase), hipMemcpyHostToDevice));
+    std::vector<PhaseBufs> pbufs;
+    std::vector<Phase> shapes;
+    split_program(prog.data(), (int)prog.size(), pbufs, shapes);
+    PhaseBufs* d_prog = (PhaseBufs*)dalloc(pbufs.size() * sizeof(PhaseBufs));
+    QNE_HIP(hipMemcpy(d_prog, pbufs.data(), pbufs.size() * sizeof(PhaseBufs), hipMemcpyHostToDevice));
+    Phase* d_shapes = (Phase*)dalloc(shapes.size() * sizeof(Phase));
+    QNE_HIP(hipMemcpy(d_shapes, shapes.data(), shapes.size() * sizeof(Phase), hipMemcpyHostToDevice));
     am_ = (uint64_t*)dalloc((size_t)4 * grid * 8);
     QNE_HIP(hipMemset(am_, 0, (size_t)4 * grid * 8));
 
     DecodeArgs* a = new DecodeArgs();
     engine_args_ = a;
     a->prog = d_prog;
+    a->shapes = d_shapes;
     a->nph = nph_;
     a->reg0 = links.reg0; a->reg1 = links.reg1; a->head_reg = links.head_reg;
     a->emb_w = embed_.w; a->emb_sz = embed_.sz; a->emb_kind = embed_.kind; a->emb_group = embed_.group;
