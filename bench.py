@@ -605,6 +605,9 @@ def main():
     ap.add_argument("--stream-workgroups", type=int, default=2048, help="workgroups of the --config stream probe")
     ap.add_argument("--cpu-tokens", type=int, default=4)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--prefill", default="chunk", choices=["chunk", "tokens"],
+                    help="fill the context with prefill_chunk (batched GEMM passes, the default) or with "
+                         "prefill (the persistent token kernel)")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--engine", default="persistent", choices=["persistent", "graph"])
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -653,19 +656,31 @@ def main():
     m = qne.Model.load(index, buf, options={"max_context": 4096, "engine": args.engine})
     rng = np.random.default_rng(args.seed)
     prompt = rng.integers(0, cfg["vocab"], size=args.ctx).astype(np.uint32)
-    assert args.ctx + max(args.steps, args.warmup) <= 4096, "context + steps must fit in 4096"
     t = time.perf_counter()
-    for s in range(0, args.ctx - 1, 512):
-        m.prefill_chunk(prompt[s: min(s + 512, args.ctx - 1)], s, False)
-    prefill_s = time.perf_counter() - t
-    # Snapshot after ctx - 1 tokens. The last prompt token is replayed before each decode run to
-    # set the greedy pick and position, which snapshot/restore do not cover (model.rs:394-414).
-    m.snapshot()
-    if args.warmup:
+    ctx_timed = args.ctx
+    if args.prefill == "tokens":
+        # the whole prompt through the persistent token kernel (Model::prefill, model.rs:324); the
+        # warmup window then runs at ctx and the timed one right after it
+        assert args.ctx + args.warmup + args.steps <= 4096, "context + warmup + steps must fit in 4096"
+        m.prefill(prompt)
+        prefill_s = time.perf_counter() - t
+        if args.warmup:
+            m.decode(args.warmup + 1, args.warmup, [])
+        ctx_timed = args.ctx + args.warmup
+    else:
+        assert args.ctx + max(args.steps, args.warmup) <= 4096, "context + steps must fit in 4096"
+        for s in range(0, args.ctx - 1, 512):
+            m.prefill_chunk(prompt[s: min(s + 512, args.ctx - 1)], s, False)
+        prefill_s = time.perf_counter() - t
+        # Snapshot after ctx - 1 tokens. The last prompt token is replayed before each decode run
+        # to set the greedy pick and position, which snapshot/restore do not cover
+        # (model.rs:394-414).
+        m.snapshot()
+        if args.warmup:
+            m.prefill_chunk(prompt[-1:], args.ctx - 1, True)
+            m.decode(args.warmup + 1, args.warmup, [])
+            m.restore()
         m.prefill_chunk(prompt[-1:], args.ctx - 1, True)
-        m.decode(args.warmup + 1, args.warmup, [])
-        m.restore()
-    m.prefill_chunk(prompt[-1:], args.ctx - 1, True)
     # decode() returns after its stream has drained, so the wall clock brackets the device work
     t0 = time.perf_counter()
     ids = m.decode(args.steps + 1, args.steps, [])
@@ -673,7 +688,7 @@ def main():
     dev_ms, dev_steps = m.last_decode_timing()
     assert dev_steps == args.steps and len(ids) == args.steps + 1
     tok_s = args.steps / wall
-    bytes_tok = algorithmic_bytes_per_token(cfg, mats, args.ctx + (args.steps - 1) / 2)
+    bytes_tok = algorithmic_bytes_per_token(cfg, mats, ctx_timed + (args.steps - 1) / 2)
     # one k_decode launch covers the whole timed window: bytes per launch / launch duration
     achieved = bytes_tok["total"] * args.steps / (dev_ms / 1e3) / 1e9
     traffic = profiled_traffic(args.steps) if args.ctx == 4000 and args.config == "2b" else None
@@ -693,7 +708,8 @@ def main():
         "data": "synthetic",
         "config": {"workload": f"Qwen3.5-{args.config.upper()}-shaped hybrid decoder, "
                                f"{'f16' if small else 'int4 g64'} body, f16 embed/lm_head, "
-                               f"batch 1 greedy decode after a {args.ctx}-token prefill",
+                               f"batch 1 greedy decode after a {args.ctx}-token prefill"
+                               + (" (token kernel)" if args.prefill == "tokens" else ""),
                    "layers": cfg["layers"], "hidden": cfg["hidden"], "vocab": cfg["vocab"], "ctx": args.ctx,
                    "batch": 1, "window": args.steps},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
