@@ -106,10 +106,15 @@ int qne_max_context(qne_model* m, uint32_t* out);
 int qne_profile_token(qne_model* m, double* ms);
 /* Model::profile_token -- model.rs:305 (per-label sums of Gpu::profile, kernels/src/lib.rs:366-396):
  * consumes one greedy token with the device timeline of the persistent decode kernel on and writes
- * NUL-terminated JSON {"total_ms", "labels": {label: ms}, "work_ms": {...}, "barrier_ms": {...},
- * "phases": [[label, slowest work ms, fastest work ms, barrier ms], ...]} into buf. Labels are
- * gdn.* / attn.* per layer phase and lm_head. QNE_EINVAL if cap is too small (the message names
- * the size) or the model was loaded with the graph engine. Diagnostic only. */
+ * NUL-terminated JSON into buf: "total_ms", "tick_ms" (the timestamp unit); "labels" (label -> span
+ * ms, summed over layers), "compute_median_ms", "handover_median_ms", and "phases" (per phase:
+ * label, span, compute median / max, hand-over median / max); "sub_step_names" and
+ * "sub_steps_median_ms" (per label, the medians of each phase kind's sub-steps); "chain" (per
+ * phase: label, input-staged and published median / max, in ms after the previous phase's last
+ * publish); and per phase and workgroup, in ticks after that same instant (-1: not recorded),
+ * "publish_ticks", "input_ticks" and "sub_ticks" (the 8 sub-step timestamps). Labels are gdn.* /
+ * attn.* per layer phase and lm_head. QNE_EINVAL if cap is too small (the message names the size)
+ * or the model was loaded with the graph engine. Diagnostic only; about 2 MB for the 2B model. */
 int qne_profile_token_json(qne_model* m, char* buf, size_t cap);
 /* Device time (HIP events on the model's stream) of the windows of the last qne_decode call, in
  * ms, and the number of decode steps they ran; the counterpart of timing a submission with

@@ -123,10 +123,12 @@ __device__ __forceinline__ void put(uint64_t* buf, uint32_t i, float v, uint32_t
                        __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// 16 bytes of K or V stored with an agent-scope (write-through) store.
-__device__ __forceinline__ void st16_agent(uint16_t* p, u32x4 v) {
-    const rsrc_t r = make_rsrc(p, 16);
-    __builtin_amdgcn_raw_buffer_store_b128(v, r, 0, 0, kSC1);
+// 16 bytes of K or V stored with an agent-scope (write-through) store at byte `off` of a 512-byte
+// row. `row` is the same in every lane: one buffer resource serves the wave, so the store is one
+// instruction (a resource that differs between lanes makes the compiler loop over them).
+__device__ __forceinline__ void st16_agent(uint16_t* row, uint32_t off, u32x4 v) {
+    const rsrc_t r = make_rsrc(row, 2 * kHeadDim);
+    __builtin_amdgcn_raw_buffer_store_b128(v, r, off, 0, kSC1);
 }
 
 struct Ctl {
@@ -934,8 +936,8 @@ __device__ __forceinline__ void attn_phase(const Env& e, CPhase& P, CBufs& B, in
                 u32x4 kw, vw;
                 kw.x = k01; kw.y = k23; kw.z = nk01; kw.w = nk23;
                 vw.x = v01; vw.y = v23; vw.z = nv01; vw.w = nv23;
-                st16_agent(kp + at + 4 * lane, kw);
-                st16_agent(vp + at + 4 * lane, vw);
+                st16_agent(kp + at, 8 * lane, kw);
+                st16_agent(vp + at, 8 * lane, vw);
             }
         }
     }

@@ -931,6 +931,7 @@ std::string Model::profile_token_json() {
     // critical chain: per phase, when each workgroup had its input staged and when it had
     // published, relative to the previous phase's last publish (sub-step slots per kind)
     std::string chain = "[";
+    std::string pubs = "[", ins = "[", subt = "[";
     unsigned long long pub_prev = 0;
     std::map<std::string, std::vector<double>> sub_l;
     std::string phases = "[";
@@ -989,6 +990,33 @@ std::string Model::profile_token_json() {
                     tpub.push_back((double)((long long)q[pub_slot] - (long long)pub_prev) * tick_ms);
                 }
             }
+            {
+                // every workgroup's publish time relative to the previous phase's last publish,
+                // in ticks (-1: not recorded), for the analysis of which workgroups are late
+                pubs += pubs.size() > 1 ? ",[" : "[";
+                ins += ins.size() > 1 ? ",[" : "[";
+                for (int w = 0; w < grid; w++) {
+                    const unsigned long long* q = sub.data() + 8 * ((size_t)b * grid + w);
+                    const long long d = pub_prev && q[pub_slot] ? (long long)q[pub_slot] - (long long)pub_prev : -1;
+                    const long long di = pub_prev && q[in_slot] ? (long long)q[in_slot] - (long long)pub_prev : -1;
+                    pubs += (w ? "," : "") + std::to_string(d);
+                    ins += (w ? "," : "") + std::to_string(di);
+                }
+                pubs += "]";
+                ins += "]";
+                // and every workgroup's sub-step timestamps (slots 0..7, same origin; -1: none)
+                subt += subt.size() > 1 ? ",[" : "[";
+                for (int w = 0; w < grid; w++) {
+                    const unsigned long long* q = sub.data() + 8 * ((size_t)b * grid + w);
+                    subt += w ? ",[" : "[";
+                    for (int k2 = 0; k2 < 8; k2++) {
+                        const long long d = pub_prev && q[k2] ? (long long)q[k2] - (long long)pub_prev : -1;
+                        subt += (k2 ? "," : "") + std::to_string(d);
+                    }
+                    subt += "]";
+                }
+                subt += "]";
+            }
             if (!tin.empty()) {
                 char buf[224];
                 std::snprintf(buf, sizeof buf, "%s[\"%s\",%.5f,%.5f,%.5f,%.5f]", chain.size() > 1 ? "," : "", label.c_str(),
@@ -1043,7 +1071,7 @@ std::string Model::profile_token_json() {
            ",\"phase_columns\":[\"label\",\"span\",\"compute_median\",\"compute_max\",\"handover_median\",\"handover_max\"]" +
            ",\"phases\":" + phases +
            ",\"chain_columns\":[\"label\",\"input_median\",\"input_max\",\"published_median\",\"published_max\"]" +
-           ",\"chain\":" + chain + "]}";
+           ",\"chain\":" + chain + "]" + ",\"publish_ticks\":" + pubs + "],\"input_ticks\":" + ins + "],\"sub_ticks\":" + subt + "]}";
 }
 
 }  // namespace qne

@@ -242,7 +242,7 @@ class Model:
     def profile_token_detail(self) -> dict:
         """Model::profile_token (model.rs:305) with the per-phase timeline: consumes one greedy token."""
         import json
-        buf = ctypes.create_string_buffer(1 << 20)
+        buf = ctypes.create_string_buffer(16 << 20)
         self._c(self._lib.qne_profile_token_json(self._h, buf, len(buf)))
         return json.loads(buf.value.decode())
 
