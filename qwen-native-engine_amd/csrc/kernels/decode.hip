@@ -1189,6 +1189,10 @@ __device__ __forceinline__ void decode_program(const DecodeArgs& a) {
     bar();
 
     uint32_t token = a.feed ? a.tok[0] : a.ids[0];
+    // ids appended so far (tok[2]); only workgroup 0's thread 0 writes it during a launch, so it
+    // is read once, here, before any prefetch: a load at the end of each step would complete only
+    // behind that wave's prefetch of the next step, and the workgroup would start every step late
+    uint32_t n_out = a.out_ids && e.wg == 0 && threadIdx.x == 0 ? a.tok[2] : 0u;
     int half = 0;  // half of the next region phase (region phases alternate between the halves)
     // the window's first two region phases (each region phase sends the one two ahead)
     prefetch(e, shapes[prog[a.reg0].shape], prog[a.reg0], 0, region(0));
@@ -1334,9 +1338,8 @@ __device__ __forceinline__ void decode_program(const DecodeArgs& a) {
                 a.tok[0] = pick;
                 a.tok[1] = pos + 1;
                 if (a.out_ids) {
-                    const uint32_t n = a.tok[2];
-                    if (n < a.out_cap) a.out_ids[n] = pick;
-                    a.tok[2] = n + 1;
+                    if (n_out < a.out_cap) a.out_ids[n_out] = pick;
+                    a.tok[2] = ++n_out;
                 }
             }
             token = pick;
