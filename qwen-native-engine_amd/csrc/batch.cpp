@@ -29,7 +29,7 @@ int attn_splits_for(int max_blocks) {
 int operand_order(const DevMat& W) { return W.kind == KIND_Q4 ? 1 : 0; }
 
 void rows_gemm(const DevMat& W, int n, float eps, uint8_t* frag, int norm, float* part, float* y, int y_stride, int epi,
-               uint8_t* frag_out, const float* gain_out, int order_out, hipStream_t st) {
+               uint8_t* frag_out, const float* gain_out, int order_out, hipStream_t st, int row_tiles) {
     GemmArgs a;
     a.m = n;
     a.frag = frag;
@@ -41,7 +41,7 @@ void rows_gemm(const DevMat& W, int n, float eps, uint8_t* frag, int norm, float
     a.N = W.rows;
     a.K = W.k;
     a.group = W.group;
-    a.splits = gemm_splits(W.kind, W.rows, W.k, W.group);
+    a.splits = gemm_splits(W.kind, W.rows, W.k, W.group, row_tiles);
     a.part = part;
     a.epi = epi;
     a.y = y;
@@ -62,7 +62,9 @@ void rows_shapes_check(const ModelConfig& c) {
                                  "1, 2 or 4 query heads per kv head, hidden and intermediate multiples of 64)");
 }
 
-void rows_workspace(const std::vector<DevLayer>& layers, const DevMat& head, size_t* part_floats, size_t* frag_bytes) {
+void rows_workspace(const std::vector<DevLayer>& layers, const DevMat& head, int rows, int row_tiles, size_t* part_floats,
+                    size_t* frag_bytes) {
+    const size_t rpad = (size_t)(rows + 63) / 64 * 64;
     size_t part = 0, frag = 0;
     // layer GEMMs write partials even with one split (their reduce stages the next operand); the
     // LM head only when it has more than one
@@ -70,9 +72,9 @@ void rows_workspace(const std::vector<DevLayer>& layers, const DevMat& head, siz
         if (!gemm_shape_ok(W.kind, W.rows, W.k, W.group, 1) || W.k % 4 != 0)
             throw Error(QNE_EFORMAT, "unsupported matrix shape for the batched GEMM (k must be a multiple of 64, "
                                      "q4 groups a multiple of 64)");
-        const int s = gemm_splits(W.kind, W.rows, W.k, W.group);
-        if (layer || s > 1) part = std::max(part, (size_t)s * kRowsMax * W.rows);
-        frag = std::max(frag, gemm_frag_bytes(W.k));
+        const int s = gemm_splits(W.kind, W.rows, W.k, W.group, row_tiles);
+        if (layer || s > 1) part = std::max(part, (size_t)s * rpad * W.rows);
+        frag = std::max(frag, gemm_frag_bytes(W.k, rows));
     };
     for (const DevLayer& L : layers)
         for (const DevMat* W : {&L.in, &L.out, &L.gate_up, &L.down}) need(*W, true);
@@ -100,7 +102,7 @@ BatchDecoder::BatchDecoder(Model& m, int max_rows, int max_context) : m_(m), max
     const ModelConfig& c = m.cfg_;
     rows_shapes_check(c);
     size_t part = 0, frag = 0;
-    rows_workspace(m.layers_, m.lm_head_, &part, &frag);
+    rows_workspace(m.layers_, m.lm_head_, kRowsMax, 1, &part, &frag);
     QNE_HIP(hipSetDevice(m.device_));
     QNE_HIP(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking));
     QNE_HIP(hipEventCreate(&ev0_));

@@ -16,18 +16,20 @@
 
 namespace qne {
 
-// One GEMM of a pass over up to 64 rows (a batched decode step or a prefill chunk), with its
-// reduce: W applied to the x operand staged in `frag` (norm: its rows carry a deferred RMSNorm),
+// One GEMM of a pass over up to 512 rows (a batched decode step of up to 64, or a prefill pass),
+// with its reduce, the split count chosen for row_tiles tiles of 64 rows: W applied to the x operand staged in `frag` (norm: its rows carry a deferred RMSNorm),
 // epilogue into y, and with frag_out the result staged for the next GEMM (times gain_out).
 void rows_gemm(const DevMat& W, int n, float eps, uint8_t* frag, int norm, float* part, float* y, int y_stride,
-               int epi, uint8_t* frag_out, const float* gain_out, int order_out, hipStream_t st);
+               int epi, uint8_t* frag_out, const float* gain_out, int order_out, hipStream_t st, int row_tiles = 1);
 // 1 when a GEMM on W takes its x operand in the q4 column order.
 int operand_order(const DevMat& W);
 // Throws QNE_EFORMAT unless the model's shapes fit the batched kernels.
 void rows_shapes_check(const ModelConfig& c);
-// Scratch of the GEMMs of a pass over the layers: split partials (floats) and one staged x
-// operand (bytes). Throws when a matrix shape is not supported by the batched GEMM.
-void rows_workspace(const std::vector<DevLayer>& layers, const DevMat& head, size_t* part_floats, size_t* frag_bytes);
+// Scratch of the GEMMs of a pass of up to `rows` rows over the layers, with the split counts of
+// gemm_splits(..., row_tiles): split partials (floats) and one staged x operand (bytes). Throws
+// when a matrix shape is not supported by the batched GEMM.
+void rows_workspace(const std::vector<DevLayer>& layers, const DevMat& head, int rows, int row_tiles, size_t* part_floats,
+                    size_t* frag_bytes);
 
 class BatchDecoder {
   public:

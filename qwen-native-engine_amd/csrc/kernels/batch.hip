@@ -80,21 +80,26 @@ __device__ __forceinline__ int frag_offset(int s, int mt, int lane) { return ((s
 // Writes one value of the x operand of a GEMM: row r, column c, value v (times gain g). The 64
 // lanes of the calling wave hold the 64 columns of one chunk of row r (all lanes call it), so the
 // chunk's sums of hi + lo and of v^2 are wave sums. q4order: the column order of the q4 GEMM's B
-// operand within each 8 columns, [0, 4, 1, 5, 2, 6, 3, 7] (nibbles8); else natural.
-__device__ __forceinline__ void emit_x(uint8_t* __restrict__ frag, int r, int c, float v, float g, int q4order, int lane) {
+// operand within each 8 columns, [0, 4, 1, 5, 2, 6, 3, 7] (nibbles8); else natural. Rows come in
+// tiles of 64: tile r / 64 of the operand starts tile_bytes (the K / 64 chunks of one tile) after
+// the previous one.
+__device__ __forceinline__ void emit_x(uint8_t* __restrict__ frag, size_t tile_bytes, int r, int c, float v, float g,
+                                       int q4order, int lane) {
     const float xg = v * g;
     const float hi = (float)(_Float16)xg;
     const float lo = (float)(_Float16)(xg - hi);
     const int chunk = c / kChunk, kk = c % kChunk, hf = kk / 32, st = (kk % 32) / 8, i = kk % 8;
     const int slot = q4order ? 2 * (i % 4) + i / 4 : i;
-    uint8_t* dst = frag + (size_t)chunk * kChunkBytes + frag_offset(st, r >> 5, 32 * hf + (r & 31)) + 2 * slot;
+    const int rr = r & (kBM - 1);
+    uint8_t* tile = frag + (size_t)(r / kBM) * tile_bytes + (size_t)chunk * kChunkBytes;
+    uint8_t* dst = tile + frag_offset(st, rr >> 5, 32 * hf + (rr & 31)) + 2 * slot;
     *(uint16_t*)dst = __builtin_bit_cast(uint16_t, (_Float16)hi);
     *(uint16_t*)(dst + kFragBytes) = __builtin_bit_cast(uint16_t, (_Float16)lo);
     const float xs = wave_sum_dpp(hi + lo), ss = wave_sum_dpp(v * v);
     if (lane == 0) {
-        float* sums = (float*)(frag + (size_t)chunk * kChunkBytes);
-        sums[kXsumOff / 4 + r] = xs;
-        sums[kSsOff / 4 + r] = ss;
+        float* sums = (float*)tile;
+        sums[kXsumOff / 4 + rr] = xs;
+        sums[kSsOff / 4 + rr] = ss;
     }
 }
 
@@ -102,26 +107,30 @@ __device__ __forceinline__ void emit_x(uint8_t* __restrict__ frag, int r, int c,
 // its output: y = (1 / rms) W (x * gain)). Called by every thread of a 256-thread workgroup.
 __device__ __forceinline__ float row_inv_rms(const uint8_t* __restrict__ frag, int nchunks, int K, float eps, int r,
                                              float* red) {
+    const uint8_t* tile = frag + (size_t)(r / kBM) * nchunks * kChunkBytes;
     float ss = 0.0f;
-    for (int c = threadIdx.x; c < nchunks; c += 256) ss += ((const float*)(frag + (size_t)c * kChunkBytes))[kSsOff / 4 + r];
+    for (int c = threadIdx.x; c < nchunks; c += 256) ss += ((const float*)(tile + (size_t)c * kChunkBytes))[kSsOff / 4 + (r & (kBM - 1))];
     ss = block_sum(ss, red);
     return 1.0f / sqrtf(ss / (float)K + eps);
 }
 
-// Grid (ceil(K / 256), 64): the x operand of a GEMM from f32 rows (x + r * x_stride; rows >= m are
-// zero), times `gain` when set; the row's RMSNorm factor is applied by the GEMM's epilogue.
+// Grid (ceil(K / 256), rows rounded up to 64): the x operand of a GEMM from f32 rows
+// (x + r * x_stride; rows >= m are zero), times `gain` when set; the row's RMSNorm factor is applied
+// by the GEMM's epilogue.
 __global__ __launch_bounds__(256) void k_stage_x(const float* __restrict__ x, int x_stride, int m, int K,
                                                  const float* __restrict__ gain, int q4order, uint8_t* __restrict__ frag) {
     const int c = blockIdx.x * 256 + threadIdx.x, r = blockIdx.y;
     if (blockIdx.x * 256 >= K) return;  // whole workgroup; K is a multiple of 64, so waves are whole chunks
     if ((threadIdx.x & ~63) + blockIdx.x * 256 >= K) return;  // whole wave
     const float v = r < m ? x[(size_t)r * x_stride + c] : 0.0f;
-    emit_x(frag, r, c, v, gain ? gain[c] : 1.0f, q4order, threadIdx.x & 63);
+    emit_x(frag, (size_t)(K / kChunk) * kChunkBytes, r, c, v, gain ? gain[c] : 1.0f, q4order, threadIdx.x & 63);
 }
 
-// Grid (ceil(N / (32 WAVES)), splits); split s covers chunks [s * cps, (s + 1) * cps). Wave w owns
-// W rows 32 (WAVES blockIdx.x + w) .. + 31. The chunks stream through a ring of D LDS slots, each
-// holding one x chunk and every wave's W chunk; D - 1 chunks are in flight while one is computed.
+// Grid (ceil(N / (32 WAVES)), splits, row tiles); split s covers chunks [s * cps, (s + 1) * cps) of
+// the x rows 64 blockIdx.z .. + 63. Wave w owns W rows 32 (WAVES blockIdx.x + w) .. + 31. The chunks
+// stream through a ring of D LDS slots, each holding one x chunk and every wave's W chunk; D - 1
+// chunks are in flight while one is computed. The row tiles of one W tile read the same W chunks,
+// which the MALL serves after the first.
 template <int KIND, int WAVES, int D>
 __global__ __launch_bounds__(64 * WAVES) void k_gemm(const GemmArgs a) {
     constexpr int kWBytes = KIND == KIND_Q4 ? 1024 + 128 : 4096;  // one wave's W chunk (q4: + scale/zero words)
@@ -138,10 +147,12 @@ __global__ __launch_bounds__(64 * WAVES) void k_gemm(const GemmArgs a) {
     const int ngroups = nchunks / cpg;
     const int c0 = blockIdx.y * a.cps, c1 = min(nchunks, c0 + a.cps);
     const int nch = max(0, c1 - c0);
+    const int mt = blockIdx.z;  // row tile
+    const uint8_t* xfrag = a.frag + (size_t)mt * nchunks * kChunkBytes;
 
     auto issue = [&](int j, int slot) {
         uint8_t* base = ring[slot];
-        const uint8_t* src = a.frag + (size_t)(c0 + j) * kChunkBytes;
+        const uint8_t* src = xfrag + (size_t)(c0 + j) * kChunkBytes;
 #pragma unroll
         for (int u = 0; u < kXPart / 1024; u++) dma16(src + kXPart * w + 1024 * u + 16 * lane, base + kXPart * w + 1024 * u);
         constexpr int kSumLanes = kBM * 4 / 16 / WAVES;  // lanes copying the chunk sums (16 B each)
@@ -228,7 +239,7 @@ __global__ __launch_bounds__(64 * WAVES) void k_gemm(const GemmArgs a) {
     }
     if (!a.direct) {
         if (n >= a.N) return;
-        float* pp = a.part + (size_t)blockIdx.y * kBM * a.N + n;
+        float* pp = a.part + ((size_t)blockIdx.y * a.mpad + (size_t)kBM * mt) * a.N + n;
 #pragma unroll
         for (int j = 0; j < 16; j++) {
             const int m = 8 * (j / 4) + 4 * hf + (j % 4);
@@ -243,7 +254,7 @@ __global__ __launch_bounds__(64 * WAVES) void k_gemm(const GemmArgs a) {
     if (a.norm) {
         if (threadIdx.x < kBM) {
             float ss = 0.0f;
-            for (int c = 0; c < nchunks; c++) ss += ((const float*)(a.frag + (size_t)c * kChunkBytes))[kSsOff / 4 + threadIdx.x];
+            for (int c = 0; c < nchunks; c++) ss += ((const float*)(xfrag + (size_t)c * kChunkBytes))[kSsOff / 4 + threadIdx.x];
             sinv[threadIdx.x] = 1.0f / sqrtf(ss / (float)K + a.eps);
         }
     } else if (threadIdx.x < kBM) {
@@ -251,16 +262,17 @@ __global__ __launch_bounds__(64 * WAVES) void k_gemm(const GemmArgs a) {
     }
     __syncthreads();
     if (n >= a.N) return;
+    const int rows = a.m - kBM * mt;  // rows of this tile
 #pragma unroll
     for (int j = 0; j < 16; j++) {
         const int m = 8 * (j / 4) + 4 * hf + (j % 4);
-        if (m < a.m) {
-            float* d = a.y + (size_t)m * a.y_stride + n;
+        if (m < rows) {
+            float* d = a.y + (size_t)(kBM * mt + m) * a.y_stride + n;
             const float v = acc0[j] * sinv[m];
             *d = a.epi == EPI_ACCUMULATE ? *d + v : v;
         }
-        if (32 + m < a.m) {
-            float* d = a.y + (size_t)(32 + m) * a.y_stride + n;
+        if (32 + m < rows) {
+            float* d = a.y + (size_t)(kBM * mt + 32 + m) * a.y_stride + n;
             const float v = acc1[j] * sinv[32 + m];
             *d = a.epi == EPI_ACCUMULATE ? *d + v : v;
         }
@@ -282,7 +294,7 @@ __global__ __launch_bounds__(256) void k_gemm_reduce(const GemmArgs a) {
     if (live) {
         float g = 0.0f, u = 0.0f;
         const float* p = a.part + (size_t)r * a.N + c;
-        const size_t ss = (size_t)kBM * a.N;  // between splits
+        const size_t ss = (size_t)a.mpad * a.N;  // between splits
         // every split's load in flight at once (up to kSplitsInFlight), then the sum in split order
         constexpr int kSplitsInFlight = 24;
         const bool swiglu = a.epi == EPI_SWIGLU;
@@ -312,7 +324,9 @@ __global__ __launch_bounds__(256) void k_gemm_reduce(const GemmArgs a) {
         else v = silu(g) * u;
         if (d) *d = v;
     }
-    if (a.frag_out) emit_x(a.frag_out, r, c, v, a.gain_out ? a.gain_out[live ? c : 0] : 1.0f, a.order_out, threadIdx.x & 63);
+    if (a.frag_out)
+        emit_x(a.frag_out, (size_t)(a.n_out / kChunk) * kChunkBytes, r, c, v, a.gain_out ? a.gain_out[live ? c : 0] : 1.0f,
+               a.order_out, threadIdx.x & 63);
 }
 
 // h[r] = embedding row tokens[r] (f16 row, or q4 values (q - z) s), shaders.rs:405-434 per row.
@@ -334,7 +348,7 @@ __global__ __launch_bounds__(256) void k_embed_rows(int kind, const void* __rest
         v = ((float)((word >> (4 * (c % 8))) & 15u) - hi_h(sz)) * lo_h(sz);
     }
     h[(size_t)r * hidden + c] = v;
-    if (frag) emit_x(frag, r, c, v, gain ? gain[c] : 1.0f, q4order, threadIdx.x & 63);
+    if (frag) emit_x(frag, (size_t)(hidden / kChunk) * kChunkBytes, r, c, v, gain ? gain[c] : 1.0f, q4order, threadIdx.x & 63);
 }
 
 // Greedy pick of every logits row (argmax_partial / argmax_final, shaders.rs:635-699): the largest
@@ -417,10 +431,10 @@ __global__ __launch_bounds__(64) void k_argmax_final(const float* __restrict__ p
 // CU) beat 4 waves by 8-20 % including the reduce.
 static int gemm_waves(int kind, int N) { return kind == KIND_Q4 || N > 4096 ? 8 : 4; }
 
-int gemm_splits(int kind, int N, int K, int group) {
+int gemm_splits(int kind, int N, int K, int group, int row_tiles) {
     (void)group;
     const int waves = gemm_waves(kind, N);
-    const int tiles = (N + 32 * waves - 1) / (32 * waves);
+    const int tiles = (N + 32 * waves - 1) / (32 * waves) * std::max(1, row_tiles);
     const int nch = K / kChunk;
     // as many splits as keep the grid within one workgroup per CU (a second one on a CU shares its
     // chunk throughput), at least 2 chunks per split, at most 24 (the reduce reads every split's
@@ -432,28 +446,30 @@ int gemm_splits(int kind, int N, int K, int group) {
 }
 
 bool gemm_shape_ok(int kind, int N, int K, int group, int m) {
-    if (m < 1 || m > kBM || N < 1 || K < kChunk || K % kChunk != 0) return false;
+    if (m < 1 || m > kGemmRowsMax || N < 1 || K < kChunk || K % kChunk != 0) return false;
     if (kind == KIND_Q4 && (group < kChunk || group % kChunk != 0 || K % group != 0)) return false;
     return true;
 }
 
-size_t gemm_frag_bytes(int K) { return (size_t)(K / kChunk) * kChunkBytes; }
+size_t gemm_frag_bytes(int K, int m) { return (size_t)((m + kBM - 1) / kBM) * (K / kChunk) * kChunkBytes; }
 
 void launch_stage_x(const float* x, int x_stride, int m, int K, const float* gain, int q4order, uint8_t* frag,
                     hipStream_t st) {
-    hipLaunchKernelGGL(k_stage_x, dim3((K + 255) / 256, kBM), dim3(256), 0, st, x, x_stride, m, K, gain, q4order, frag);
+    const int mpad = (m + kBM - 1) / kBM * kBM;
+    hipLaunchKernelGGL(k_stage_x, dim3((K + 255) / 256, mpad), dim3(256), 0, st, x, x_stride, m, K, gain, q4order, frag);
 }
 
 void launch_gemm(GemmArgs a, hipStream_t st) {
     const int nch = a.K / kChunk;
     a.cps = (nch + a.splits - 1) / a.splits;
+    a.mpad = (a.m + kBM - 1) / kBM * kBM;
     a.direct = a.splits == 1 && a.epi != EPI_SWIGLU && !a.frag_out;
     if (a.x) {  // stage the x operand here (RMSNorm gain folded in, 1 / rms deferred to the epilogue)
         launch_stage_x(a.x, a.x_stride, a.m, a.K, a.gain, a.kind == KIND_Q4 ? 1 : 0, a.frag, st);
         a.norm = a.gain ? 1 : 0;
     }
     const int waves = gemm_waves(a.kind, a.N);
-    const dim3 grid((a.N + 32 * waves - 1) / (32 * waves), a.splits);
+    const dim3 grid((a.N + 32 * waves - 1) / (32 * waves), a.splits, a.mpad / kBM);
     if (a.kind == KIND_Q4) {
         // 3 chunk slots (77.6 KiB): deeper rings measured slower, and two workgroups fit a CU
         hipLaunchKernelGGL((k_gemm<KIND_Q4, 8, 3>), grid, dim3(512), 0, st, a);

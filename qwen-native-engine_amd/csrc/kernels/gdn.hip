@@ -7,6 +7,8 @@
 // touching 256 contiguous bytes per load. S^T k and S^T q are 32-term register dot products
 // merged across quarters through LDS. The multi-token kernel keeps the tile in registers across
 // all tokens of the launch.
+#include <algorithm>
+
 #include "common.hpp"
 #include "launch.hpp"
 
@@ -348,12 +350,25 @@ __global__ __launch_bounds__(384) void k_gdn_chunk_post(const float* __restrict_
 
 void launch_gdn_chunk(const float* proj, int proj_stride, float* conv_state, const float* conv_w, float* state,
                       const float* prm, int heads, int tokens, float* q, float* k, float* v, float* g, float* beta,
-                      float* o, float* mixed, int mixed_stride, hipStream_t st) {
+                      float* o, float* mixed, int mixed_stride, hipStream_t st, int lead, float* wy_ws) {
     hipLaunchKernelGGL(k_gdn_chunk_prep, dim3(tokens, heads), dim3(384), 0, st, proj, proj_stride, conv_state, conv_w,
                        prm, heads, q, k, v, g, beta);
     const int waves = heads * (kDV / 4);
-    hipLaunchKernelGGL(k_delta_rule_cols, dim3((waves + 3) / 4), dim3(256), 0, st, q, k, v, beta, g, state, o, tokens,
-                       heads, waves, 1);
+    const size_t hk = (size_t)heads * kDK;  // floats of q, k, v, o per token
+    // tokens [t0, t0 + n) in order on the state, one wave per 4 value columns
+    auto sequential = [&](int t0, int n) {
+        if (n > 0)
+            hipLaunchKernelGGL(k_delta_rule_cols, dim3((waves + 3) / 4), dim3(256), 0, st, q + t0 * hk, k + t0 * hk,
+                               v + t0 * hk, beta + (size_t)t0 * heads, g + (size_t)t0 * heads, state, o + t0 * hk, n,
+                               heads, waves, 1);
+    };
+    const int head = wy_ws ? std::min(std::max(lead, 0), tokens) : tokens;
+    const int blocks = wy_ws ? (tokens - head) / 64 : 0;
+    sequential(0, head);
+    if (blocks > 0)
+        launch_delta_rule_wy(q + head * hk, k + head * hk, v + head * hk, beta + (size_t)head * heads,
+                             g + (size_t)head * heads, state, o + head * hk, 1, 64 * blocks, heads, wy_ws, st, 1);
+    sequential(head + 64 * blocks, tokens - head - 64 * blocks);
     hipLaunchKernelGGL(k_gdn_chunk_post, dim3(tokens, heads), dim3(384), 0, st, proj, proj_stride, conv_state, prm,
                        heads, tokens, o, mixed, mixed_stride);
 }

@@ -270,7 +270,7 @@ constexpr int kSW = 0, kSU = 8192, kSP = 12288, kSQ = 16384, kSK = 24576, kSL = 
 // 16 of those columns. Per chunk: D = U - W S, O = diag(gamma) Q S + P D, S = gamma_63 S + Kf D.
 __global__ __launch_bounds__(256) void k_wy_chain(const float* __restrict__ q, const float* __restrict__ ws,
                                                   float* __restrict__ state, float* __restrict__ out, int T, int H,
-                                                  int BH) {
+                                                  int BH, int value_major) {
     __shared__ __attribute__((aligned(16))) float sm[kSFloats];
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, lr = lane & 15, lg = lane >> 4;
     const int id = blockIdx.x, xcd = id & 7, slot = id >> 3;
@@ -318,12 +318,14 @@ __global__ __launch_bounds__(256) void k_wy_chain(const float* __restrict__ q, c
         }
     };
 
+    // state entry (key j, value column col): [dk][dv], or the model's value-major [dv][dk]
     float* S0 = state + (size_t)bh * kD * kD;
+    auto sidx = [&](int j) { return value_major ? (size_t)col * kD + j : (size_t)j * kD + col; };
     f4 S[8];
 #pragma unroll
     for (int kt = 0; kt < 8; kt++)
 #pragma unroll
-        for (int r = 0; r < 4; r++) S[kt][r] = S0[(16 * kt + 4 * lg + r) * kD + col];
+        for (int r = 0; r < 4; r++) S[kt][r] = S0[sidx(16 * kt + 4 * lg + r)];
     // the state loads complete before the first copies are counted
     wait_vm<0>();
     issue_wul(0);
@@ -425,7 +427,7 @@ __global__ __launch_bounds__(256) void k_wy_chain(const float* __restrict__ q, c
 #pragma unroll
     for (int kt = 0; kt < 8; kt++)
 #pragma unroll
-        for (int r = 0; r < 4; r++) S0[(16 * kt + 4 * lg + r) * kD + col] = S[kt][r];
+        for (int r = 0; r < 4; r++) S0[sidx(16 * kt + 4 * lg + r)] = S[kt][r];
 }
 
 }  // namespace
@@ -435,10 +437,12 @@ size_t wy_workspace_bytes(int batch, int tokens, int heads) {
 }
 
 void launch_delta_rule_wy(const float* q, const float* k, const float* v, const float* beta, const float* g,
-                          float* state, float* out, int batch, int tokens, int heads, float* ws, hipStream_t st) {
+                          float* state, float* out, int batch, int tokens, int heads, float* ws, hipStream_t st,
+                          int value_major) {
     const int NC = (tokens + kC - 1) / kC, BH = batch * heads;
     hipLaunchKernelGGL(k_wy_prep, dim3(NC, heads, batch), dim3(256), 0, st, q, k, v, beta, g, ws, tokens, heads);
-    hipLaunchKernelGGL(k_wy_chain, dim3(16 * ((BH + 7) / 8)), dim3(256), 0, st, q, ws, state, out, tokens, heads, BH);
+    hipLaunchKernelGGL(k_wy_chain, dim3(16 * ((BH + 7) / 8)), dim3(256), 0, st, q, ws, state, out, tokens, heads, BH,
+                       value_major);
 }
 
 }  // namespace qne

@@ -53,8 +53,10 @@ void launch_delta_rule_chunked(const float* q, const float* k, const float* v, c
                                float* state, float* out, int batch, int tokens, int heads, hipStream_t st);
 // The delta rule over T tokens in the chunk-64 WY form on MFMA; ws holds wy_workspace_bytes.
 size_t wy_workspace_bytes(int batch, int tokens, int heads);
+// value_major: the state is the model's [B][H][dv][dk] instead of [B][H][dk][dv].
 void launch_delta_rule_wy(const float* q, const float* k, const float* v, const float* beta, const float* g,
-                          float* state, float* out, int batch, int tokens, int heads, float* ws, hipStream_t st);
+                          float* state, float* out, int batch, int tokens, int heads, float* ws, hipStream_t st,
+                          int value_major = 0);
 
 // Attention decode, model form: q/k RMSNorm + RoPE, f16 append at tok[1], split-context partials,
 // combine with the sigmoid gate into `out`.
@@ -101,19 +103,26 @@ struct GdnRowStrides {
 // Prefill of `tokens` consecutive tokens of one sequence: conv + norms + gates, the recurrence on
 // the model's value-major state, the gated RMSNorm into mixed + n * mixed_stride, the conv state
 // shifted by the chunk. q, k, v, o: tokens * heads * 128 floats of scratch; g, beta: tokens * heads.
+// With wy_ws (wy_workspace_bytes(1, tokens, heads)), the recurrence runs in the chunk-64 WY form
+// over every complete block of 64 tokens that starts `lead` tokens in or 64 k after that, and
+// sequentially over the tokens before and after them: with lead = the tokens up to the next
+// multiple of 64 positions, the blocks are fixed by absolute position.
 void launch_gdn_chunk(const float* proj, int proj_stride, float* conv_state, const float* conv_w, float* state,
                       const float* prm, int heads, int tokens, float* q, float* k, float* v, float* g, float* beta,
-                      float* o, float* mixed, int mixed_stride, hipStream_t st);
+                      float* o, float* mixed, int mixed_stride, hipStream_t st, int lead = 0, float* wy_ws = nullptr);
 void launch_gdn_decode_rows(const float* proj, float* conv_state, const float* conv_w, float* state, float* out,
                             const float* prm, int heads, int rows, const GdnRowStrides& rs, hipStream_t st);
 
-// y = x W^T for up to 64 rows of x (batched decode), on MFMA. The x operand is staged in `frag`
-// (gemm_frag_bytes(K)): with x set, launch_gemm stages rows x + r * x_stride (times `gain`, the
+// y = x W^T for up to kGemmRowsMax rows of x (batched decode: up to 64; chunked prefill: a pass of
+// tokens), on MFMA, in tiles of 64 rows. The x operand is staged in `frag` (gemm_frag_bytes(K, m)):
+// with x set, launch_gemm stages rows x + r * x_stride (times `gain`, the
 // RMSNorm's 1 / rms then applied to the output: norm); with x null, `frag` already holds the
 // operand and `norm` says whether its rows carry a deferred RMSNorm. Epilogues as the GEMV (store,
 // residual add, SwiGLU with n_out = N / 2); y may be null when frag_out is set. With frag_out the
 // result (times gain_out, column order order_out) is also staged as the next GEMM's x operand.
-// `part` holds splits * 64 * N floats unless the GEMM applies the epilogue itself.
+// `part` holds splits * mpad * N floats (mpad: m rounded up to 64) unless the GEMM applies the
+// epilogue itself. The split count depends on the matrix only (gemm_splits), so a row's sums are
+// added in the same order whatever the number of rows.
 struct GemmArgs {
     const float* x = nullptr;
     int x_stride = 0;
@@ -128,6 +137,7 @@ struct GemmArgs {
     int N = 0, K = 0, group = 64;
     int splits = 1;
     int cps = 0;     // set by launch_gemm: chunks per split
+    int mpad = 0;    // set by launch_gemm: m rounded up to a multiple of 64 (rows of the partials)
     int direct = 0;  // set by launch_gemm: the GEMM applies the epilogue itself
     float* part = nullptr;
     int epi = EPI_STORE;
@@ -159,8 +169,12 @@ constexpr uint32_t kSampleMaxK = 1024;
 size_t sample_scratch_bytes();
 void launch_sample(const SampleArgs& a, void* scratch, hipStream_t st);
 
-size_t gemm_frag_bytes(int K);
-int gemm_splits(int kind, int N, int K, int group);
+constexpr int kGemmRowsMax = 512;
+size_t gemm_frag_bytes(int K, int m);
+// Split-K count of a GEMM on an N x K matrix: as many splits as keep a grid of N tiles x row_tiles
+// x splits within one workgroup per CU (at least 2 chunks per split, at most 24). A caller passes a
+// fixed row_tiles (not the rows of the call), so that a row's sums do not depend on the call.
+int gemm_splits(int kind, int N, int K, int group, int row_tiles = 1);
 bool gemm_shape_ok(int kind, int N, int K, int group, int m);
 void launch_gemm(GemmArgs a, hipStream_t st);
 // The x operand of a GEMM from f32 rows (rows >= m zero), times gain when set.

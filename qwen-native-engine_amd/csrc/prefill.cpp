@@ -22,7 +22,7 @@ ChunkPrefill::ChunkPrefill(Model& m) : m_(m), st_(m.stream_) {
     const ModelConfig& c = m.cfg_;
     rows_shapes_check(c);
     size_t part = 0, frag = 0;
-    rows_workspace(m.layers_, m.lm_head_, &part, &frag);
+    rows_workspace(m.layers_, m.lm_head_, kChunk, kRowTiles, &part, &frag);
     try {
         const size_t T = kChunk;
         proj_w_ = std::max(c.attn_proj(), c.gdn_proj());
@@ -48,6 +48,7 @@ ChunkPrefill::ChunkPrefill(Model& m) : m_(m), st_(m.stream_) {
         go_ = (float*)dalloc(hk * 4);
         gg_ = (float*)dalloc(T * c.gdn_heads * 4);
         gb_ = (float*)dalloc(T * c.gdn_heads * 4);
+        wy_ws_ = (float*)dalloc(wy_workspace_bytes(1, (int)T, c.gdn_heads));
         frag_a_ = (uint8_t*)dalloc(frag);
         frag_b_ = (uint8_t*)dalloc(frag);
         QNE_HIP(hipMemset(frag_a_, 0, frag));
@@ -73,14 +74,14 @@ void ChunkPrefill::release() {
 
 // The tokens of one chunk (ids_, positions pos_) through every layer: the same graph as a batched
 // decode step (BatchDecoder::enqueue_step) with the rows being consecutive tokens of one sequence.
-void ChunkPrefill::enqueue_chunk(int n) {
+void ChunkPrefill::enqueue_chunk(int n, int lead) {
     const ModelConfig& c = m_.cfg_;
     const DevLayer& first = m_.layers_.front();
     launch_embed_rows(m_.embed_.kind, m_.embed_.w, m_.embed_.sz, m_.embed_.group, c.hidden, ids_, n, h_, frag_a_,
                       first.input_norm, operand_order(first.in), st_);
     auto gemm = [&](const DevMat& W, uint8_t* frag, int norm, float* y, int y_stride, int epi, uint8_t* frag_out,
                     const float* gain_out, int order_out) {
-        rows_gemm(W, n, c.eps, frag, norm, part_, y, y_stride, epi, frag_out, gain_out, order_out, st_);
+        rows_gemm(W, n, c.eps, frag, norm, part_, y, y_stride, epi, frag_out, gain_out, order_out, st_, kRowTiles);
     };
     const int max_blocks = (m_.max_context_ + 15) / 16;
     for (size_t li = 0; li < m_.layers_.size(); li++) {
@@ -111,7 +112,7 @@ void ChunkPrefill::enqueue_chunk(int n) {
             launch_attention_rows(a, st_);
         } else {
             launch_gdn_chunk(proj_, proj_w_, L.conv_state, L.conv_w, L.rec, L.gdn_params, c.gdn_heads, n, gq_, gk_, gv_,
-                             gg_, gb_, go_, mixed_, L.out.k, st_);
+                             gg_, gb_, go_, mixed_, L.out.k, st_, lead, wy_ws_);
         }
         launch_stage_x(mixed_, L.out.k, n, L.out.k, nullptr, operand_order(L.out), frag_b_, st_);
         gemm(L.out, frag_b_, 0, h_, c.hidden, EPI_ACCUMULATE, frag_a_, L.post_norm, operand_order(L.gate_up));
@@ -123,14 +124,15 @@ void ChunkPrefill::enqueue_chunk(int n) {
     }
 }
 
-hipGraphExec_t ChunkPrefill::graph_for(int n) {
-    auto it = graphs_.find(n);
+hipGraphExec_t ChunkPrefill::graph_for(int n, int lead) {
+    const int key = n * 64 + lead;
+    auto it = graphs_.find(key);
     if (it != graphs_.end()) return it->second;
     hipGraph_t g = nullptr;
     hipGraphExec_t e = nullptr;
     QNE_HIP(hipStreamBeginCapture(st_, hipStreamCaptureModeThreadLocal));
     try {
-        enqueue_chunk(n);
+        enqueue_chunk(n, lead);
     } catch (...) {
         (void)hipStreamEndCapture(st_, &g);
         if (g) (void)hipGraphDestroy(g);
@@ -139,7 +141,7 @@ hipGraphExec_t ChunkPrefill::graph_for(int n) {
     QNE_HIP(hipStreamEndCapture(st_, &g));
     QNE_HIP(hipGraphInstantiate(&e, g, nullptr, nullptr, 0));
     (void)hipGraphDestroy(g);
-    graphs_[n] = e;
+    graphs_[key] = e;
     return e;
 }
 
@@ -153,7 +155,10 @@ void ChunkPrefill::run(const uint32_t* ids_dev, size_t n, uint32_t start, bool f
         for (int i = 0; i < t; i++) host_pos_[i] = (int32_t)(start + off + i);
         QNE_HIP(hipMemcpyAsync(pos_, host_pos_, t * 4, hipMemcpyHostToDevice, st_));
         QNE_HIP(hipMemcpyAsync(ids_, ids_dev + off, t * 4, hipMemcpyDeviceToDevice, st_));
-        QNE_HIP(hipGraphLaunch(graph_for(t), st_));
+        // tokens until the next multiple of 64 positions: the GDN blocks after them are fixed by
+        // absolute position, so calls cut at multiples of 64 give the same bits
+        const int lead = (int)((64 - (start + off) % 64) % 64);
+        QNE_HIP(hipGraphLaunch(graph_for(t, lead), st_));
         last = t;
     }
     if (finish_logits) {

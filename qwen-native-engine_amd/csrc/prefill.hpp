@@ -1,9 +1,11 @@
 // Chunked prefill on the batched GEMM: Model::prefill_chunk (kernels/src/model.rs:349-372) runs
-// the prompt 64 tokens per pass, as the reference's prefill_batched runs 16 (kernels/src/batch.rs).
-// A chunk's tokens are the rows of one pass through the layers: every projection is one MFMA GEMM
-// over the chunk, attention appends the chunk's K/V and each token attends positions up to its own
-// (causal by construction), and the GDN recurrence runs over the chunk's tokens in order on the
-// model's state. The LM head runs on the last token only.
+// the prompt up to 512 tokens per pass, as the reference's prefill_batched runs 16
+// (kernels/src/batch.rs). A pass's tokens are the rows of one pass through the layers: every
+// projection is one MFMA GEMM over the pass (in tiles of 64 rows, so the weights stream once per
+// pass), attention appends the pass's K/V and each token attends positions up to its own (causal by
+// construction), and the GDN recurrence runs over the pass's tokens in order on the model's state.
+// The LM head runs on the last token only. The GEMMs' split counts are fixed for the model (those
+// of a full pass), so a token's result does not depend on how the prompt is cut into calls.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -18,7 +20,8 @@ namespace qne {
 
 class ChunkPrefill {
   public:
-    static constexpr int kChunk = 64;
+    static constexpr int kChunk = 512;              // tokens per pass
+    static constexpr int kRowTiles = kChunk / 64;   // the GEMMs' split counts are chosen for this
     explicit ChunkPrefill(Model& m);
     ~ChunkPrefill();
     ChunkPrefill(const ChunkPrefill&) = delete;
@@ -31,13 +34,15 @@ class ChunkPrefill {
   private:
     void release();
     void* dalloc(size_t bytes);
-    void enqueue_chunk(int n);
-    hipGraphExec_t graph_for(int n);
+    // one pass of n tokens whose first `lead` tokens end at a multiple of 64 positions (the GDN
+    // recurrence runs the whole 64-position blocks after them in the WY form)
+    void enqueue_chunk(int n, int lead);
+    hipGraphExec_t graph_for(int n, int lead);
 
     Model& m_;
     hipStream_t st_;
     std::vector<void*> allocations_;
-    std::map<int, hipGraphExec_t> graphs_;
+    std::map<int, hipGraphExec_t> graphs_;  // by n * 64 + lead
     int proj_w_ = 0, mixed_w_ = 0, splits_ = 1;
     uint32_t* ids_ = nullptr;  // the chunk's token ids
     int32_t* pos_ = nullptr;   // the chunk's positions
@@ -45,6 +50,7 @@ class ChunkPrefill {
     float *h_ = nullptr, *proj_ = nullptr, *mixed_ = nullptr, *qbuf_ = nullptr, *part_ = nullptr;
     float *attn_ml_ = nullptr, *attn_acc_ = nullptr;
     float *gq_ = nullptr, *gk_ = nullptr, *gv_ = nullptr, *go_ = nullptr, *gg_ = nullptr, *gb_ = nullptr;
+    float* wy_ws_ = nullptr;  // the WY form's per-chunk operands
     uint8_t *frag_a_ = nullptr, *frag_b_ = nullptr;
 };
 

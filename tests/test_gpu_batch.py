@@ -60,6 +60,22 @@ def test_gemm_matches_oracle(k, kind, group, epi, norm, M):
 
 
 @pytest.mark.parametrize("kind,group", [(Q.MAT_Q4, 64), (Q.MAT_F16, 0)])
+@pytest.mark.parametrize("epi", [Q.EPI_STORE, Q.EPI_SWIGLU])
+@pytest.mark.parametrize("M", [65, 200])
+def test_gemm_row_tiles_match_oracle(kind, group, epi, M):
+    """More than 64 rows run as tiles of 64 rows (the prefill's passes), each over the same weights;
+    a ragged last tile."""
+    rows = 2 * 150 if epi == Q.EPI_SWIGLU else 300
+    got, want = run_gemm(kind, group, rows, 1024, M, epi, True, seed=41 + M + 5 * epi + group)
+    assert rel_err(got, want) < 2e-5
+
+
+def test_gemm_full_pass_of_512_rows():
+    got, want = run_gemm(Q.MAT_Q4, 64, 256, 512, 512, Q.EPI_ACCUMULATE, True, seed=77)
+    assert rel_err(got, want) < 2e-5
+
+
+@pytest.mark.parametrize("kind,group", [(Q.MAT_Q4, 64), (Q.MAT_F16, 0)])
 def test_gemm_one_split_direct_epilogue(kind, group):
     """More than 512 tiles of 128 rows: one split, the GEMM applies 1 / rms and the epilogue itself
     (the LM head's path)."""
@@ -86,12 +102,19 @@ def test_gemm_row_result_does_not_depend_on_other_rows():
     Q.gemm(Q.MAT_Q4, dw.data_ptr(), dsz.data_ptr(), rows, k, 64, dx.data_ptr(), k, 64, full.data_ptr(), rows)
     dx1 = to_dev(X[37:38])
     Q.gemm(Q.MAT_Q4, dw.data_ptr(), dsz.data_ptr(), rows, k, 64, dx1.data_ptr(), k, 1, one.data_ptr(), rows)
+    # and in the fourth row tile of a 250-row call
+    X4 = rng.normal(size=(250, k)).astype(np.float32)
+    X4[237] = X[37]
+    big = D.zeros((250, rows), np.float32)
+    dx4 = to_dev(X4)
+    Q.gemm(Q.MAT_Q4, dw.data_ptr(), dsz.data_ptr(), rows, k, 64, dx4.data_ptr(), k, 250, big.data_ptr(), rows)
     D.sync()
     assert np.array_equal(full.numpy()[37], one.numpy()[0])
+    assert np.array_equal(big.numpy()[237], one.numpy()[0])
 
 
 def test_gemm_rejects_bad_shapes():
-    for args in [(Q.MAT_F16, 0, 256, 1000, 4), (Q.MAT_Q4, 32, 256, 1024, 4), (Q.MAT_F16, 0, 256, 1024, 65),
+    for args in [(Q.MAT_F16, 0, 256, 1000, 4), (Q.MAT_Q4, 32, 256, 1024, 4), (Q.MAT_F16, 0, 256, 1024, 513),
                  (Q.MAT_F16, 0, 256, 1024, 0)]:
         kind, group, rows, k, M = args
         with pytest.raises(Q.QneError) as e:

@@ -159,23 +159,31 @@ def test_token_prefill_equals_chunked_prefill(pair):
 
 
 def test_chunked_prefill_does_not_depend_on_the_chunking(pair):
-    """Every token's result in the batched prefill depends only on its own row (GEMM split order,
-    attention splits and the GDN recurrence are fixed), so any chunking gives the same bits."""
+    """A token's result in the batched prefill depends only on its own row (the GEMMs' split counts
+    and the attention splits are fixed for the model) and on the recurrent state, and the GDN
+    recurrence runs every 64-position block in one form (WY when the call holds the whole block,
+    else sequential): calls cut at multiples of 64 positions give the same bits, across the 512-token
+    passes too; any other cut runs some blocks in the other form, the same math to f32 rounding."""
     name, m, om, _, _ = pair
-    ids = prompt(m.vocab, 150, 9)
+    ids = prompt(m.vocab, 600, 9)
     m.reset()
     m.prefill_chunk(ids, 0, True)
     a, ta = m.logits(), m.last_token()
     m.reset()
+    m.prefill_chunk(ids[:64], 0, False)
+    m.prefill_chunk(ids[64:576], 64, False)
+    m.prefill_chunk(ids[576:], 576, True)
+    assert np.array_equal(a, m.logits()) and ta == m.last_token()
+    m.reset()
     m.prefill_chunk(ids[:7], 0, False)
     m.prefill_chunk(ids[7:71], 7, False)
     m.prefill_chunk(ids[71:], 71, True)
-    assert np.array_equal(a, m.logits()) and ta == m.last_token()
+    assert np.max(np.abs(a - m.logits())) < 1e-4 and ta == m.last_token()
 
 
 def test_chunked_prefill_matches_oracle_over_many_chunks(pair):
     name, m, om, _, _ = pair
-    ids = prompt(m.vocab, 200, 12)  # 4 chunks of up to 64 tokens
+    ids = prompt(m.vocab, 1100, 12)  # passes of 512, 512 and 76 tokens
     m.reset()
     om.reset()
     m.prefill_batched(ids)
