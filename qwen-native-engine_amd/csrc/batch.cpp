@@ -29,7 +29,7 @@ int attn_splits_for(int max_blocks) {
 int operand_order(const DevMat& W) { return W.kind == KIND_Q4 ? 1 : 0; }
 
 void rows_gemm(const DevMat& W, int n, float eps, uint8_t* frag, int norm, float* part, float* y, int y_stride, int epi,
-               uint8_t* frag_out, const float* gain_out, int order_out, hipStream_t st, int row_tiles) {
+               uint8_t* frag_out, const float* gain_out, int order_out, hipStream_t st, int row_tiles, bool partials_only) {
     GemmArgs a;
     a.m = n;
     a.frag = frag;
@@ -50,6 +50,7 @@ void rows_gemm(const DevMat& W, int n, float eps, uint8_t* frag, int norm, float
     a.frag_out = frag_out;
     a.gain_out = gain_out;
     a.order_out = order_out;
+    a.partials_only = partials_only ? 1 : 0;
     launch_gemm(a, st);
 }
 
@@ -207,8 +208,11 @@ void BatchDecoder::enqueue_step(int n) {
     for (size_t li = 0; li < m_.layers_.size(); li++) {
         const DevLayer& L = m_.layers_[li];
         const bool last = li + 1 == m_.layers_.size();
-        // in-projection of RMSNorm(h, input_norm), staged in frag_a
-        gemm(L.in, frag_a_, 1, proj_, proj_w_, EPI_STORE, nullptr, nullptr, 0);
+        // in-projection of RMSNorm(h, input_norm), staged in frag_a: split partials only, summed
+        // (times the rows' 1 / rms) by the GDN step or the attention prep that reads them
+        rows_gemm(L.in, n, c.eps, frag_a_, 1, part_, nullptr, 0, EPI_STORE, nullptr, nullptr, 0, stream_, 1, true);
+        const int in_splits = gemm_splits(L.in.kind, L.in.rows, L.in.k, L.in.group, 1);
+        const size_t split_stride = (size_t)64 * L.in.rows;  // the partials of one split: 64 rows (n <= 64)
         if (L.attn) {
             AttnRowsArgs a;
             a.proj = proj_;
@@ -230,6 +234,17 @@ void BatchDecoder::enqueue_step(int n) {
             a.max_blocks = max_blocks_;
             a.rows = n;
             a.bt_stride = max_blocks_;
+            a.part = part_;
+            a.in_splits = in_splits;
+            a.in_n = L.in.rows;
+            a.split_stride = split_stride;
+            a.x_in = frag_a_;
+            a.k_in = L.in.k;
+            a.eps = c.eps;
+            a.gate_dst = proj_;
+            a.out = nullptr;
+            a.frag_out = frag_b_;  // the out-projection's operand
+            a.order_out = order(L.out);
             launch_attention_rows(a, stream_);
         } else {
             GdnRowStrides rs;
@@ -237,10 +252,19 @@ void BatchDecoder::enqueue_step(int n) {
             rs.conv = conv_floats_;
             rs.state = rec_floats_;
             rs.out = (size_t)L.out.k;
-            launch_gdn_decode_rows(proj_, conv_[li], L.conv_w, rec_[li], mixed_, L.gdn_params, c.gdn_heads, n, rs,
-                                   stream_);
+            GdnRowsIO io;
+            io.part = part_;
+            io.splits = in_splits;
+            io.n = L.in.rows;
+            io.split_stride = split_stride;
+            io.x_in = frag_a_;
+            io.k_in = L.in.k;
+            io.eps = c.eps;
+            io.frag_out = frag_b_;  // the out-projection's operand
+            io.order_out = order(L.out);
+            launch_gdn_decode_rows(nullptr, conv_[li], L.conv_w, rec_[li], nullptr, L.gdn_params, c.gdn_heads, n, rs,
+                                   stream_, io);
         }
-        launch_stage_x(mixed_, L.out.k, n, L.out.k, nullptr, order(L.out), frag_b_, stream_);
         // h += W_out mixed; stage RMSNorm(h, post_norm) for gate_up
         gemm(L.out, frag_b_, 0, h_, c.hidden, EPI_ACCUMULATE, frag_a_, L.post_norm, order(L.gate_up));
         // act = SwiGLU(W_gu RMSNorm(h)), staged for down

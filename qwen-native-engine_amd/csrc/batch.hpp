@@ -17,10 +17,13 @@
 namespace qne {
 
 // One GEMM of a pass over up to 512 rows (a batched decode step of up to 64, or a prefill pass),
-// with its reduce, the split count chosen for row_tiles tiles of 64 rows: W applied to the x operand staged in `frag` (norm: its rows carry a deferred RMSNorm),
-// epilogue into y, and with frag_out the result staged for the next GEMM (times gain_out).
+// with its reduce, the split count chosen for row_tiles tiles of 64 rows: W applied to the x
+// operand staged in `frag` (norm: its rows carry a deferred RMSNorm), epilogue into y, and with
+// frag_out the result staged for the next GEMM (times gain_out). partials_only: only the split
+// partials are written (into part); the kernel that reads the output sums them.
 void rows_gemm(const DevMat& W, int n, float eps, uint8_t* frag, int norm, float* part, float* y, int y_stride,
-               int epi, uint8_t* frag_out, const float* gain_out, int order_out, hipStream_t st, int row_tiles = 1);
+               int epi, uint8_t* frag_out, const float* gain_out, int order_out, hipStream_t st, int row_tiles = 1,
+               bool partials_only = false);
 // 1 when a GEMM on W takes its x operand in the q4 column order.
 int operand_order(const DevMat& W);
 // Throws QNE_EFORMAT unless the model's shapes fit the batched kernels.

@@ -17,6 +17,7 @@
 #include "../error.hpp"
 #include "common.hpp"
 #include "launch.hpp"
+#include "operand.hpp"
 
 namespace qne {
 
@@ -102,16 +103,33 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_prep_rows(AttnRowsArgs a)
     const int t = threadIdx.x, hb = blockIdx.x, b = blockIdx.y;
     const uint32_t pos = (uint32_t)a.pos[b];
     const float* proj = a.proj + (size_t)b * a.proj_stride;
+    // The row's projection values: stored, or the in-projection's split partials (every load in
+    // flight at once) summed in split order times the row's 1 / rms from the sums of x^2 of its
+    // operand, as k_gemm_reduce computes them.
+    const int k0 = 2 * a.nq * kHD, g = hb - a.nq;
+    const int c0 = hb < a.nq ? hb * kHD + t : k0 + g * kHD + t;                      // q, or k
+    const int c1 = hb < a.nq ? (a.nq + hb) * kHD + t : k0 + (a.nkv + g) * kHD + t;  // the gate, or v
+    const int nchunks_in = a.k_in / kChunk;
+    const float ss_in = a.part && t < nchunks_in ? ((const float*)(a.x_in + (size_t)t * kChunkBytes))[kSsOff / 4 + b] : 0.0f;
+    const float* pbase = a.part ? a.part + (size_t)b * a.in_n : proj;
+    const int nsp = a.part ? a.in_splits : 1;
+    Split8 p0, p1;
+    p0.load(pbase + c0, nsp, a.split_stride);
+    if (a.part || hb >= a.nq) p1.load(pbase + c1, nsp, a.split_stride);
+    float inv = 1.0f;
+    if (a.part) {
+        inv = 1.0f / sqrtf(block_sum(ss_in, red) / (float)a.k_in + a.eps);  // row_inv_rms
+        __syncthreads();  // red is reused below
+    }
+    const float x0 = p0.sum(pbase + c0, nsp, a.split_stride) * inv;
     if (hb < a.nq) {
-        const float x = proj[hb * kHD + t];
-        a.qbuf[((size_t)b * a.nq + hb) * kHD + t] = norm_rope(x, a.norms, a.inv_freq, a.rope_dim, pos, sh, red);
+        a.qbuf[((size_t)b * a.nq + hb) * kHD + t] = norm_rope(x0, a.norms, a.inv_freq, a.rope_dim, pos, sh, red);
+        if (a.part) a.gate_dst[(size_t)b * a.proj_stride + c1] = p1.sum(pbase + c1, nsp, a.split_stride) * inv;
     } else {
-        const int g = hb - a.nq;
-        const float* kp = proj + 2 * a.nq * kHD;
-        const float kr = norm_rope(kp[g * kHD + t], a.norms + kHD, a.inv_freq, a.rope_dim, pos, sh, red);
+        const float kr = norm_rope(x0, a.norms + kHD, a.inv_freq, a.rope_dim, pos, sh, red);
         const size_t at = kv_index(a.block_table + (size_t)b * a.bt_stride, (int)pos, a.nkv, g) + t;
         a.k_pool[at] = f2h(kr);
-        a.v_pool[at] = f2h(kp[a.nkv * kHD + g * kHD + t]);
+        a.v_pool[at] = f2h(p1.sum(pbase + c1, nsp, a.split_stride) * inv);
     }
 }
 
@@ -295,7 +313,8 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_partial(const float* __re
 // sigmoid(gate) (shaders.rs:626-629).
 __global__ __launch_bounds__(kAttnThreads) void k_attn_combine(const float* __restrict__ part_ml, const float* __restrict__ part_acc,
                                                                int nkv, int G, int splits, const float* __restrict__ gate,
-                                                               int gate_stride, float* __restrict__ out) {
+                                                               int gate_stride, float* __restrict__ out, uint8_t* __restrict__ frag_out,
+                                                               int order_out) {
     const int h = blockIdx.x, b = blockIdx.y, t = threadIdx.x, g = h / G, gi = h % G, nq = nkv * G;
     float mn = -INFINITY;
     for (int s = 0; s < splits; s++) mn = fmaxf(mn, part_ml[((((size_t)b * nkv + g) * splits + s) * G + gi) * 2]);
@@ -311,7 +330,9 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_combine(const float* __re
     }
     float o = a / lsum;
     if (gate) o = o / (1.0f + expf(-gate[(size_t)b * gate_stride + h * kHD + t]));
-    out[((size_t)b * nq + h) * kHD + t] = o;
+    if (out) out[((size_t)b * nq + h) * kHD + t] = o;
+    if (frag_out)  // each wave: 64 columns of row b
+        emit_x(frag_out, (size_t)(nq * kHD / kChunk) * kChunkBytes, b, h * kHD + t, o, 1.0f, order_out, t & (kWave - 1));
 }
 
 template <int G>
@@ -339,7 +360,7 @@ void launch_attention_model(const AttnModelArgs& a, hipStream_t st) {
     partial_by_g(G, a.qbuf, a.k_pool, a.v_pool, a.block_table, a.max_blocks, a.max_blocks, (const int32_t*)(a.tok + 1),
                  a.nkv, a.part_ml, a.part_acc, a.splits, 1, st);
     hipLaunchKernelGGL(k_attn_combine, dim3(a.nq, 1), dim3(kAttnThreads), 0, st, a.part_ml, a.part_acc, a.nkv, G,
-                       a.splits, a.proj + a.nq * kHD, 0, a.out);
+                       a.splits, a.proj + a.nq * kHD, 0, a.out, (uint8_t*)nullptr, 0);
 }
 
 void launch_attention_rows(const AttnRowsArgs& a, hipStream_t st) {
@@ -347,8 +368,9 @@ void launch_attention_rows(const AttnRowsArgs& a, hipStream_t st) {
     const int G = a.nq / a.nkv;
     partial_by_g(G, a.qbuf, a.k_pool, a.v_pool, a.block_table, a.max_blocks, a.bt_stride, a.pos, a.nkv, a.part_ml,
                  a.part_acc, a.splits, a.rows, st);
+    const float* gate = a.part ? a.gate_dst + a.nq * kHD : a.proj + a.nq * kHD;
     hipLaunchKernelGGL(k_attn_combine, dim3(a.nq, a.rows), dim3(kAttnThreads), 0, st, a.part_ml, a.part_acc, a.nkv, G,
-                       a.splits, a.proj + a.nq * kHD, (int)a.proj_stride, a.out);
+                       a.splits, gate, (int)a.proj_stride, a.out, a.frag_out, a.order_out);
 }
 
 void launch_paged_attn(const float* q, const float* k_new, const float* v_new, uint16_t* k_pool, uint16_t* v_pool,
@@ -359,7 +381,7 @@ void launch_paged_attn(const float* q, const float* k_new, const float* v_new, u
     const int G = nq / nkv;
     partial_by_g(G, q, k_pool, v_pool, block_table, max_blocks, max_blocks, ctx, nkv, part_ml, part_acc, splits, batch, st);
     hipLaunchKernelGGL(k_attn_combine, dim3(nq, batch), dim3(kAttnThreads), 0, st, part_ml, part_acc, nkv, G, splits,
-                       (const float*)nullptr, 0, out);
+                       (const float*)nullptr, 0, out, (uint8_t*)nullptr, 0);
 }
 
 }  // namespace qne

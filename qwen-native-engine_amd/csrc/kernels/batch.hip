@@ -26,6 +26,7 @@
 #include "common.hpp"
 #include "launch.hpp"
 #include "lds_dma.hpp"
+#include "operand.hpp"
 
 namespace qne {
 
@@ -33,13 +34,7 @@ namespace {
 
 using namespace lds_dma;
 
-constexpr int kBM = 64;            // rows of x per GEMM (sequences)
-constexpr int kChunk = 64;         // columns per staged chunk
-constexpr int kFragBytes = 8192;   // one half (hi or lo) of a chunk: 4 k-steps x 2 row tiles x 64 lanes x 16 B
-constexpr int kXsumOff = 2 * kFragBytes;           // per-row sums of hi + lo over the chunk
-constexpr int kSsOff = kXsumOff + kBM * 4;           // per-row sums of x^2 (raw x) over the chunk
-constexpr int kChunkBytes = kSsOff + kBM * 4;        // a staged chunk in memory
-constexpr int kChunkLds = kSsOff;                    // the part of a chunk the GEMM copies to LDS
+constexpr int kChunkLds = kSsOff;  // the part of a chunk the GEMM copies to LDS
 
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
@@ -69,50 +64,7 @@ __device__ __forceinline__ uint32_t pack_h2(float a, float b) {
     return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)a) | ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)b) << 16);
 }
 
-// Operand layout of v_mfma_f32_32x32x16_f16 (lane l): A[l % 32][8 (l / 32) + i], B[8 (l / 32) + i][l % 32],
-// D register j = [8 (j / 4) + 4 (l / 32) + j % 4][l % 32]. The 16 k-slots of k-step s of a chunk are
-// chunk columns 32 (l / 32) + 8 s + i, the same for A and B, so a lane's q4 bytes of a chunk (16) are
-// contiguous. In a staged chunk, fragment (s, row tile mt) of a half is 64 lanes x 16 bytes.
-__device__ __forceinline__ int frag_offset(int s, int mt, int lane) { return ((s * 2 + mt) * 64 + lane) * 16; }
-
 }  // namespace
-
-// Writes one value of the x operand of a GEMM: row r, column c, value v (times gain g). The 64
-// lanes of the calling wave hold the 64 columns of one chunk of row r (all lanes call it), so the
-// chunk's sums of hi + lo and of v^2 are wave sums. q4order: the column order of the q4 GEMM's B
-// operand within each 8 columns, [0, 4, 1, 5, 2, 6, 3, 7] (nibbles8); else natural. Rows come in
-// tiles of 64: tile r / 64 of the operand starts tile_bytes (the K / 64 chunks of one tile) after
-// the previous one.
-__device__ __forceinline__ void emit_x(uint8_t* __restrict__ frag, size_t tile_bytes, int r, int c, float v, float g,
-                                       int q4order, int lane) {
-    const float xg = v * g;
-    const float hi = (float)(_Float16)xg;
-    const float lo = (float)(_Float16)(xg - hi);
-    const int chunk = c / kChunk, kk = c % kChunk, hf = kk / 32, st = (kk % 32) / 8, i = kk % 8;
-    const int slot = q4order ? 2 * (i % 4) + i / 4 : i;
-    const int rr = r & (kBM - 1);
-    uint8_t* tile = frag + (size_t)(r / kBM) * tile_bytes + (size_t)chunk * kChunkBytes;
-    uint8_t* dst = tile + frag_offset(st, rr >> 5, 32 * hf + (rr & 31)) + 2 * slot;
-    *(uint16_t*)dst = __builtin_bit_cast(uint16_t, (_Float16)hi);
-    *(uint16_t*)(dst + kFragBytes) = __builtin_bit_cast(uint16_t, (_Float16)lo);
-    const float xs = wave_sum_dpp(hi + lo), ss = wave_sum_dpp(v * v);
-    if (lane == 0) {
-        float* sums = (float*)tile;
-        sums[kXsumOff / 4 + rr] = xs;
-        sums[kSsOff / 4 + rr] = ss;
-    }
-}
-
-// 1 / rms of row r from the staged chunk sums of x^2 (the RMSNorm of the GEMM's input, applied to
-// its output: y = (1 / rms) W (x * gain)). Called by every thread of a 256-thread workgroup.
-__device__ __forceinline__ float row_inv_rms(const uint8_t* __restrict__ frag, int nchunks, int K, float eps, int r,
-                                             float* red) {
-    const uint8_t* tile = frag + (size_t)(r / kBM) * nchunks * kChunkBytes;
-    float ss = 0.0f;
-    for (int c = threadIdx.x; c < nchunks; c += 256) ss += ((const float*)(tile + (size_t)c * kChunkBytes))[kSsOff / 4 + (r & (kBM - 1))];
-    ss = block_sum(ss, red);
-    return 1.0f / sqrtf(ss / (float)K + eps);
-}
 
 // Grid (ceil(K / 256), rows rounded up to 64): the x operand of a GEMM from f32 rows
 // (x + r * x_stride; rows >= m are zero), times `gain` when set; the row's RMSNorm factor is applied
@@ -463,7 +415,7 @@ void launch_gemm(GemmArgs a, hipStream_t st) {
     const int nch = a.K / kChunk;
     a.cps = (nch + a.splits - 1) / a.splits;
     a.mpad = (a.m + kBM - 1) / kBM * kBM;
-    a.direct = a.splits == 1 && a.epi != EPI_SWIGLU && !a.frag_out;
+    a.direct = a.splits == 1 && a.epi != EPI_SWIGLU && !a.frag_out && !a.partials_only;
     if (a.x) {  // stage the x operand here (RMSNorm gain folded in, 1 / rms deferred to the epilogue)
         launch_stage_x(a.x, a.x_stride, a.m, a.K, a.gain, a.kind == KIND_Q4 ? 1 : 0, a.frag, st);
         a.norm = a.gain ? 1 : 0;
@@ -478,7 +430,7 @@ void launch_gemm(GemmArgs a, hipStream_t st) {
         if (waves == 8) hipLaunchKernelGGL((k_gemm<KIND_F16, 8, 3>), grid, dim3(512), 0, st, a);
         else hipLaunchKernelGGL((k_gemm<KIND_F16, 4, 4>), grid, dim3(256), 0, st, a);
     }
-    if (!a.direct) hipLaunchKernelGGL(k_gemm_reduce, dim3((a.n_out + 255) / 256, a.m), dim3(256), 0, st, a);
+    if (!a.direct && !a.partials_only) hipLaunchKernelGGL(k_gemm_reduce, dim3((a.n_out + 255) / 256, a.m), dim3(256), 0, st, a);
 }
 
 void launch_embed_rows(int kind, const void* W, const uint32_t* SZ, int group, int hidden, const uint32_t* tokens, int m,

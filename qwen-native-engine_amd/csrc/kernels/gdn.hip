@@ -11,6 +11,7 @@
 
 #include "common.hpp"
 #include "launch.hpp"
+#include "operand.hpp"
 
 namespace qne {
 
@@ -106,25 +107,49 @@ __device__ __forceinline__ void store_tile_t(const float* tile, float* S) {
 __global__ __launch_bounds__(kGdnThreads) void k_gdn_decode(const float* __restrict__ proj, float* __restrict__ conv_state,
                                                             const float* __restrict__ conv_w, float* __restrict__ state,
                                                             float* __restrict__ out, const float* __restrict__ prm, int H,
-                                                            GdnRowStrides rs) {
+                                                            GdnRowStrides rs, GdnRowsIO io) {
     __shared__ DeltaShared sh;
     __shared__ __attribute__((aligned(16))) float tile[kDV * kTileStride];
-    const int h = blockIdx.x, t = threadIdx.x, lane = t % kWave, w = t / kWave;
-    // row blockIdx.y of a batch: its own projection, conv and recurrent state, output
-    proj += (size_t)blockIdx.y * rs.proj;
-    conv_state += (size_t)blockIdx.y * rs.conv;
-    state += (size_t)blockIdx.y * rs.state;
-    out += (size_t)blockIdx.y * rs.out;
+    const int h = blockIdx.x, t = threadIdx.x, lane = t % kWave, w = t / kWave, b = blockIdx.y;
+    // row b of a batch: its own projection, conv and recurrent state, output
+    proj += (size_t)b * rs.proj;
+    conv_state += (size_t)b * rs.conv;
+    state += (size_t)b * rs.state;
+    if (out) out += (size_t)b * rs.out;
     const int col = t & (kDV - 1), qq = t >> 7;
     float* S = state + (size_t)h * kDK * kDV;
     float s[32];
     f4v tv[8];
+    // The row's projection values this thread reads: channel ch (q, k or v; threads < 384), z
+    // (threads < 128) and a, b (thread 0). Stored, or the in-projection's split partials summed in
+    // split order times the row's 1 / rms from the sums of x^2 of its operand, as k_gemm_reduce
+    // computes them. Those loads are issued before the state tile's (loads complete in order).
+    const int ch = t < 128 ? h * kDK + t : (t < 256 ? H * kDK + h * kDK + (t - 128) : 2 * H * kDK + h * kDV + (t - 256));
+    const int zoff = 2 * H * kDK + 2 * H * kDV;  // a[H] then b[H] follow z
+    const int zch = 2 * H * kDK + H * kDV + h * kDV + col;
+    const int nchunks_in = io.k_in / kChunk;
+    const float ss_in = io.part && t < nchunks_in ? ((const float*)(io.x_in + (size_t)t * kChunkBytes))[kSsOff / 4 + b] : 0.0f;
+    const float* pbase = io.part ? io.part + (size_t)b * io.n : proj;
+    const int nsp = io.part ? io.splits : 1;
+    Split8 pc, pz, pa, pb;
+    if (t < 384) pc.load(pbase + ch, nsp, io.split_stride);
+    if (t < 128) pz.load(pbase + zch, nsp, io.split_stride);
+    if (t == 0) {
+        pa.load(pbase + zoff + h, nsp, io.split_stride);
+        pb.load(pbase + zoff + H + h, nsp, io.split_stride);
+    }
+    asm volatile("" ::: "memory");  // keeps the loads above ahead of the tile's
     load_tile_t_issue(tv, S);  // in flight while the conv runs
+    float inv = 1.0f;
+    if (io.part) {
+        // row_inv_rms: one chunk sum per thread (nchunks_in <= 256), the block sum in wave order
+        inv = 1.0f / sqrtf(block_sum(ss_in, sh.red) / (float)io.k_in + io.eps);
+        __syncthreads();  // sh.red is reused below
+    }
 
     float val = 0.0f;
     if (t < 384) {
-        const int ch = t < 128 ? h * kDK + t : (t < 256 ? H * kDK + h * kDK + (t - 128) : 2 * H * kDK + h * kDV + (t - 256));
-        const float x = proj[ch];
+        const float x = pc.sum(pbase + ch, nsp, io.split_stride) * inv;
         float* st = conv_state + (size_t)ch * 4;
         const float* cw = conv_w + (size_t)ch * 4;
         const float s0 = st[0], s1 = st[1], s2 = st[2];
@@ -140,10 +165,10 @@ __global__ __launch_bounds__(kGdnThreads) void k_gdn_decode(const float* __restr
     else if (t < 256) sh.k[t - 128] = val * (1.0f / sqrtf(sh.red[2] + sh.red[3] + 1e-6f));
     else if (t < 384) sh.v[t - 256] = val;
     if (t == 0) {
-        const int zoff = 2 * H * kDK + 2 * H * kDV;  // a[H] then b[H] follow z
-        const float a = proj[zoff + h], b = proj[zoff + H + h];
-        sh.g = expf(prm[H + h] * logf(1.0f + expf(a + prm[h])));
-        sh.beta = 1.0f / (1.0f + expf(-b));
+        const float ga = pa.sum(pbase + zoff + h, nsp, io.split_stride) * inv;
+        const float gb = pb.sum(pbase + zoff + H + h, nsp, io.split_stride) * inv;
+        sh.g = expf(prm[H + h] * logf(1.0f + expf(ga + prm[h])));
+        sh.beta = 1.0f / (1.0f + expf(-gb));
     }
     __syncthreads();
     if (w == 0) {
@@ -162,9 +187,12 @@ __global__ __launch_bounds__(kGdnThreads) void k_gdn_decode(const float* __restr
     if (lane == 0) sh.red[w] = oo;
     __syncthreads();
     if (qq == 0) {
-        const float inv = 1.0f / sqrtf((sh.red[0] + sh.red[1]) / (float)kDV + 1e-6f);
-        const float z = proj[2 * H * kDK + H * kDV + h * kDV + col];
-        out[h * kDV + col] = o * inv * silu(z) * prm[2 * H + col];
+        const float rinv = 1.0f / sqrtf((sh.red[0] + sh.red[1]) / (float)kDV + 1e-6f);
+        const float z = pz.sum(pbase + zch, nsp, io.split_stride) * inv;
+        const float y = o * rinv * silu(z) * prm[2 * H + col];
+        if (out) out[h * kDV + col] = y;
+        if (io.frag_out)  // waves 0 and 1: 64 columns of the row each
+            emit_x(io.frag_out, (size_t)(H * kDV / kChunk) * kChunkBytes, b, h * kDV + col, y, 1.0f, io.order_out, lane);
     }
 }
 
@@ -376,13 +404,14 @@ void launch_gdn_chunk(const float* proj, int proj_stride, float* conv_state, con
 void launch_gdn_decode(const float* proj, float* conv_state, const float* conv_w, float* state, float* out,
                        const float* prm, int heads, hipStream_t st) {
     hipLaunchKernelGGL(k_gdn_decode, dim3(heads), dim3(kGdnThreads), 0, st, proj, conv_state, conv_w, state, out, prm,
-                       heads, GdnRowStrides{});
+                       heads, GdnRowStrides{}, GdnRowsIO{});
 }
 
 void launch_gdn_decode_rows(const float* proj, float* conv_state, const float* conv_w, float* state, float* out,
-                            const float* prm, int heads, int rows, const GdnRowStrides& rs, hipStream_t st) {
+                            const float* prm, int heads, int rows, const GdnRowStrides& rs, hipStream_t st,
+                            const GdnRowsIO& io) {
     hipLaunchKernelGGL(k_gdn_decode, dim3(heads, rows), dim3(kGdnThreads), 0, st, proj, conv_state, conv_w, state, out,
-                       prm, heads, rs);
+                       prm, heads, rs, io);
 }
 
 void launch_delta_rule(const float* q, const float* k, const float* v, const float* beta, const float* g, float* state,

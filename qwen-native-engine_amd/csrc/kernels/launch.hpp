@@ -93,6 +93,20 @@ struct AttnRowsArgs {
     float* out;                  // [rows][nq][hd]
     int nq, nkv, rope_dim, splits, max_blocks, rows;
     int bt_stride;               // entries between rows of block_table (0: one shared row)
+    // With `part`, the projection is the in-projection's split partials (splits x split_stride
+    // floats, rows n apart) summed here in split order times the row's 1 / rms (from the sums of
+    // x^2 of its operand x_in, K = k_in): the GEMM's reduce folded in. The gate, which the
+    // combine reads from proj, is then written to gate_dst (rows proj_stride apart).
+    const float* part = nullptr;
+    int in_splits = 0, in_n = 0, k_in = 0;
+    size_t split_stride = 0;
+    const uint8_t* x_in = nullptr;
+    float eps = 1e-6f;
+    float* gate_dst = nullptr;
+    // With frag_out, the output rows are also staged as the out-projection's operand (column
+    // order order_out); out may then be null.
+    uint8_t* frag_out = nullptr;
+    int order_out = 0;
 };
 void launch_attention_rows(const AttnRowsArgs& a, hipStream_t st);
 
@@ -110,8 +124,23 @@ struct GdnRowStrides {
 void launch_gdn_chunk(const float* proj, int proj_stride, float* conv_state, const float* conv_w, float* state,
                       const float* prm, int heads, int tokens, float* q, float* k, float* v, float* g, float* beta,
                       float* o, float* mixed, int mixed_stride, hipStream_t st, int lead = 0, float* wy_ws = nullptr);
+// Where the batched GDN step reads its projection and writes its output. With `part`, the
+// projection is the in-projection's split partials (splits x split_stride floats, rows n apart)
+// summed here in split order times the row's 1 / rms (from the sums of x^2 of its operand x_in,
+// K = k_in): the GEMM's reduce folded in. With frag_out, the output rows are also staged as the
+// out-projection's operand (column order order_out); out may then be null.
+struct GdnRowsIO {
+    const float* part = nullptr;
+    int splits = 0, n = 0, k_in = 0;
+    size_t split_stride = 0;
+    const uint8_t* x_in = nullptr;
+    float eps = 1e-6f;
+    uint8_t* frag_out = nullptr;
+    int order_out = 0;
+};
 void launch_gdn_decode_rows(const float* proj, float* conv_state, const float* conv_w, float* state, float* out,
-                            const float* prm, int heads, int rows, const GdnRowStrides& rs, hipStream_t st);
+                            const float* prm, int heads, int rows, const GdnRowStrides& rs, hipStream_t st,
+                            const GdnRowsIO& io = GdnRowsIO());
 
 // y = x W^T for up to kGemmRowsMax rows of x (batched decode: up to 64; chunked prefill: a pass of
 // tokens), on MFMA, in tiles of 64 rows. The x operand is staged in `frag` (gemm_frag_bytes(K, m)):
@@ -147,6 +176,8 @@ struct GemmArgs {
     uint8_t* frag_out = nullptr;
     const float* gain_out = nullptr;
     int order_out = 0;  // 1: the column order of a q4 GEMM's operand
+    int partials_only = 0;  // write the split partials (even with one split) and launch no reduce:
+                            // the kernel that reads the output sums them
 };
 // One row of token sampling (the O(vocab) part of src/sampling.rs choose / try_sample).
 struct SampleArgs {
