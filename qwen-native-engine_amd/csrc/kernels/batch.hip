@@ -78,22 +78,49 @@ __global__ __launch_bounds__(256) void k_stage_x(const float* __restrict__ x, in
     emit_x(frag, (size_t)(K / kChunk) * kChunkBytes, r, c, v, gain ? gain[c] : 1.0f, q4order, threadIdx.x & 63);
 }
 
+// Until at most n of the wave's vector-memory operations are outstanding (n wave-uniform; counts
+// past 31 wait for 31, which is only stricter).
+__device__ __forceinline__ void wait_vm_upto(int n) {
+    switch (n < 31 ? n : 31) {
+#define QNE_WAIT_CASE(k) \
+    case k: wait_vm<k>(); break;
+        QNE_WAIT_CASE(0) QNE_WAIT_CASE(1) QNE_WAIT_CASE(2) QNE_WAIT_CASE(3) QNE_WAIT_CASE(4) QNE_WAIT_CASE(5)
+        QNE_WAIT_CASE(6) QNE_WAIT_CASE(7) QNE_WAIT_CASE(8) QNE_WAIT_CASE(9) QNE_WAIT_CASE(10) QNE_WAIT_CASE(11)
+        QNE_WAIT_CASE(12) QNE_WAIT_CASE(13) QNE_WAIT_CASE(14) QNE_WAIT_CASE(15) QNE_WAIT_CASE(16) QNE_WAIT_CASE(17)
+        QNE_WAIT_CASE(18) QNE_WAIT_CASE(19) QNE_WAIT_CASE(20) QNE_WAIT_CASE(21) QNE_WAIT_CASE(22) QNE_WAIT_CASE(23)
+        QNE_WAIT_CASE(24) QNE_WAIT_CASE(25) QNE_WAIT_CASE(26) QNE_WAIT_CASE(27) QNE_WAIT_CASE(28) QNE_WAIT_CASE(29)
+        QNE_WAIT_CASE(30)
+#undef QNE_WAIT_CASE
+        default: wait_vm<31>();
+    }
+}
+
 // Grid (ceil(N / (32 WAVES)), splits, row tiles); split s covers chunks [s * cps, (s + 1) * cps) of
-// the x rows 64 blockIdx.z .. + 63. Wave w owns W rows 32 (WAVES blockIdx.x + w) .. + 31. The chunks
-// stream through a ring of D LDS slots, each holding one x chunk and every wave's W chunk; D - 1
-// chunks are in flight while one is computed. The row tiles of one W tile read the same W chunks,
-// which the MALL serves after the first.
-template <int KIND, int WAVES, int D>
-__global__ __launch_bounds__(64 * WAVES) void k_gemm(const GemmArgs a) {
+// the x rows 64 blockIdx.z .. + 63. Compute wave w < WAVES owns W rows 32 (WAVES blockIdx.x + w)
+// .. + 31. The chunks stream through a ring of D LDS slots, each holding one x chunk and every
+// wave's W chunk; D - 1 chunks are in flight while one is computed. With DW > 0 the workgroup has
+// DW more waves that only issue the LDS DMA (x, chunk sums, every W tile), so a compute wave's
+// instruction stream holds LDS reads, MFMAs and VALU only and the transfers overlap the
+// computation; with DW = 0 every compute wave sends its own W tile and a part of x. The row tiles
+// of one W tile read the same W chunks, which the MALL serves after the first.
+template <int KIND, int WAVES, int D, int DW>
+__global__ __launch_bounds__(64 * (WAVES + DW)) void k_gemm(const GemmArgs a) {
     constexpr int kWBytes = KIND == KIND_Q4 ? 1024 + 128 : 4096;  // one wave's W chunk (q4: + scale/zero words)
     constexpr int kSlot = kChunkLds + WAVES * kWBytes;
-    constexpr int kXPart = 2 * kFragBytes / WAVES;                 // x bytes each wave copies
-    constexpr int kPer = kXPart / 1024 + 1 + (KIND == KIND_Q4 ? 2 : 4);  // DMAs per wave per chunk
+    constexpr int kSenders = DW > 0 ? DW : WAVES;                   // waves that issue the DMA
+    constexpr int kXPart = 2 * kFragBytes / kSenders;               // x bytes each sender copies
+    constexpr int kTilesPer = WAVES / kSenders;                     // W tiles each sender sends
+    constexpr int kWDmas = KIND == KIND_Q4 ? 2 : 4;                 // DMAs of one W tile chunk
+    static_assert(kXPart % 1024 == 0 && WAVES % kSenders == 0, "the senders split x and W evenly");
+    constexpr int kSumLanes = kBM * 4 / 16 / kSenders;              // lanes copying the chunk sums (16 B each)
+    static_assert(kSumLanes >= 1, "every sender copies a part of the chunk sums");
+    constexpr int kPer = kXPart / 1024 + 1 + kTilesPer * kWDmas;    // DMAs per sender per chunk
     __shared__ __attribute__((aligned(16))) uint8_t ring[D][kSlot];
     const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const bool computes = w < WAVES;
+    const int sender = DW > 0 ? w - WAVES : w;  // index among the senders (< 0: none)
     const int hf = lane >> 5, l32 = lane & 31;
     const int n = (blockIdx.x * WAVES + w) * 32 + l32;
-    const int nr = min(n, a.N - 1);  // rows past N load row N - 1 and are not stored
     const int K = a.K, nchunks = K / kChunk;
     const int cpg = KIND == KIND_Q4 ? a.group / kChunk : 1;
     const int ngroups = nchunks / cpg;
@@ -102,83 +129,81 @@ __global__ __launch_bounds__(64 * WAVES) void k_gemm(const GemmArgs a) {
     const int mt = blockIdx.z;  // row tile
     const uint8_t* xfrag = a.frag + (size_t)mt * nchunks * kChunkBytes;
 
-    auto issue = [&](int j, int slot) {
+    auto issue = [&](int j, int slot) {  // senders only
         uint8_t* base = ring[slot];
         const uint8_t* src = xfrag + (size_t)(c0 + j) * kChunkBytes;
 #pragma unroll
-        for (int u = 0; u < kXPart / 1024; u++) dma16(src + kXPart * w + 1024 * u + 16 * lane, base + kXPart * w + 1024 * u);
-        constexpr int kSumLanes = kBM * 4 / 16 / WAVES;  // lanes copying the chunk sums (16 B each)
-        if (lane < kSumLanes) dma16(src + kXsumOff + 16 * (kSumLanes * w + lane), base + kXsumOff + 16 * kSumLanes * w);
-        uint8_t* dst = base + kChunkLds + w * kWBytes;
+        for (int u = 0; u < kXPart / 1024; u++) dma16(src + kXPart * sender + 1024 * u + 16 * lane, base + kXPart * sender + 1024 * u);
+        if (lane < kSumLanes) dma16(src + kXsumOff + 16 * (kSumLanes * sender + lane), base + kXsumOff + 16 * kSumLanes * sender);
         const int c = c0 + j;
-        if (KIND == KIND_Q4) {
-            dma16((const uint8_t*)a.W + (size_t)nr * (K / 2) + c * 32 + 16 * hf, dst);
-            if (lane < 32) dma4(a.SZ + (size_t)nr * ngroups + c / cpg, dst + 1024);
-        } else {
 #pragma unroll
-            for (int s = 0; s < 4; s++) dma16((const uint16_t*)a.W + (size_t)nr * K + c * kChunk + 32 * hf + 8 * s, dst + 1024 * s);
+        for (int i = 0; i < kTilesPer; i++) {
+            const int wt = sender * kTilesPer + i;  // W tile (compute wave) sent
+            const int nr = min((int)(blockIdx.x * WAVES + wt) * 32 + l32, a.N - 1);  // rows past N: row N - 1, not stored
+            uint8_t* dst = base + kChunkLds + wt * kWBytes;
+            if (KIND == KIND_Q4) {
+                dma16((const uint8_t*)a.W + (size_t)nr * (K / 2) + c * 32 + 16 * hf, dst);
+                if (lane < 32) dma4(a.SZ + (size_t)nr * ngroups + c / cpg, dst + 1024);
+            } else {
+#pragma unroll
+                for (int s = 0; s < 4; s++) dma16((const uint16_t*)a.W + (size_t)nr * K + c * kChunk + 32 * hf + 8 * s, dst + 1024 * s);
+            }
         }
     };
-    // until chunk j has landed: `ahead` chunks were issued after it
-    auto wait_chunk = [&](int ahead) {
-        if (ahead <= 0) wait_vm<0>();
-        else if (ahead == 1) wait_vm<kPer>();
-        else if (ahead == 2) wait_vm<2 * kPer>();
-        else if (ahead == 3) wait_vm<3 * kPer>();
-        else if (ahead == 4) wait_vm<4 * kPer>();
-        else wait_vm<5 * kPer>();
-    };
-    static_assert(D - 2 <= 5 && 5 * kPer <= 63, "ring deeper than the waits cover");
+    static_assert(D >= 2 && (D - 2) * kPer <= 31, "ring deeper than the waits cover");
 
     float16_t acc0, acc1, grp0, grp1;
 #pragma unroll
     for (int j = 0; j < 16; j++) acc0[j] = acc1[j] = grp0[j] = grp1[j] = 0.0f;
 
-    for (int j = 0; j < min(D - 1, nch); j++) issue(j, j);
+    if (sender >= 0)
+        for (int j = 0; j < min(D - 1, nch); j++) issue(j, j);
     int slot = 0;           // slot of chunk j
     int next_slot = D - 1;  // slot of chunk j + D - 1
     for (int j = 0; j < nch; j++) {
-        wait_chunk(min(j + D - 2, nch - 1) - j);
-        __syncthreads();  // every wave's part of chunk j has landed; every wave is done with chunk j - 1
-        if (j + D - 1 < nch) issue(j + D - 1, next_slot);
-        const uint8_t* xs = ring[slot];
-        const uint8_t* ws = ring[slot] + kChunkLds + w * kWBytes;
-        uint4 wq;
-        if (KIND == KIND_Q4) wq = *(const uint4*)(ws + 16 * lane);
+        if (sender >= 0) wait_vm_upto(kPer * (min(j + D - 2, nch - 1) - j));  // this sender's part of chunk j is in
+        __syncthreads();  // every part of chunk j has landed; every wave is done with chunk j - 1
+        if (sender >= 0 && j + D - 1 < nch) issue(j + D - 1, next_slot);
+        if (computes) {
+            const uint8_t* xs = ring[slot];
+            const uint8_t* ws = ring[slot] + kChunkLds + w * kWBytes;
+            uint4 wq;
+            if (KIND == KIND_Q4) wq = *(const uint4*)(ws + 16 * lane);
 #pragma unroll
-        for (int s = 0; s < 4; s++) {
-            half8_t b;
-            if (KIND == KIND_Q4) b = nibbles8(s == 0 ? wq.x : s == 1 ? wq.y : s == 2 ? wq.z : wq.w);
-            else b = *(const half8_t*)(ws + 1024 * s + 16 * lane);
-            const half8_t a0h = *(const half8_t*)(xs + frag_offset(s, 0, lane));
-            const half8_t a1h = *(const half8_t*)(xs + frag_offset(s, 1, lane));
-            const half8_t a0l = *(const half8_t*)(xs + kFragBytes + frag_offset(s, 0, lane));
-            const half8_t a1l = *(const half8_t*)(xs + kFragBytes + frag_offset(s, 1, lane));
-            if (KIND == KIND_Q4 && s == 0) {  // a fresh tile per chunk: C = 0
-                const float16_t zero = {};
-                grp0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0h, b, zero, 0, 0, 0);
-                grp1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1h, b, zero, 0, 0, 0);
-            } else {
-                grp0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0h, b, grp0, 0, 0, 0);
-                grp1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1h, b, grp1, 0, 0, 0);
+            for (int s = 0; s < 4; s++) {
+                half8_t b;
+                if (KIND == KIND_Q4) b = nibbles8(s == 0 ? wq.x : s == 1 ? wq.y : s == 2 ? wq.z : wq.w);
+                else b = *(const half8_t*)(ws + 1024 * s + 16 * lane);
+                const half8_t a0h = *(const half8_t*)(xs + frag_offset(s, 0, lane));
+                const half8_t a1h = *(const half8_t*)(xs + frag_offset(s, 1, lane));
+                const half8_t a0l = *(const half8_t*)(xs + kFragBytes + frag_offset(s, 0, lane));
+                const half8_t a1l = *(const half8_t*)(xs + kFragBytes + frag_offset(s, 1, lane));
+                if (KIND == KIND_Q4 && s == 0) {  // a fresh tile per chunk: C = 0
+                    const float16_t zero = {};
+                    grp0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0h, b, zero, 0, 0, 0);
+                    grp1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1h, b, zero, 0, 0, 0);
+                } else {
+                    grp0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0h, b, grp0, 0, 0, 0);
+                    grp1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1h, b, grp1, 0, 0, 0);
+                }
+                grp0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0l, b, grp0, 0, 0, 0);
+                grp1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1l, b, grp1, 0, 0, 0);
             }
-            grp0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0l, b, grp0, 0, 0, 0);
-            grp1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1l, b, grp1, 0, 0, 0);
-        }
-        if (KIND == KIND_Q4) {
-            // y += s (sum q x) - s z (sum x) over the chunk (scale and zero of the chunk's group)
-            const uint32_t szw = *(const uint32_t*)(ws + 1024 + 4 * l32);
-            const float sc = lo_h(szw), sz = sc * hi_h(szw);
-            const float* xsum = (const float*)(xs + kXsumOff);
+            if (KIND == KIND_Q4) {
+                // y += s (sum q x) - s z (sum x) over the chunk (scale and zero of the chunk's group)
+                const uint32_t szw = *(const uint32_t*)(ws + 1024 + 4 * l32);
+                const float sc = lo_h(szw), sz = sc * hi_h(szw);
+                const float* xsum = (const float*)(xs + kXsumOff);
 #pragma unroll
-            for (int q = 0; q < 4; q++) {
-                const float4 s0 = *(const float4*)(xsum + 8 * q + 4 * hf);
-                const float4 s1 = *(const float4*)(xsum + 32 + 8 * q + 4 * hf);
-                const float v0[4] = {s0.x, s0.y, s0.z, s0.w}, v1[4] = {s1.x, s1.y, s1.z, s1.w};
+                for (int q = 0; q < 4; q++) {
+                    const float4 s0 = *(const float4*)(xsum + 8 * q + 4 * hf);
+                    const float4 s1 = *(const float4*)(xsum + 32 + 8 * q + 4 * hf);
+                    const float v0[4] = {s0.x, s0.y, s0.z, s0.w}, v1[4] = {s1.x, s1.y, s1.z, s1.w};
 #pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    acc0[4 * q + e] = fmaf(sc, grp0[4 * q + e], fmaf(-sz, v0[e], acc0[4 * q + e]));
-                    acc1[4 * q + e] = fmaf(sc, grp1[4 * q + e], fmaf(-sz, v1[e], acc1[4 * q + e]));
+                    for (int e = 0; e < 4; e++) {
+                        acc0[4 * q + e] = fmaf(sc, grp0[4 * q + e], fmaf(-sz, v0[e], acc0[4 * q + e]));
+                        acc1[4 * q + e] = fmaf(sc, grp1[4 * q + e], fmaf(-sz, v1[e], acc1[4 * q + e]));
+                    }
                 }
             }
         }
@@ -190,7 +215,7 @@ __global__ __launch_bounds__(64 * WAVES) void k_gemm(const GemmArgs a) {
         acc1 = grp1;
     }
     if (!a.direct) {
-        if (n >= a.N) return;
+        if (!computes || n >= a.N) return;
         float* pp = a.part + ((size_t)blockIdx.y * a.mpad + (size_t)kBM * mt) * a.N + n;
 #pragma unroll
         for (int j = 0; j < 16; j++) {
@@ -213,7 +238,7 @@ __global__ __launch_bounds__(64 * WAVES) void k_gemm(const GemmArgs a) {
         sinv[threadIdx.x] = 1.0f;
     }
     __syncthreads();
-    if (n >= a.N) return;
+    if (!computes || n >= a.N) return;
     const int rows = a.m - kBM * mt;  // rows of this tile
 #pragma unroll
     for (int j = 0; j < 16; j++) {
@@ -422,13 +447,20 @@ void launch_gemm(GemmArgs a, hipStream_t st) {
     }
     const int waves = gemm_waves(a.kind, a.N);
     const dim3 grid((a.N + 32 * waves - 1) / (32 * waves), a.splits, a.mpad / kBM);
+    // One row tile (a batched decode step): about one workgroup per CU, so 4 DMA waves beside the
+    // 8 compute waves let the transfers overlap the computation (64 rows: gate_up 23.9 -> 22.4 us,
+    // LM head 222 -> 205 us). Several row tiles (a prefill pass): two 8-wave workgroups per CU
+    // (125 VGPRs in a 12-wave workgroup leave room for one). The arithmetic is the same either way.
+    const bool dma_waves = a.mpad == kBM;
     if (a.kind == KIND_Q4) {
         // 3 chunk slots (77.6 KiB): deeper rings measured slower, and two workgroups fit a CU
-        hipLaunchKernelGGL((k_gemm<KIND_Q4, 8, 3>), grid, dim3(512), 0, st, a);
+        if (dma_waves) hipLaunchKernelGGL((k_gemm<KIND_Q4, 8, 3, 4>), grid, dim3(768), 0, st, a);
+        else hipLaunchKernelGGL((k_gemm<KIND_Q4, 8, 3, 0>), grid, dim3(512), 0, st, a);
     } else {
         // f16: as many chunk slots as fit in 160 KiB of LDS
-        if (waves == 8) hipLaunchKernelGGL((k_gemm<KIND_F16, 8, 3>), grid, dim3(512), 0, st, a);
-        else hipLaunchKernelGGL((k_gemm<KIND_F16, 4, 4>), grid, dim3(256), 0, st, a);
+        if (waves == 8 && dma_waves) hipLaunchKernelGGL((k_gemm<KIND_F16, 8, 3, 4>), grid, dim3(768), 0, st, a);
+        else if (waves == 8) hipLaunchKernelGGL((k_gemm<KIND_F16, 8, 3, 0>), grid, dim3(512), 0, st, a);
+        else hipLaunchKernelGGL((k_gemm<KIND_F16, 4, 4, 0>), grid, dim3(256), 0, st, a);
     }
     if (!a.direct && !a.partials_only) hipLaunchKernelGGL(k_gemm_reduce, dim3((a.n_out + 255) / 256, a.m), dim3(256), 0, st, a);
 }
