@@ -1,12 +1,12 @@
 // Gated DeltaNet kernels (dk = dv = 128).
 //
 // Reference: the decode step `gdn` (kernels/src/shaders.rs:436-520) and the chunk kernel `gdn_b`
-// (kernels/src/batch.rs:166-255). Design for gfx950: one 512-thread workgroup per (sequence,
-// head); thread (column t, quarter q) owns the 32 state values S[32q .. 32q+31][t] in VGPRs, so
-// the 64 KiB state tile of a head is read once and written once per launch, with each wave
-// touching 256 contiguous bytes per load. S^T k and S^T q are 32-term register dot products
-// merged across quarters through LDS. The multi-token kernel keeps the tile in registers across
-// all tokens of the launch.
+// (kernels/src/batch.rs:166-255). Design for gfx950: the decode step runs one 512-thread
+// workgroup per (sequence, head) and reads the head's 64 KiB value-major state tile once, in
+// address order (each wave instruction one contiguous KiB), into registers: thread t holds keys
+// 4 (t % 32)..+3 of the value columns t / 32 + 16 r, so a column lies in one half-wave and S^T k,
+// S^T q are half-wave DPP sums; the tile is written back from the same registers. The
+// multi-token kernels keep the tile in registers across all tokens of the launch.
 #include <algorithm>
 
 #include "common.hpp"
@@ -21,6 +21,8 @@ struct DeltaShared {
     float q[kDK], k[kDK], v[kDV];
     float part[2][4][kDV];
     float dv[kDV];
+    float o[kDV];
+    float z[kDV];
     float red[16];
     float kq, g, beta;
 };
@@ -64,80 +66,49 @@ __device__ __forceinline__ void store_tile(const float (&s)[32], float* S, int c
 // The model keeps each head's state value-major, S_T[t][j] = S[j][t]: the 128 keys of one value
 // column are contiguous, so a column (what one wave updates in the persistent decode kernel) is a
 // single 512-byte read.
-// The value-major tile goes through LDS: the 512 threads read and write it as 16-byte pieces in
-// address order (each wave instruction one contiguous KiB), and each thread takes its 32 values
-// from the staged copy. Rows are padded to 132 floats, so the 8 lanes of a 16-byte LDS access
-// (consecutive columns) fall on distinct banks.
-constexpr int kTileStride = kDK + 4;
+// The decode step reads the value-major tile as 16-byte pieces in address order (piece f of the
+// tile: column f / 32, keys 4 (f % 32)..+3; each wave instruction one contiguous KiB) and keeps
+// them in that layout: thread t owns piece t + 512 r (r = 0..7).
 typedef float f4v __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ void load_tile_t_issue(f4v (&v)[8], const float* S) {
 #pragma unroll
     for (int r = 0; r < 8; r++) v[r] = __builtin_nontemporal_load((const f4v*)S + threadIdx.x + kGdnThreads * r);
 }
-__device__ __forceinline__ void stage_tile_t(const f4v (&v)[8], float* tile) {
-#pragma unroll
-    for (int r = 0; r < 8; r++) {
-        const int f = threadIdx.x + kGdnThreads * r;  // 16-byte piece f: column f / 32, keys 4 (f % 32)..+3
-        *(f4v*)&tile[(f >> 5) * kTileStride + 4 * (f & 31)] = v[r];
-    }
-}
-__device__ __forceinline__ void read_tile_t(float (&s)[32], const float* tile, int col, int qq) {
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-        const float4 x = *(const float4*)&tile[col * kTileStride + 32 * qq + 4 * i];
-        s[4 * i] = x.x; s[4 * i + 1] = x.y; s[4 * i + 2] = x.z; s[4 * i + 3] = x.w;
-    }
-}
-__device__ __forceinline__ void write_tile_t(const float (&s)[32], float* tile, int col, int qq) {
-#pragma unroll
-    for (int i = 0; i < 8; i++)
-        *(float4*)&tile[col * kTileStride + 32 * qq + 4 * i] = make_float4(s[4 * i], s[4 * i + 1], s[4 * i + 2], s[4 * i + 3]);
-}
-__device__ __forceinline__ void store_tile_t(const float* tile, float* S) {
-#pragma unroll
-    for (int r = 0; r < 8; r++) {
-        const int f = threadIdx.x + kGdnThreads * r;
-        __builtin_nontemporal_store(*(const f4v*)&tile[(f >> 5) * kTileStride + 4 * (f & 31)], (f4v*)S + f);
-    }
-}
 
 // Model decode step for head blockIdx.x: conv + SiLU on the head's q, k, v channels, L2 norms,
 // gates, delta rule, gated RMSNorm (shaders.rs:436-520).
 // proj = [q(H*dk) k(H*dk) v(H*dv) z(H*dv) a(H) b(H)], prm = [dt_bias(H) A_neg_exp(H) norm_w(dv)].
-__global__ __launch_bounds__(kGdnThreads) void k_gdn_decode(const float* __restrict__ proj, float* __restrict__ conv_state,
+__global__ __launch_bounds__(kGdnThreads, 6) void k_gdn_decode(const float* __restrict__ proj, float* __restrict__ conv_state,
                                                             const float* __restrict__ conv_w, float* __restrict__ state,
                                                             float* __restrict__ out, const float* __restrict__ prm, int H,
                                                             GdnRowStrides rs, GdnRowsIO io) {
     __shared__ DeltaShared sh;
-    __shared__ __attribute__((aligned(16))) float tile[kDV * kTileStride];
     const int h = blockIdx.x, t = threadIdx.x, lane = t % kWave, w = t / kWave, b = blockIdx.y;
     // row b of a batch: its own projection, conv and recurrent state, output
     proj += (size_t)b * rs.proj;
     conv_state += (size_t)b * rs.conv;
     state += (size_t)b * rs.state;
     if (out) out += (size_t)b * rs.out;
-    const int col = t & (kDV - 1), qq = t >> 7;
+    const int col = t & (kDV - 1);
     float* S = state + (size_t)h * kDK * kDV;
-    float s[32];
     f4v tv[8];
-    // The row's projection values this thread reads: channel ch (q, k or v; threads < 384), z
-    // (threads < 128) and a, b (thread 0). Stored, or the in-projection's split partials summed in
-    // split order times the row's 1 / rms from the sums of x^2 of its operand, as k_gemm_reduce
-    // computes them. Those loads are issued before the state tile's (loads complete in order).
-    const int ch = t < 128 ? h * kDK + t : (t < 256 ? H * kDK + h * kDK + (t - 128) : 2 * H * kDK + h * kDV + (t - 256));
+    // The row's projection values this thread reads: channel ch (q, k or v; threads < 384; z of
+    // column t - 384 for threads 384..511) and a (thread 0) or b (thread 1). Stored, or the
+    // in-projection's split partials summed in split order times the row's 1 / rms from the sums
+    // of x^2 of its operand, as k_gemm_reduce computes them. Those loads are issued before the
+    // state tile's (loads complete in order).
     const int zoff = 2 * H * kDK + 2 * H * kDV;  // a[H] then b[H] follow z
-    const int zch = 2 * H * kDK + H * kDV + h * kDV + col;
+    const int ch = t < 128 ? h * kDK + t
+                           : (t < 256 ? H * kDK + h * kDK + (t - 128)
+                                      : (t < 384 ? 2 * H * kDK + h * kDV + (t - 256) : 2 * H * kDK + H * kDV + h * kDV + col));
+    const int gch = zoff + (t == 0 ? h : H + h);
     const int nchunks_in = io.k_in / kChunk;
     const float ss_in = io.part && t < nchunks_in ? ((const float*)(io.x_in + (size_t)t * kChunkBytes))[kSsOff / 4 + b] : 0.0f;
     const float* pbase = io.part ? io.part + (size_t)b * io.n : proj;
     const int nsp = io.part ? io.splits : 1;
-    Split8 pc, pz, pa, pb;
-    if (t < 384) pc.load(pbase + ch, nsp, io.split_stride);
-    if (t < 128) pz.load(pbase + zch, nsp, io.split_stride);
-    if (t == 0) {
-        pa.load(pbase + zoff + h, nsp, io.split_stride);
-        pb.load(pbase + zoff + H + h, nsp, io.split_stride);
-    }
+    Split8 pc, pg;
+    pc.load(pbase + ch, nsp, io.split_stride);
+    if (t < 2) pg.load(pbase + gch, nsp, io.split_stride);
     asm volatile("" ::: "memory");  // keeps the loads above ahead of the tile's
     load_tile_t_issue(tv, S);  // in flight while the conv runs
     float inv = 1.0f;
@@ -146,10 +117,12 @@ __global__ __launch_bounds__(kGdnThreads) void k_gdn_decode(const float* __restr
         inv = 1.0f / sqrtf(block_sum(ss_in, sh.red) / (float)io.k_in + io.eps);
         __syncthreads();  // sh.red is reused below
     }
+    const float x = pc.sum(pbase + ch, nsp, io.split_stride) * inv;
+    const float gx = t < 2 ? pg.sum(pbase + gch, nsp, io.split_stride) * inv : 0.0f;
+    if (t >= 384) sh.z[t - 384] = x;
 
     float val = 0.0f;
     if (t < 384) {
-        const float x = pc.sum(pbase + ch, nsp, io.split_stride) * inv;
         float* st = conv_state + (size_t)ch * 4;
         const float* cw = conv_w + (size_t)ch * 4;
         const float s0 = st[0], s1 = st[1], s2 = st[2];
@@ -157,39 +130,59 @@ __global__ __launch_bounds__(kGdnThreads) void k_gdn_decode(const float* __restr
         st[0] = s1; st[1] = s2; st[2] = x;
         val = silu(y);
     }
-    stage_tile_t(tv, tile);
     const float ss = wave_sum(val * val);
     if (lane == 0) sh.red[w] = ss;
     __syncthreads();
     if (t < 128) sh.q[t] = val * (1.0f / sqrtf(sh.red[0] + sh.red[1] + 1e-6f)) * 0.08838834764831845f;
     else if (t < 256) sh.k[t - 128] = val * (1.0f / sqrtf(sh.red[2] + sh.red[3] + 1e-6f));
     else if (t < 384) sh.v[t - 256] = val;
-    if (t == 0) {
-        const float ga = pa.sum(pbase + zoff + h, nsp, io.split_stride) * inv;
-        const float gb = pb.sum(pbase + zoff + H + h, nsp, io.split_stride) * inv;
-        sh.g = expf(prm[H + h] * logf(1.0f + expf(ga + prm[h])));
-        sh.beta = 1.0f / (1.0f + expf(-gb));
-    }
+    if (t == 0) sh.g = expf(prm[H + h] * logf(1.0f + expf(gx + prm[h])));
+    if (t == 1) sh.beta = 1.0f / (1.0f + expf(-gx));
     __syncthreads();
     if (w == 0) {
         float p = sh.k[lane] * sh.q[lane] + sh.k[lane + 64] * sh.q[lane + 64];
         p = wave_sum(p);
         if (lane == 0) sh.kq = p;
     }
-    __syncthreads();  // also orders the staged tile before the reads below
-    read_tile_t(s, tile, col, qq);
-    const float o = delta_token(s, sh, col, qq);
-    write_tile_t(s, tile, col, qq);  // only this thread's slots: no hazard with the reads above
-    // gated RMSNorm over the head's dv outputs (quarter 0 = waves 0 and 1)
-    const float oo = wave_sum(o * o);
     __syncthreads();
-    store_tile_t(tile, S);
+    // The delta rule on the tile as loaded: thread t holds keys 4 (t % 32)..+3 of the value
+    // columns t / 32 + 16 r (r = 0..7), so each column lies in one half-wave and its S^T k and
+    // S^T q are half-wave sums; the updated pieces are stored back where they were read.
+    {
+        const int kb = 4 * (t & 31), hw = t >> 5;
+        const f4v k4 = *(const f4v*)&sh.k[kb], q4 = *(const f4v*)&sh.q[kb];
+        const float g = sh.g, beta = sh.beta, kq = sh.kq;
+#pragma unroll
+        for (int r = 0; r < 8; r++) {
+            float sk = tv[r].x * k4.x, sq = tv[r].x * q4.x;
+            sk = fmaf(tv[r].y, k4.y, sk);
+            sq = fmaf(tv[r].y, q4.y, sq);
+            sk = fmaf(tv[r].z, k4.z, sk);
+            sq = fmaf(tv[r].z, q4.z, sq);
+            sk = fmaf(tv[r].w, k4.w, sk);
+            sq = fmaf(tv[r].w, q4.w, sq);
+            sk = half_sum_dpp(sk, lane);
+            sq = half_sum_dpp(sq, lane);
+            const int c = hw + 16 * r;
+            const float d = beta * (sh.v[c] - g * sk);
+            tv[r].x = fmaf(g, tv[r].x, d * k4.x);
+            tv[r].y = fmaf(g, tv[r].y, d * k4.y);
+            tv[r].z = fmaf(g, tv[r].z, d * k4.z);
+            tv[r].w = fmaf(g, tv[r].w, d * k4.w);
+            if ((t & 31) == 0) sh.o[c] = g * sq + d * kq;
+        }
+#pragma unroll
+        for (int r = 0; r < 8; r++) __builtin_nontemporal_store(tv[r], (f4v*)S + t + kGdnThreads * r);
+    }
+    __syncthreads();
+    // gated RMSNorm over the head's dv outputs (threads 0..127 = waves 0 and 1, one column each)
+    const float o = t < kDV ? sh.o[t] : 0.0f;
+    const float oo = wave_sum(o * o);
     if (lane == 0) sh.red[w] = oo;
     __syncthreads();
-    if (qq == 0) {
+    if (t < kDV) {
         const float rinv = 1.0f / sqrtf((sh.red[0] + sh.red[1]) / (float)kDV + 1e-6f);
-        const float z = pz.sum(pbase + zch, nsp, io.split_stride) * inv;
-        const float y = o * rinv * silu(z) * prm[2 * H + col];
+        const float y = o * rinv * silu(sh.z[col]) * prm[2 * H + col];
         if (out) out[h * kDV + col] = y;
         if (io.frag_out)  // waves 0 and 1: 64 columns of the row each
             emit_x(io.frag_out, (size_t)(H * kDV / kChunk) * kChunkBytes, b, h * kDV + col, y, 1.0f, io.order_out, lane);
