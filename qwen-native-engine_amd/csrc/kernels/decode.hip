@@ -1175,6 +1175,14 @@ __device__ __forceinline__ void decode_program(const DecodeArgs& a) {
     e.bail = &bail;
     unsigned long long tts[8];
     e.tt = tts;
+    // profiling: the workgroup's place, (XCC_ID << 32 | HW_ID) + 1, kept in sub-step slot 6
+    unsigned long long where = 0;
+    if (a.sub) {
+        unsigned xcc, hw;
+        asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+        asm volatile("s_getreg_b32 %0, hwreg(HW_REG_HW_ID)" : "=s"(hw));
+        where = (((unsigned long long)xcc << 32) | hw) + 1ull;
+    }
     Ctl c{a.err, a.spin_limit, &bail};
     CBufs* prog = (CBufs*)a.prog;
     CPhase* shapes = (CPhase*)a.shapes;
@@ -1240,6 +1248,7 @@ __device__ __forceinline__ void decode_program(const DecodeArgs& a) {
             if (a.sub) {
 #pragma unroll
                 for (int k = 0; k < 8; k++) tts[k] = 0;
+                tts[6] = where;  // not a timestamp: where this workgroup runs
             }
             switch (P.kind) {
                 case PH_GEMV: {

@@ -134,7 +134,8 @@ struct DecodeArgs {
     // rows done, 3 all rows published. GDN: 1 input staged, 2 state update published. Attention
     // partials: 1 input staged, 2 q/k normed and rotated, 3 context loop done, 4 partials
     // published. Combine: 1 partials staged, 2 gate staged, 3 published. Region phases: 7 the DMA
-    // of the region phase two ahead issued.
+    // of the region phase two ahead issued. Slot 6 is not a timestamp: (XCC_ID << 32 | HW_ID) + 1
+    // of the workgroup.
     unsigned long long* sub = nullptr;
 };
 

@@ -964,7 +964,7 @@ std::string Model::profile_token_json() {
                 if (q[0] == 0) continue;
                 int last = 0, n = 0;
                 for (int k2 = 1; k2 < 8; k2++) {
-                    if (q[k2] == 0) continue;
+                    if (q[k2] == 0 || k2 == 6) continue;  // slot 6: the workgroup's place
                     if ((int)parts.size() <= n) parts.resize(n + 1);
                     parts[n++].push_back(ms(q[last], q[k2]));
                     last = k2;
@@ -1010,7 +1010,7 @@ std::string Model::profile_token_json() {
                     const unsigned long long* q = sub.data() + 8 * ((size_t)b * grid + w);
                     subt += w ? ",[" : "[";
                     for (int k2 = 0; k2 < 8; k2++) {
-                        const long long d = pub_prev && q[k2] ? (long long)q[k2] - (long long)pub_prev : -1;
+                        const long long d = k2 == 6 ? -1 : pub_prev && q[k2] ? (long long)q[k2] - (long long)pub_prev : -1;
                         subt += (k2 ? "," : "") + std::to_string(d);
                     }
                     subt += "]";
@@ -1050,6 +1050,14 @@ std::string Model::profile_token_json() {
     char head[200];
     std::snprintf(head, sizeof head, "{\"total_ms\":%.5f,\"tail_ms\":%.5f,\"tick_ms\":%.3g,", ms(tr[0], tr[1]),
                   ms(prev, tr[1]), tick_ms);
+    // each workgroup's place: XCC_ID and the HW_ID register (CU, SIMD, shader array / engine bits)
+    std::string places = "[";
+    for (int w = 0; w < grid; w++) {
+        const unsigned long long v = sub[8 * (size_t)w + 6];
+        places += (w ? "," : "") + (v ? "[" + std::to_string((v - 1) >> 32) + "," + std::to_string((v - 1) & 0xFFFFFFFFull) + "]"
+                                      : std::string("null"));
+    }
+    places += "]";
     std::string subs = "{";
     for (auto& kv : sub_l) {
         subs += (subs.size() > 1 ? ",\"" : "\"") + kv.first + "\":[";
@@ -1071,7 +1079,7 @@ std::string Model::profile_token_json() {
            ",\"phase_columns\":[\"label\",\"span\",\"compute_median\",\"compute_max\",\"handover_median\",\"handover_max\"]" +
            ",\"phases\":" + phases +
            ",\"chain_columns\":[\"label\",\"input_median\",\"input_max\",\"published_median\",\"published_max\"]" +
-           ",\"chain\":" + chain + "]" + ",\"publish_ticks\":" + pubs + "],\"input_ticks\":" + ins + "],\"sub_ticks\":" + subt + "]}";
+           ",\"chain\":" + chain + "]" + ",\"publish_ticks\":" + pubs + "],\"input_ticks\":" + ins + "],\"sub_ticks\":" + subt + "],\"places\":" + places + "}";
 }
 
 }  // namespace qne
