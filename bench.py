@@ -574,6 +574,37 @@ def bench_stream(args) -> dict:
             "cpu_baseline": None}
 
 
+def bench_exchange(args) -> dict:
+    """The hand-over probe (qne_exchange_probe): the all-to-all exchange of a tagged 2048-value
+    vector that every phase of the persistent decode kernel pays, without its compute or its weight
+    stream, at 8 / 32 / 64 / 128 / 256 co-resident workgroups (256: one per CU, the decode
+    kernel's grid). `value` is the time of one exchange round at 256 workgroups. For scale, the
+    first line is two workgroups exchanging one value each (a store seen by one other poller)."""
+    import ctypes
+    import qne
+    hip = _Hip()
+    lib = qne.load_library()
+    n, rounds = 2048, 2002
+    buf = hip.malloc(2 * n * 8)
+    ctl = hip.malloc(64)
+    runs = []
+    for wgs, nv in ((2, 2), (8, n), (32, n), (64, n), (128, n), (256, n)):
+        for rep in range(2):
+            hip.fill32(buf, 0, 2 * n * 2)
+            us = ctypes.c_double()
+            hip.ck(lib.qne_exchange_probe(buf, nv, rounds, wgs, ctl, ctypes.byref(us)), "qne_exchange_probe")
+            runs.append({"workgroups": wgs, "values": nv, "rep": rep, "us_per_round": round(us.value, 3)})
+    hip.free(buf)
+    hip.free(ctl)
+    best = min(r["us_per_round"] for r in runs if r["workgroups"] == 256)
+    return {"metric": "hand-over round us (256 workgroups, 2048-value tagged vector)", "value": best, "unit": "us",
+            "n_gpus": 1, "steps": rounds - 2, "warmup": 2, "ms_per_step": round(best / 1e3, 6), "higher_is_better": False,
+            "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+            "config": {"workload": "all-to-all exchange of a 2048-value tagged vector, 2000 rounds",
+                       "threads_per_workgroup": 512},
+            "roofline": None, "detail": {"runs": runs}, "cpu_baseline": None}
+
+
 def copy_calibration(mib: int) -> None:
     """A plain device-to-device copy of a known size: under a hardware-counter profiler its
     FETCH_SIZE / WRITE_SIZE readings per dispatch, divided into the bytes it must move, give the
@@ -600,7 +631,8 @@ def main():
     ap.add_argument("--config", default="2b",
                     help="2b (the decode benchmark), 0.8b (f16 weights, 128-id prompt, 128 steps), batch "
                          "(64-sequence batched decode), sample (sampled decode with the device sampler), stream "
-                         "(the read-bandwidth and dispatch-cost probes), or the kernel microbenches attn / gdn / gemv")
+                         "(the read-bandwidth and dispatch-cost probes), exchange (the decode kernel's hand-over "
+                         "probe), or the kernel microbenches attn / gdn / gemv")
     ap.add_argument("--batch", type=int, default=64, help="sequences (--config attn / batch)")
     ap.add_argument("--stream-workgroups", type=int, default=2048, help="workgroups of the --config stream probe")
     ap.add_argument("--cpu-tokens", type=int, default=4)
@@ -634,6 +666,10 @@ def main():
     if args.config == "stream":
         sys.path[:0] = [str(ROOT / "qwen-native-engine_amd")]
         print(json.dumps(bench_stream(args)))
+        return
+    if args.config == "exchange":
+        sys.path[:0] = [str(ROOT / "qwen-native-engine_amd")]
+        print(json.dumps(bench_exchange(args)))
         return
     if args.config == "sample":
         sys.path[:0] = [str(ROOT / "qwen-native-engine_amd")]

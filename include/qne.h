@@ -199,6 +199,15 @@ int qne_stream_read(const void* data, size_t bytes, uint32_t* sink, uint32_t wor
 /* The dispatch-cost probe: `noop` (kernels/src/shaders.rs:719-729) timed by dispatch_cost
  * (kernels/src/lib.rs:718-724). One 64-thread workgroup adds 1 to y[0]. Enqueued on `stream`. */
 int qne_noop_dispatch(float* y, void* stream);
+/* The hand-over probe. No counterpart in the reference: it measures the cost the persistent decode
+ * kernel pays at each of its phases, for its callers' and maintainers' capacity planning. buf holds
+ * 2 n uint64 entries (zeroed before the first call), ctl 2 (device memory). `workgroups`
+ * 512-thread workgroups, all resident at once (cooperative launch on the null stream), exchange
+ * an n-value vector `rounds` times: each publishes its share as (value, tag) pairs with
+ * agent-scope stores and polls the whole vector until every tag is the round's, as the decode
+ * kernel's phases do. Waits for the device; *us_per_round = the mean round over rounds 3..rounds
+ * (workgroup 0's wall clock). QNE_EDEVICE if a poll timed out. n even, 2..6144. */
+int qne_exchange_probe(uint64_t* buf, uint32_t n, uint32_t rounds, uint32_t workgroups, uint64_t* ctl, double* us_per_round);
 
 /* ---- token sampling on the device ----
  * src/sampling.rs Sampler (the agent's temperature + top-k + top-p sampler with presence penalty

@@ -403,6 +403,26 @@ int qne_stream_read(const void* data, size_t bytes, uint32_t* sink, uint32_t wor
     });
 }
 
+int qne_exchange_probe(uint64_t* buf, uint32_t n, uint32_t rounds, uint32_t workgroups, uint64_t* ctl, double* us_per_round) {
+    return guard([&] {
+        need(buf && ctl && us_per_round, "null argument");
+        need(n >= 2 && n <= 6144 && n % 2 == 0, "n must be even and in 2..6144");
+        need(rounds >= 3 && rounds <= (1u << 30), "rounds must be 3..2^30");
+        need(workgroups >= 1 && workgroups <= 65536, "workgroups must be 1..65536");
+        qne::hip_check(hipMemset(ctl, 0, 16), "exchange probe");
+        qne::hip_check(qne::launch_exchange_probe(buf, (int)n, (int)rounds, (int)workgroups, (unsigned long long*)ctl,
+                                                   (unsigned*)(ctl + 1), nullptr),
+                       "exchange probe (cooperative launch: the workgroups must fit on the device at once)");
+        qne::hip_check(hipDeviceSynchronize(), "exchange probe");
+        uint64_t h[2] = {0, 0};
+        qne::hip_check(hipMemcpy(h, ctl, sizeof h, hipMemcpyDeviceToHost), "exchange probe");
+        if (h[1] & 0xFFFFFFFFull) throw qne::Error(QNE_EDEVICE, "exchange probe: a poll timed out");
+        int khz = 0;
+        qne::hip_check(hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, 0), "exchange probe");
+        *us_per_round = khz > 0 ? (double)h[0] * 1000.0 / khz / (double)(rounds - 2) : 0.0;
+    });
+}
+
 int qne_noop_dispatch(float* y, void* stream) {
     return guard([&] {
         need(y != nullptr, "null argument");

@@ -34,6 +34,10 @@ void launch_set_tok(uint32_t* tok, const uint32_t* ids, int i, uint32_t pos, hip
 // [workgroups * 256], and a dispatch that does almost nothing.
 void launch_stream_read(const void* data, size_t bytes, uint32_t* sink, int workgroups, hipStream_t st);
 void launch_noop(float* y, hipStream_t st);
+// The hand-over probe (k_exchange_probe): `workgroups` co-resident 512-thread workgroups exchange
+// an n-value tagged vector `rounds` times through buf (2 n entries).
+hipError_t launch_exchange_probe(uint64_t* buf, int n, int rounds, int workgroups, unsigned long long* ticks, unsigned* err,
+                                 hipStream_t st);
 
 // Pseudo-random uniform [-amp, amp) fill of n f16 or f32 values (benchmark state).
 void launch_fill_uniform(void* p, size_t n, bool f16, uint64_t seed, float amp, hipStream_t st);

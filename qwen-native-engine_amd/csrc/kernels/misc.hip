@@ -64,6 +64,68 @@ __global__ void k_noop(float* y) {
     if (threadIdx.x == 0) y[0] = y[0] + 1.0f;
 }
 
+// Hand-over probe: the all-to-all exchange the persistent decode kernel pays at every phase, without
+// its compute or its weight stream. Each of the (co-resident) workgroups publishes its share of an
+// n-value vector every round: value o = round + o next to the 32-bit tag `round`, one 8-byte
+// agent-scope store per value, the workgroups interleaved (o = wg + workgroups * k). Then every
+// workgroup polls all n / 2 pairs with agent-scope 16-byte loads (up to 6 per thread in flight)
+// until each carries the round's tag, and ends the round with a barrier. Rounds alternate between
+// two buffers of n entries. ticks[0] = wall-clock ticks of workgroup 0 over rounds 3..rounds;
+// err[0] = 1 after a poll spins 2^20 times (then every workgroup stops).
+__global__ __launch_bounds__(512, 1) void k_exchange_probe(uint64_t* __restrict__ buf, int n, int rounds,
+                                                           unsigned long long* __restrict__ ticks, unsigned* __restrict__ err) {
+    constexpr int kT = 512, kP = 6;
+    const int wg = blockIdx.x, nwg = gridDim.x, np = n / 2;
+    __shared__ int bail;
+    __shared__ float sink[2 * kT * kP];
+    if (threadIdx.x == 0) bail = 0;
+    __syncthreads();
+    unsigned long long t0 = 0;
+    for (int r = 1; r <= rounds; r++) {
+        if (r == 3) t0 = __builtin_amdgcn_s_memrealtime();
+        uint64_t* b = buf + (size_t)(r & 1) * n;
+        for (int o = wg + nwg * (int)threadIdx.x; o < n; o += nwg * kT)
+            __hip_atomic_store(b + o, ((uint64_t)r << 32) | __float_as_uint((float)(r + o)), __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(b, (short)0, n * 8, 0x00020000);
+        unsigned pend = 0;
+#pragma unroll
+        for (int j = 0; j < kP; j++)
+            if (j * kT + (int)threadIdx.x < np) pend |= 1u << j;
+        unsigned spins = 0;
+        while (pend) {
+            u32x4 v[kP];
+#pragma unroll
+            for (int j = 0; j < kP; j++)
+                if ((pend >> j) & 1u) v[j] = __builtin_amdgcn_raw_buffer_load_b128(rs, 16 * (j * kT + (int)threadIdx.x), 0, 16);
+#pragma unroll
+            for (int j = 0; j < kP; j++) {
+                if (((pend >> j) & 1u) && v[j].y == (unsigned)r && v[j].w == (unsigned)r) {
+                    const int q = j * kT + (int)threadIdx.x;
+                    sink[2 * q] = __uint_as_float(v[j].x);
+                    sink[2 * q + 1] = __uint_as_float(v[j].z);
+                    pend &= ~(1u << j);
+                }
+            }
+            asm volatile("" ::: "memory");  // every spin loads again
+            if (pend && ++spins > (1u << 20)) {
+                err[0] = 1u;
+                bail = 1;
+                break;
+            }
+        }
+        __syncthreads();
+        if (bail) break;
+    }
+    if (wg == 0 && threadIdx.x == 0) ticks[0] = __builtin_amdgcn_s_memrealtime() - t0;
+}
+
+hipError_t launch_exchange_probe(uint64_t* buf, int n, int rounds, int workgroups, unsigned long long* ticks, unsigned* err,
+                                 hipStream_t st) {
+    void* args[] = {&buf, &n, &rounds, &ticks, &err};
+    return hipLaunchCooperativeKernel((const void*)k_exchange_probe, dim3(workgroups), dim3(512), args, 0, st);
+}
+
 void launch_stream_read(const void* data, size_t bytes, uint32_t* sink, int workgroups, hipStream_t st) {
     hipLaunchKernelGGL(k_stream_read, dim3(workgroups), dim3(256), 0, st, (const u32x4*)data, bytes / 16, sink);
 }

@@ -86,6 +86,7 @@ def load_library(path: str | os.PathLike | None = None):
         "qne_logits_device": ([c_p, ctypes.POINTER(c_p)], c_i),
         "qne_stream_read": ([c_p, c_sz, c_p, c_u32, c_p], c_i),
         "qne_noop_dispatch": ([c_p, c_p], c_i),
+        "qne_exchange_probe": ([c_p, c_u32, c_u32, c_u32, c_p, ctypes.POINTER(ctypes.c_double)], c_i),
         "qne_sampler_create": ([c_f, c_u32, c_f, ctypes.c_uint64, c_f, c_u32, ctypes.POINTER(c_p)], c_i),
         "qne_sampler_free": ([c_p], c_i),
         "qne_sample": ([c_p, c_p, c_p, c_u32, c_u32, c_f, ctypes.POINTER(c_u32), c_p], c_i),

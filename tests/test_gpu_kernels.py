@@ -309,6 +309,26 @@ def test_gdn_prefill_config4_shape():
     assert rel_err(d[5].numpy(), want_S) < 1e-4
 
 
+@pytest.mark.parametrize("workgroups,n,rounds", [(2, 2, 5), (8, 2048, 11), (64, 2048, 8)])
+def test_exchange_probe_runs_every_round(workgroups, n, rounds):
+    """The hand-over probe: every round every workgroup publishes its share and sees everyone's, so
+    after the last round its buffer holds every value of that round, tagged with it (value r + o at
+    entry o), and the other buffer those of the round before."""
+    import ctypes
+    lib = Q.load_library()
+    buf, ctl = D.zeros(2 * n, np.uint64), D.zeros(2, np.uint64)
+    us = ctypes.c_double()
+    assert lib.qne_exchange_probe(buf.ptr, n, rounds, workgroups, ctl.ptr, ctypes.byref(us)) == 0
+    assert us.value > 0.0
+    got = buf.numpy().reshape(2, n)
+    for r in (rounds, rounds - 1):
+        e = got[r & 1]
+        assert np.all((e >> np.uint64(32)) == r)
+        vals = (e & np.uint64(0xFFFFFFFF)).astype(np.uint32).view(np.float32)
+        np.testing.assert_array_equal(vals, (r + np.arange(n)).astype(np.float32))
+    assert lib.qne_exchange_probe(buf.ptr, 3, rounds, workgroups, ctl.ptr, ctypes.byref(us)) == Q.EINVAL
+
+
 @pytest.mark.parametrize("words,groups", [(4 * 1000003, 64), (4 * 256 * 4, 1), (4 * 7, 3)])
 def test_stream_read_probe_reads_every_word_once(words, groups):
     """The streaming-read probe (shaders.rs:701-717) folds every 16-byte word into the sink: the xor
