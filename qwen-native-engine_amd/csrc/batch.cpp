@@ -159,6 +159,7 @@ BatchDecoder::BatchDecoder(Model& m, int max_rows, int max_context) : m_(m), max
         picks_ = (uint32_t*)dalloc(kRowsMax * 4);
         am_scratch_ = dalloc(argmax_rows_scratch(kRowsMax));
         pos_ = (int32_t*)dalloc(kRowsMax * 4);
+        order_ = (int32_t*)dalloc(kRowsMax * 4);
         QNE_HIP(hipMemset(tokens_, 0, kRowsMax * 4));
         QNE_HIP(hipMemset(pos_, 0, kRowsMax * 4));
         QNE_HIP(hipHostMalloc((void**)&host_u32_, 2 * kRowsMax * 4, hipHostMallocDefault));
@@ -199,7 +200,7 @@ void BatchDecoder::enqueue_step(int n) {
     const auto order = operand_order;
     const DevLayer& first = m_.layers_.front();
     launch_embed_rows(m_.embed_.kind, m_.embed_.w, m_.embed_.sz, m_.embed_.group, c.hidden, tokens_, n, h_, frag_a_,
-                      first.input_norm, order(first.in), stream_);
+                      first.input_norm, order(first.in), stream_, pos_, order_);
     auto gemm = [&](const DevMat& W, uint8_t* frag, int norm, float* y, int y_stride, int epi, uint8_t* frag_out,
                     const float* gain_out, int order_out) {
         rows_gemm(W, n, c.eps, frag, norm, part_, y, y_stride, epi, frag_out, gain_out, order_out, stream_);
@@ -231,6 +232,7 @@ void BatchDecoder::enqueue_step(int n) {
             a.nkv = c.n_kv_heads;
             a.rope_dim = c.rope_dim;
             a.splits = splits;
+            a.order = order_;
             a.max_blocks = max_blocks_;
             a.rows = n;
             a.bt_stride = max_blocks_;

@@ -96,6 +96,7 @@ class BatchDecoder {
     size_t attn_part_rows_ = 0;  // rows * splits the attention partials hold
     uint32_t *tokens_ = nullptr, *picks_ = nullptr, *ids_ = nullptr;
     int32_t* pos_ = nullptr;
+    int32_t* order_ = nullptr;  // the step's rows by decreasing position (attention partials' order)
     void* am_scratch_ = nullptr;  // per-row argmax partials
     uint32_t* host_u32_ = nullptr;  // pinned, 2 * 64 entries
     double last_ms_ = 0.0;

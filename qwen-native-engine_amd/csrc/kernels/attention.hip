@@ -173,12 +173,13 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_partial(const float* __re
                                                                const uint16_t* __restrict__ v_pool,
                                                                const int32_t* __restrict__ block_table, int max_blocks,
                                                                int bt_stride, const int32_t* __restrict__ lens, int nkv,
+                                                               const int32_t* __restrict__ order,
                                                                float* __restrict__ part_ml, float* __restrict__ part_acc) {
     __shared__ __attribute__((aligned(16))) uint16_t s_q[G][2][kHD];  // per head: hi, lo halves as f16
     __shared__ __attribute__((aligned(16))) float s_p[4][16][4];      // per wave: weights [position][head]
     __shared__ float s_ml[4][G][2];
     __shared__ __attribute__((aligned(16))) float s_acc[4][G][kHD];
-    const int split = blockIdx.x, g = blockIdx.y, b = blockIdx.z, splits = gridDim.x;
+    const int split = blockIdx.x, g = blockIdx.y, b = order ? order[blockIdx.z] : (int)blockIdx.z, splits = gridDim.x;
     const int t = threadIdx.x, lane = t % kWave, w = t / kWave;
     const int len = max(1, min(lens[b] + 1, max_blocks * kBlock));  // never past the block table
     int per = (len + splits - 1) / splits;
@@ -338,18 +339,18 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_combine(const float* __re
 template <int G>
 static void launch_partial(const float* q, const uint16_t* kp, const uint16_t* vp, const int32_t* bt, int max_blocks,
                            int bt_stride, const int32_t* lens, int nkv, float* ml, float* acc, int splits, int batch,
-                           hipStream_t st) {
+                           hipStream_t st, const int32_t* order = nullptr) {
     hipLaunchKernelGGL((k_attn_partial<G>), dim3(splits, nkv, batch), dim3(kAttnThreads), 0, st, q, kp, vp, bt,
-                       max_blocks, bt_stride, lens, nkv, ml, acc);
+                       max_blocks, bt_stride, lens, nkv, order, ml, acc);
 }
 
 static void partial_by_g(int G, const float* q, const uint16_t* kp, const uint16_t* vp, const int32_t* bt, int max_blocks,
                          int bt_stride, const int32_t* lens, int nkv, float* ml, float* acc, int splits, int batch,
-                         hipStream_t st) {
+                         hipStream_t st, const int32_t* order = nullptr) {
     switch (G) {
-        case 1: launch_partial<1>(q, kp, vp, bt, max_blocks, bt_stride, lens, nkv, ml, acc, splits, batch, st); break;
-        case 2: launch_partial<2>(q, kp, vp, bt, max_blocks, bt_stride, lens, nkv, ml, acc, splits, batch, st); break;
-        default: launch_partial<4>(q, kp, vp, bt, max_blocks, bt_stride, lens, nkv, ml, acc, splits, batch, st); break;
+        case 1: launch_partial<1>(q, kp, vp, bt, max_blocks, bt_stride, lens, nkv, ml, acc, splits, batch, st, order); break;
+        case 2: launch_partial<2>(q, kp, vp, bt, max_blocks, bt_stride, lens, nkv, ml, acc, splits, batch, st, order); break;
+        default: launch_partial<4>(q, kp, vp, bt, max_blocks, bt_stride, lens, nkv, ml, acc, splits, batch, st, order); break;
     }
 }
 
@@ -367,7 +368,7 @@ void launch_attention_rows(const AttnRowsArgs& a, hipStream_t st) {
     hipLaunchKernelGGL(k_attn_prep_rows, dim3(a.nq + a.nkv, a.rows), dim3(kAttnThreads), 0, st, a);
     const int G = a.nq / a.nkv;
     partial_by_g(G, a.qbuf, a.k_pool, a.v_pool, a.block_table, a.max_blocks, a.bt_stride, a.pos, a.nkv, a.part_ml,
-                 a.part_acc, a.splits, a.rows, st);
+                 a.part_acc, a.splits, a.rows, st, a.order);
     const float* gate = a.part ? a.gate_dst + a.nq * kHD : a.proj + a.nq * kHD;
     hipLaunchKernelGGL(k_attn_combine, dim3(a.nq, a.rows), dim3(kAttnThreads), 0, st, a.part_ml, a.part_acc, a.nkv, G,
                        a.splits, gate, (int)a.proj_stride, a.out, a.frag_out, a.order_out);

@@ -312,8 +312,20 @@ __global__ __launch_bounds__(256) void k_gemm_reduce(const GemmArgs a) {
 __global__ __launch_bounds__(256) void k_embed_rows(int kind, const void* __restrict__ W, const uint32_t* __restrict__ SZ,
                                                     int group, int hidden, const uint32_t* __restrict__ tokens,
                                                     float* __restrict__ h, uint8_t* __restrict__ frag,
-                                                    const float* __restrict__ gain, int q4order) {
+                                                    const float* __restrict__ gain, int q4order,
+                                                    const int32_t* __restrict__ pos, int32_t* __restrict__ order) {
     const int r = blockIdx.y, c = blockIdx.x * 256 + threadIdx.x;
+    if (order && blockIdx.x == 0 && blockIdx.y == 0 && (int)threadIdx.x < (int)gridDim.y) {
+        // rank of row t by decreasing position, ties to the lower row
+        const int t = threadIdx.x, m = gridDim.y;
+        const int pt = pos[t];
+        int rank = 0;
+        for (int u = 0; u < m; u++) {
+            const int pu = pos[u];
+            rank += pu > pt || (pu == pt && u < t);
+        }
+        order[rank] = t;
+    }
     if ((threadIdx.x & ~63) + blockIdx.x * 256 >= hidden) return;  // whole waves
     const size_t tok = tokens[r];
     float v;
@@ -466,9 +478,11 @@ void launch_gemm(GemmArgs a, hipStream_t st) {
 }
 
 void launch_embed_rows(int kind, const void* W, const uint32_t* SZ, int group, int hidden, const uint32_t* tokens, int m,
-                       float* h, uint8_t* frag, const float* gain, int q4order, hipStream_t st) {
+                       float* h, uint8_t* frag, const float* gain, int q4order, hipStream_t st, const int32_t* pos,
+                       int32_t* order) {
+    if (order && m > 256) order = nullptr;  // one thread per row: larger batches keep the row order
     hipLaunchKernelGGL(k_embed_rows, dim3((hidden + 255) / 256, m), dim3(256), 0, st, kind, W, SZ, group, hidden, tokens,
-                       h, frag, gain, q4order);
+                       h, frag, gain, q4order, order ? pos : nullptr, order);
 }
 
 size_t argmax_rows_scratch(int m) { return (size_t)m * kArgParts * 8; }

@@ -97,6 +97,9 @@ struct AttnRowsArgs {
     float* out;                  // [rows][nq][hd]
     int nq, nkv, rope_dim, splits, max_blocks, rows;
     int bt_stride;               // entries between rows of block_table (0: one shared row)
+    // With order, the partials' workgroups take the rows in that order (longest context first, so
+    // the longest workgroups start first); the results do not depend on it.
+    const int32_t* order = nullptr;
     // With `part`, the projection is the in-projection's split partials (splits x split_stride
     // floats, rows n apart) summed here in split order times the row's 1 / rms (from the sums of
     // x^2 of its operand x_in, K = k_in): the GEMM's reduce folded in. The gate, which the
@@ -216,8 +219,11 @@ void launch_gemm(GemmArgs a, hipStream_t st);
 void launch_stage_x(const float* x, int x_stride, int m, int K, const float* gain, int q4order, uint8_t* frag,
                     hipStream_t st);
 // h[r] = embedding row tokens[r], r < m; with frag, h * gain is also staged as a GEMM's x operand.
+// With order, order[0..m) = the rows 0..m-1 by decreasing pos (ties: lower row first), the order
+// the attention partials run them in.
 void launch_embed_rows(int kind, const void* W, const uint32_t* SZ, int group, int hidden, const uint32_t* tokens, int m,
-                       float* h, uint8_t* frag, const float* gain, int q4order, hipStream_t st);
+                       float* h, uint8_t* frag, const float* gain, int q4order, hipStream_t st,
+                       const int32_t* pos = nullptr, int32_t* order = nullptr);
 // Greedy pick per row into out[r]; with `tokens`, also tokens[r] = pick and pos[r] += 1. `scratch`
 // holds argmax_rows_scratch(m) bytes.
 size_t argmax_rows_scratch(int m);
