@@ -316,9 +316,9 @@ int qne_paged_attn_decode(const float* q, const float* k_new, const float* v_new
         if (splits > max_blocks) splits = max_blocks;
         const size_t parts = (size_t)batch * nkv * splits * G;
         hipStream_t st = (hipStream_t)stream;
-        float* ws = workspace(kWsAttention, parts * 258 * 4);
+        float* ws = workspace(kWsAttention, parts * 258 * 4 + (size_t)batch * 4);
         qne::launch_paged_attn(q, k_new, v_new, (uint16_t*)k_pool, (uint16_t*)v_pool, block_table, max_blocks, ctx,
-                               out, batch, nq, nkv, ws, ws + parts * 2, splits, st);
+                               out, batch, nq, nkv, ws, ws + parts * 2, splits, st, (int32_t*)(ws + parts * 258));
         check_launch();
         // the null stream keeps the call synchronous; on a caller's stream it is ordered like a kernel
         if (!stream) qne::hip_check(hipStreamSynchronize(st), "paged attention");
@@ -339,15 +339,15 @@ int qne_paged_attn_decode_noalloc(const float* q, const float* k_new, const floa
         if (splits < 1) splits = 1;
         if (splits > max_blocks) splits = max_blocks;
         const size_t parts = (size_t)batch * nkv * splits * G;
-        const size_t bytes = parts * 258 * 4;
+        const size_t bytes = parts * 258 * 4 + (size_t)batch * 4;  // partials, then the sequences' order
         if (bytes > qne::kNoAllocScratchBytes)
             throw qne::Error(QNE_EINVAL, "qne_paged_attn_decode_noalloc: this call needs " + std::to_string(bytes) +
-                                             " bytes of split partials; its fixed scratch holds " +
+                                             " bytes of scratch (split partials and the sequences' order); its fixed scratch holds " +
                                              std::to_string(qne::kNoAllocScratchBytes) + " (use qne_paged_attn_decode)");
         float* ws = qne::noalloc_scratch();
         hipStream_t st = (hipStream_t)stream;
         qne::launch_paged_attn(q, k_new, v_new, (uint16_t*)k_pool, (uint16_t*)v_pool, block_table, max_blocks, ctx,
-                               out, batch, nq, nkv, ws, ws + parts * 2, splits, st);
+                               out, batch, nq, nkv, ws, ws + parts * 2, splits, st, (int32_t*)(ws + parts * 258));
         check_launch();
         if (!stream) qne::hip_check(hipStreamSynchronize(st), "paged attention");
     });

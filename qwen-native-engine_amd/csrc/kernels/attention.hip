@@ -137,8 +137,18 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_prep_rows(AttnRowsArgs a)
 __global__ __launch_bounds__(kAttnThreads) void k_kv_append(const float* __restrict__ k_new, const float* __restrict__ v_new,
                                                             uint16_t* __restrict__ k_pool, uint16_t* __restrict__ v_pool,
                                                             const int32_t* __restrict__ bt, int max_blocks,
-                                                            const int32_t* __restrict__ ctx, int nkv) {
+                                                            const int32_t* __restrict__ ctx, int nkv, int32_t* __restrict__ order) {
     const int g = blockIdx.x, b = blockIdx.y, t = threadIdx.x;
+    if (order && g == 0 && b == 0 && t < (int)gridDim.y) {
+        // rank of sequence t by decreasing context, ties to the lower index
+        const int m = gridDim.y, ct = ctx[t];
+        int rank = 0;
+        for (int u = 0; u < m; u++) {
+            const int cu = ctx[u];
+            rank += cu > ct || (cu == ct && u < t);
+        }
+        order[rank] = t;
+    }
     if (ctx[b] < 0 || ctx[b] >= max_blocks * kBlock) return;  // beyond the table: nothing to write
     const size_t at = kv_index(bt + (size_t)b * max_blocks, ctx[b], nkv, g) + t;
     const size_t src = ((size_t)b * nkv + g) * kHD + t;
@@ -376,11 +386,13 @@ void launch_attention_rows(const AttnRowsArgs& a, hipStream_t st) {
 
 void launch_paged_attn(const float* q, const float* k_new, const float* v_new, uint16_t* k_pool, uint16_t* v_pool,
                        const int32_t* block_table, int max_blocks, const int32_t* ctx, float* out, int batch, int nq,
-                       int nkv, float* part_ml, float* part_acc, int splits, hipStream_t st) {
+                       int nkv, float* part_ml, float* part_acc, int splits, hipStream_t st, int32_t* order) {
+    if (batch > kAttnThreads) order = nullptr;  // one thread per sequence ranks them
     hipLaunchKernelGGL(k_kv_append, dim3(nkv, batch), dim3(kAttnThreads), 0, st, k_new, v_new, k_pool, v_pool,
-                       block_table, max_blocks, ctx, nkv);
+                       block_table, max_blocks, ctx, nkv, order);
     const int G = nq / nkv;
-    partial_by_g(G, q, k_pool, v_pool, block_table, max_blocks, max_blocks, ctx, nkv, part_ml, part_acc, splits, batch, st);
+    partial_by_g(G, q, k_pool, v_pool, block_table, max_blocks, max_blocks, ctx, nkv, part_ml, part_acc, splits, batch, st,
+                 order);
     hipLaunchKernelGGL(k_attn_combine, dim3(nq, batch), dim3(kAttnThreads), 0, st, part_ml, part_acc, nkv, G, splits,
                        (const float*)nullptr, 0, out, (uint8_t*)nullptr, 0);
 }

@@ -238,8 +238,10 @@ constexpr size_t kNoAllocScratchBytes = (size_t)8 << 20;
 float* noalloc_scratch();
 
 // Raw paged decode for `batch` sequences: append k/v at ctx[b], attend over 0..ctx[b].
+// With order (batch ints of scratch; used for batch <= 256), the append kernel ranks the sequences
+// by decreasing context and the partials take them longest first.
 void launch_paged_attn(const float* q, const float* k_new, const float* v_new, uint16_t* k_pool, uint16_t* v_pool,
                        const int32_t* block_table, int max_blocks, const int32_t* ctx, float* out, int batch, int nq,
-                       int nkv, float* part_ml, float* part_acc, int splits, hipStream_t st);
+                       int nkv, float* part_ml, float* part_acc, int splits, hipStream_t st, int32_t* order = nullptr);
 
 }  // namespace qne
