@@ -113,7 +113,8 @@ int qne_profile_token(qne_model* m, double* ms);
  * "sub_steps_median_ms" (per label, the medians of each phase kind's sub-steps); "chain" (per
  * phase: label, input-staged and published median / max, in ms after the previous phase's last
  * publish); and per phase and workgroup, in ticks after that same instant (-1: not recorded),
- * "publish_ticks", "input_ticks" and "sub_ticks" (the 8 sub-step timestamps). Labels are gdn.* /
+ * "publish_ticks", "input_ticks" and "sub_ticks" (the 8 sub-step timestamps; slot 6 is -1), and
+ * "places" (per workgroup: [XCC_ID, the HW_ID register]). Labels are gdn.* /
  * attn.* per layer phase and lm_head. QNE_EINVAL if cap is too small (the message names the size)
  * or the model was loaded with the graph engine. Diagnostic only; about 2 MB for the 2B model. */
 int qne_profile_token_json(qne_model* m, char* buf, size_t cap);

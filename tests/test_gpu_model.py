@@ -2,6 +2,8 @@
 
 Bar (BASELINE parity target): max |logit error| <= 1e-2 and identical greedy ids; the kernels are
 f32-accumulating, so the logits are expected far closer than that (checked at 1e-3 here)."""
+import json
+
 import numpy as np
 import pytest
 
@@ -278,3 +280,36 @@ def test_reference_format1_model_loads_and_matches():
     want = om.prefill_chunk(ids, 0, True)
     assert np.max(np.abs(m.logits() - want)) < 1e-3 * max(1.0, np.max(np.abs(want)))
     m.close()
+
+
+def test_profile_token_consumes_one_greedy_token_and_reports_every_phase(pair):
+    """Model::profile_token (model.rs:305): one greedy token, timed. The profiled token is the one a
+    plain greedy decode step takes from the same state, and the persistent engine's timeline names
+    every phase of the token and where each workgroup ran."""
+    name, m, om, index, _ = pair
+    ids = prompt(m.vocab, 24, 5)
+    m.reset()
+    m.prefill_batched(ids)
+    want = m.decode_ids(2, 1)  # the pending pick, then one greedy step from it
+    m.reset()
+    m.prefill_batched(ids)
+    assert m.profile_token() > 0.0
+    assert m.last_token() == (want[1], len(ids) + 1)
+    m.reset()
+    m.prefill_batched(ids)
+    try:
+        d = m.profile_token_detail()
+    except Q.QneError as e:  # the graph engine has no device timeline
+        assert e.code == Q.EINVAL
+        return
+    assert m.last_token() == (want[1], len(ids) + 1)
+    cfg = json.loads(index)["config"]
+    layers = cfg["layers"]
+    attn = sum(1 for i in range(layers) if (i + 1) % cfg["full_attention_every"] == 0)
+    assert len(d["phases"]) == 5 * (layers - attn) + 6 * attn + 1
+    assert all(v >= 0.0 for v in d["labels"].values())
+    phases = ("mixer_in", "gdn", "attention", "combine", "mixer_out", "gate_up", "down")
+    assert set(d["labels"]) <= {f"{k}.{p}" for k in ("gdn", "attn") for p in phases} | {"lm_head"}
+    places = d["places"]
+    assert len(places) == len(d["input_ticks"][0]) and all(p is not None and p[0] >= 0 for p in places)
+    assert d["total_ms"] > 0.0
