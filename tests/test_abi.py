@@ -229,3 +229,16 @@ def test_index_errors_come_before_tile_errors(tiny):
     prof["down"]["splits"] = 0
     rc, msg, _ = load_rc(bad_index, buf, {"tiles": prof})
     assert rc == Q.EFORMAT and "tile" not in msg
+
+
+def test_pack_sz_interleaves_scale_and_zero():
+    """qne_pack_sz_q4g: the device layout of a q4 matrix's group parameters is (scale, zero) pairs."""
+    lib = Q.load_library()
+    rng = np.random.default_rng(3)
+    scales = rng.integers(0, 2**16, size=37, dtype=np.uint16)
+    zeros = rng.integers(0, 2**16, size=37, dtype=np.uint16)
+    out = np.zeros(74, np.uint16)
+    assert lib.qne_pack_sz_q4g(scales.ctypes.data, zeros.ctypes.data, 37, out.ctypes.data) == 0
+    np.testing.assert_array_equal(out[0::2], scales)
+    np.testing.assert_array_equal(out[1::2], zeros)
+    assert lib.qne_pack_sz_q4g(None, zeros.ctypes.data, 37, out.ctypes.data) == Q.EINVAL

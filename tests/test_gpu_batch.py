@@ -154,6 +154,8 @@ def test_batch_continues_each_sequence_like_the_oracle(pair):
         assert list(pos) == lengths
         picks, logits = b.step(len(ps), logits=True)
         ids = b.decode(len(ps), steps - 1)
+        ms, n = b.last_decode_timing()  # the device time of the chained steps
+        assert n == steps - 1 and ms > 0.0
     for r, p in enumerate(ps):
         om.reset()
         want_ids, want_logits = om.greedy(p, steps + 1)

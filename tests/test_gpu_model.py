@@ -62,6 +62,8 @@ def test_decode_window_returns_every_id(pair):
     m.prefill_batched(ids)
     w8 = m.decode_ids(20, 8, [])
     assert w1 == w8 and len(w8) == 20
+    ms, steps = m.last_decode_timing()  # windows of 8, 8 and 3 steps after the pending id
+    assert steps == 19 and ms > 0.0
 
 
 def test_decode_windows_push_placeholders_like_the_reference(pair):
