@@ -220,8 +220,8 @@ __global__ __launch_bounds__(64 * (WAVES + DW)) void k_gemm(const GemmArgs a) {
 #pragma unroll
         for (int j = 0; j < 16; j++) {
             const int m = 8 * (j / 4) + 4 * hf + (j % 4);
-            pp[(size_t)m * a.N] = acc0[j];
-            pp[(size_t)(32 + m) * a.N] = acc1[j];
+            store_through(pp + (size_t)m * a.N, acc0[j]);
+            store_through(pp + (size_t)(32 + m) * a.N, acc1[j]);
         }
         return;
     }
@@ -246,12 +246,12 @@ __global__ __launch_bounds__(64 * (WAVES + DW)) void k_gemm(const GemmArgs a) {
         if (m < rows) {
             float* d = a.y + (size_t)(kBM * mt + m) * a.y_stride + n;
             const float v = acc0[j] * sinv[m];
-            *d = a.epi == EPI_ACCUMULATE ? *d + v : v;
+            store_through(d, a.epi == EPI_ACCUMULATE ? *d + v : v);
         }
         if (32 + m < rows) {
             float* d = a.y + (size_t)(kBM * mt + 32 + m) * a.y_stride + n;
             const float v = acc1[j] * sinv[32 + m];
-            *d = a.epi == EPI_ACCUMULATE ? *d + v : v;
+            store_through(d, a.epi == EPI_ACCUMULATE ? *d + v : v);
         }
     }
 }
@@ -299,7 +299,7 @@ __global__ __launch_bounds__(256) void k_gemm_reduce(const GemmArgs a) {
         if (a.epi == EPI_STORE) v = g;
         else if (a.epi == EPI_ACCUMULATE) v = *d + g;
         else v = silu(g) * u;
-        if (d) *d = v;
+        if (d) store_through(d, v);
     }
     if (a.frag_out)
         emit_x(a.frag_out, (size_t)(a.n_out / kChunk) * kChunkBytes, r, c, v, a.gain_out ? a.gain_out[live ? c : 0] : 1.0f,
@@ -336,7 +336,7 @@ __global__ __launch_bounds__(256) void k_embed_rows(int kind, const void* __rest
         const uint32_t sz = SZ[tok * (hidden / group) + c / group];
         v = ((float)((word >> (4 * (c % 8))) & 15u) - hi_h(sz)) * lo_h(sz);
     }
-    h[(size_t)r * hidden + c] = v;
+    store_through(h + (size_t)r * hidden + c, v);
     if (frag) emit_x(frag, (size_t)(hidden / kChunk) * kChunkBytes, r, c, v, gain ? gain[c] : 1.0f, q4order, threadIdx.x & 63);
 }
 
