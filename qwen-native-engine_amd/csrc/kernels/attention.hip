@@ -57,7 +57,7 @@ __device__ __forceinline__ size_t kv_index(const int32_t* bt, int pos, int nkv, 
 __device__ __forceinline__ float norm_rope(float x, const float* __restrict__ w, const float* __restrict__ inv_freq,
                                            int rope_dim, uint32_t pos, float* sh, float* red) {
     const int t = threadIdx.x;
-    const float ss = block_sum(x * x, red);
+    const float ss = block_sum<kAttnThreads>(x * x, red);
     const float y = x * (1.0f / sqrtf(ss / (float)kHD + 1e-6f)) * w[t];
     sh[t] = y;
     __syncthreads();
@@ -118,7 +118,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_prep_rows(AttnRowsArgs a)
     if (a.part || hb >= a.nq) p1.load(pbase + c1, nsp, a.split_stride);
     float inv = 1.0f;
     if (a.part) {
-        inv = 1.0f / sqrtf(block_sum(ss_in, red) / (float)a.k_in + a.eps);  // row_inv_rms
+        inv = 1.0f / sqrtf(block_sum<kAttnThreads>(ss_in, red) / (float)a.k_in + a.eps);  // row_inv_rms
         __syncthreads();  // red is reused below
     }
     const float x0 = p0.sum(pbase + c0, nsp, a.split_stride) * inv;

@@ -264,26 +264,28 @@ __global__ __launch_bounds__(64 * (WAVES + DW)) void k_gemm(const GemmArgs a) {
 __global__ __launch_bounds__(256) void k_gemm_reduce(const GemmArgs a) {
     __shared__ float red[16];
     const int c = blockIdx.x * 256 + threadIdx.x, r = blockIdx.y;
-    const float inv = a.norm ? row_inv_rms(a.frag, a.K / kChunk, a.K, a.eps, r, red) : 1.0f;
-    if ((threadIdx.x & ~63) + blockIdx.x * 256 >= a.n_out) return;  // whole waves past the outputs
+    const bool wave_live = (threadIdx.x & ~63) + blockIdx.x * 256 < a.n_out;  // false: whole waves past the outputs
     const bool live = c < a.n_out;
+    // The partials' loads go first and the row's sums of x^2 (1 / rms, a workgroup sum) after
+    // them, so the two round trips overlap; the arithmetic and its order are unchanged.
+    float* d = a.y && live ? a.y + (size_t)r * a.y_stride + c : nullptr;
+    const float* p = a.part + (size_t)r * a.N + c;
+    const size_t ss = (size_t)a.mpad * a.N;  // between splits
+    // every split's load in flight at once (up to kSplitsInFlight), then the sum in split order
+    constexpr int kSplitsInFlight = 24;
+    const bool swiglu = a.epi == EPI_SWIGLU;
+    float gv[kSplitsInFlight], uv[kSplitsInFlight], hv = 0.0f;
+#pragma unroll
+    for (int s = 0; s < kSplitsInFlight; s++) {
+        gv[s] = live && s < a.splits ? p[s * ss] : 0.0f;
+        uv[s] = live && s < a.splits && swiglu ? p[s * ss + a.n_out] : 0.0f;
+    }
+    if (live && a.epi == EPI_ACCUMULATE) hv = *d;
+    const float inv = a.norm ? row_inv_rms<256>(a.frag, a.K / kChunk, a.K, a.eps, r, red) : 1.0f;
+    if (!wave_live) return;
     float v = 0.0f;
     if (live) {
-        float g = 0.0f, u = 0.0f;
-        const float* p = a.part + (size_t)r * a.N + c;
-        const size_t ss = (size_t)a.mpad * a.N;  // between splits
-        // every split's load in flight at once (up to kSplitsInFlight), then the sum in split order
-        constexpr int kSplitsInFlight = 24;
-        const bool swiglu = a.epi == EPI_SWIGLU;
-        float gv[kSplitsInFlight], uv[kSplitsInFlight];
-#pragma unroll
-        for (int s = 0; s < kSplitsInFlight; s++) {
-            gv[s] = s < a.splits ? p[s * ss] : 0.0f;
-            uv[s] = s < a.splits && swiglu ? p[s * ss + a.n_out] : 0.0f;
-        }
-        __builtin_amdgcn_sched_barrier(0);
-        g = gv[0];  // a.splits >= 1
-        u = uv[0];
+        float g = gv[0], u = uv[0];  // a.splits >= 1
 #pragma unroll
         for (int s = 1; s < kSplitsInFlight; s++) {  // past a.splits the terms are +0: g and u unchanged
             g += gv[s];
@@ -295,9 +297,8 @@ __global__ __launch_bounds__(256) void k_gemm_reduce(const GemmArgs a) {
         }
         g *= inv;
         u *= inv;
-        float* d = a.y ? a.y + (size_t)r * a.y_stride + c : nullptr;
         if (a.epi == EPI_STORE) v = g;
-        else if (a.epi == EPI_ACCUMULATE) v = *d + g;
+        else if (a.epi == EPI_ACCUMULATE) v = hv + g;
         else v = silu(g) * u;
         if (d) store_through(d, v);
     }

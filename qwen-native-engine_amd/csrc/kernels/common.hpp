@@ -109,10 +109,15 @@ __device__ __forceinline__ float group16_sum(float v) {
     return v;
 }
 
-// Block-wide sum for blockDim.x a multiple of 64 (at most 1024). `red` needs 16 floats of LDS.
+// Block-wide sum over the NT threads of the workgroup (NT, the launch's block size, a multiple of
+// 64, at most 1024: a constant, as blockDim.x costs two dependent loads of the dispatch's implicit
+// arguments). `red` needs 16 floats of LDS.
+template <int NT>
 __device__ __forceinline__ float block_sum(float v, float* red) {
+    static_assert(NT % kWave == 0 && NT <= 1024, "whole waves, at most 16");
     v = wave_sum(v);
-    const int w = threadIdx.x / kWave, nw = blockDim.x / kWave;
+    const int w = threadIdx.x / kWave;
+    constexpr int nw = NT / kWave;
     __syncthreads();
     if ((threadIdx.x & (kWave - 1)) == 0) red[w] = v;
     __syncthreads();

@@ -114,7 +114,7 @@ __global__ __launch_bounds__(kGdnThreads, 6) void k_gdn_decode(const float* __re
     float inv = 1.0f;
     if (io.part) {
         // row_inv_rms: one chunk sum per thread (nchunks_in <= 256), the block sum in wave order
-        inv = 1.0f / sqrtf(block_sum(ss_in, sh.red) / (float)io.k_in + io.eps);
+        inv = 1.0f / sqrtf(block_sum<kGdnThreads>(ss_in, sh.red) / (float)io.k_in + io.eps);
         __syncthreads();  // sh.red is reused below
     }
     const float x = pc.sum(pbase + ch, nsp, io.split_stride) * inv;

@@ -55,15 +55,16 @@ __device__ __forceinline__ void emit_x(uint8_t* __restrict__ frag, size_t tile_b
 }
 
 // 1 / rms of row r from the staged chunk sums of x^2 (the RMSNorm of the GEMM's input, applied to
-// its output: y = (1 / rms) W (x * gain)). Called by every thread of the workgroup (a multiple of
-// 256 threads: with K <= 16384 the wave sums and their order are those of a 256-thread workgroup,
-// the waves past the fourth adding zeros).
+// its output: y = (1 / rms) W (x * gain)). Called by every one of the NT threads of the workgroup
+// (a multiple of 256: with K <= 16384 the wave sums and their order are those of a 256-thread
+// workgroup, the waves past the fourth adding zeros).
+template <int NT>
 __device__ __forceinline__ float row_inv_rms(const uint8_t* __restrict__ frag, int nchunks, int K, float eps, int r,
                                              float* red) {
     const uint8_t* tile = frag + (size_t)(r / kBM) * nchunks * kChunkBytes;
     float ss = 0.0f;
-    for (int c = threadIdx.x; c < nchunks; c += blockDim.x) ss += ((const float*)(tile + (size_t)c * kChunkBytes))[kSsOff / 4 + (r & (kBM - 1))];
-    ss = block_sum(ss, red);
+    for (int c = threadIdx.x; c < nchunks; c += NT) ss += ((const float*)(tile + (size_t)c * kChunkBytes))[kSsOff / 4 + (r & (kBM - 1))];
+    ss = block_sum<NT>(ss, red);
     return 1.0f / sqrtf(ss / (float)K + eps);
 }
 
