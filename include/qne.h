@@ -246,8 +246,9 @@ int qne_batch_free(qne_batch* b);
 int qne_batch_admit(qne_batch* b, uint32_t row);
 /* Row `row` of dst takes over row `src_row` of src (a batch over the same model, possibly dst
  * itself): its KV cache, recurrent state and next (token, position). No counterpart in the
- * reference (one sequence per Model); it moves a sequence between batches of different sizes, and
- * a row's results do not depend on the batch it runs in (bit for bit). */
+ * reference (one sequence per Model); it moves a sequence between batches of different sizes. For
+ * batches created with the same max_context, a row's results do not depend on the batch it runs in
+ * (bit for bit): the attention split count follows from max_context alone. */
 int qne_batch_copy_row(qne_batch* dst, uint32_t row, qne_batch* src, uint32_t src_row);
 /* Row `row` becomes an empty sequence at position 0 whose next token is `token`. */
 int qne_batch_reset_row(qne_batch* b, uint32_t row, uint32_t token);

@@ -413,12 +413,15 @@ int qne_exchange_probe(uint64_t* buf, uint32_t n, uint32_t rounds, uint32_t work
         qne::hip_check(qne::launch_exchange_probe(buf, (int)n, (int)rounds, (int)workgroups, (unsigned long long*)ctl,
                                                    (unsigned*)(ctl + 1), nullptr),
                        "exchange probe (cooperative launch: the workgroups must fit on the device at once)");
-        qne::hip_check(hipDeviceSynchronize(), "exchange probe");
+        // the probe ran on the null stream: wait for it alone, not for every stream of the device
+        qne::hip_check(hipStreamSynchronize(nullptr), "exchange probe");
         uint64_t h[2] = {0, 0};
         qne::hip_check(hipMemcpy(h, ctl, sizeof h, hipMemcpyDeviceToHost), "exchange probe");
         if (h[1] & 0xFFFFFFFFull) throw qne::Error(QNE_EDEVICE, "exchange probe: a poll timed out");
-        int khz = 0;
-        qne::hip_check(hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, 0), "exchange probe");
+        int dev = 0, khz = 0;
+        qne::hip_check(hipGetDevice(&dev), "exchange probe");
+        // the wall clock the probe's timestamps count is the current device's
+        qne::hip_check(hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev), "exchange probe");
         *us_per_round = khz > 0 ? (double)h[0] * 1000.0 / khz / (double)(rounds - 2) : 0.0;
     });
 }

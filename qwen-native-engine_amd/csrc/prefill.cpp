@@ -64,7 +64,8 @@ ChunkPrefill::~ChunkPrefill() { release(); }
 
 void ChunkPrefill::release() {
     if (st_) (void)hipStreamSynchronize(st_);
-    for (auto& g : graphs_) (void)hipGraphExecDestroy(g.second);
+    for (auto& g : lru_) (void)hipGraphExecDestroy(g.second);
+    lru_.clear();
     graphs_.clear();
     for (void* p : allocations_) (void)hipFree(p);
     allocations_.clear();
@@ -125,9 +126,20 @@ void ChunkPrefill::enqueue_chunk(int n, int lead) {
 }
 
 hipGraphExec_t ChunkPrefill::graph_for(int n, int lead) {
-    const int key = n * 64 + lead;
+    const int key = graph_key(n, lead);
     auto it = graphs_.find(key);
-    if (it != graphs_.end()) return it->second;
+    if (it != graphs_.end()) {
+        lru_.splice(lru_.begin(), lru_, it->second);  // now the most recently used
+        return it->second->second;
+    }
+    if (lru_.size() >= kGraphCap) {
+        // drop the least recently used graph; the stream is idle (run() synchronizes before every
+        // pass), so no launch of it is pending
+        QNE_HIP(hipStreamSynchronize(st_));
+        (void)hipGraphExecDestroy(lru_.back().second);
+        graphs_.erase(lru_.back().first);
+        lru_.pop_back();
+    }
     hipGraph_t g = nullptr;
     hipGraphExec_t e = nullptr;
     QNE_HIP(hipStreamBeginCapture(st_, hipStreamCaptureModeThreadLocal));
@@ -141,7 +153,8 @@ hipGraphExec_t ChunkPrefill::graph_for(int n, int lead) {
     QNE_HIP(hipStreamEndCapture(st_, &g));
     QNE_HIP(hipGraphInstantiate(&e, g, nullptr, nullptr, 0));
     (void)hipGraphDestroy(g);
-    graphs_[key] = e;
+    lru_.emplace_front(key, e);
+    graphs_[key] = lru_.begin();
     return e;
 }
 

@@ -10,8 +10,11 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdint>
+#include <list>
 #include <map>
+#include <utility>
 #include <vector>
 
 #include "model.hpp"
@@ -22,6 +25,7 @@ class ChunkPrefill {
   public:
     static constexpr int kChunk = 512;              // tokens per pass
     static constexpr int kRowTiles = kChunk / 64;   // the GEMMs' split counts are chosen for this
+    static constexpr size_t kGraphCap = 48;         // instantiated pass graphs kept (least recently used dropped)
     explicit ChunkPrefill(Model& m);
     ~ChunkPrefill();
     ChunkPrefill(const ChunkPrefill&) = delete;
@@ -39,10 +43,20 @@ class ChunkPrefill {
     void enqueue_chunk(int n, int lead);
     hipGraphExec_t graph_for(int n, int lead);
 
+  public:
+    // The launch sequence of a pass depends on n and on the sequential head min(lead, n) only (the
+    // WY block count and the sequential tail follow from them): the graph cache key.
+    static int graph_key(int n, int lead) { return n * 64 + std::min(std::max(lead, 0), n); }
+    size_t graphs_cached() const { return lru_.size(); }
+
+  private:
+
     Model& m_;
     hipStream_t st_;
     std::vector<void*> allocations_;
-    std::map<int, hipGraphExec_t> graphs_;  // by n * 64 + lead
+    // instantiated pass graphs by graph_key, most recently used first (at most kGraphCap)
+    std::list<std::pair<int, hipGraphExec_t>> lru_;
+    std::map<int, std::list<std::pair<int, hipGraphExec_t>>::iterator> graphs_;
     int proj_w_ = 0, mixed_w_ = 0, splits_ = 1;
     uint32_t* ids_ = nullptr;  // the chunk's token ids
     int32_t* pos_ = nullptr;   // the chunk's positions

@@ -25,7 +25,21 @@ def hip():
         h.hipMemset.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t]
         h.hipGetErrorString.argtypes = [ctypes.c_int]
         h.hipGetErrorString.restype = ctypes.c_char_p
-        for f in (h.hipMalloc, h.hipFree, h.hipMemcpy, h.hipMemset, h.hipDeviceSynchronize):
+        vp, pvp = ctypes.c_void_p, ctypes.POINTER(ctypes.c_void_p)
+        h.hipMemGetInfo.argtypes = [ctypes.POINTER(ctypes.c_size_t), ctypes.POINTER(ctypes.c_size_t)]
+        h.hipStreamCreate.argtypes = [pvp]
+        h.hipStreamDestroy.argtypes = [vp]
+        h.hipStreamSynchronize.argtypes = [vp]
+        h.hipStreamBeginCapture.argtypes = [vp, ctypes.c_int]
+        h.hipStreamEndCapture.argtypes = [vp, pvp]
+        h.hipGraphInstantiate.argtypes = [pvp, vp, vp, vp, ctypes.c_size_t]
+        h.hipGraphLaunch.argtypes = [vp, vp]
+        h.hipGraphExecDestroy.argtypes = [vp]
+        h.hipGraphDestroy.argtypes = [vp]
+        for f in (h.hipMalloc, h.hipFree, h.hipMemcpy, h.hipMemset, h.hipDeviceSynchronize, h.hipMemGetInfo,
+                  h.hipStreamCreate, h.hipStreamDestroy, h.hipStreamSynchronize, h.hipStreamBeginCapture,
+                  h.hipStreamEndCapture, h.hipGraphInstantiate, h.hipGraphLaunch, h.hipGraphExecDestroy,
+                  h.hipGraphDestroy):
             f.restype = ctypes.c_int
         _hip = h
     return _hip
@@ -96,6 +110,61 @@ def zeros(shape, dtype=np.float32) -> DeviceArray:
 
 def sync():
     check(hip().hipDeviceSynchronize(), "hipDeviceSynchronize")
+
+
+def mem_free() -> int:
+    """Free device memory in bytes (hipMemGetInfo)."""
+    free, total = ctypes.c_size_t(), ctypes.c_size_t()
+    check(hip().hipMemGetInfo(ctypes.byref(free), ctypes.byref(total)), "hipMemGetInfo")
+    return int(free.value)
+
+
+class Stream:
+    """A created HIP stream (default priority), with graph capture of the work enqueued on it."""
+
+    CAPTURE_GLOBAL = 0  # hipStreamCaptureModeGlobal
+
+    def __init__(self):
+        p = ctypes.c_void_p()
+        check(hip().hipStreamCreate(ctypes.byref(p)), "hipStreamCreate")
+        self.ptr = p.value
+
+    def sync(self):
+        check(hip().hipStreamSynchronize(self.ptr), "hipStreamSynchronize")
+
+    def capture(self, enqueue):
+        """Captures what enqueue() puts on this stream; returns an instantiated graph."""
+        check(hip().hipStreamBeginCapture(self.ptr, self.CAPTURE_GLOBAL), "hipStreamBeginCapture")
+        g = ctypes.c_void_p()
+        try:
+            enqueue()
+        finally:
+            rc = hip().hipStreamEndCapture(self.ptr, ctypes.byref(g))
+        check(rc, "hipStreamEndCapture")
+        e = ctypes.c_void_p()
+        try:
+            check(hip().hipGraphInstantiate(ctypes.byref(e), g, None, None, 0), "hipGraphInstantiate")
+        finally:
+            hip().hipGraphDestroy(g)
+        return Graph(e.value)
+
+    def destroy(self):
+        if self.ptr:
+            hip().hipStreamDestroy(self.ptr)
+            self.ptr = 0
+
+
+class Graph:
+    def __init__(self, exec_ptr):
+        self.ptr = exec_ptr
+
+    def launch(self, stream: Stream):
+        check(hip().hipGraphLaunch(self.ptr, stream.ptr), "hipGraphLaunch")
+
+    def destroy(self):
+        if self.ptr:
+            hip().hipGraphExecDestroy(self.ptr)
+            self.ptr = 0
 
 
 def mapped_hip_runtimes() -> list[str]:

@@ -13,6 +13,9 @@ for one seeded synthetic model and seeded prompts:
   steps       i32[4]     steps whose logits are sampled: logits after the prompt and s fed ids
   logit_idx   i32[4, N]  sampled vocabulary indices: the 16 largest logits, then a fixed random set
   logit_val   f32[4, N]  oracle logits at those indices (rows cases: an extra leading row axis)
+  logits_full f32[4, V]  every oracle logit at the logged steps (single-sequence cases), for the
+                         full-vocabulary check and the reference's model-level gate (cosine, top-1,
+                         top-5 overlap; kernels/src/bin/model_bench.rs:125-153)
   weights_sha256         hash of weights.bin, so a change of the synthetic generator is caught
 
 The models: "c1" is the 0.8B-shaped decoder with f16 weights, "c2" the 2B-shaped decoder with the
@@ -137,9 +140,10 @@ def make(name: str) -> Path:
     else:
         ids, logits = run_sequence(om, prompt, case["steps"], name)
         idx, val = sampled(logits, logged, rand)
+        full = np.stack([np.asarray(logits[s], dtype=np.float32) for s in logged])
         np.savez_compressed(out, prompt=prompt, ids=np.asarray(ids, dtype=np.uint32),
                             margin=np.asarray([top2_margin(v) for v in logits], dtype=np.float32),
-                            logit_idx=idx, logit_val=val, **common)
+                            logit_idx=idx, logit_val=val, logits_full=full, **common)
         margins = [top2_margin(v) for v in logits]
     print(f"{name}: {out.name} written in {time.time() - t0:.0f} s; min margin {min(margins):.4f}", flush=True)
     return out

@@ -1,15 +1,18 @@
 """Whole-model parity on the GPU against the committed oracle fixtures (tests/golden/*.npz).
 
 C1 is the 0.8B-shaped decoder with f16 weights, C2 the 2B-shaped decoder with the int4 g64 body (the
-decode benchmark's model): 128 seeded prompt ids, then 128 greedy steps. The bar: every sampled
-logit within 1e-2 of the oracle (max abs error), and the greedy ids identical over all 128 steps,
-through decode() (kernels/src/model.rs:426-449) and through step() (model.rs:380-392)."""
+decode benchmark's model): 128 seeded prompt ids, then 128 greedy steps. The bar: at every logged
+step, all 151 936 logits within 1e-2 of the oracle's (max abs error) and the reference's own
+model-level gate (cosine > 0.9999, same top-1, top-5 overlap >= 4; kernels/src/bin/model_bench.rs:
+125-153); and the greedy ids identical over all 128 steps, through decode()
+(kernels/src/model.rs:426-449) and through step() (model.rs:380-392)."""
 import json
 from pathlib import Path
 
 import numpy as np
 import pytest
 
+import parity
 import qne as Q
 import weights as W
 
@@ -21,6 +24,14 @@ TIE = 1e-3  # oracle top-2 margins below this are ties at the engine's precision
 def fixture(name):
     f = np.load(GOLDEN / f"{name}_greedy.npz")
     return {k: f[k] for k in f.files}
+
+
+def check_step(g, j, got, what):
+    """Logits after logged step j against the fixture: every logit and the reference's gate when
+    the fixture holds the full vector, else the sampled logits. Returns max |dlogit|."""
+    if "logits_full" in g:
+        return parity.check_logits(got, g["logits_full"][j], what)["max_diff"]
+    return float(np.max(np.abs(got[g["logit_idx"][j]] - g["logit_val"][j])))
 
 
 def synth(case):
@@ -46,8 +57,7 @@ def test_greedy_ids_and_logits_match_oracle_fixture(golden, engine):
         worst = 0.0
         got = m.logits()
         assert int(g["steps"][0]) == 0
-        err = float(np.max(np.abs(got[g["logit_idx"][0]] - g["logit_val"][0])))
-        worst = max(worst, err)
+        worst = max(worst, check_step(g, 0, got, f"{name}/{engine} after the prompt"))
         assert m.last_token() == (ids[0], P)
         out = m.decode_ids(len(ids), 32, [])
         assert out == ids, f"{name}/{engine}: first divergence at step {next(i for i, (a, b) in enumerate(zip(out, ids)) if a != b)}"
@@ -60,10 +70,10 @@ def test_greedy_ids_and_logits_match_oracle_fixture(golden, engine):
             assert int(np.argmax(v)) == ids[i + 1], f"{name}/{engine}: step {i + 1}"
             if i + 1 in logged:
                 j = logged[i + 1]
-                err = float(np.max(np.abs(v[g["logit_idx"][j]] - g["logit_val"][j])))
-                worst = max(worst, err)
-        print(f"{name}/{engine}: 128 greedy ids identical; max |dlogit| over sampled logits {worst:.2e}; "
-              f"smallest top-2 margin {float(np.min(g['margin'])):.4f}")
+                worst = max(worst, check_step(g, j, v, f"{name}/{engine} step {i + 1}"))
+        scope = "all logits" if "logits_full" in g else "sampled logits"
+        print(f"{name}/{engine}: 128 greedy ids identical; max |dlogit| over {scope} at steps "
+              f"{g['steps'].tolist()} {worst:.2e}; smallest top-2 margin {float(np.min(g['margin'])):.4f}")
         assert worst <= LOGIT_TOL
 
 
@@ -72,7 +82,8 @@ def test_greedy_ids_and_logits_match_oracle_fixture(golden, engine):
 def test_long_context_decode_matches_oracle_fixture(name, window):
     """The decode benchmark's own positions: the 2B int4 model after a 4000-id prompt, greedy decode
     over positions 4000..4094 through the persistent decode kernel (prefill_chunk in 512-id calls,
-    then decode windows of 16), ids identical to the oracle's and the sampled logits within 1e-2.
+    then decode windows of 16), ids identical to the oracle's, and at the logged steps every logit within
+    1e-2 and the reference's model-level gate.
     small_long: the 8-layer model with an 8192-position cache after a 5500-id prompt, where an
     attention split holds more positions than the kernel prefetches into LDS (its direct-load
     path)."""
@@ -90,22 +101,31 @@ def test_long_context_decode_matches_oracle_fixture(name, window):
         for s in range(0, P, 512):
             m.prefill_chunk(prompt[s:s + 512], s, s + 512 >= P)
         got = m.logits()
-        worst = float(np.max(np.abs(got[g["logit_idx"][0]] - g["logit_val"][0])))
+        worst = check_step(g, 0, got, f"{name} after the prompt")
         assert m.last_token() == (ids[0], P)
         m.snapshot()
         out = m.decode_ids(len(ids), window, [])
-        assert out[:tie] == ids[:tie], \
-            f"{name}: first divergence at step {next(i for i, (a, b) in enumerate(zip(out, ids)) if a != b)}"
+        same = next((i for i, (a, b) in enumerate(zip(out, ids)) if a != b), len(ids))
+        assert same >= tie, f"{name}: first divergence at step {same}"
         # teacher-forced: the logits after every fed id from the same prompt state
         m.restore()
         logged = {int(s): i for i, s in enumerate(g["steps"])}
+        forced_all = True  # every teacher-forced pick equals the oracle's, ties included
         for i in range(len(ids) - 1):
             v = m.step(ids[i], P + i)
+            pick = int(np.argmax(v))
+            forced_all &= pick == ids[i + 1]
             if margin[i + 1] >= TIE:
-                assert int(np.argmax(v)) == ids[i + 1], f"{name}: step {i + 1}"
+                assert pick == ids[i + 1], f"{name}: step {i + 1}"
             if i + 1 in logged:
                 j = logged[i + 1]
-                worst = max(worst, float(np.max(np.abs(v[g["logit_idx"][j]] - g["logit_val"][j]))))
-    print(f"{name}: free-running ids identical over {tie} steps (first oracle tie at {tie}), teacher-forced picks "
-          f"identical wherever the oracle margin >= {TIE}; max |dlogit| {worst:.2e}")
+                worst = max(worst, check_step(g, j, v, f"{name} step {i + 1}"))
+    if forced_all:
+        # the engine took the oracle's branch at every step, near-ties included: the free-running
+        # decode is then the oracle's whole sequence
+        assert out == ids, f"{name}: free-running decode diverged at step {same} although every forced pick matched"
+    scope = "all logits" if "logits_full" in g else "sampled logits"
+    print(f"{name}: free-running ids identical over {same} of {len(ids)} steps (first oracle tie at {tie}); "
+          f"teacher-forced picks identical {'at every step' if forced_all else f'wherever the oracle margin >= {TIE}'}; "
+          f"max |dlogit| over {scope} at steps {g['steps'].tolist()} {worst:.2e}")
     assert worst <= LOGIT_TOL
