@@ -94,6 +94,26 @@ def _profile_value(path, key):
     return None
 
 
+BATCH_PROFILE = ROOT / "profiles" / "batched_decode_2b_int4_b64_counters.md"
+
+
+def profile_values(path) -> dict:
+    """The `key: value` lines a profile summary ends with."""
+    vals = {}
+    try:
+        text = path.read_text()
+    except OSError:
+        return vals
+    for line in text.splitlines():
+        if ":" in line and line.split(":", 1)[0].strip().replace("_", "").isalnum() and not line.startswith(("#", "|")):
+            k, v = line.split(":", 1)
+            try:
+                vals[k.strip()] = float(v)
+            except ValueError:
+                pass
+    return vals
+
+
 def profiled_traffic(steps: int):
     """HBM bytes of a `steps`-token decode launch from the FETCH_SIZE / WRITE_SIZE counter passes
     recorded in the profile summary (scaled by a plain copy of known size): the profiled launch's
@@ -424,6 +444,10 @@ def bench_batch(args) -> dict:
     weights = one["weights"] - embed_row + one["lm_head"] + B * embed_row
     per_step = weights + kv + B * (one["gdn_state"] + one["conv_state"])
     achieved = per_step / (dev_ms / args.steps / 1e3) / 1e9
+    # HBM bytes and MFMA busy cycles per step from the counter passes of this workload (64 rows)
+    prof = profile_values(BATCH_PROFILE) if B == 64 else {}
+    traffic = prof.get("traffic_bytes_per_step")
+    busy = prof.get("mfma_busy_simd_cycles_per_step")
     macs = sum(mm["rows"] * mm["k"] for name, mm in mats.items() if name != "embed")
     mfma_flops = 2 * 2 * 64 * macs  # hi and lo passes over 64 rows
     mfma_tflops = mfma_flops / (dev_ms / args.steps / 1e3) / 1e12
@@ -436,11 +460,15 @@ def bench_batch(args) -> dict:
                                f"with contexts uniform in [256, 4096) (mean {float(pos0.mean()):.0f}), one greedy "
                                f"token per sequence per step", "batch": B, "layers": cfg["layers"]},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                     "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None,
+                     "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": traffic,
+                     "traffic_source": BATCH_PROFILE.name if traffic else None,
                      "kernel": "batched decode step (HIP graph: GEMMs, GDN, attention)",
                      "bytes_per_step": int(per_step), "device_ms_per_step": round(dev_ms / args.steps, 4)},
         "mfma": {"flops_per_step": mfma_flops, "achieved_tflops_over_step": round(mfma_tflops, 1),
-                 "peak_tflops_f16": 2500.0, "frac_over_step": round(mfma_tflops / 2500.0, 4)},
+                 "peak_tflops_f16": 2500.0, "frac_over_step": round(mfma_tflops / 2500.0, 4),
+                 # counter-based: busy SIMD-cycles of the MFMA pipes over the step's device time
+                 "busy_frac_over_step": round(busy / (dev_ms / args.steps / 1e3 * 2.4e9 * 1024), 4) if busy else None,
+                 "busy_source": BATCH_PROFILE.name if busy else None},
         "detail": {"bytes_per_step": {"weights": int(weights), "kv": int(kv),
                                       "gdn_state": int(B * one["gdn_state"]), "conv_state": int(B * one["conv_state"])},
                    "weights_gen_s": round(gen_s, 2), "adapter": m.adapter},
@@ -605,6 +633,49 @@ def bench_exchange(args) -> dict:
             "roofline": None, "detail": {"runs": runs}, "cpu_baseline": None}
 
 
+def bench_prefill(args) -> dict:
+    """Chunked prefill of the 2B-shaped int4 model (Model::prefill_chunk, kernels/src/model.rs:
+    349-372): a `--ctx`-id prompt (4000) in 512-id calls, each one pass of the batched MFMA GEMMs
+    over the call's tokens, the GDN recurrence in its WY form and causal attention over the cache;
+    the last call computes the logits. One untimed prefill first (it captures the pass graphs),
+    then the timed one from a reset state. MFMA work: every body GEMM runs two f16 MFMA passes (x
+    split into hi and lo halves) over every token; the weights stream once per 512-token pass."""
+    import qne
+    import weights as W
+    cfg = W.full_config("2b")
+    index, buf = W.synth_model("2b", seed=args.seed, body="q4", head="f16", group=64)
+    mats = json.loads(index)["matrices"]
+    m = qne.Model.load(index, buf, options={"max_context": 4096, "prefill_graphs": not args.prefill_direct})
+    n = args.ctx
+    prompt = np.random.default_rng(args.seed).integers(0, cfg["vocab"], size=n).astype(np.uint32)
+
+    def run():
+        m.reset()
+        for s in range(0, n, 512):
+            m.prefill_chunk(prompt[s:s + 512], s, s + 512 >= n)
+
+    run()
+    t0 = time.perf_counter()
+    run()  # prefill_chunk returns after its stream has drained
+    wall = time.perf_counter() - t0
+    body = sum(mm["rows"] * mm["k"] for name, mm in mats.items() if name not in ("embed", "lm_head"))
+    mfma_flops = 2 * 2 * n * body  # hi and lo passes over every token
+    passes = (n + 511) // 512
+    one = algorithmic_bytes_per_token(cfg, mats, 0.0)
+    result = {
+        "metric": f"chunked prefill tok/s ({n}-id prompt, 2B int4)", "value": round(n / wall, 1), "unit": "tok/s",
+        "n_gpus": 1, "prefill_s": round(wall, 4), "higher_is_better": True, "dtype": "f32 activations, f16 MFMA "
+        "(x as hi + lo f16), int4 weights", "data": "synthetic",
+        "config": {"workload": f"Qwen3.5-2B-shaped hybrid decoder, int4 g64 body, {n}-id prompt in 512-id "
+                               f"prefill_chunk calls", "prefill_graphs": not args.prefill_direct},
+        "mfma": {"gemm_flops": mfma_flops, "achieved_tflops_over_prefill": round(mfma_flops / wall / 1e12, 1),
+                 "peak_tflops_f16": 2500.0, "frac_over_prefill": round(mfma_flops / wall / 1e12 / 2500.0, 4)},
+        "detail": {"passes": passes, "weight_bytes_per_pass": int(one["weights"]), "adapter": m.adapter},
+    }
+    m.close()
+    return result
+
+
 def copy_calibration(mib: int) -> None:
     """A plain device-to-device copy of a known size: under a hardware-counter profiler its
     FETCH_SIZE / WRITE_SIZE readings per dispatch, divided into the bytes it must move, give the
@@ -630,7 +701,7 @@ def main():
     ap.add_argument("--ctx", type=int, default=None, help="prompt length (default 4000; 128 for --config 0.8b)")
     ap.add_argument("--config", default="2b",
                     help="2b (the decode benchmark), 0.8b (f16 weights, 128-id prompt, 128 steps), batch "
-                         "(64-sequence batched decode), sample (sampled decode with the device sampler), stream "
+                         "(64-sequence batched decode), prefill (4000-id chunked prefill), sample (sampled decode with the device sampler), stream "
                          "(the read-bandwidth and dispatch-cost probes), exchange (the decode kernel's hand-over "
                          "probe), or the kernel microbenches attn / gdn / gemv")
     ap.add_argument("--batch", type=int, default=64, help="sequences (--config attn / batch)")
@@ -640,6 +711,8 @@ def main():
     ap.add_argument("--prefill", default="chunk", choices=["chunk", "tokens"],
                     help="fill the context with prefill_chunk (batched GEMM passes, the default) or with "
                          "prefill (the persistent token kernel)")
+    ap.add_argument("--prefill-direct", action="store_true",
+                    help="--config prefill: launch each pass's kernels one by one instead of replaying its graph")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--engine", default="persistent", choices=["persistent", "graph"])
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -662,6 +735,9 @@ def main():
         return
     if args.config == "batch":
         print(json.dumps(bench_batch(args)))
+        return
+    if args.config == "prefill":
+        print(json.dumps(bench_prefill(args)))
         return
     if args.config == "stream":
         sys.path[:0] = [str(ROOT / "qwen-native-engine_amd")]

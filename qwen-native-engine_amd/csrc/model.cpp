@@ -95,6 +95,11 @@ LoadOptions parse_options(const char* json) {
         if (e != "graph" && e != "persistent") throw Error(QNE_EINVAL, "engine must be \"persistent\" or \"graph\"");
         o.graph_engine = e == "graph";
     }
+    if (j.has("prefill_graphs")) {
+        const Json& v = j.at("prefill_graphs");
+        if (v.type != Json::Bool) throw Error(QNE_EINVAL, "prefill_graphs must be true or false");
+        o.prefill_graphs = v.b;
+    }
     return o;
 }
 
@@ -139,6 +144,7 @@ Model::Model(const ModelIndex& ix, const uint8_t* weights, uint64_t /*wlen*/, co
     QNE_HIP(hipEventCreate(&ev_start_));
     QNE_HIP(hipEventCreate(&ev_stop_));
     persistent_ = !opt.graph_engine;
+    prefill_graphs_ = opt.prefill_graphs;
     try {
         upload(ix, weights);
         alloc_state();

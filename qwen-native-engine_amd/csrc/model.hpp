@@ -36,6 +36,7 @@ struct LoadOptions {
     int max_context = 4096;
     int device = 0;
     bool graph_engine = false;  // per-kernel hipGraph path instead of the persistent kernel
+    bool prefill_graphs = true;  // prefill_chunk passes replay captured graphs (false: direct launches)
 };
 
 struct EngineRun {
@@ -143,6 +144,7 @@ class Model {
     bool use_graphs_ = true;
     // persistent engine
     bool persistent_ = true;
+    bool prefill_graphs_ = true;  // ChunkPrefill replays captured graphs (else launches directly)
     int engine_grid_ = 0;
     void* engine_args_ = nullptr;  // host copy of DecodeArgs (opaque here)
     unsigned* eng_bar_ = nullptr;  // [0] error flag of the decode kernel

@@ -171,7 +171,8 @@ void ChunkPrefill::run(const uint32_t* ids_dev, size_t n, uint32_t start, bool f
         // tokens until the next multiple of 64 positions: the GDN blocks after them are fixed by
         // absolute position, so calls cut at multiples of 64 give the same bits
         const int lead = (int)((64 - (start + off) % 64) % 64);
-        QNE_HIP(hipGraphLaunch(graph_for(t, lead), st_));
+        if (m_.prefill_graphs_) QNE_HIP(hipGraphLaunch(graph_for(t, lead), st_));
+        else enqueue_chunk(t, lead);  // the same kernels, launched one by one
         last = t;
     }
     if (finish_logits) {
