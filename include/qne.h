@@ -38,7 +38,9 @@ const char* qne_last_error(void);
  * recognised keys: "max_context" (default 4096, the reference's MAX_CONTEXT), "device" (HIP
  * ordinal, default 0), "engine" ("persistent" or "graph"), "prefill_graphs" (default true: each
  * qne_prefill_chunk pass replays a captured HIP graph; false launches the same kernels one by one,
- * for tools that trace kernel launches but not graph replays), "tiles" (a serialised ModelTiles,
+ * for tools that trace kernel launches but not graph replays), "gdn_fusion" (default true: the
+ * persistent decode kernel runs a GDN layer's in-projection and recurrent step as one phase where
+ * the shapes allow; false keeps them two phases, with identical results), "tiles" (a serialised ModelTiles,
  * model.rs:90-98). A serialised ModelTiles may also be passed as the whole object. A tile profile
  * is validated like ModelTiles::validate (model.rs:101-109, called at model.rs:174, after the index
  * and before any device work): QNE_EINVAL "invalid kernel tile profile: Tile { ... }" for a tile the

@@ -93,6 +93,7 @@ __device__ __forceinline__ void wait_vm(int n) {
 typedef const __attribute__((address_space(4))) Phase CPhase;
 typedef const __attribute__((address_space(4))) PhaseBufs CBufs;
 typedef const __attribute__((address_space(4))) float cfloat;
+typedef const __attribute__((address_space(4))) GdnExtra CGdnX;
 
 __device__ __forceinline__ void cbar() { asm volatile("" ::: "memory"); }
 // 2^x on the hardware unit (exp2(-inf) = 0).
@@ -495,6 +496,26 @@ __device__ __forceinline__ bool region_after(const DecodeArgs& a, CPhase& P, int
 // First position of context split sp of S over len positions (sp * len < 2^32: len <= 2^16, S <= 92).
 __device__ __forceinline__ int split_at(int sp, uint32_t len, int S) { return (int)(((uint32_t)sp * len) / (uint32_t)S); }
 
+// ---- the fused GDN phase (PH_GDNF): geometry ----
+// Workgroup w takes item (head h, value columns 8cb..8cb+7); with P.xcd the 16 items of a head go
+// to workgroups of one w % 8 class, which the dispatcher places on one XCD, so the head's q / k
+// exchange stays in that XCD's L2. Wave `wave` of the item owns channel t = 8cb + wave of the head:
+// its projection rows q_t, k_t, v_t, z_t (slots 0..3) and, for cb 0 and waves 0 / 1, the head's
+// a / b row (slot 4). LDS half: the slots' rows [5][rb], their (scale, zero) rows [5][szb], the
+// conv state and weights of slots 0..2 (6 x 16 bytes), then the 512-byte state column t.
+constexpr int kGfSlots = 5;
+__device__ __forceinline__ int gf_item(CPhase& P, int w) {
+    if (!P.xcd) return w;
+    const int x = w & 7, j = w >> 3;
+    return (x * (P.heads >> 3) + (j >> 4)) * 16 + (j & 15);
+}
+__device__ __forceinline__ int gf_nrows(int cb, int wave) { return cb == 0 && wave < 2 ? 5 : 4; }
+__device__ __forceinline__ int gf_row(int H, int h, int t, int wave, int slot) {
+    return slot < 4 ? slot * H * kDK + h * kDK + t : 4 * H * kDK + wave * H + h;
+}
+__device__ __forceinline__ int gf_conv(CPhase& P) { return kGfSlots * P.stride; }
+__device__ __forceinline__ int gf_state(CPhase& P) { return (kGfSlots * P.stride + 96 + 127) & ~127; }
+
 // ---- prefetch of a region phase's data into one half of the wave's LDS region ----
 // GEMV: the wave's first outputs (rows, then their scale/zero pairs; for the GDN in-projection the
 // conv state and conv weights of those rows after them). GDN: the wave's 512-byte state column.
@@ -516,6 +537,27 @@ __device__ __forceinline__ void prefetch(const Env& e, CPhase& P, CBufs& B, int 
                 lds_dma16<false>((const float*)B.aux + (size_t)row * 4, cv + 16 * g.cap);
             }
         }
+    } else if (P.kind == PH_GDNF) {
+        const int it = gf_item(P, e.wg), H = P.heads, h = it >> 4, cb = it & 15, t = cb * 8 + e.wave;
+        const int nr = gf_nrows(cb, e.wave);
+        const uint8_t* w = (const uint8_t*)B.w;
+        for (int sl = 0; sl < nr; sl++) dma_bytes(w + (size_t)gf_row(H, h, t, e.wave, sl) * P.rb, P.rb, nxt + sl * P.rb, lane);
+        // every slot's (scale, zero) row in one transfer: lane l carries 16 bytes of slot l / (szb / 16)
+        const int per = P.szb >> 4;
+        if (lane < nr * per) {
+            const int sl = lane / per, part = lane - sl * per;
+            lds_dma16<true>((const uint8_t*)B.sz + (size_t)gf_row(H, h, t, e.wave, sl) * P.szb + 16 * part,
+                            nxt + kGfSlots * P.rb);
+        }
+        // conv state (lanes 0..2) and conv weights (lanes 3..5) of the q, k, v channels
+        if (lane < 6) {
+            const int sl = lane < 3 ? lane : lane - 3;
+            const size_t ch = (size_t)gf_row(H, h, t, e.wave, sl) * 4;
+            lds_dma16<false>(lane < 3 ? (const void*)(B.conv + ch) : (const void*)((const float*)B.aux + ch),
+                             nxt + gf_conv(P));
+        }
+        const float* rec = ((CGdnX*)a.gdnx)[B.xi].rec;
+        dma_bytes((const uint8_t*)(rec + ((size_t)h * kDK + t) * kDK), 512, nxt + gf_state(P), lane);
     } else if (P.kind == PH_GDN) {
         const int it = e.wg;
         const float* rec = (const float*)B.w;
@@ -838,6 +880,108 @@ __device__ __forceinline__ void gdn_body(const Env& e, CPhase& P, CBufs& B, int 
         }
         bar();
     }
+}
+
+// The fused GDN phase (PH_GDNF): kernels/src/model.rs:233-241 for one GDN layer up to the mixer
+// output, i.e. the in-projection GEMV (shaders.rs:45-376) with the causal conv + SiLU epilogue,
+// then the gated delta rule step (shaders.rs:436-520). The input vector (1 / rms in `inv`) is staged
+// in xs; the wave's projection rows, conv state and state column were prefetched into `cur`.
+//  1. each wave dots its 4 (or 5) rows with x; q_t and k_t (and a / b) are published to the
+//     head-group buffer, v_t and z_t stay in the wave;
+//  2. the workgroup polls the head's 128 q, 128 k, a and b from the 16 workgroups of the head;
+//  3. each wave steps value column t of the head's state and publishes o_t * silu(z_t) * norm_w[t];
+//     the workgroup publishes the sum of its 8 o_t^2 (the out-projection folds the output norm).
+__device__ __forceinline__ void gdnf_phase(const Env& e, CPhase& P, CBufs& B, int step, int p, float inv, uint8_t* cur,
+                                           const Ctl& c) {
+    const DecodeArgs& a = *e.a;
+    const int lane = e.lane, H = P.heads;
+    mark(e, 0);
+    wait_all();  // rows, conv and state column (issued two region phases ago) are in
+    const int it = gf_item(P, e.wg), h = it >> 4, cb = it & 15, t = cb * 8 + e.wave;
+    const int nr = gf_nrows(cb, e.wave);
+    const uint32_t tag = tag_of(a, step, p);
+    CGdnX& X = ((CGdnX*)a.gdnx)[B.xi];
+    uint64_t* grp = X.grp + (size_t)(step & 1) * X.grp_stride;
+    uint64_t* out = B.out + (size_t)(step & 1) * P.out_stride;
+    // 1. the rows
+    const Step st = make_step(P);
+    XC xc;
+    if (st.nsteps == 1) load_step(e.xs, st, 0, xc, lane);
+    int roff[8], soff[8];
+#pragma unroll
+    for (int r = 0; r < 8; r++) {
+        const int sl = r < nr ? r : nr - 1;
+        roff[r] = sl * P.rb;
+        soff[r] = kGfSlots * P.rb + sl * P.szb;
+    }
+    float acc[8];
+#pragma unroll
+    for (int r = 0; r < 8; r++) acc[r] = 0.0f;
+    if (nr == 5) rows_dot<5>(st, P.gshift, cur, roff, soff, e.xs, xc, lane, acc);
+    else rows_dot<4>(st, P.gshift, cur, roff, soff, e.xs, xc, lane, acc);
+    const float tot = reduce8(acc, lane) * inv;  // lanes 8r..8r+7: row r
+    const int r = lane >> 3;
+    float y = tot;
+    if ((lane & 7) == 0 && r < 3) {
+        // causal conv (kernel 4) + SiLU of the q / k / v channel (shaders.rs:457-468)
+        const float4 sv = *(const float4*)(cur + gf_conv(P) + 16 * r);
+        const float4 cw = *(const float4*)(cur + gf_conv(P) + 48 + 16 * r);
+        const float cv = sv.x * cw.x + sv.y * cw.y + sv.z * cw.z + tot * cw.w;
+        float* sp = B.conv + (size_t)gf_row(H, h, t, e.wave, r) * 4;
+        sp[0] = sv.y;
+        sp[1] = sv.z;
+        sp[2] = tot;
+        y = silu(cv);
+    }
+    if ((lane & 7) == 0) {
+        if (r == 0) put(grp, (uint32_t)(h * 258 + t), y, tag);
+        else if (r == 1) put(grp, (uint32_t)(h * 258 + 128 + t), y, tag);
+        else if (r == 4 && r < nr) put(grp, (uint32_t)(h * 258 + 256 + e.wave), y, tag);
+    }
+    const float v = __shfl(y, 16, kWave), z = __shfl(y, 24, kWave);
+    mark(e, 1);
+    // 2. the head's q, k, a, b
+    float* gs = e.xs + 4096;
+    poll_pairs(grp, X.grp_stride, 129, tag, [&](int q) { return h * 258 + 2 * q; },
+               [&](int q, float v0, float v1) {
+                   gs[2 * q] = v0;
+                   gs[2 * q + 1] = v1;
+               },
+               c);
+    bar();
+    if (*e.bail) return;
+    mark(e, 2);
+    // 3. the delta rule step of value column t (the same arithmetic as gdn_body)
+    cfloat* prm = (cfloat*)X.prm;
+    const float2 q2 = *(const float2*)(gs + 2 * lane);
+    const float2 k2 = *(const float2*)(gs + 128 + 2 * lane);
+    const float av = gs[256], bv = gs[257];
+    const float2 sc = *(const float2*)(cur + gf_state(P) + 8 * lane);
+    const float nq = 1.0f / sqrtf(wave_sum_dpp(q2.x * q2.x + q2.y * q2.y) + 1e-6f) * rsqrtf((float)kDK);
+    const float nk = 1.0f / sqrtf(wave_sum_dpp(k2.x * k2.x + k2.y * k2.y) + 1e-6f);
+    const float qx = q2.x * nq, qy = q2.y * nq, kx = k2.x * nk, ky = k2.y * nk;
+    const float kq = wave_sum_dpp(kx * qx + ky * qy);
+    const float gg = expf(prm[H + h] * logf(1.0f + expf(av + prm[h])));
+    const float beta = 1.0f / (1.0f + expf(-bv));
+    const float sk = wave_sum_dpp(sc.x * kx + sc.y * ky);
+    const float sq = wave_sum_dpp(sc.x * qx + sc.y * qy);
+    const float d = beta * (v - gg * sk);
+    float2 sn;
+    sn.x = fmaf(gg, sc.x, d * kx);
+    sn.y = fmaf(gg, sc.y, d * ky);
+    *(float2*)(X.rec + ((size_t)h * kDK + t) * kDK + 2 * lane) = sn;
+    const float o = gg * sq + d * kq;
+    if (lane == 0) {
+        put(out, (uint32_t)(h * kDK + t), o * silu(z) * prm[2 * H + t], tag);
+        e.red[e.wave] = o * o;
+    }
+    bar();
+    if (threadIdx.x == 0) {
+        float ss = 0.0f;
+        for (int w = 0; w < kNW; w++) ss += e.red[w];
+        put(out, (uint32_t)(H * kDK + h * 16 + cb), ss, tag);
+    }
+    mark(e, 3);
 }
 
 // RMSNorm (weight w) + rotate-half RoPE of one 256-vector held 4 values per lane
@@ -1271,6 +1415,13 @@ __device__ __forceinline__ void decode_program(const DecodeArgs& a) {
                     gdn_body(e, P, B, step, p, c, region(rh), xs, red);
                     mark(e, 2);
                     break;
+                case PH_GDNF: {
+                    const float inv = gemv_input(e, P, B, step, p, c);
+                    if (bail) { wait_all(); return; }
+                    trace_in(e, inst);
+                    gdnf_phase(e, P, B, step, p, inv, region(rh), c);
+                    break;
+                }
                 case PH_ATTN:
                     trace_in(e, inst);
                     attn_phase(e, P, B, step, p, c, rh, rope);
@@ -1373,7 +1524,7 @@ int decode_gemv_variant(int kind, int k) {
 
 void finalize_phase(Phase& P, int grid) {
     const int nw = grid * kNW;
-    if (P.kind == PH_GEMV) {
+    if (P.kind == PH_GEMV || P.kind == PH_GDNF) {
         P.fast_head = P.epi == EP_HEAD && (P.mkind == 0 || P.group == 64) && (P.k == 512 || P.k == 1024 || P.k == 2048);
         P.rper = P.rows / nw;
         P.rrem = P.rows % nw;
@@ -1393,7 +1544,19 @@ void finalize_phase(Phase& P, int grid) {
         P.nsteps = P.mkind ? P.n4 + P.n2 + P.n1 : P.k / 512;
     }
     if ((P.kind == PH_ATTN || P.kind == PH_COMB) && P.kv_heads > 0) P.splits = std::min(grid / P.kv_heads, kMaxSplits);
-    P.region = (P.kind == PH_GEMV && !P.fast_head) || P.kind == PH_GDN || P.kind == PH_ATTN;
+    if (P.kind == PH_GDNF) {
+        P.fast_head = 0;
+        P.xcd = grid % 8 == 0 && P.heads % 8 == 0 && grid == 16 * P.heads;
+    }
+    P.region = (P.kind == PH_GEMV && !P.fast_head) || P.kind == PH_GDN || P.kind == PH_ATTN || P.kind == PH_GDNF;
+}
+
+bool gdn_fusable(int kind, int k, int group, int heads, int grid) {
+    if (kind != 1 || k % 512 != 0 || k > 4096 || heads <= 0 || grid != 16 * heads) return false;
+    const int rb = k / 2, szb = (k / group) * 4;
+    if (szb % 16 != 0 || kGfSlots * (szb / 16) > kWave) return false;  // one transfer for every slot's pairs
+    const int state = (kGfSlots * (rb + szb) + 96 + 127) & ~127;
+    return state + 512 <= kHalf;
 }
 
 bool finalize_program(Phase* prog, int nph, DecodeArgs& a) {
@@ -1413,7 +1576,9 @@ bool finalize_program(Phase* prog, int nph, DecodeArgs& a) {
     return a.reg1 >= 0 && (a.head_reg < 0 || a.head_reg == nph - 1);
 }
 
-void split_program(const Phase* prog, int nph, std::vector<PhaseBufs>& bufs, std::vector<Phase>& shapes) {
+void split_program(const Phase* prog, int nph, std::vector<PhaseBufs>& bufs, std::vector<Phase>& shapes,
+                   std::vector<GdnExtra>& gdnx) {
+    gdnx.clear();
     // the shape is every field before the buffers (all 4-byte fields: no padding inside)
     constexpr size_t kShapeBytes = offsetof(Phase, w);
     static_assert(kShapeBytes % 4 == 0, "shape fields are 4-byte");
@@ -1433,11 +1598,20 @@ void split_program(const Phase* prog, int nph, std::vector<PhaseBufs>& bufs, std
         b.gain = P.gain;
         b.in = P.in;
         b.out = P.out;
-        if (P.kind == PH_GEMV) {
+        if (P.kind == PH_GEMV || P.kind == PH_GDNF) {
             b.w = P.w;
             b.sz = P.sz;
             b.aux = P.conv_w;
             b.conv = P.conv;
+            if (P.kind == PH_GDNF) {
+                GdnExtra x;
+                x.rec = P.rec;
+                x.prm = P.prm;
+                x.grp = P.grp;
+                x.grp_stride = P.grp_stride;
+                b.xi = (uint32_t)gdnx.size();
+                gdnx.push_back(x);
+            }
         } else if (P.kind == PH_GDN) {
             b.w = P.rec;
         } else if (P.kind == PH_ATTN) {

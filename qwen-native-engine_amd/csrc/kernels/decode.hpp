@@ -15,7 +15,9 @@
 
 namespace qne {
 
-enum PhaseKind { PH_GEMV = 0, PH_GDN = 1, PH_ATTN = 2, PH_COMB = 3 };
+// PH_GDNF: a GDN layer's in-projection and recurrent step in one phase (the workgroups of a head
+// compute its projection rows, exchange q and k among themselves, then step the head's state).
+enum PhaseKind { PH_GEMV = 0, PH_GDN = 1, PH_ATTN = 2, PH_COMB = 3, PH_GDNF = 4 };
 // Input of a GEMV phase: the previous phase's published vector, or the step's embedding row.
 enum { XI_EXCH = 0, XI_EMBED = 1 };
 // Transform of that input: none, RMSNorm with `gain`, or the GDN output norm (per-head 1/rms from
@@ -45,6 +47,7 @@ struct Phase {
     int in_rel = 1;     // the input was published `in_rel` phases earlier in the same step
     int in2_rel = 0;    // second input (COMB: the gate in the in-projection output)
     int is_head = 0;    // phase runs only on steps that compute logits
+    int xcd = 0;        // PH_GDNF: the 16 workgroups of a head share an XCD (workgroup w runs on XCD w % 8 + c)
     uint32_t in_stride = 0, in2_stride = 0, out_stride = 0;  // u64 entries
     uint32_t in_cap = 0, in2_cap = 0;  // entries readable from in / in2 (bounds of the polling loads)
     // Derived by finalize_phase from the fields above and the launch grid, so the kernel reads
@@ -71,7 +74,21 @@ struct Phase {
     uint64_t* in = nullptr;         // input exchange buffer (step parity 0; parity 1 at + in_stride)
     uint64_t* in2 = nullptr;
     uint64_t* out = nullptr;        // output exchange buffer
+    // PH_GDNF: the GDN parameters, and the head-group exchange of q, k, a, b ([heads][258] entries
+    // per step parity, parity 1 at + grp_stride)
+    const float* prm = nullptr;
+    uint64_t* grp = nullptr;
+    uint32_t grp_stride = 0;
 };
+
+// Per-phase buffers of a PH_GDNF phase beyond its PhaseBufs record (indexed by PhaseBufs::xi).
+struct GdnExtra {
+    float* rec = nullptr;          // recurrent state [heads][dv][dk]
+    const float* prm = nullptr;    // dt_bias[heads], A_neg_exp[heads], norm_w[dv]
+    uint64_t* grp = nullptr;       // head-group exchange
+    uint32_t grp_stride = 0, pad = 0;
+};
+static_assert(sizeof(GdnExtra) == 32, "four 8-byte fields");
 
 // The kernel's per-phase record: the phase's buffers and the index of its shape, in one 64-byte
 // line. The program is read through the scalar data cache at every phase; with the shapes shared
@@ -85,13 +102,15 @@ struct PhaseBufs {
     float* conv = nullptr;       // EP_CONV conv state
     uint64_t* in = nullptr;
     uint64_t* out = nullptr;
-    uint32_t shape = 0, pad = 0;
+    uint32_t shape = 0;
+    uint32_t xi = 0;  // PH_GDNF: index of its GdnExtra record
 };
 static_assert(sizeof(PhaseBufs) == 64, "one scalar-cache line per phase");
 
 struct DecodeArgs {
     const PhaseBufs* prog = nullptr;  // per phase
     const Phase* shapes = nullptr;    // distinct shapes, indexed by PhaseBufs::shape
+    const GdnExtra* gdnx = nullptr;   // PH_GDNF records, indexed by PhaseBufs::xi
     int nph = 0;  // phases per token
     // embedding (read by every workgroup at the start of a step)
     const void* emb_w = nullptr;
@@ -146,7 +165,11 @@ void finalize_phase(Phase& P, int grid);
 bool finalize_program(Phase* prog, int nph, DecodeArgs& a);
 // Splits a finalized program into the kernel's tables: one PhaseBufs per phase and the distinct
 // shapes (phases equal in every field before the buffers share one).
-void split_program(const Phase* prog, int nph, std::vector<PhaseBufs>& bufs, std::vector<Phase>& shapes);
+void split_program(const Phase* prog, int nph, std::vector<PhaseBufs>& bufs, std::vector<Phase>& shapes,
+                   std::vector<GdnExtra>& gdnx);
+// Whether a GDN layer's in-projection (matrix kind, K, group) fits the fused PH_GDNF phase on a
+// grid of `grid` workgroups with `heads` GDN heads of 128 channels.
+bool gdn_fusable(int kind, int k, int group, int heads, int grid);
 // GEMV shapes compiled into the kernel: variant id of (matrix kind, K), or -1.
 int decode_gemv_variant(int kind, int k);
 hipError_t launch_decode(const DecodeArgs& a, int grid, hipStream_t st);

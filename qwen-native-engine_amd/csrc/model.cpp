@@ -95,6 +95,11 @@ LoadOptions parse_options(const char* json) {
         if (e != "graph" && e != "persistent") throw Error(QNE_EINVAL, "engine must be \"persistent\" or \"graph\"");
         o.graph_engine = e == "graph";
     }
+    if (j.has("gdn_fusion")) {
+        const Json& v = j.at("gdn_fusion");
+        if (v.type != Json::Bool) throw Error(QNE_EINVAL, "gdn_fusion must be true or false");
+        o.gdn_fusion = v.b;
+    }
     if (j.has("prefill_graphs")) {
         const Json& v = j.at("prefill_graphs");
         if (v.type != Json::Bool) throw Error(QNE_EINVAL, "prefill_graphs must be true or false");
@@ -145,6 +150,7 @@ Model::Model(const ModelIndex& ix, const uint8_t* weights, uint64_t /*wlen*/, co
     QNE_HIP(hipEventCreate(&ev_stop_));
     persistent_ = !opt.graph_engine;
     prefill_graphs_ = opt.prefill_graphs;
+    gdn_fusion_ = opt.gdn_fusion;
     try {
         upload(ix, weights);
         alloc_state();
@@ -469,9 +475,38 @@ void Model::setup_engine() {
     };
     // input links: (phase index, buffer id) of each published vector
     std::vector<int> out_buf;
+    std::vector<int> grp_buf;  // PH_GDNF: its head-group exchange buffer (else -1)
     int h_prev = -1;  // buffer of the residual stream published by the previous layer's down
+    auto push = [&](const Phase& P, int out, int grp, const char* label) {
+        prog.push_back(P);
+        out_buf.push_back(out);
+        grp_buf.push_back(grp);
+        phase_label_.push_back(label);
+    };
+    phase_label_.clear();
     for (int i = 0; i < c.layers; i++) {
         const DevLayer& L = layers_[i];
+        const bool fuse = !L.attn && gdn_fusion_ && L.in.rows == c.gdn_proj() && c.gdn_dk == 128 &&
+                          gdn_fusable(L.in.kind, L.in.k, L.in.group, H, grid);
+        int b_mixed;
+        if (fuse) {
+            // in-projection, conv and the delta rule step in one phase (PH_GDNF)
+            Phase f = gemv(L.in, L.in.rows, EP_CONV);
+            f.kind = PH_GDNF;
+            f.xin = i == 0 ? XI_EMBED : XI_EXCH;
+            f.xnorm = XN_NORM;
+            f.gain = L.input_norm;
+            f.in_n = c.hidden;
+            f.conv_ch = c.conv_channels();
+            f.conv = L.conv_state;
+            f.conv_w = L.conv_w;
+            f.heads = H;
+            f.rec = L.rec;
+            f.prm = L.gdn_params;
+            const int b_grp = buf((uint32_t)(H * 258));
+            b_mixed = buf((uint32_t)(H * 128 + H * 16));
+            push(f, b_mixed, b_grp, "gdn.mixer_in+gdn");
+        }
         // mixer_in
         Phase in = gemv(L.in, L.in.rows, L.attn ? EP_STORE : EP_CONV);
         in.xin = i == 0 ? XI_EMBED : XI_EXCH;
@@ -483,19 +518,21 @@ void Model::setup_engine() {
             in.conv = L.conv_state;
             in.conv_w = L.conv_w;
         }
-        const int b_proj = buf((uint32_t)L.in.rows);
-        prog.push_back(in); out_buf.push_back(b_proj);
-        int b_mixed;
         int in_rel_out = 1;
-        if (!L.attn) {
+        if (fuse) {
+        } else if (!L.attn) {
+            const int b_proj = buf((uint32_t)L.in.rows);
+            push(in, b_proj, -1, "gdn.mixer_in");
             Phase g;
             g.kind = PH_GDN;
             g.heads = H;
             g.gain = L.gdn_params;
             g.rec = L.rec;
             b_mixed = buf((uint32_t)(H * 128 + H * 16));
-            prog.push_back(g); out_buf.push_back(b_mixed);
+            push(g, b_mixed, -1, "gdn.gdn");
         } else {
+            const int b_proj = buf((uint32_t)L.in.rows);
+            push(in, b_proj, -1, "attn.mixer_in");
             Phase at;
             at.kind = PH_ATTN;
             at.heads = c.n_q_heads;
@@ -504,40 +541,42 @@ void Model::setup_engine() {
             at.kp = L.k_pool;
             at.vp = L.v_pool;
             const int b_part = buf((uint32_t)(c.n_kv_heads * S * G * 258));
-            prog.push_back(at); out_buf.push_back(b_part);
+            push(at, b_part, -1, "attn.attention");
             Phase cb;
             cb.kind = PH_COMB;
             cb.heads = c.n_q_heads;
             cb.kv_heads = c.n_kv_heads;
             cb.in2_rel = 2;
             b_mixed = buf((uint32_t)(c.n_q_heads * 256));
-            prog.push_back(cb); out_buf.push_back(b_mixed);
+            push(cb, b_mixed, -1, "attn.combine");
         }
+        const char* kind = L.attn ? "attn." : "gdn.";
+        auto lab = [&](const char* n) { return (std::string(kind) + n); };
         Phase mo = gemv(L.out, c.hidden, EP_RESID);
         mo.xnorm = L.attn ? XN_PLAIN : XN_GDN;
         mo.heads = H;
         mo.in_n = L.attn ? c.attn_out() : H * 128 + H * 16;
         mo.in_rel = in_rel_out;
         const int b_h1 = buf((uint32_t)c.hidden);
-        prog.push_back(mo); out_buf.push_back(b_h1);
+        push(mo, b_h1, -1, lab("mixer_out").c_str());
         if (L.gate_up.rows != 2 * c.intermediate) throw unsupported("gate_up rows");
         Phase gu = gemv(L.gate_up, c.intermediate, EP_SWIGLU);
         gu.xnorm = XN_NORM;
         gu.gain = L.post_norm;
         gu.in_n = c.hidden;
         const int b_act = buf((uint32_t)c.intermediate);
-        prog.push_back(gu); out_buf.push_back(b_act);
+        push(gu, b_act, -1, lab("gate_up").c_str());
         Phase dn = gemv(L.down, c.hidden, EP_RESID);
         dn.in_n = c.intermediate;
         h_prev = buf((uint32_t)c.hidden);
-        prog.push_back(dn); out_buf.push_back(h_prev);
+        push(dn, h_prev, -1, lab("down").c_str());
     }
     Phase hd = gemv(lm_head_, c.vocab, EP_HEAD);
     hd.xnorm = XN_NORM;
     hd.gain = final_norm_;
     hd.in_n = c.hidden;
     hd.is_head = 1;
-    prog.push_back(hd); out_buf.push_back(-1);
+    push(hd, -1, -1, "lm_head");
     if ((int)prog.size() > kMaxPhases) throw unsupported("too many layers");
     for (const Phase& P : prog)
         if (P.kind == PH_GEMV && (P.in_n > 6144 || P.in_n > P.k + 2048 * (P.xnorm == XN_GDN)))
@@ -553,7 +592,11 @@ void Model::setup_engine() {
             P.out = base(out_buf[p]);
             P.out_stride = bufs[out_buf[p]].n;
         }
-        if (P.kind == PH_GEMV && P.xin == XI_EMBED) continue;
+        if (grp_buf[p] >= 0) {
+            P.grp = base(grp_buf[p]);
+            P.grp_stride = bufs[grp_buf[p]].n;
+        }
+        if ((P.kind == PH_GEMV || P.kind == PH_GDNF) && P.xin == XI_EMBED) continue;
         const int src = (int)p - P.in_rel;
         if (src < 0 || out_buf[src] < 0) throw Error(QNE_EINVAL, "decode program: bad input link");
         P.in = base(out_buf[src]);
@@ -572,7 +615,13 @@ void Model::setup_engine() {
     for (const Phase& P : prog) phase_kind_.push_back(P.kind);
     std::vector<PhaseBufs> pbufs;
     std::vector<Phase> shapes;
-    split_program(prog.data(), (int)prog.size(), pbufs, shapes);
+    std::vector<GdnExtra> gdnx;
+    split_program(prog.data(), (int)prog.size(), pbufs, shapes, gdnx);
+    GdnExtra* d_gdnx = nullptr;
+    if (!gdnx.empty()) {
+        d_gdnx = (GdnExtra*)dalloc(gdnx.size() * sizeof(GdnExtra));
+        QNE_HIP(hipMemcpy(d_gdnx, gdnx.data(), gdnx.size() * sizeof(GdnExtra), hipMemcpyHostToDevice));
+    }
     PhaseBufs* d_prog = (PhaseBufs*)dalloc(pbufs.size() * sizeof(PhaseBufs));
     QNE_HIP(hipMemcpy(d_prog, pbufs.data(), pbufs.size() * sizeof(PhaseBufs), hipMemcpyHostToDevice));
     Phase* d_shapes = (Phase*)dalloc(shapes.size() * sizeof(Phase));
@@ -584,6 +633,7 @@ void Model::setup_engine() {
     engine_args_ = a;
     a->prog = d_prog;
     a->shapes = d_shapes;
+    a->gdnx = d_gdnx;
     a->nph = nph_;
     a->reg0 = links.reg0; a->reg1 = links.reg1; a->head_reg = links.head_reg;
     a->emb_w = embed_.w; a->emb_sz = embed_.sz; a->emb_kind = embed_.kind; a->emb_group = embed_.group;
@@ -942,18 +992,8 @@ std::string Model::profile_token_json() {
     std::map<std::string, std::vector<double>> sub_l;
     std::string phases = "[";
     unsigned long long prev = tr[0];
-    int l = 0, k = 0;
     for (int b = 0; b < nph; b++) {
-        std::string label;
-        if (l >= cfg_.layers) {
-            label = "lm_head";
-        } else {
-            const bool at = layers_[l].attn;
-            static const char* gdn_names[5] = {"mixer_in", "gdn", "mixer_out", "gate_up", "down"};
-            static const char* attn_names[6] = {"mixer_in", "attention", "combine", "mixer_out", "gate_up", "down"};
-            label = std::string(at ? "attn." : "gdn.") + (at ? attn_names[k] : gdn_names[k]);
-            if (++k == (at ? 6 : 5)) { k = 0; l++; }
-        }
+        const std::string label = phase_label_[b];
         unsigned long long dmax = 0;
         std::vector<double> comp, exch;
         for (int w = 0; w < grid; w++) {
@@ -983,8 +1023,9 @@ std::string Model::profile_token_json() {
             }
         }
         {
-            const int kind = phase_kind_[b];  // 0 GEMV, 1 GDN, 2 attention, 3 combine
-            const int in_slot = kind == 0 ? 0 : kind == 3 ? 2 : 1, pub_slot = kind == 0 ? 3 : kind == 1 ? 2 : kind == 2 ? 5 : 3;
+            const int kind = phase_kind_[b];  // 0 GEMV, 1 GDN, 2 attention, 3 combine, 4 fused GDN
+            const int in_slot = kind == 0 || kind == 4 ? 0 : kind == 3 ? 2 : 1;
+            const int pub_slot = kind == 0 || kind == 4 ? 3 : kind == 1 ? 2 : kind == 2 ? 5 : 3;
             std::vector<double> tin, tpub;
             unsigned long long pmax = 0;
             for (int w = 0; w < grid; w++) {
@@ -1078,6 +1119,7 @@ std::string Model::profile_token_json() {
     return std::string(head) +
            "\"sub_step_names\":{\"gemv\":[\"x load\",\"first group\",\"other groups\",\"dma issue (two ahead)\"],"
            "\"gdn\":[\"input\",\"state update\",\"dma issue (two ahead)\"],"
+           "\"gdn_fused\":[\"rows + q/k publish\",\"head q/k exchange\",\"state update\",\"dma issue (two ahead)\"],"
            "\"attention\":[\"input\",\"q/k prep\",\"K/V landed\",\"context loop\",\"merge + publish\",\"dma issue (two ahead)\"],"
            "\"combine\":[\"partials\",\"gate\",\"combine + publish\"]}," +
            "\"sub_steps_median_ms\":" + subs + ",\"labels\":" + obj(span_l) + ",\"compute_median_ms\":" + obj(comp_l) +

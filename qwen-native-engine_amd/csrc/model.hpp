@@ -37,6 +37,7 @@ struct LoadOptions {
     int device = 0;
     bool graph_engine = false;  // per-kernel hipGraph path instead of the persistent kernel
     bool prefill_graphs = true;  // prefill_chunk passes replay captured graphs (false: direct launches)
+    bool gdn_fusion = true;      // persistent kernel: GDN in-projection and step in one phase where the shapes allow
 };
 
 struct EngineRun {
@@ -145,6 +146,8 @@ class Model {
     // persistent engine
     bool persistent_ = true;
     bool prefill_graphs_ = true;  // ChunkPrefill replays captured graphs (else launches directly)
+    bool gdn_fusion_ = true;      // the decode program fuses each GDN layer's in-projection and step
+    std::vector<std::string> phase_label_;  // per decode-program phase, for the profile
     int engine_grid_ = 0;
     void* engine_args_ = nullptr;  // host copy of DecodeArgs (opaque here)
     unsigned* eng_bar_ = nullptr;  // [0] error flag of the decode kernel

@@ -308,10 +308,38 @@ def test_profile_token_consumes_one_greedy_token_and_reports_every_phase(pair):
     cfg = json.loads(index)["config"]
     layers = cfg["layers"]
     attn = sum(1 for i in range(layers) if (i + 1) % cfg["full_attention_every"] == 0)
-    assert len(d["phases"]) == 5 * (layers - attn) + 6 * attn + 1
+    # a GDN layer is 4 phases when its in-projection and step run fused ("gdn.mixer_in+gdn"), else 5
+    fused = "gdn.mixer_in+gdn" in d["labels"]
+    assert fused == (name == "small")  # 16 GDN heads and q4 rows: fused on a 256-workgroup grid
+    assert len(d["phases"]) == (4 if fused else 5) * (layers - attn) + 6 * attn + 1
     assert all(v >= 0.0 for v in d["labels"].values())
-    phases = ("mixer_in", "gdn", "attention", "combine", "mixer_out", "gate_up", "down")
+    phases = ("mixer_in", "gdn", "mixer_in+gdn", "attention", "combine", "mixer_out", "gate_up", "down")
     assert set(d["labels"]) <= {f"{k}.{p}" for k in ("gdn", "attn") for p in phases} | {"lm_head"}
     places = d["places"]
     assert len(places) == len(d["input_ticks"][0]) and all(p is not None and p[0] >= 0 for p in places)
     assert d["total_ms"] > 0.0
+
+
+@pytest.mark.parametrize("name", ["small", "2b"])
+def test_fused_gdn_phase_equals_the_separate_phases(name):
+    """The decode program's fused GDN phase (in-projection rows, head-group q/k exchange and the
+    delta rule step in one phase) against the same model with the in-projection and the step as two
+    phases ({"gdn_fusion": false}): every row and the state update run the same arithmetic, so the
+    logits after the prompt and after each of 24 greedy steps, and the ids, are identical bit for
+    bit. "small" has q4 rows of 1024 columns, "2b" the benchmark model's rows of 2048."""
+    index, buf = W.synth_model(name, seed=21, body="q4", head="f16")
+    ids = prompt(json.loads(index)["config"]["vocab"], 33, 9)
+    runs = []
+    for fusion in (True, False):
+        with Q.Model.load(index, buf, options={"gdn_fusion": fusion}) as m:
+            m.prefill_batched(ids)
+            lg = [m.logits()]
+            out = m.decode_ids(24, 8, [])
+            m.reset()
+            m.prefill_batched(ids)
+            for i in range(23):
+                lg.append(m.step(out[i], len(ids) + i))
+            runs.append((out, np.stack(lg)))
+    (a_ids, a_lg), (b_ids, b_lg) = runs
+    assert a_ids == b_ids
+    assert np.array_equal(a_lg.view(np.uint32), b_lg.view(np.uint32)), float(np.max(np.abs(a_lg - b_lg)))
