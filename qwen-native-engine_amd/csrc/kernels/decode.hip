@@ -96,6 +96,13 @@ typedef const __attribute__((address_space(4))) float cfloat;
 typedef const __attribute__((address_space(4))) GdnExtra CGdnX;
 
 __device__ __forceinline__ void cbar() { asm volatile("" ::: "memory"); }
+// The lane id computed where it is used (volatile: the compiler does not hoist it, or values derived
+// from it, out of the phase loop, where they would hold registers for the whole launch).
+__device__ __forceinline__ int lane_here() {
+    uint32_t l;
+    asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
+    return (int)l;
+}
 // 2^x on the hardware unit (exp2(-inf) = 0).
 __device__ __forceinline__ float exp2_hw(float x) { return __builtin_amdgcn_exp2f(x); }
 // Workgroup barrier for LDS hand-offs only. Unlike __syncthreads it does not wait for the wave's
@@ -202,6 +209,19 @@ __device__ __forceinline__ void lds_dma16(const void* src, void* dst) {
                      : "=&s"(saved) : "v"(src), "s"(lds) : "memory");
     else
         asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off\n\ts_mov_b32 m0, %0"
+                     : "=&s"(saved) : "v"(src), "s"(lds) : "memory");
+}
+
+// 4 bytes per active lane (global_load_lds_dword: lane l lands at dst + 4 l), as lds_dma16.
+template <bool NT>
+__device__ __forceinline__ void lds_dma4(const void* src, void* dst) {
+    const uint32_t lds = __builtin_amdgcn_readfirstlane((uint32_t)(size_t)(lds_ptr_t)dst);
+    uint32_t saved;
+    if (NT)
+        asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %1, off nt\n\ts_mov_b32 m0, %0"
+                     : "=&s"(saved) : "v"(src), "s"(lds) : "memory");
+    else
+        asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %1, off\n\ts_mov_b32 m0, %0"
                      : "=&s"(saved) : "v"(src), "s"(lds) : "memory");
 }
 
@@ -457,7 +477,7 @@ struct Env {
     uint8_t* regs;  // all waves' regions
     float* red;
     int* bail;
-    unsigned long long* tt;  // profiling: the running phase's sub-step timestamps (registers)
+    unsigned long long* tt;  // profiling: the running phase's sub-step timestamps (thread 0's, in LDS)
 };
 
 __device__ __forceinline__ uint32_t tag_of(const DecodeArgs& a, int step, int p) {
@@ -466,7 +486,7 @@ __device__ __forceinline__ uint32_t tag_of(const DecodeArgs& a, int step, int p)
 
 // Profiling only: timestamp k (0..7) of the running phase, kept in registers until the phase ends.
 __device__ __forceinline__ void mark(const Env& e, int k) {
-    if (e.a->sub) e.tt[k] = __builtin_amdgcn_s_memrealtime();
+    if (e.a->sub && threadIdx.x == 0) e.tt[k] = __builtin_amdgcn_s_memrealtime();
 }
 
 // Whether the LM head has a register-streaming path (else it goes through the LDS region).
@@ -516,14 +536,69 @@ __device__ __forceinline__ int gf_row(int H, int h, int t, int wave, int slot) {
 __device__ __forceinline__ int gf_conv(CPhase& P) { return kGfSlots * P.stride; }
 __device__ __forceinline__ int gf_state(CPhase& P) { return (kGfSlots * P.stride + 96 + 127) & ~127; }
 
+// ---- the tiled q4 GEMV (PH_GEMV with P.tiled): geometry ----
+// Workgroup g owns outputs [o0, o0 + n) (rper / rrem per workgroup), in tiles of 16 matrix rows
+// (16 outputs, or 8 gate rows then the same 8 outputs' up rows), each tile two groups of 8 rows. K is
+// cut into 64-column chunks (one q4 group of 64, or half of a group of 128); wave w takes the
+// contiguous chunks [w Cw, (w + 1) Cw) of every tile, in blocks of 4 (128 bytes of a row: one cache
+// line). It prefetches exactly those into its half: nibbles [tile][block][row group 2][16-byte piece
+// 8][row 8][16 B] (one DMA instruction per (tile, block, row group): 8 whole lines; a chunk's 64-lane
+// B operand is then 512 contiguous bytes), then (scale, zero) pairs [tile][chunk][row 16][4 B].
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+// the workgroup's residual rows in the tiled layout (h_tiled), and the waves' partial row sums of a
+// tiled GEMV [kNW][4 tiles][16 rows]: fixed LDS addresses, no register holds them
+__shared__ float s_hres[kTiledMaxRes];
+__shared__ float s_tsum[kNW * 4 * 16];
+__device__ __forceinline__ void t_outputs(CPhase& P, int g, int& o0, int& n) {
+    o0 = g * P.rper + min(g, P.rrem);
+    n = P.rper + (g < P.rrem ? 1 : 0);
+}
+// Matrix row of tile slot (t, j), or -1 for a padding slot.
+__device__ __forceinline__ int t_row(CPhase& P, int o0, int n, int t, int j) {
+    if (P.epi == EP_SWIGLU) {
+        const int o = 8 * t + (j & 7);
+        return o < n ? (j < 8 ? 0 : P.rows) + o0 + o : -1;
+    }
+    const int o = 16 * t + j;
+    return o < n ? o0 + o : -1;
+}
+__device__ __forceinline__ int t_blocks(CPhase& P) { return (P.tcw + 3) >> 2; }
+__device__ __forceinline__ int t_pairs(CPhase& P) { return P.ttiles * t_blocks(P) * 2048; }
+
 // ---- prefetch of a region phase's data into one half of the wave's LDS region ----
 // GEMV: the wave's first outputs (rows, then their scale/zero pairs; for the GDN in-projection the
 // conv state and conv weights of those rows after them). GDN: the wave's 512-byte state column.
 // Attention: the K/V rows of the wave's positions, through the block table.
 __device__ __forceinline__ void prefetch(const Env& e, CPhase& P, CBufs& B, int step, uint8_t* __restrict__ nxt) {
     const DecodeArgs& a = *e.a;
-    const int lane = e.lane;
-    if (P.kind == PH_GEMV) {
+    const int lane = lane_here();
+    if (P.kind == PH_GEMV && P.tiled) {
+        int o0, n;
+        t_outputs(P, e.wg, o0, n);
+        const int T = P.ttiles, Cw = P.tcw, NB = t_blocks(P), c0 = e.wave * Cw;
+        const uint8_t* W = (const uint8_t*)B.w;
+        const uint8_t* SZ = (const uint8_t*)B.sz;
+        for (int t = 0; t < T; t++) {
+            // nibbles: per block of 4 chunks and group of 8 rows, lane l carries piece l / 8 of row l % 8
+            for (int b = 0; b < NB; b++) {
+                const int pc = 8 * b + (lane >> 3);  // piece of the wave's 32 Cw bytes of a row
+#pragma unroll
+                for (int g = 0; g < 2; g++) {
+                    const int r = t_row(P, o0, n, t, 8 * g + (lane & 7));
+                    if (pc < 2 * Cw && r >= 0)
+                        lds_dma16<true>(W + (size_t)r * P.rb + 32 * c0 + 16 * pc, nxt + ((t * NB + b) * 2 + g) * 1024);
+                }
+            }
+            // (scale, zero) pairs, four chunks per transfer: lane l carries chunk i0 + l / 16 of row l % 16
+            const int r = t_row(P, o0, n, t, lane & 15);
+            for (int i0 = 0; i0 < Cw; i0 += 4) {
+                const int i = i0 + (lane >> 4);
+                if (i < Cw && r >= 0)
+                    lds_dma4<true>(SZ + (size_t)r * P.szb + 4 * ((64 * (c0 + i)) >> P.gshift),
+                                   nxt + t_pairs(P) + (t * Cw + i0) * 64);
+            }
+        }
+    } else if (P.kind == PH_GEMV) {
         const GemvGeo g = geo(P);
         const Rows R = part_p(P, e.gwm);
         const int cnt = min(R.n, g.cap);
@@ -604,7 +679,7 @@ __device__ __forceinline__ float gemv_input(const Env& e, CPhase& P, CBufs& B, i
     float* xs = e.xs;
     const bool norm = P.xnorm == XN_NORM;
     const Step st = make_step(P);
-    const bool cm = !head_fast(P);  // the LDS-region GEMV reads chunk-major slices
+    const bool cm = !head_fast(P) && !P.tiled;  // the LDS-region GEMV reads chunk-major slices
     // the RMSNorm gains of the pairs this thread will poll, loaded before the poll so that their
     // latency overlaps it (norm inputs fit one polling round: in_n <= 2 * kT * kPoll)
     float2 gn[kPoll];
@@ -803,6 +878,160 @@ __device__ __forceinline__ void gemv_body(const Env& e, CPhase& P, CBufs& B, int
     }
 }
 
+// The tiled q4 GEMV phase (the GEMV of kernels/src/shaders.rs:45-376 with the Store / Accumulate /
+// SwiGlu epilogues) on v_mfma_i32_16x16x64_i8. x (staged in xs in column order, times the RMSNorm
+// gain) becomes, per 64-column chunk and in place, a fixed-point vector X = rint(x * 2^(22 - e))
+// (e: the chunk's exponent, so |X| < 2^22) held as three signed base-256 digits, X = d0 + 256 d1 +
+// 65536 d2. Those digits are the MFMA's A rows 0..2, the tile's 16 rows of nibbles (q in 0..15 as
+// int8) its B columns: D[d][row] = sum_k d_k q_k exactly, and per chunk and row
+//   y += s * 2^(e - 22) * (D0 + 256 D1 + 65536 D2 - z * sum_k X_k)
+// is sum_k s (q_k - z) x_k to within the quantisation of x (2^-23 of the chunk's largest value).
+// Chunk layout after the conversion (256 bytes, was 64 floats): [k group 0..3][digit 0..2][16 bytes,
+// columns in the order the nibble unpacking gives: 0 2 4 6 1 3 5 7 8 10 12 14 9 11 13 15], then
+// sum X (int) at byte 192 and 2^(e - 22) (float) at 196.
+__device__ __forceinline__ void tiled_digits(const Env& e, CPhase& P) {
+    float* xs = e.xs;
+    const int C = P.k >> 6;
+    const bool gdn = P.xnorm == XN_GDN;
+    for (int base = 0; base < 16 * C; base += kT) {
+        const int q = base + (int)threadIdx.x;
+        if (q >= 16 * C) break;  // whole waves: 16 C is a multiple of 64 (K a multiple of 256)
+        const int c = q >> 4, i = q & 15;
+        // thread i takes the 4 columns whose digits form one word of the A layout: k group kq = i / 4,
+        // columns 16 kq + {0, 2, 4, 6}, {1, 3, 5, 7}, {8, 10, 12, 14} or {9, 11, 13, 15} (sub = i % 4)
+        const int kq = i >> 2, sub = i & 3, col = 64 * c + 16 * kq + 8 * (sub >> 1) + (sub & 1);
+        float4 v;
+        v.x = xs[col];
+        v.y = xs[col + 2];
+        v.z = xs[col + 4];
+        v.w = xs[col + 6];
+        if (gdn) {
+            // GDN output norm (kernels/src/shaders.rs:514): the chunk lies in head (64 c) / 128, whose
+            // 1/rms comes from the head's 16 published partial sums of squares (staged past K)
+            const float4* ps = (const float4*)(xs + P.k + 16 * ((64 * c) / kDK));
+            const float4 a0 = ps[0], a1 = ps[1], a2 = ps[2], a3 = ps[3];
+            const float ssum = (((a0.x + a0.y) + (a0.z + a0.w)) + ((a1.x + a1.y) + (a1.z + a1.w))) +
+                               (((a2.x + a2.y) + (a2.z + a2.w)) + ((a3.x + a3.y) + (a3.z + a3.w)));
+            const float sc = 1.0f / sqrtf(ssum / (float)kDK + 1e-6f);
+            v.x *= sc; v.y *= sc; v.z *= sc; v.w *= sc;
+        }
+        float m = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+        // the chunk's 16 threads (a DPP row): every lane receives the maximum
+        m = fmaxf(m, QNE_DPP(m, kDppXor1));
+        m = fmaxf(m, QNE_DPP(m, kDppXor2));
+        m = fmaxf(m, QNE_DPP(m, kDppHalfMirror));
+        m = fmaxf(m, QNE_DPP(m, kDppMirror));
+        int ex = 0;
+        (void)frexpf(m, &ex);  // m < 2^ex (m = 0: ex = 0, every digit 0)
+        const float f = ldexpf(1.0f, 22 - ex);
+        const int x0 = (int)rintf(v.x * f), x1 = (int)rintf(v.y * f), x2 = (int)rintf(v.z * f), x3 = (int)rintf(v.w * f);
+        int sx = (x0 + x1) + (x2 + x3);
+        sx += __builtin_amdgcn_update_dpp(0, sx, kDppXor1, 0xF, 0xF, false);
+        sx += __builtin_amdgcn_update_dpp(0, sx, kDppXor2, 0xF, 0xF, false);
+        sx += __builtin_amdgcn_update_dpp(0, sx, kDppHalfMirror, 0xF, 0xF, false);
+        sx += __builtin_amdgcn_update_dpp(0, sx, kDppMirror, 0xF, 0xF, false);
+        // signed base-256 digits: the bytes of (X + 0x808080) ^ 0x808080
+        const uint32_t z0 = (uint32_t)(x0 + 0x808080) ^ 0x808080u, z1 = (uint32_t)(x1 + 0x808080) ^ 0x808080u;
+        const uint32_t z2 = (uint32_t)(x2 + 0x808080) ^ 0x808080u, z3 = (uint32_t)(x3 + 0x808080) ^ 0x808080u;
+        cbar();  // every value of the chunk is read before its bytes are overwritten (one wave, in order)
+        uint8_t* ch = (uint8_t*)(xs + 64 * c);
+#pragma unroll
+        for (int d = 0; d < 3; d++) {
+            const uint32_t sh = 8 * d;
+            *(uint32_t*)(ch + (kq * 3 + d) * 16 + 4 * sub) = ((z0 >> sh) & 0xFFu) | (((z1 >> sh) & 0xFFu) << 8) |
+                                                             (((z2 >> sh) & 0xFFu) << 16) | (((z3 >> sh) & 0xFFu) << 24);
+        }
+        if (i == 0) {
+            *(int*)(ch + 192) = sx;
+            *(float*)(ch + 196) = ldexpf(1.0f, ex - 22);
+        }
+    }
+}
+
+__device__ __forceinline__ void tiled_body(const Env& e, CPhase& P, CBufs& B, int step, int p, float inv, uint8_t* cur) {
+    const DecodeArgs& a = *e.a;
+    const int lane = lane_here();
+    mark(e, 0);
+    wait_all();  // this wave's chunks (issued two region phases ago) are in
+    tiled_digits(e, P);
+    bar();
+    mark(e, 1);
+    int o0, n;
+    t_outputs(P, e.wg, o0, n);
+    const int T = P.ttiles, Cw = P.tcw, j = lane & 15, kq = lane >> 4;
+    const uint8_t* xb = (const uint8_t*)e.xs + 256 * (e.wave * Cw);  // the wave's first chunk
+    const i32x4 zero = {0, 0, 0, 0};
+    const int NB = t_blocks(P);
+    static_assert(12 * 64 * kNW >= 6144, "the widest q4 GEMV: 12 chunks per wave");
+    // B operand of lane (j, kq) for chunk i of tile t: row group j / 8, row j % 8, piece 2 (i % 4) + kq / 2
+    const int boff = (j >> 3) * 1024 + (kq >> 1) * 128 + (j & 7) * 16 + 8 * (kq & 1);
+    for (int t = 0; t < T; t++) {
+        float acc = 0.0f;
+        for (int i0 = 0; i0 < Cw; i0 += 4) {
+            // four chunks at a time (one block): every load issued before the first MFMA waits
+            const uint8_t* blk = cur + (t * NB + (i0 >> 2)) * 2048 + boff;
+            i32x4 A[4], Bv[4];
+            uint32_t pr[4];
+            float sxf[4], xf[4];
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const int i = min(i0 + u, Cw - 1);
+                const uint8_t* ch = xb + 256 * i;
+                // A rows 3..15 are zero (their lanes read row 0 and drop it)
+                const i32x4 a = *(const i32x4*)(ch + (kq * 3 + (j < 3 ? j : 0)) * 16);
+                A[u] = j < 3 ? a : zero;
+                const u32x2 hx = *(const u32x2*)(ch + 192);
+                sxf[u] = (float)(int)hx.x;
+                xf[u] = __uint_as_float(hx.y);
+                pr[u] = *(const uint32_t*)(cur + t_pairs(P) + ((t * Cw + i) * 16 + j) * 4);
+                const u32x2 w = *(const u32x2*)(blk + 256 * (i - i0));
+                Bv[u].x = (int)(w.x & 0x0F0F0F0Fu);
+                Bv[u].y = (int)((w.x >> 4) & 0x0F0F0F0Fu);
+                Bv[u].z = (int)(w.y & 0x0F0F0F0Fu);
+                Bv[u].w = (int)((w.y >> 4) & 0x0F0F0F0Fu);
+            }
+            i32x4 D[4];
+#pragma unroll
+            for (int u = 0; u < 4; u++) D[u] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[u], Bv[u], zero, 0, 0, 0);
+            // lanes 0..15: D[digit 0..2][row j] in D.x, D.y, D.z
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                if (i0 + u < Cw) {
+                    const float comb = fmaf(65536.0f, (float)D[u].z, fmaf(256.0f, (float)D[u].y, (float)D[u].x));
+                    acc = fmaf(lo_h(pr[u]) * xf[u], comb - hi_h(pr[u]) * sxf[u], acc);
+                }
+            }
+        }
+        if (lane < 16) s_tsum[(e.wave * 4 + t) * 16 + lane] = acc;
+    }
+    mark(e, 2);
+    bar();
+    // one thread per output: the waves' partials in wave order, then the epilogue
+    const int o = (int)threadIdx.x;
+    if (o < n) {
+        const uint32_t tag = tag_of(a, step, p);
+        uint64_t* out = B.out + (size_t)(step & 1) * P.out_stride;
+        auto rowsum = [&](int slot) {
+            float s = 0.0f;
+            for (int w = 0; w < kNW; w++) s += s_tsum[(w * 4 + (slot >> 4)) * 16 + (slot & 15)];
+            return s * inv;
+        };
+        float y;
+        if (P.epi == EP_SWIGLU) {
+            const int t = o >> 3, jj = o & 7;
+            y = silu(rowsum(16 * t + jj)) * rowsum(16 * t + 8 + jj);
+        } else {
+            y = rowsum(o);
+            if (P.epi == EP_RESID) {
+                s_hres[o] += y;
+                y = s_hres[o];
+            }
+        }
+        put(out, (uint32_t)(o0 + o), y, tag);
+    }
+    mark(e, 3);
+}
+
 // The inputs of GDN item `it` (head h, value columns 8cb..8cb+7): q_h, k_h (64 pairs each), v and
 // z of the 8 columns (4 pairs each), a_h and b_h; staged at xs[0..276).
 __device__ __forceinline__ void gdn_input(const Env& e, CPhase& P, CBufs& B, int step, int p, int it, const Ctl& c) {
@@ -894,7 +1123,7 @@ __device__ __forceinline__ void gdn_body(const Env& e, CPhase& P, CBufs& B, int 
 __device__ __forceinline__ void gdnf_phase(const Env& e, CPhase& P, CBufs& B, int step, int p, float inv, uint8_t* cur,
                                            const Ctl& c) {
     const DecodeArgs& a = *e.a;
-    const int lane = e.lane, H = P.heads;
+    const int lane = lane_here(), H = P.heads;
     mark(e, 0);
     wait_all();  // rows, conv and state column (issued two region phases ago) are in
     const int it = gf_item(P, e.wg), h = it >> 4, cb = it & 15, t = cb * 8 + e.wave;
@@ -987,7 +1216,8 @@ __device__ __forceinline__ void gdnf_phase(const Env& e, CPhase& P, CBufs& B, in
 // RMSNorm (weight w) + rotate-half RoPE of one 256-vector held 4 values per lane
 // (kernels/src/shaders.rs:575-593). rope = {cos[64], sin[64]} of the step's angles.
 __device__ __forceinline__ void norm_rope4(float (&v)[4], const float* w, const DecodeArgs& a, const float* rope,
-                                           int lane) {
+                                           int) {
+    const int lane = lane_here();
     float ss = v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3];
     ss = wave_sum_dpp(ss);
     const float inv = 1.0f / sqrtf(ss / (float)kHeadDim + 1e-6f);
@@ -1317,7 +1547,9 @@ __device__ __forceinline__ void decode_program(const DecodeArgs& a) {
     e.regs = regs;
     e.red = red;
     e.bail = &bail;
-    unsigned long long tts[8];
+    // profiling: thread 0's sub-step timestamps of the running phase (LDS, so that no register
+    // holds them for the whole launch)
+    __shared__ unsigned long long tts[8];
     e.tt = tts;
     // profiling: the workgroup's place, (XCC_ID << 32 | HW_ID) + 1, kept in sub-step slot 6
     unsigned long long where = 0;
@@ -1371,8 +1603,15 @@ __device__ __forceinline__ void decode_program(const DecodeArgs& a) {
             }
             ss = wave_sum_dpp(ss);
             if (e.lane == 0) red[e.wave] = ss;
-            if (own.n > 0) ws.hown[0] = embed_val(a, token, own.r0);
-            if (own.n > 1) ws.hown[1] = embed_val(a, token, own.r0 + 1);
+            if (a.h_tiled) {
+                // the residual rows this workgroup's tiled GEMVs own (their outputs of a hidden-wide phase)
+                const int per = a.hidden / e.nwg, rem = a.hidden % e.nwg;
+                const int r0 = e.wg * per + min(e.wg, rem), rn = per + (e.wg < rem ? 1 : 0);
+                if ((int)threadIdx.x < rn) s_hres[threadIdx.x] = embed_val(a, token, r0 + (int)threadIdx.x);
+            } else {
+                if (own.n > 0) ws.hown[0] = embed_val(a, token, own.r0);
+                if (own.n > 1) ws.hown[1] = embed_val(a, token, own.r0 + 1);
+            }
             bar();
             if (threadIdx.x == 0) {
                 float t = 0.0f;
@@ -1390,9 +1629,10 @@ __device__ __forceinline__ void decode_program(const DecodeArgs& a) {
             const int inst = step * a.nph + p;
             const int rh = half;
             if (a.sub) {
-#pragma unroll
-                for (int k = 0; k < 8; k++) tts[k] = 0;
-                tts[6] = where;  // not a timestamp: where this workgroup runs
+                if (threadIdx.x == 0) {
+                    for (int k = 0; k < 8; k++) tts[k] = 0;
+                    tts[6] = where;  // not a timestamp: where this workgroup runs
+                }
             }
             switch (P.kind) {
                 case PH_GEMV: {
@@ -1401,6 +1641,8 @@ __device__ __forceinline__ void decode_program(const DecodeArgs& a) {
                     trace_in(e, inst);
                     if (head_fast(P)) {
                         head_phase(e, P, B, ws, inv);
+                    } else if (P.tiled) {
+                        tiled_body(e, P, B, step, p, inv, region(rh));
                     } else {
                         gemv_body(e, P, B, step, p, ws, inv, region(rh), xs);
                     }
@@ -1544,11 +1786,32 @@ void finalize_phase(Phase& P, int grid) {
         P.nsteps = P.mkind ? P.n4 + P.n2 + P.n1 : P.k / 512;
     }
     if ((P.kind == PH_ATTN || P.kind == PH_COMB) && P.kv_heads > 0) P.splits = std::min(grid / P.kv_heads, kMaxSplits);
+    if (P.kind == PH_GEMV && P.tiled) {
+        // outputs per workgroup, not per wave
+        P.rper = P.rows / grid;
+        P.rrem = P.rows % grid;
+        const int n = P.rper + (P.rrem ? 1 : 0);
+        P.ttiles = P.epi == EP_SWIGLU ? (n + 7) / 8 : (n + 15) / 16;
+        P.tcw = P.k / 64 / kNW;
+        P.nm = P.epi == EP_SWIGLU ? 2 : 1;
+    }
     if (P.kind == PH_GDNF) {
         P.fast_head = 0;
         P.xcd = grid % 8 == 0 && P.heads % 8 == 0 && grid == 16 * P.heads;
     }
     P.region = (P.kind == PH_GEMV && !P.fast_head) || P.kind == PH_GDN || P.kind == PH_ATTN || P.kind == PH_GDNF;
+}
+
+bool gemv_tileable(const Phase& P, int grid) {
+    if (P.kind != PH_GEMV || P.mkind != 1 || P.group % 64 != 0 || P.k % (64 * kNW) != 0 || P.xin != XI_EXCH) return false;
+    if (P.epi != EP_STORE && P.epi != EP_RESID && P.epi != EP_SWIGLU) return false;
+    const int n = (P.rows + grid - 1) / grid;
+    const int T = P.epi == EP_SWIGLU ? (n + 7) / 8 : (n + 15) / 16;
+    if (T < 1 || T > 4 || n > kT) return false;
+    if (P.epi == EP_RESID && n > kTiledMaxRes) return false;
+    if (P.xnorm == XN_GDN && P.k % kDK != 0) return false;
+    const int Cw = P.k / 64 / kNW, NB = (Cw + 3) / 4;
+    return T * NB * 2048 + T * Cw * 64 <= kHalf;  // nibble blocks, then pairs
 }
 
 bool gdn_fusable(int kind, int k, int group, int heads, int grid) {

@@ -48,6 +48,8 @@ struct Phase {
     int in2_rel = 0;    // second input (COMB: the gate in the in-projection output)
     int is_head = 0;    // phase runs only on steps that compute logits
     int xcd = 0;        // PH_GDNF: the 16 workgroups of a head share an XCD (workgroup w runs on XCD w % 8 + c)
+    int tiled = 0;      // q4 GEMV on the matrix cores: rows owned by workgroups in tiles of 16, K split over waves
+    int ttiles = 0, tcw = 0;  // tiled: row tiles per workgroup, 64-column chunks per wave
     uint32_t in_stride = 0, in2_stride = 0, out_stride = 0;  // u64 entries
     uint32_t in_cap = 0, in2_cap = 0;  // entries readable from in / in2 (bounds of the polling loads)
     // Derived by finalize_phase from the fields above and the launch grid, so the kernel reads
@@ -139,6 +141,9 @@ struct DecodeArgs {
     // region phases (those that read prefetched data): the first two of a step (LM head excluded)
     // and the LM head when it is one (else -1); set by finalize_program
     int reg0 = -1, reg1 = -1, head_reg = -1;
+    // 1: the residual stream's rows are owned by workgroups (the tiled GEMVs' output rows), kept in
+    // LDS; 0: by waves (two rows at most per wave, in registers)
+    int h_tiled = 0;
     unsigned* err = nullptr;  // [0] set on a polling timeout
     unsigned spin_limit = 1u << 20;
     // Optional device timeline (ticks of the constant-rate wall clock): trace[0] start, trace[1]
@@ -170,6 +175,9 @@ void split_program(const Phase* prog, int nph, std::vector<PhaseBufs>& bufs, std
 // Whether a GDN layer's in-projection (matrix kind, K, group) fits the fused PH_GDNF phase on a
 // grid of `grid` workgroups with `heads` GDN heads of 128 channels.
 bool gdn_fusable(int kind, int k, int group, int heads, int grid);
+// Whether a GEMV phase (finalized fields not needed) can run tiled on the matrix cores.
+bool gemv_tileable(const Phase& P, int grid);
+constexpr int kTiledMaxRes = 16;  // residual rows a workgroup may own in the tiled layout
 // GEMV shapes compiled into the kernel: variant id of (matrix kind, K), or -1.
 int decode_gemv_variant(int kind, int k);
 hipError_t launch_decode(const DecodeArgs& a, int grid, hipStream_t st);

@@ -95,6 +95,11 @@ LoadOptions parse_options(const char* json) {
         if (e != "graph" && e != "persistent") throw Error(QNE_EINVAL, "engine must be \"persistent\" or \"graph\"");
         o.graph_engine = e == "graph";
     }
+    if (j.has("mfma_gemv")) {
+        const Json& v = j.at("mfma_gemv");
+        if (v.type != Json::Bool) throw Error(QNE_EINVAL, "mfma_gemv must be true or false");
+        o.mfma_gemv = v.b;
+    }
     if (j.has("gdn_fusion")) {
         const Json& v = j.at("gdn_fusion");
         if (v.type != Json::Bool) throw Error(QNE_EINVAL, "gdn_fusion must be true or false");
@@ -151,6 +156,7 @@ Model::Model(const ModelIndex& ix, const uint8_t* weights, uint64_t /*wlen*/, co
     persistent_ = !opt.graph_engine;
     prefill_graphs_ = opt.prefill_graphs;
     gdn_fusion_ = opt.gdn_fusion;
+    mfma_gemv_ = opt.mfma_gemv;
     try {
         upload(ix, weights);
         alloc_state();
@@ -607,6 +613,13 @@ void Model::setup_engine() {
             P.in2_stride = P.in2_cap = bufs[out_buf[s2]].n;
         }
     }
+    // q4 GEMVs on the matrix cores (tiled): all or none of the residual phases, since the tiled
+    // phases keep the residual rows they own per workgroup
+    bool tiled = mfma_gemv_ && (c.hidden + grid - 1) / grid <= kTiledMaxRes;
+    for (const Phase& P : prog)
+        if (P.kind == PH_GEMV && P.epi == EP_RESID && !gemv_tileable(P, grid)) tiled = false;
+    if (tiled)
+        for (Phase& P : prog) P.tiled = gemv_tileable(P, grid) ? 1 : 0;
     for (Phase& P : prog) finalize_phase(P, grid);
     DecodeArgs links;
     if (!finalize_program(prog.data(), (int)prog.size(), links)) throw unsupported("too few region phases per step");
@@ -634,6 +647,7 @@ void Model::setup_engine() {
     a->prog = d_prog;
     a->shapes = d_shapes;
     a->gdnx = d_gdnx;
+    a->h_tiled = tiled ? 1 : 0;
     a->nph = nph_;
     a->reg0 = links.reg0; a->reg1 = links.reg1; a->head_reg = links.head_reg;
     a->emb_w = embed_.w; a->emb_sz = embed_.sz; a->emb_kind = embed_.kind; a->emb_group = embed_.group;

@@ -38,6 +38,7 @@ struct LoadOptions {
     bool graph_engine = false;  // per-kernel hipGraph path instead of the persistent kernel
     bool prefill_graphs = true;  // prefill_chunk passes replay captured graphs (false: direct launches)
     bool gdn_fusion = true;      // persistent kernel: GDN in-projection and step in one phase where the shapes allow
+    bool mfma_gemv = true;       // persistent kernel: q4 GEMVs on the int8 matrix cores where the shapes allow
 };
 
 struct EngineRun {
@@ -147,6 +148,7 @@ class Model {
     bool persistent_ = true;
     bool prefill_graphs_ = true;  // ChunkPrefill replays captured graphs (else launches directly)
     bool gdn_fusion_ = true;      // the decode program fuses each GDN layer's in-projection and step
+    bool mfma_gemv_ = true;       // the decode program runs q4 GEMVs tiled on the matrix cores
     std::vector<std::string> phase_label_;  // per decode-program phase, for the profile
     int engine_grid_ = 0;
     void* engine_args_ = nullptr;  // host copy of DecodeArgs (opaque here)

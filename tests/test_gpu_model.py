@@ -343,3 +343,30 @@ def test_fused_gdn_phase_equals_the_separate_phases(name):
     (a_ids, a_lg), (b_ids, b_lg) = runs
     assert a_ids == b_ids
     assert np.array_equal(a_lg.view(np.uint32), b_lg.view(np.uint32)), float(np.max(np.abs(a_lg - b_lg)))
+
+
+@pytest.mark.parametrize("name", ["small", "2b"])
+def test_mfma_gemv_matches_the_vector_path(name):
+    """The decode program's q4 GEMVs on the int8 matrix cores (x as three signed base-256 digits of a
+    22-bit fixed-point value per 64 columns, exact integer products) against the same GEMVs on the
+    vector ALUs in f32 ({"mfma_gemv": false}): the same greedy ids over 24 steps, and logits after
+    the prompt and every step within 2e-4 of each other (the two paths round x differently: the
+    digits keep 2^-22 of each 64-column group's largest value, f32 products 2^-24 of each product)."""
+    index, buf = W.synth_model(name, seed=23, body="q4", head="f16")
+    ids = prompt(json.loads(index)["config"]["vocab"], 33, 10)
+    runs = []
+    for mfma in (True, False):
+        with Q.Model.load(index, buf, options={"mfma_gemv": mfma}) as m:
+            m.prefill_batched(ids)
+            lg = [m.logits()]
+            out = m.decode_ids(24, 8, [])
+            m.reset()
+            m.prefill_batched(ids)
+            for i in range(23):
+                lg.append(m.step(out[i], len(ids) + i))
+            runs.append((out, np.stack(lg)))
+    (a_ids, a_lg), (b_ids, b_lg) = runs
+    err = float(np.max(np.abs(a_lg - b_lg)))
+    print(f"{name}: matrix-core vs vector GEMVs: ids identical {a_ids == b_ids}, max |dlogit| {err:.2e}")
+    assert a_ids == b_ids
+    assert err <= 2e-4
