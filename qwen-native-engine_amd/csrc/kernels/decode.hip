@@ -1213,6 +1213,72 @@ __device__ __forceinline__ void gdnf_phase(const Env& e, CPhase& P, CBufs& B, in
     mark(e, 3);
 }
 
+// Combine of the attention partials (the merge of shaders.rs:522-633's split form): item = (q head
+// h, 64 dims c); the S splits' (max, sum, acc) of the head, times sigmoid(gate). `part` holds the
+// partials (tag tin), `gsrc` the in-projection output with the gate (tag tin2); the 64 outputs go to
+// `out` with `tag`. Every thread of the workgroup takes part (polls end with barriers).
+static_assert(66 * kMaxSplits + 64 + 64 * kNW + kNW <= kXs, "the combine's staging must fit in xs");
+__device__ __forceinline__ void comb_core(const Env& e, int nq, int G, int S, int h, int cq, const uint64_t* part,
+                                          uint32_t part_cap, uint32_t tin, const uint64_t* gsrc, uint32_t g_cap,
+                                          uint32_t tin2, uint64_t* out, uint32_t tag, const Ctl& c) {
+    const int g = h / G, gi = h % G;
+    float* xs = e.xs;
+    // xs: ml[2S] then acc[S][64] then gate[64]
+    poll_pairs(part, part_cap, S * 33, tin,
+               [&](int q) {
+                   const int s = q / 33, j = q % 33;
+                   const int base = ((g * S + s) * G + gi) * 258;
+                   return j == 0 ? base : base + 2 + 64 * cq + 2 * (j - 1);
+               },
+               [&](int q, float v0, float v1) {
+                   const int s = q / 33, j = q % 33;
+                   const int d = j == 0 ? 2 * s : 2 * S + 64 * s + 2 * (j - 1);
+                   xs[d] = v0;
+                   xs[d + 1] = v1;
+               },
+               c);
+    const int ga = nq * kHeadDim + h * kHeadDim + 64 * cq;
+    poll_pairs(gsrc, g_cap, 32, tin2, [&](int q) { return ga + 2 * q; },
+               [&](int q, float v0, float v1) {
+                   xs[2 * S + 64 * S + 2 * q] = v0;
+                   xs[2 * S + 64 * S + 2 * q + 1] = v1;
+               },
+               c);
+    bar();
+    if (*e.bail) return;
+    {
+        // wave sg takes splits sg, sg + 8, ...; lane = dim. Their sums meet in xs after the gate.
+        const int d = threadIdx.x & 63, sg = threadIdx.x >> 6;
+        // every wave finds the maximum over the splits with its lanes (one split each), in parallel
+        float mm = -INFINITY;
+        for (int s = d; s < S; s += kWave) mm = fmaxf(mm, xs[2 * s]);
+        const float mn = wave_max(mm);
+        float ls = 0.0f, ac = 0.0f;
+        for (int s = sg; s < S; s += kNW) {
+            const float ms = xs[2 * s];
+            if (ms == -INFINITY) continue;
+            const float cw = exp2_hw(ms - mn);  // the partials' maxima and sums are in base 2
+            ls += xs[2 * s + 1] * cw;
+            ac += xs[2 * S + 64 * s + d] * cw;
+        }
+        float* rd = xs + 2 * S + 64 * S + 64;  // [kNW][64] sums of acc, then [kNW] sums of l
+        rd[64 * sg + d] = ac;
+        if (d == 0) rd[64 * kNW + sg] = ls;
+        bar();
+        if (threadIdx.x < 64) {
+            float at = 0.0f, lt = 0.0f;
+#pragma unroll
+            for (int w = 0; w < kNW; w++) {
+                at += rd[64 * w + d];
+                lt += rd[64 * kNW + w];
+            }
+            const float gate = xs[2 * S + 64 * S + d];
+            put(out, (uint32_t)(h * kHeadDim + 64 * cq + d), at / lt / (1.0f + expf(-gate)), tag);
+        }
+    }
+    bar();
+}
+
 // RMSNorm (weight w) + rotate-half RoPE of one 256-vector held 4 values per lane
 // (kernels/src/shaders.rs:575-593). rope = {cos[64], sin[64]} of the step's angles.
 __device__ __forceinline__ void norm_rope4(float (&v)[4], const float* w, const DecodeArgs& a, const float* rope,
@@ -1256,7 +1322,9 @@ __device__ __forceinline__ void attn_phase(const Env& e, CPhase& P, CBufs& B, in
     const int p0 = split_at(sp, len, S), p1 = split_at(sp + 1, len, S);
     const uint32_t tin = tag_of(a, step, p - P.in_rel), tag = tag_of(a, step, p);
     const uint64_t* in = B.in + (size_t)(step & 1) * P.in_stride;
-    uint64_t* out = B.out + (size_t)(step & 1) * P.out_stride;
+    // the partials: this phase's output, or with the combine folded in, the phase's own exchange
+    // buffer (B.aux) and the combined vector its output
+    uint64_t* out = P.fold ? (uint64_t*)B.aux + (size_t)(step & 1) * P.part_stride : B.out + (size_t)(step & 1) * P.out_stride;
     uint16_t* kp = (uint16_t*)B.w;
     uint16_t* vp = (uint16_t*)B.sz;
     float* xs = e.xs;
@@ -1427,78 +1495,29 @@ __device__ __forceinline__ void attn_phase(const Env& e, CPhase& P, CBufs& B, in
         }
     }
     bar();  // the regions are free again
+    if (P.fold) {
+        // the combine, folded in: workgroup (g, sp) with sp < 4 G merges q head g G + sp / 4, dims
+        // 64 (sp % 4) .. + 63 over the group's S splits (an exchange among the group's workgroups)
+        if (sp < 4 * G)
+            comb_core(e, nq, G, S, g * G + sp / 4, sp % 4, out, P.part_stride, tag, in, P.in_cap, tin,
+                      B.out + (size_t)(step & 1) * P.out_stride, tag, c);
+    }
     mark(e, 5);
 }
 
-// Combine of the attention partials: workgroup = (q head h, 64 dims c); times sigmoid(gate).
-static_assert(66 * kMaxSplits + 64 + 64 * kNW + kNW <= kXs, "the combine's staging must fit in xs");
+// The combine as a phase of its own (PH_COMB): workgroup = (q head h, 64 dims c).
 __device__ __forceinline__ void comb_phase(const Env& e, CPhase& P, CBufs& B, int step, int p, const Ctl& c) {
     const DecodeArgs& a = *e.a;
     const int nq = P.heads, nkv = P.kv_heads, G = nq / nkv, S = P.splits;
     if (e.wg >= nq * 4) return;
     mark(e, 0);
-    const int h = e.wg / 4, cq = e.wg % 4, g = h / G, gi = h % G;
     const uint32_t tin = tag_of(a, step, p - P.in_rel), tin2 = tag_of(a, step, p - P.in2_rel), tag = tag_of(a, step, p);
     const uint64_t* in = B.in + (size_t)(step & 1) * P.in_stride;
     const uint64_t* in2 = (const uint64_t*)B.aux + (size_t)(step & 1) * P.in2_stride;
     uint64_t* out = B.out + (size_t)(step & 1) * P.out_stride;
-    float* xs = e.xs;
-    // xs: ml[2S] then acc[S][64] then gate[64]
-    poll_pairs(in, P.in_cap, S * 33, tin,
-               [&](int q) {
-                   const int s = q / 33, j = q % 33;
-                   const int base = ((g * S + s) * G + gi) * 258;
-                   return j == 0 ? base : base + 2 + 64 * cq + 2 * (j - 1);
-               },
-               [&](int q, float v0, float v1) {
-                   const int s = q / 33, j = q % 33;
-                   const int d = j == 0 ? 2 * s : 2 * S + 64 * s + 2 * (j - 1);
-                   xs[d] = v0;
-                   xs[d + 1] = v1;
-               },
-               c);
     mark(e, 1);
-    const int ga = nq * kHeadDim + h * kHeadDim + 64 * cq;
-    poll_pairs(in2, P.in2_cap, 32, tin2, [&](int q) { return ga + 2 * q; },
-               [&](int q, float v0, float v1) {
-                   xs[2 * S + 64 * S + 2 * q] = v0;
-                   xs[2 * S + 64 * S + 2 * q + 1] = v1;
-               },
-               c);
-    bar();
-    if (*e.bail) return;
+    comb_core(e, nq, G, S, e.wg / 4, e.wg % 4, in, P.in_cap, tin, in2, P.in2_cap, tin2, out, tag, c);
     mark(e, 2);
-    {
-        // wave sg takes splits sg, sg + 8, ...; lane = dim. Their sums meet in xs after the gate.
-        const int d = threadIdx.x & 63, sg = threadIdx.x >> 6;
-        // every wave finds the maximum over the splits with its lanes (one split each), in parallel
-        float mm = -INFINITY;
-        for (int s = d; s < S; s += kWave) mm = fmaxf(mm, xs[2 * s]);
-        const float mn = wave_max(mm);
-        float ls = 0.0f, ac = 0.0f;
-        for (int s = sg; s < S; s += kNW) {
-            const float ms = xs[2 * s];
-            if (ms == -INFINITY) continue;
-            const float cw = exp2_hw(ms - mn);  // the partials' maxima and sums are in base 2
-            ls += xs[2 * s + 1] * cw;
-            ac += xs[2 * S + 64 * s + d] * cw;
-        }
-        float* rd = xs + 2 * S + 64 * S + 64;  // [kNW][64] sums of acc, then [kNW] sums of l
-        rd[64 * sg + d] = ac;
-        if (d == 0) rd[64 * kNW + sg] = ls;
-        bar();
-        if (threadIdx.x < 64) {
-            float at = 0.0f, lt = 0.0f;
-#pragma unroll
-            for (int w = 0; w < kNW; w++) {
-                at += rd[64 * w + d];
-                lt += rd[64 * kNW + w];
-            }
-            const float gate = xs[2 * S + 64 * S + d];
-            put(out, (uint32_t)(h * kHeadDim + 64 * cq + d), at / lt / (1.0f + expf(-gate)), tag);
-        }
-    }
-    bar();
     mark(e, 3);
 }
 
@@ -1880,6 +1899,7 @@ void split_program(const Phase* prog, int nph, std::vector<PhaseBufs>& bufs, std
         } else if (P.kind == PH_ATTN) {
             b.w = P.kp;
             b.sz = P.vp;
+            b.aux = P.part;
         } else {
             b.aux = P.in2;
         }

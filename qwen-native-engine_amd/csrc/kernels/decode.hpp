@@ -49,6 +49,8 @@ struct Phase {
     int is_head = 0;    // phase runs only on steps that compute logits
     int xcd = 0;        // PH_GDNF: the 16 workgroups of a head share an XCD (workgroup w runs on XCD w % 8 + c)
     int tiled = 0;      // q4 GEMV on the matrix cores: rows owned by workgroups in tiles of 16, K split over waves
+    int fold = 0;       // PH_ATTN: the combine of the partials runs in the same phase (no PH_COMB)
+    uint32_t part_stride = 0;  // fold: entries of the partials buffer per step parity
     int ttiles = 0, tcw = 0;  // tiled: row tiles per workgroup, 64-column chunks per wave
     uint32_t in_stride = 0, in2_stride = 0, out_stride = 0;  // u64 entries
     uint32_t in_cap = 0, in2_cap = 0;  // entries readable from in / in2 (bounds of the polling loads)
@@ -81,6 +83,7 @@ struct Phase {
     const float* prm = nullptr;
     uint64_t* grp = nullptr;
     uint32_t grp_stride = 0;
+    uint64_t* part = nullptr;  // PH_ATTN with fold: the partials buffer
 };
 
 // Per-phase buffers of a PH_GDNF phase beyond its PhaseBufs record (indexed by PhaseBufs::xi).
@@ -100,7 +103,7 @@ struct PhaseBufs {
     const void* w = nullptr;     // GEMV rows; GDN recurrent state; attention K pool
     const void* sz = nullptr;    // GEMV q4 (scale, zero) rows; attention V pool
     const float* gain = nullptr;
-    const void* aux = nullptr;   // EP_CONV conv weights; combine: the second input
+    const void* aux = nullptr;   // EP_CONV conv weights; combine: the second input; folded attention: its partials
     float* conv = nullptr;       // EP_CONV conv state
     uint64_t* in = nullptr;
     uint64_t* out = nullptr;

@@ -481,7 +481,7 @@ void Model::setup_engine() {
     };
     // input links: (phase index, buffer id) of each published vector
     std::vector<int> out_buf;
-    std::vector<int> grp_buf;  // PH_GDNF: its head-group exchange buffer (else -1)
+    std::vector<int> grp_buf;  // PH_GDNF: its head-group exchange buffer; PH_ATTN with fold: its partials (else -1)
     int h_prev = -1;  // buffer of the residual stream published by the previous layer's down
     auto push = [&](const Phase& P, int out, int grp, const char* label) {
         prog.push_back(P);
@@ -547,14 +547,22 @@ void Model::setup_engine() {
             at.kp = L.k_pool;
             at.vp = L.v_pool;
             const int b_part = buf((uint32_t)(c.n_kv_heads * S * G * 258));
-            push(at, b_part, -1, "attn.attention");
-            Phase cb;
-            cb.kind = PH_COMB;
-            cb.heads = c.n_q_heads;
-            cb.kv_heads = c.n_kv_heads;
-            cb.in2_rel = 2;
-            b_mixed = buf((uint32_t)(c.n_q_heads * 256));
-            push(cb, b_mixed, -1, "attn.combine");
+            if (S >= 4 * G) {
+                // the combine folded into the attention phase: the partials are the phase's own
+                // exchange, the combined vector its output
+                at.fold = 1;
+                b_mixed = buf((uint32_t)(c.n_q_heads * 256));
+                push(at, b_mixed, b_part, "attn.attention+combine");
+            } else {
+                push(at, b_part, -1, "attn.attention");
+                Phase cb;
+                cb.kind = PH_COMB;
+                cb.heads = c.n_q_heads;
+                cb.kv_heads = c.n_kv_heads;
+                cb.in2_rel = 2;
+                b_mixed = buf((uint32_t)(c.n_q_heads * 256));
+                push(cb, b_mixed, -1, "attn.combine");
+            }
         }
         const char* kind = L.attn ? "attn." : "gdn.";
         auto lab = [&](const char* n) { return (std::string(kind) + n); };
@@ -598,9 +606,13 @@ void Model::setup_engine() {
             P.out = base(out_buf[p]);
             P.out_stride = bufs[out_buf[p]].n;
         }
-        if (grp_buf[p] >= 0) {
+        if (grp_buf[p] >= 0 && P.kind == PH_GDNF) {
             P.grp = base(grp_buf[p]);
             P.grp_stride = bufs[grp_buf[p]].n;
+        }
+        if (grp_buf[p] >= 0 && P.kind == PH_ATTN) {
+            P.part = base(grp_buf[p]);
+            P.part_stride = bufs[grp_buf[p]].n;
         }
         if ((P.kind == PH_GEMV || P.kind == PH_GDNF) && P.xin == XI_EMBED) continue;
         const int src = (int)p - P.in_rel;

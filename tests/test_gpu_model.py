@@ -308,12 +308,16 @@ def test_profile_token_consumes_one_greedy_token_and_reports_every_phase(pair):
     cfg = json.loads(index)["config"]
     layers = cfg["layers"]
     attn = sum(1 for i in range(layers) if (i + 1) % cfg["full_attention_every"] == 0)
-    # a GDN layer is 4 phases when its in-projection and step run fused ("gdn.mixer_in+gdn"), else 5
+    # a GDN layer is 4 phases when its in-projection and step run fused ("gdn.mixer_in+gdn"), else 5;
+    # an attention layer 5 when the combine of the partials runs in the attention phase, else 6
     fused = "gdn.mixer_in+gdn" in d["labels"]
+    folded = "attn.attention+combine" in d["labels"]
     assert fused == (name == "small")  # 16 GDN heads and q4 rows: fused on a 256-workgroup grid
-    assert len(d["phases"]) == (4 if fused else 5) * (layers - attn) + 6 * attn + 1
+    assert folded  # every test model has splits >= 4 q heads per kv head
+    assert len(d["phases"]) == (4 if fused else 5) * (layers - attn) + (5 if folded else 6) * attn + 1
     assert all(v >= 0.0 for v in d["labels"].values())
-    phases = ("mixer_in", "gdn", "mixer_in+gdn", "attention", "combine", "mixer_out", "gate_up", "down")
+    phases = ("mixer_in", "gdn", "mixer_in+gdn", "attention", "attention+combine", "combine", "mixer_out", "gate_up",
+              "down")
     assert set(d["labels"]) <= {f"{k}.{p}" for k in ("gdn", "attn") for p in phases} | {"lm_head"}
     places = d["places"]
     assert len(places) == len(d["input_ticks"][0]) and all(p is not None and p[0] >= 0 for p in places)
