@@ -713,10 +713,6 @@ def main():
                          "prefill (the persistent token kernel)")
     ap.add_argument("--prefill-direct", action="store_true",
                     help="--config prefill: launch each pass's kernels one by one instead of replaying its graph")
-    ap.add_argument("--reset-device-at-exit", action="store_true",
-                    help="after the result line, release the device (hipDeviceReset on the HIP runtime libqne "
-                         "uses) before the process exits, so that a profiler loaded into the process sees the "
-                         "runtime's queues torn down while it is still active")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--engine", default="persistent", choices=["persistent", "graph"])
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -851,21 +847,5 @@ def main():
     print(json.dumps(result))
 
 
-def reset_device() -> None:
-    """hipDeviceReset on the HIP runtime libqne.so is linked against (every allocation, stream and
-    queue of the device released), after every model of the process has been freed."""
-    import ctypes
-    sys.stdout.flush()
-    sys.path[:0] = [str(ROOT / "qwen-native-engine_amd")]
-    import qne
-    qne.load_library()
-    hip = ctypes.CDLL("libamdhip64.so.7")
-    hip.hipDeviceReset.restype = ctypes.c_int
-    rc = hip.hipDeviceReset()
-    print(f"bench.py: hipDeviceReset -> {rc}", file=sys.stderr, flush=True)
-
-
 if __name__ == "__main__":
     main()
-    if "--reset-device-at-exit" in sys.argv:
-        reset_device()
