@@ -320,20 +320,218 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_partial(const float* __re
     }
 }
 
+typedef _Float16 h8v __attribute__((ext_vector_type(8)));
+
+constexpr int kPfUnit = 32;       // positions per step of the prefill kernel: two cache blocks
+constexpr int kPfKStride = 528;   // bytes per K row in LDS: 512 + 16, so the 16 rows of a column read hit distinct banks
+constexpr int kPfVStride = 80;    // bytes per dim of the transposed V in LDS: 32 positions (64 B) + 16
+
+__device__ __forceinline__ uint32_t pack_lo16(uint32_t a, uint32_t b) { return (a & 0xFFFFu) | (b << 16); }
+__device__ __forceinline__ uint32_t pack_hi16(uint32_t a, uint32_t b) { return (a >> 16) | (b & 0xFFFF0000u); }
+
+// Causal attention of the rows of a prompt chunk (consecutive tokens of one sequence, row b at
+// position pos[b], cache rows already appended): the same partials as k_attn_partial, computed for
+// a tile of query rows at a time so that every K/V row is read once per tile instead of once per
+// row. Grid (splits, nkv, tiles), 4 waves; a tile is 16 * (4 / G) rows and wave w takes query head
+// g * G + w % G of the 16 rows 16 * (w / G)...; split s covers positions [s * split_len,
+// (s + 1) * split_len), cut at the tile's last position.
+// Per step of 32 positions (two 16-position blocks) the workgroup stages the K rows (as stored,
+// rows padded to 528 B) and V transposed (dim-major: for every dim the 8 positions k-slot group kq
+// of the MFMA takes, {4 kq..4 kq + 3, 16 + 4 kq..16 + 4 kq + 3}) in LDS, double-buffered, with the
+// next step's global loads in flight during this step's math:
+//  - scores S[position][row] = K . Q^T on v_mfma_f32_16x16x32_f16, q as two f16 terms in registers,
+//    hi = f16(x) and lo = f16(x - hi) (often subnormal: the matrix cores take f16 subnormals
+//    exactly), so q keeps ~22 bits; both terms accumulate into the same scores;
+//  - the score tile's layout (lane: row lane % 16, positions 4 (lane / 16) + r) is the B operand of
+//    O^T[dim][row] += V^T . P^T, so the weights go to the matrix cores without a shuffle, again as
+//    hi and lo f16 terms into one accumulator; the running maximum / sum and the rescale are per
+//    lane (= per row). 64 accumulator registers per lane leave room for two waves per SIMD.
+// Masked entries (past the row's position or the split) weigh exactly 0 and leave the row's
+// maximum alone, so a row's partial does not depend on the other rows of its tile: a token's
+// result does not depend on how the prompt was cut into calls. V rows past the split end are
+// zeroed in LDS (a block may hold rows never written).
+template <int G>
+__global__ __launch_bounds__(kAttnThreads, 2) void k_attn_prefill(const float* __restrict__ q, const uint16_t* __restrict__ k_pool,
+                                                               const uint16_t* __restrict__ v_pool,
+                                                               const int32_t* __restrict__ bt, int max_blocks,
+                                                               const int32_t* __restrict__ pos, int rows, int nkv, int split_len,
+                                                               float* __restrict__ part_ml, float* __restrict__ part_acc) {
+    constexpr int RT = 4 / G;  // 16-row subtiles per tile
+    __shared__ __attribute__((aligned(16))) uint8_t s_k[2][kPfUnit * kPfKStride];
+    __shared__ __attribute__((aligned(16))) uint8_t s_v[2][kHD * kPfVStride];
+    const int split = blockIdx.x, g = blockIdx.y, splits = gridDim.x;
+    const int t = threadIdx.x, lane = t % kWave, w = t / kWave;
+    const int gi = w % G, n = lane & 15, kq = lane >> 4;
+    const int row0 = blockIdx.z * 16 * RT;
+    const int b = row0 + 16 * (w / G) + n;  // this lane's row (column of the score tile)
+    const int rpos = b < rows ? pos[b] : -1;
+    const int tpos = lane < 16 * RT && row0 + lane < rows ? pos[row0 + lane] : -1;
+    const int tile_len = min((int)wave_max((float)tpos) + 1, max_blocks * kBlock);
+    const int p0 = split * split_len;
+    if (p0 >= tile_len) return;  // the whole workgroup: nothing of this split is attended
+    const int p1 = min(tile_len, p0 + split_len);
+    const int steps = (p1 - p0 + kPfUnit - 1) / kPfUnit;
+    const int nq = nkv * G, h = g * G + gi;
+    constexpr float kScale = 1.4426950408889634f * 0.0625f;  // log2(e) / sqrt(256)
+
+    // q as the B operand: lane (n, kq) holds dims 32 i + 8 kq .. + 7 of row b, hi and lo terms
+    h8v qh[8], ql[8];
+    {
+        const float* qr = q + ((size_t)b * nq + h) * kHD + 8 * kq;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            float4 x0 = make_float4(0.f, 0.f, 0.f, 0.f), x1 = x0;
+            if (b < rows) {
+                x0 = *(const float4*)(qr + 32 * i);
+                x1 = *(const float4*)(qr + 32 * i + 4);
+            }
+            const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const float x = xs[e] * kScale;
+                const _Float16 hi = (_Float16)x;
+                qh[i][e] = hi;
+                ql[i][e] = (_Float16)(x - (float)hi);
+            }
+        }
+    }
+
+    // The split's block table entries, lane i holding entry p0 / 16 + i (a split spans at most 64
+    // blocks): every step picks its two with readlane, so no load waits on a table entry. A block
+    // past the split end (the second of a last step) reads the first block instead; those rows
+    // weigh 0 and their values are zeroed below.
+    const int nblk = (p1 - p0 + kBlock - 1) / kBlock;
+    const int btv = lane < nblk ? bt[p0 / kBlock + lane] : 0;
+    // staging assignment: K row kr (of the step's 32), bytes 64 kp..64 kp + 63; V positions
+    // {4 w + j, 16 + 4 w + j} (j = 0..3) of dims 4 lane..4 lane + 3
+    const int kr = t >> 3, kp = t & 7;
+    u32x4 kw[4];
+    u32x2 vr[8];
+    auto load = [&](int base) {
+        const int j0 = (base - p0) / kBlock;
+        const int blk0 = __builtin_amdgcn_readlane(btv, j0);
+        const int blk1 = j0 + 1 < nblk ? __builtin_amdgcn_readlane(btv, j0 + 1) : blk0;
+        const uint16_t* src = k_pool + (((size_t)(kr < kBlock ? blk0 : blk1) * nkv + g) * kBlock + kr % kBlock) * kHD + 32 * kp;
+#pragma unroll
+        for (int j = 0; j < 4; j++) kw[j] = __builtin_nontemporal_load((const u32x4*)(src + 8 * j));
+        const uint16_t* v0 = v_pool + (((size_t)blk0 * nkv + g) * kBlock + 4 * w) * kHD + 4 * lane;
+        const uint16_t* v1 = v_pool + (((size_t)blk1 * nkv + g) * kBlock + 4 * w) * kHD + 4 * lane;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            vr[j] = __builtin_nontemporal_load((const u32x2*)(v0 + j * kHD));
+            vr[4 + j] = __builtin_nontemporal_load((const u32x2*)(v1 + j * kHD));
+        }
+    };
+    auto stage = [&](int buf, int base) {
+#pragma unroll
+        for (int j = 0; j < 8; j++) {  // rows past the split end weigh 0: zero their values
+            const int pv = base + (j < 4 ? 4 * w + j : 16 + 4 * w + j - 4);
+            if (pv >= p1) vr[j] = u32x2{0u, 0u};
+        }
+        uint8_t* kd = s_k[buf] + kr * kPfKStride + 64 * kp;
+#pragma unroll
+        for (int j = 0; j < 4; j++) *(u32x4*)(kd + 16 * j) = kw[j];
+        uint8_t* vd = s_v[buf] + (4 * lane) * kPfVStride + 16 * w;
+        *(u32x4*)(vd) = u32x4{pack_lo16(vr[0].x, vr[1].x), pack_lo16(vr[2].x, vr[3].x), pack_lo16(vr[4].x, vr[5].x),
+                              pack_lo16(vr[6].x, vr[7].x)};
+        *(u32x4*)(vd + kPfVStride) = u32x4{pack_hi16(vr[0].x, vr[1].x), pack_hi16(vr[2].x, vr[3].x),
+                                           pack_hi16(vr[4].x, vr[5].x), pack_hi16(vr[6].x, vr[7].x)};
+        *(u32x4*)(vd + 2 * kPfVStride) = u32x4{pack_lo16(vr[0].y, vr[1].y), pack_lo16(vr[2].y, vr[3].y),
+                                               pack_lo16(vr[4].y, vr[5].y), pack_lo16(vr[6].y, vr[7].y)};
+        *(u32x4*)(vd + 3 * kPfVStride) = u32x4{pack_hi16(vr[0].y, vr[1].y), pack_hi16(vr[2].y, vr[3].y),
+                                               pack_hi16(vr[4].y, vr[5].y), pack_hi16(vr[6].y, vr[7].y)};
+    };
+
+    float m = -INFINITY, l = 0.0f;  // this lane's row: running maximum (base 2) and weight sum
+    f32x4 o[16];                    // O^T: dims 16 d + 4 kq + r of row b
+#pragma unroll
+    for (int d = 0; d < 16; d++) o[d] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    load(p0);
+    for (int it = 0; it < steps; it++) {
+        const int buf = it & 1, base = p0 + kPfUnit * it;
+        stage(buf, base);
+        __syncthreads();  // also: every wave is done with the step that last read this buffer
+        if (it + 1 < steps) load(base + kPfUnit);
+        float s[8];
+#pragma unroll
+        for (int hb = 0; hb < 2; hb++) {
+            f32x4 sh = {0.f, 0.f, 0.f, 0.f}, sl = sh;
+            const uint8_t* kb = s_k[buf] + (16 * hb + n) * kPfKStride + 16 * kq;
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const h8v a = *(const h8v*)(kb + 64 * i);
+                sh = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qh[i], sh, 0, 0, 0);
+                sl = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, ql[i], sl, 0, 0, 0);
+            }
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int pp = base + 16 * hb + 4 * kq + r;
+                s[4 * hb + r] = pp < p1 && pp <= rpos ? sh[r] + sl[r] : -INFINITY;
+            }
+        }
+        float bm = s[0];
+#pragma unroll
+        for (int e = 1; e < 8; e++) bm = fmaxf(bm, s[e]);
+        bm = fmaxf(bm, lane_xor16(bm, lane));
+        bm = fmaxf(bm, lane_xor32(bm, lane));
+        const float mn = fmaxf(m, bm);
+        const float ms = mn == -INFINITY ? 0.0f : mn;  // a row with nothing attended yet stays (-inf, 0)
+        const float corr = __builtin_amdgcn_exp2f(m - ms);
+        float ps = 0.0f;
+        h8v ph, pl;
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            const float p = __builtin_amdgcn_exp2f(s[e] - ms);  // 0 where masked
+            ps += p;
+            const _Float16 hi = (_Float16)p;
+            ph[e] = hi;
+            pl[e] = (_Float16)(p - (float)hi);
+        }
+        ps += lane_xor16(ps, lane);
+        ps += lane_xor32(ps, lane);
+        l = l * corr + ps;
+        m = mn;
+        if (__builtin_amdgcn_ballot_w64(corr != 1.0f)) {  // multiplying by exactly 1 changes nothing
+#pragma unroll
+            for (int d = 0; d < 16; d++) o[d] *= corr;
+        }
+        const uint8_t* vb = s_v[buf] + n * kPfVStride + 16 * kq;
+#pragma unroll
+        for (int d = 0; d < 16; d++) {
+            const h8v a = *(const h8v*)(vb + 16 * d * kPfVStride);
+            o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, ph, o[d], 0, 0, 0);
+            o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, pl, o[d], 0, 0, 0);
+        }
+    }
+    if (b >= rows || rpos < p0) return;  // no partial for a row that attends nothing here
+    const size_t pi = (((size_t)b * nkv + g) * splits + split) * G + gi;
+    float* dst = part_acc + pi * kHD + 4 * kq;
+#pragma unroll
+    for (int d = 0; d < 16; d++) *(f32x4*)(dst + 16 * d) = o[d];
+    if (kq == 0) {
+        part_ml[pi * 2] = m;
+        part_ml[pi * 2 + 1] = l;
+    }
+}
+
 // Merge the splits of query head blockIdx.x of sequence blockIdx.y; with `gate`, multiply by
-// sigmoid(gate) (shaders.rs:626-629).
+// sigmoid(gate) (shaders.rs:626-629). With split_len, row b merges only the splits that hold its
+// positions 0..pos[b] (the prefill kernel writes no others).
 __global__ __launch_bounds__(kAttnThreads) void k_attn_combine(const float* __restrict__ part_ml, const float* __restrict__ part_acc,
                                                                int nkv, int G, int splits, const float* __restrict__ gate,
                                                                int gate_stride, float* __restrict__ out, uint8_t* __restrict__ frag_out,
-                                                               int order_out) {
+                                                               int order_out, const int32_t* __restrict__ pos = nullptr,
+                                                               int split_len = 0) {
     const int h = blockIdx.x, b = blockIdx.y, t = threadIdx.x, g = h / G, gi = h % G, nq = nkv * G;
+    const int used = split_len ? min(splits, pos[b] / split_len + 1) : splits;  // splits holding row b's positions
     float mn = -INFINITY;
-    for (int s = 0; s < splits; s++) mn = fmaxf(mn, part_ml[((((size_t)b * nkv + g) * splits + s) * G + gi) * 2]);
-    // every split wrote its partial (an empty one: maximum -inf, sum 0, acc 0), and split 0 holds
-    // position 0, so mn is finite and an empty split weighs exp2(-inf) = 0
+    for (int s = 0; s < used; s++) mn = fmaxf(mn, part_ml[((((size_t)b * nkv + g) * splits + s) * G + gi) * 2]);
+    // every merged split wrote its partial (an empty one: maximum -inf, sum 0, acc 0), and split 0
+    // holds position 0, so mn is finite and an empty split weighs exp2(-inf) = 0
     float lsum = 0.0f, a = 0.0f;
 #pragma unroll 8
-    for (int s = 0; s < splits; s++) {
+    for (int s = 0; s < used; s++) {
         const size_t i = (((size_t)b * nkv + g) * splits + s) * G + gi;
         const float c = exp2f(part_ml[i * 2] - mn);  // the partials' maxima are in base 2
         lsum += part_ml[i * 2 + 1] * c;
@@ -374,14 +572,42 @@ void launch_attention_model(const AttnModelArgs& a, hipStream_t st) {
                        a.splits, a.proj + a.nq * kHD, 0, a.out, (uint8_t*)nullptr, 0);
 }
 
+template <int G>
+static void launch_prefill(const AttnRowsArgs& a, hipStream_t st) {
+    const int tile = 16 * (4 / G);
+    hipLaunchKernelGGL((k_attn_prefill<G>), dim3(a.splits, a.nkv, (a.rows + tile - 1) / tile), dim3(kAttnThreads), 0, st,
+                       a.qbuf, a.k_pool, a.v_pool, a.block_table, a.max_blocks, a.pos, a.rows, a.nkv, a.split_len,
+                       a.part_ml, a.part_acc);
+}
+
+bool prefill_attention_supported(int nq, int nkv) {
+    const int G = nkv > 0 && nq % nkv == 0 ? nq / nkv : 0;
+    return G == 1 || G == 2 || G == 4;
+}
+
 void launch_attention_rows(const AttnRowsArgs& a, hipStream_t st) {
     hipLaunchKernelGGL(k_attn_prep_rows, dim3(a.nq + a.nkv, a.rows), dim3(kAttnThreads), 0, st, a);
     const int G = a.nq / a.nkv;
-    partial_by_g(G, a.qbuf, a.k_pool, a.v_pool, a.block_table, a.max_blocks, a.bt_stride, a.pos, a.nkv, a.part_ml,
-                 a.part_acc, a.splits, a.rows, st, a.order);
+    if (a.split_len) {
+        // rows of one sequence (a prompt chunk): query tiles; the host checked the shape
+        if (a.bt_stride != 0 || a.split_len % kPfUnit != 0 || a.split_len > kWave * kBlock ||
+            !prefill_attention_supported(a.nq, a.nkv) ||
+            (long)a.splits * a.split_len < (long)a.max_blocks * kBlock)
+            throw Error(QNE_EINVAL, "prefill attention: rows must share one block table, split_len must be a multiple "
+                                    "of 32 up to 1024 covering the context, and 1, 2 or 4 query heads per kv head");
+        switch (G) {
+            case 1: launch_prefill<1>(a, st); break;
+            case 2: launch_prefill<2>(a, st); break;
+            default: launch_prefill<4>(a, st); break;
+        }
+    } else {
+        partial_by_g(G, a.qbuf, a.k_pool, a.v_pool, a.block_table, a.max_blocks, a.bt_stride, a.pos, a.nkv, a.part_ml,
+                     a.part_acc, a.splits, a.rows, st, a.order);
+    }
     const float* gate = a.part ? a.gate_dst + a.nq * kHD : a.proj + a.nq * kHD;
     hipLaunchKernelGGL(k_attn_combine, dim3(a.nq, a.rows), dim3(kAttnThreads), 0, st, a.part_ml, a.part_acc, a.nkv, G,
-                       a.splits, gate, (int)a.proj_stride, a.out, a.frag_out, a.order_out);
+                       a.splits, gate, (int)a.proj_stride, a.out, a.frag_out, a.order_out,
+                       a.split_len ? a.pos : (const int32_t*)nullptr, a.split_len);
 }
 
 void launch_paged_attn(const float* q, const float* k_new, const float* v_new, uint16_t* k_pool, uint16_t* v_pool,

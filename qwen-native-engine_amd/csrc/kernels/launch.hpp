@@ -114,8 +114,14 @@ struct AttnRowsArgs {
     // order order_out); out may then be null.
     uint8_t* frag_out = nullptr;
     int order_out = 0;
+    // With split_len (a multiple of 32, at most 1024), the rows are consecutive tokens of one sequence
+    // (bt_stride 0) and the partials come from the query-tile kernel: split s holds positions
+    // [s * split_len, (s + 1) * split_len); splits * split_len must cover max_blocks * 16.
+    int split_len = 0;
 };
 void launch_attention_rows(const AttnRowsArgs& a, hipStream_t st);
+// Whether the query-tile prefill attention takes this head grouping (1, 2 or 4 q heads per kv head).
+bool prefill_attention_supported(int nq, int nkv);
 
 // Per-row strides (in floats) of the batched GDN decode step.
 struct GdnRowStrides {

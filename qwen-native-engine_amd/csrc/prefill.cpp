@@ -27,10 +27,17 @@ ChunkPrefill::ChunkPrefill(Model& m) : m_(m), st_(m.stream_) {
         const size_t T = kChunk;
         proj_w_ = std::max(c.attn_proj(), c.gdn_proj());
         mixed_w_ = std::max(c.attn_out(), c.gdn_out());
-        // Fixed split count of the attention partials, so that a token's result does not depend on
-        // how the prompt was chunked.
+        // Attention partials over fixed position ranges (kPrefillSplitLen positions each, cut at the
+        // row's own position), so that a token's result does not depend on how the prompt was
+        // chunked; head groupings the query-tile kernel does not take use per-row partials over
+        // a fixed split count.
         const int max_blocks = (m.max_context_ + 15) / 16;
-        splits_ = std::max(1, std::min(16, max_blocks));
+        if (prefill_attention_supported(c.n_q_heads, c.n_kv_heads)) {
+            split_len_ = kPrefillSplitLen;
+            splits_ = (max_blocks * 16 + split_len_ - 1) / split_len_;
+        } else {
+            splits_ = std::max(1, std::min(16, max_blocks));
+        }
         ids_ = (uint32_t*)dalloc(T * 4);
         pos_ = (int32_t*)dalloc(T * 4);
         h_ = (float*)dalloc(T * c.hidden * 4);
@@ -108,6 +115,7 @@ void ChunkPrefill::enqueue_chunk(int n, int lead) {
             a.nkv = c.n_kv_heads;
             a.rope_dim = c.rope_dim;
             a.splits = splits_;
+            a.split_len = split_len_;
             a.max_blocks = max_blocks;
             a.rows = n;
             launch_attention_rows(a, st_);

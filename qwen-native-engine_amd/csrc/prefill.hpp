@@ -57,7 +57,8 @@ class ChunkPrefill {
     // instantiated pass graphs by graph_key, most recently used first (at most kGraphCap)
     std::list<std::pair<int, hipGraphExec_t>> lru_;
     std::map<int, std::list<std::pair<int, hipGraphExec_t>>::iterator> graphs_;
-    int proj_w_ = 0, mixed_w_ = 0, splits_ = 1;
+    static constexpr int kPrefillSplitLen = 512;  // positions per attention split of the query-tile kernel
+    int proj_w_ = 0, mixed_w_ = 0, splits_ = 1, split_len_ = 0;
     uint32_t* ids_ = nullptr;  // the chunk's token ids
     int32_t* pos_ = nullptr;   // the chunk's positions
     int32_t* host_pos_ = nullptr;  // pinned
