@@ -95,23 +95,29 @@ __device__ __forceinline__ void wait_vm_upto(int n) {
     }
 }
 
-// Grid (ceil(N / (32 WAVES)), splits, row tiles); split s covers chunks [s * cps, (s + 1) * cps) of
-// the x rows 64 blockIdx.z .. + 63. Compute wave w < WAVES owns W rows 32 (WAVES blockIdx.x + w)
-// .. + 31. The chunks stream through a ring of D LDS slots, each holding one x chunk and every
-// wave's W chunk; D - 1 chunks are in flight while one is computed. With DW > 0 the workgroup has
-// DW more waves that only issue the LDS DMA (x, chunk sums, every W tile), so a compute wave's
+// Grid (ceil(N / (32 WAVES CF)), splits, row tiles); split s covers chunks [s * cps, (s + 1) * cps)
+// of the x rows 64 blockIdx.z .. + 63. The workgroup's W rows come in TW = WAVES CF tiles of 32;
+// compute wave w < WAVES owns tiles w CF .. w CF + CF - 1, so every A fragment it reads from LDS
+// feeds CF MFMAs. The chunks stream through a ring of D LDS slots, each holding one x chunk and
+// every W tile's chunk; D - 1 chunks are in flight while one is computed. With DW > 0 the workgroup
+// has DW more waves that only issue the LDS DMA (x, chunk sums, every W tile), so a compute wave's
 // instruction stream holds LDS reads, MFMAs and VALU only and the transfers overlap the
-// computation; with DW = 0 every compute wave sends its own W tile and a part of x. The row tiles
+// computation; with DW = 0 every compute wave sends a share of the W tiles and of x. The row tiles
 // of one W tile read the same W chunks, which the MALL serves after the first.
-template <int KIND, int WAVES, int D, int DW>
+// Epilogues: partials (split-K, or an epilogue the GEMM does not apply); `direct` (one split: store
+// or residual add); `fuse` (one split, SwiGLU): tiles [0, TW / 2) are gate rows and [TW / 2, TW) the
+// matching up rows (n_out further), and the workgroup writes silu(gate) * up and stages it as the
+// next GEMM's operand, exactly as k_gemm_reduce does with one split.
+template <int KIND, int WAVES, int D, int DW, int CF>
 __global__ __launch_bounds__(64 * (WAVES + DW)) void k_gemm(const GemmArgs a) {
-    constexpr int kWBytes = KIND == KIND_Q4 ? 1024 + 128 : 4096;  // one wave's W chunk (q4: + scale/zero words)
-    constexpr int kSlot = kChunkLds + WAVES * kWBytes;
+    constexpr int TW = WAVES * CF;                                  // 32-row W tiles per workgroup
+    constexpr int kWBytes = KIND == KIND_Q4 ? 1024 + 128 : 4096;  // one W tile's chunk (q4: + scale/zero words)
+    constexpr int kSlot = kChunkLds + TW * kWBytes;
     constexpr int kSenders = DW > 0 ? DW : WAVES;                   // waves that issue the DMA
     constexpr int kXPart = 2 * kFragBytes / kSenders;               // x bytes each sender copies
-    constexpr int kTilesPer = WAVES / kSenders;                     // W tiles each sender sends
+    constexpr int kTilesPer = TW / kSenders;                        // W tiles each sender sends
     constexpr int kWDmas = KIND == KIND_Q4 ? 2 : 4;                 // DMAs of one W tile chunk
-    static_assert(kXPart % 1024 == 0 && WAVES % kSenders == 0, "the senders split x and W evenly");
+    static_assert(kXPart % 1024 == 0 && TW % kSenders == 0, "the senders split x and W evenly");
     constexpr int kSumLanes = kBM * 4 / 16 / kSenders;              // lanes copying the chunk sums (16 B each)
     static_assert(kSumLanes >= 1, "every sender copies a part of the chunk sums");
     constexpr int kPer = kXPart / 1024 + 1 + kTilesPer * kWDmas;    // DMAs per sender per chunk
@@ -120,7 +126,6 @@ __global__ __launch_bounds__(64 * (WAVES + DW)) void k_gemm(const GemmArgs a) {
     const bool computes = w < WAVES;
     const int sender = DW > 0 ? w - WAVES : w;  // index among the senders (< 0: none)
     const int hf = lane >> 5, l32 = lane & 31;
-    const int n = (blockIdx.x * WAVES + w) * 32 + l32;
     const int K = a.K, nchunks = K / kChunk;
     const int cpg = KIND == KIND_Q4 ? a.group / kChunk : 1;
     const int ngroups = nchunks / cpg;
@@ -128,6 +133,12 @@ __global__ __launch_bounds__(64 * (WAVES + DW)) void k_gemm(const GemmArgs a) {
     const int nch = max(0, c1 - c0);
     const int mt = blockIdx.z;  // row tile
     const uint8_t* xfrag = a.frag + (size_t)mt * nchunks * kChunkBytes;
+    // W row (= output column) of lane l32 in tile t of this workgroup
+    auto wrow = [&](int t) {
+        constexpr int half = TW / 2;
+        if (a.fuse) return t < half ? (blockIdx.x * half + t) * 32 + l32 : a.n_out + (blockIdx.x * half + t - half) * 32 + l32;
+        return (blockIdx.x * TW + t) * 32 + l32;
+    };
 
     auto issue = [&](int j, int slot) {  // senders only
         uint8_t* base = ring[slot];
@@ -138,8 +149,8 @@ __global__ __launch_bounds__(64 * (WAVES + DW)) void k_gemm(const GemmArgs a) {
         const int c = c0 + j;
 #pragma unroll
         for (int i = 0; i < kTilesPer; i++) {
-            const int wt = sender * kTilesPer + i;  // W tile (compute wave) sent
-            const int nr = min((int)(blockIdx.x * WAVES + wt) * 32 + l32, a.N - 1);  // rows past N: row N - 1, not stored
+            const int wt = sender * kTilesPer + i;  // W tile sent
+            const int nr = min(wrow(wt), a.N - 1);  // rows past N: row N - 1, not stored
             uint8_t* dst = base + kChunkLds + wt * kWBytes;
             if (KIND == KIND_Q4) {
                 dma16((const uint8_t*)a.W + (size_t)nr * (K / 2) + c * 32 + 16 * hf, dst);
@@ -152,9 +163,11 @@ __global__ __launch_bounds__(64 * (WAVES + DW)) void k_gemm(const GemmArgs a) {
     };
     static_assert(D >= 2 && (D - 2) * kPer <= 31, "ring deeper than the waits cover");
 
-    float16_t acc0, acc1, grp0, grp1;
+    float16_t acc[CF][2], grp[CF][2];
 #pragma unroll
-    for (int j = 0; j < 16; j++) acc0[j] = acc1[j] = grp0[j] = grp1[j] = 0.0f;
+    for (int cf = 0; cf < CF; cf++)
+#pragma unroll
+        for (int j = 0; j < 16; j++) acc[cf][0][j] = acc[cf][1][j] = grp[cf][0][j] = grp[cf][1][j] = 0.0f;
 
     if (sender >= 0)
         for (int j = 0; j < min(D - 1, nch); j++) issue(j, j);
@@ -166,43 +179,51 @@ __global__ __launch_bounds__(64 * (WAVES + DW)) void k_gemm(const GemmArgs a) {
         if (sender >= 0 && j + D - 1 < nch) issue(j + D - 1, next_slot);
         if (computes) {
             const uint8_t* xs = ring[slot];
-            const uint8_t* ws = ring[slot] + kChunkLds + w * kWBytes;
-            uint4 wq;
-            if (KIND == KIND_Q4) wq = *(const uint4*)(ws + 16 * lane);
+            const uint8_t* ws = ring[slot] + kChunkLds + w * CF * kWBytes;
+            uint4 wq[CF];
+            if (KIND == KIND_Q4)
+#pragma unroll
+                for (int cf = 0; cf < CF; cf++) wq[cf] = *(const uint4*)(ws + cf * kWBytes + 16 * lane);
 #pragma unroll
             for (int s = 0; s < 4; s++) {
-                half8_t b;
-                if (KIND == KIND_Q4) b = nibbles8(s == 0 ? wq.x : s == 1 ? wq.y : s == 2 ? wq.z : wq.w);
-                else b = *(const half8_t*)(ws + 1024 * s + 16 * lane);
                 const half8_t a0h = *(const half8_t*)(xs + frag_offset(s, 0, lane));
                 const half8_t a1h = *(const half8_t*)(xs + frag_offset(s, 1, lane));
                 const half8_t a0l = *(const half8_t*)(xs + kFragBytes + frag_offset(s, 0, lane));
                 const half8_t a1l = *(const half8_t*)(xs + kFragBytes + frag_offset(s, 1, lane));
-                if (KIND == KIND_Q4 && s == 0) {  // a fresh tile per chunk: C = 0
-                    const float16_t zero = {};
-                    grp0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0h, b, zero, 0, 0, 0);
-                    grp1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1h, b, zero, 0, 0, 0);
-                } else {
-                    grp0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0h, b, grp0, 0, 0, 0);
-                    grp1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1h, b, grp1, 0, 0, 0);
+#pragma unroll
+                for (int cf = 0; cf < CF; cf++) {
+                    half8_t b;
+                    if (KIND == KIND_Q4) b = nibbles8(s == 0 ? wq[cf].x : s == 1 ? wq[cf].y : s == 2 ? wq[cf].z : wq[cf].w);
+                    else b = *(const half8_t*)(ws + cf * kWBytes + 1024 * s + 16 * lane);
+                    if (KIND == KIND_Q4 && s == 0) {  // a fresh tile per chunk: C = 0
+                        const float16_t zero = {};
+                        grp[cf][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0h, b, zero, 0, 0, 0);
+                        grp[cf][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1h, b, zero, 0, 0, 0);
+                    } else {
+                        grp[cf][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0h, b, grp[cf][0], 0, 0, 0);
+                        grp[cf][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1h, b, grp[cf][1], 0, 0, 0);
+                    }
+                    grp[cf][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0l, b, grp[cf][0], 0, 0, 0);
+                    grp[cf][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1l, b, grp[cf][1], 0, 0, 0);
                 }
-                grp0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0l, b, grp0, 0, 0, 0);
-                grp1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1l, b, grp1, 0, 0, 0);
             }
             if (KIND == KIND_Q4) {
                 // y += s (sum q x) - s z (sum x) over the chunk (scale and zero of the chunk's group)
-                const uint32_t szw = *(const uint32_t*)(ws + 1024 + 4 * l32);
-                const float sc = lo_h(szw), sz = sc * hi_h(szw);
                 const float* xsum = (const float*)(xs + kXsumOff);
 #pragma unroll
-                for (int q = 0; q < 4; q++) {
-                    const float4 s0 = *(const float4*)(xsum + 8 * q + 4 * hf);
-                    const float4 s1 = *(const float4*)(xsum + 32 + 8 * q + 4 * hf);
-                    const float v0[4] = {s0.x, s0.y, s0.z, s0.w}, v1[4] = {s1.x, s1.y, s1.z, s1.w};
+                for (int cf = 0; cf < CF; cf++) {
+                    const uint32_t szw = *(const uint32_t*)(ws + cf * kWBytes + 1024 + 4 * l32);
+                    const float sc = lo_h(szw), sz = sc * hi_h(szw);
 #pragma unroll
-                    for (int e = 0; e < 4; e++) {
-                        acc0[4 * q + e] = fmaf(sc, grp0[4 * q + e], fmaf(-sz, v0[e], acc0[4 * q + e]));
-                        acc1[4 * q + e] = fmaf(sc, grp1[4 * q + e], fmaf(-sz, v1[e], acc1[4 * q + e]));
+                    for (int q = 0; q < 4; q++) {
+                        const float4 s0 = *(const float4*)(xsum + 8 * q + 4 * hf);
+                        const float4 s1 = *(const float4*)(xsum + 32 + 8 * q + 4 * hf);
+                        const float v0[4] = {s0.x, s0.y, s0.z, s0.w}, v1[4] = {s1.x, s1.y, s1.z, s1.w};
+#pragma unroll
+                        for (int e = 0; e < 4; e++) {
+                            acc[cf][0][4 * q + e] = fmaf(sc, grp[cf][0][4 * q + e], fmaf(-sz, v0[e], acc[cf][0][4 * q + e]));
+                            acc[cf][1][4 * q + e] = fmaf(sc, grp[cf][1][4 * q + e], fmaf(-sz, v1[e], acc[cf][1][4 * q + e]));
+                        }
                     }
                 }
             }
@@ -211,24 +232,48 @@ __global__ __launch_bounds__(64 * (WAVES + DW)) void k_gemm(const GemmArgs a) {
         next_slot = next_slot + 1 == D ? 0 : next_slot + 1;
     }
     if (KIND != KIND_Q4) {
-        acc0 = grp0;
-        acc1 = grp1;
-    }
-    if (!a.direct) {
-        if (!computes || n >= a.N) return;
-        float* pp = a.part + ((size_t)blockIdx.y * a.mpad + (size_t)kBM * mt) * a.N + n;
 #pragma unroll
-        for (int j = 0; j < 16; j++) {
-            const int m = 8 * (j / 4) + 4 * hf + (j % 4);
-            store_through(pp + (size_t)m * a.N, acc0[j]);
-            store_through(pp + (size_t)(32 + m) * a.N, acc1[j]);
+        for (int cf = 0; cf < CF; cf++) {
+            acc[cf][0] = grp[cf][0];
+            acc[cf][1] = grp[cf][1];
+        }
+    }
+    if (!a.direct && !a.fuse) {
+        if (!computes) return;
+#pragma unroll
+        for (int cf = 0; cf < CF; cf++) {
+            const int n = wrow(w * CF + cf);
+            if (n >= a.N) continue;
+            float* pp = a.part + ((size_t)blockIdx.y * a.mpad + (size_t)kBM * mt) * a.N + n;
+#pragma unroll
+            for (int j = 0; j < 16; j++) {
+                const int m = 8 * (j / 4) + 4 * hf + (j % 4);
+                store_through(pp + (size_t)m * a.N, acc[cf][0][j]);
+                store_through(pp + (size_t)(32 + m) * a.N, acc[cf][1][j]);
+            }
         }
         return;
     }
-    // direct (one split, no SwiGLU): 1 / rms of the rows (normed input), then store or residual add
+    // one split: 1 / rms of the rows (normed input), then the epilogue
     float* sinv = (float*)ring[0];
     __syncthreads();  // ring no longer read
-    if (a.norm) {
+    if (a.fuse) {
+        // as k_gemm_reduce computes it (row_inv_rms<256>), so the result is the same: with at most
+        // 64 chunks the first wave's lanes hold one chunk each and the other waves add +0, so the
+        // sum is one wave_sum; every row's loads are in flight at once
+        if (computes) {
+            constexpr int kRows = kBM / WAVES;  // rows per wave
+            float v[kRows];
+#pragma unroll
+            for (int j = 0; j < kRows; j++)
+                v[j] = a.norm && lane < nchunks ? ((const float*)(xfrag + (size_t)lane * kChunkBytes))[kSsOff / 4 + w + WAVES * j] : 0.0f;
+#pragma unroll
+            for (int j = 0; j < kRows; j++) {
+                const float inv = a.norm ? 1.0f / sqrtf(wave_sum(v[j]) / (float)K + a.eps) : 1.0f;
+                if (lane == 0) sinv[w + WAVES * j] = inv;
+            }
+        }
+    } else if (a.norm) {
         if (threadIdx.x < kBM) {
             float ss = 0.0f;
             for (int c = 0; c < nchunks; c++) ss += ((const float*)(xfrag + (size_t)c * kChunkBytes))[kSsOff / 4 + threadIdx.x];
@@ -238,21 +283,75 @@ __global__ __launch_bounds__(64 * (WAVES + DW)) void k_gemm(const GemmArgs a) {
         sinv[threadIdx.x] = 1.0f;
     }
     __syncthreads();
-    if (!computes || n >= a.N) return;
     const int rows = a.m - kBM * mt;  // rows of this tile
+    if (a.direct) {
+        if (!computes) return;
 #pragma unroll
-    for (int j = 0; j < 16; j++) {
-        const int m = 8 * (j / 4) + 4 * hf + (j % 4);
-        if (m < rows) {
-            float* d = a.y + (size_t)(kBM * mt + m) * a.y_stride + n;
-            const float v = acc0[j] * sinv[m];
-            store_through(d, a.epi == EPI_ACCUMULATE ? *d + v : v);
+        for (int cf = 0; cf < CF; cf++) {
+            const int n = wrow(w * CF + cf);
+            if (n >= a.N) continue;
+#pragma unroll
+            for (int j = 0; j < 16; j++) {
+                const int m = 8 * (j / 4) + 4 * hf + (j % 4);
+                if (m < rows) {
+                    float* d = a.y + (size_t)(kBM * mt + m) * a.y_stride + n;
+                    const float v = acc[cf][0][j] * sinv[m];
+                    store_through(d, a.epi == EPI_ACCUMULATE ? *d + v : v);
+                }
+                if (32 + m < rows) {
+                    float* d = a.y + (size_t)(kBM * mt + 32 + m) * a.y_stride + n;
+                    const float v = acc[cf][1][j] * sinv[32 + m];
+                    store_through(d, a.epi == EPI_ACCUMULATE ? *d + v : v);
+                }
+            }
         }
-        if (32 + m < rows) {
-            float* d = a.y + (size_t)(kBM * mt + 32 + m) * a.y_stride + n;
-            const float v = acc1[j] * sinv[32 + m];
-            store_through(d, a.epi == EPI_ACCUMULATE ? *d + v : v);
+        return;
+    }
+    // fused SwiGLU: the up tiles go through LDS ([row][column of the workgroup's gate columns]),
+    // the gate tiles' lanes form silu(g / rms) * (u / rms) in place, then every wave stages whole
+    // 64-column chunks of rows (lanes = columns), as the reduce does
+    constexpr int kCols = TW / 2 * 32;  // output columns of the workgroup
+    static_assert(kCols % kChunk == 0 && (kBM * kCols + kBM) * 4 <= D * kSlot, "fused SwiGLU tile");
+    float* sv = sinv + kBM;  // [kBM][kCols]
+    if (computes) {
+#pragma unroll
+        for (int cf = 0; cf < CF; cf++) {
+            const int t = w * CF + cf;
+            if (t < TW / 2) continue;
+            const int col = (t - TW / 2) * 32 + l32;
+#pragma unroll
+            for (int j = 0; j < 16; j++) {
+                const int m = 8 * (j / 4) + 4 * hf + (j % 4);
+                sv[m * kCols + col] = acc[cf][0][j];
+                sv[(32 + m) * kCols + col] = acc[cf][1][j];
+            }
         }
+    }
+    __syncthreads();
+    if (computes) {
+#pragma unroll
+        for (int cf = 0; cf < CF; cf++) {
+            const int t = w * CF + cf;
+            if (t >= TW / 2) continue;
+            const int col = t * 32 + l32;
+#pragma unroll
+            for (int j = 0; j < 16; j++) {
+                const int m = 8 * (j / 4) + 4 * hf + (j % 4);
+                sv[m * kCols + col] = silu(acc[cf][0][j] * sinv[m]) * (sv[m * kCols + col] * sinv[m]);
+                sv[(32 + m) * kCols + col] = silu(acc[cf][1][j] * sinv[32 + m]) * (sv[(32 + m) * kCols + col] * sinv[32 + m]);
+            }
+        }
+    }
+    __syncthreads();
+    if (!computes) return;
+    constexpr int nck = kCols / kChunk;
+    const size_t tile_bytes = (size_t)(a.n_out / kChunk) * kChunkBytes;
+    for (int it = w; it < min(rows, kBM) * nck; it += WAVES) {  // wave-uniform
+        const int r = it / nck, ch = it % nck;
+        const int c = blockIdx.x * kCols + ch * kChunk + lane;
+        const float v = sv[r * kCols + ch * kChunk + lane];
+        if (a.y) store_through(a.y + (size_t)(kBM * mt + r) * a.y_stride + c, v);
+        if (a.frag_out) emit_x(a.frag_out, tile_bytes, kBM * mt + r, c, v, a.gain_out ? a.gain_out[c] : 1.0f, a.order_out, lane);
     }
 }
 
@@ -453,7 +552,6 @@ void launch_gemm(GemmArgs a, hipStream_t st) {
     const int nch = a.K / kChunk;
     a.cps = (nch + a.splits - 1) / a.splits;
     a.mpad = (a.m + kBM - 1) / kBM * kBM;
-    a.direct = a.splits == 1 && a.epi != EPI_SWIGLU && !a.frag_out && !a.partials_only;
     if (a.x) {  // stage the x operand here (RMSNorm gain folded in, 1 / rms deferred to the epilogue)
         launch_stage_x(a.x, a.x_stride, a.m, a.K, a.gain, a.kind == KIND_Q4 ? 1 : 0, a.frag, st);
         a.norm = a.gain ? 1 : 0;
@@ -463,19 +561,28 @@ void launch_gemm(GemmArgs a, hipStream_t st) {
     // One row tile (a batched decode step): about one workgroup per CU, so 4 DMA waves beside the
     // 8 compute waves let the transfers overlap the computation (64 rows: gate_up 23.9 -> 22.4 us,
     // LM head 222 -> 205 us). Several row tiles (a prefill pass): two 8-wave workgroups per CU
-    // (125 VGPRs in a 12-wave workgroup leave room for one). The arithmetic is the same either way.
+    // (125 VGPRs in a 12-wave workgroup leave room for one). Measured and not kept for the prefill:
+    // 4 compute waves of 64 columns each (every A fragment read from LDS feeding two MFMAs), slower
+    // on every shape (gate_up 68 -> 108 us): each wave then issues 9 LDS DMAs per chunk instead of
+    // 5, and a DMA holds its wave for about the transfer time.
     const bool dma_waves = a.mpad == kBM;
+    // SwiGLU with one split over several row tiles: the GEMM applies it and stages the output
+    // itself, with no partials and no reduce pass
+    a.fuse = a.kind == KIND_Q4 && !dma_waves && a.splits == 1 && a.epi == EPI_SWIGLU && !a.partials_only &&
+             a.N == 2 * a.n_out && a.n_out % (32 * waves / 2) == 0 && a.K <= 64 * kChunk && (a.y || a.frag_out);
+    a.direct = a.splits == 1 && a.epi != EPI_SWIGLU && !a.frag_out && !a.partials_only;
     if (a.kind == KIND_Q4) {
         // 3 chunk slots (77.6 KiB): deeper rings measured slower, and two workgroups fit a CU
-        if (dma_waves) hipLaunchKernelGGL((k_gemm<KIND_Q4, 8, 3, 4>), grid, dim3(768), 0, st, a);
-        else hipLaunchKernelGGL((k_gemm<KIND_Q4, 8, 3, 0>), grid, dim3(512), 0, st, a);
+        if (dma_waves) hipLaunchKernelGGL((k_gemm<KIND_Q4, 8, 3, 4, 1>), grid, dim3(768), 0, st, a);
+        else hipLaunchKernelGGL((k_gemm<KIND_Q4, 8, 3, 0, 1>), grid, dim3(512), 0, st, a);
     } else {
         // f16: as many chunk slots as fit in 160 KiB of LDS
-        if (waves == 8 && dma_waves) hipLaunchKernelGGL((k_gemm<KIND_F16, 8, 3, 4>), grid, dim3(768), 0, st, a);
-        else if (waves == 8) hipLaunchKernelGGL((k_gemm<KIND_F16, 8, 3, 0>), grid, dim3(512), 0, st, a);
-        else hipLaunchKernelGGL((k_gemm<KIND_F16, 4, 4, 0>), grid, dim3(256), 0, st, a);
+        if (waves == 8 && dma_waves) hipLaunchKernelGGL((k_gemm<KIND_F16, 8, 3, 4, 1>), grid, dim3(768), 0, st, a);
+        else if (waves == 8) hipLaunchKernelGGL((k_gemm<KIND_F16, 8, 3, 0, 1>), grid, dim3(512), 0, st, a);
+        else hipLaunchKernelGGL((k_gemm<KIND_F16, 4, 4, 0, 1>), grid, dim3(256), 0, st, a);
     }
-    if (!a.direct && !a.partials_only) hipLaunchKernelGGL(k_gemm_reduce, dim3((a.n_out + 255) / 256, a.m), dim3(256), 0, st, a);
+    if (!a.direct && !a.fuse && !a.partials_only)
+        hipLaunchKernelGGL(k_gemm_reduce, dim3((a.n_out + 255) / 256, a.m), dim3(256), 0, st, a);
 }
 
 void launch_embed_rows(int kind, const void* W, const uint32_t* SZ, int group, int hidden, const uint32_t* tokens, int m,

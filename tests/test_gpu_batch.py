@@ -70,6 +70,15 @@ def test_gemm_row_tiles_match_oracle(kind, group, epi, M):
     assert rel_err(got, want) < 2e-5
 
 
+@pytest.mark.parametrize("norm", [False, True])
+def test_gemm_swiglu_applied_by_the_gemm(norm):
+    """A SwiGLU GEMM with one split over several row tiles (K = 128: two chunks) applies
+    silu(gate) * up in the GEMM itself, with no reduce pass; gate and up rows 256 apart, two
+    workgroups of 128 output columns, a ragged last row tile."""
+    got, want = run_gemm(Q.MAT_Q4, 64, 2 * 256, 128, 200, Q.EPI_SWIGLU, norm, seed=61 + norm)
+    assert rel_err(got, want) < 2e-5
+
+
 def test_gemm_full_pass_of_512_rows():
     got, want = run_gemm(Q.MAT_Q4, 64, 256, 512, 512, Q.EPI_ACCUMULATE, True, seed=77)
     assert rel_err(got, want) < 2e-5
