@@ -835,6 +835,14 @@ def main():
         "detail": {"bytes_per_token": bytes_tok, "weights_gen_s": round(gen_s, 2), "prefill_s": round(prefill_s, 2),
                    "prefill_tok_s": round((args.ctx - 1) / prefill_s, 1), "adapter": m.adapter},
     }
+    if args.engine == "persistent" and args.prefill != "tokens":
+        # the token's dependent phases: one profiled token (not timed) from the prompt state, since
+        # the timed window may have filled the context
+        m.restore()
+        m.prefill_chunk(prompt[-1:], args.ctx - 1, True)
+        nph = len(m.profile_token_detail()["phases"])
+        result["detail"]["phases_per_token"] = nph
+        result["detail"]["device_us_per_phase"] = round(dev_ms / args.steps * 1e3 / nph, 3)
     if not args.no_cpu_baseline:
         v, cores = cpu_baseline(index, buf, cfg, args.ctx, args.cpu_tokens)
         result["cpu_baseline"] = {"value": round(v, 4), "unit": "tok/s", "cores": cores, "kind": "port",
