@@ -40,8 +40,10 @@ const char* qne_last_error(void);
  * qne_prefill_chunk pass replays a captured HIP graph; false launches the same kernels one by one,
  * for tools that trace kernel launches but not graph replays), "gdn_fusion" (default true: the
  * persistent decode kernel runs a GDN layer's in-projection and recurrent step as one phase where
- * the shapes allow; false keeps them two phases, with identical results), "tiles" (a serialised ModelTiles,
- * model.rs:90-98). A serialised ModelTiles may also be passed as the whole object. A tile profile
+ * the shapes allow; false keeps them two phases, with identical results), "mfma_gemv" (default
+ * true: the persistent decode kernel's q4 GEMVs run on the int8 matrix cores, x as a 22-bit fixed
+ * point per 64 columns; false runs them on the vector ALUs, the same results to f32 rounding),
+ * "tiles" (a serialised ModelTiles, model.rs:90-98). A serialised ModelTiles may also be passed as the whole object. A tile profile
  * is validated like ModelTiles::validate (model.rs:101-109, called at model.rs:174, after the index
  * and before any device work): QNE_EINVAL "invalid kernel tile profile: Tile { ... }" for a tile the
  * reference rejects, or for a missing field. A valid profile changes nothing else: kernel shapes

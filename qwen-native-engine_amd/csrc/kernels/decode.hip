@@ -28,9 +28,13 @@
 //    in-projection rows that own those channels; the residual stream h lives in the registers of
 //    the waves that own its rows and is published after each residual add;
 //  - GDN: one workgroup per (head, 8 value columns), one wave per column, its 512-byte state column
-//    prefetched into LDS; attention: split-context partials per (kv head, split) with GQA reuse,
-//    K/V rows prefetched into LDS through the block table, then a combine phase per (q head,
-//    64 dims) with the sigmoid gate;
+//    prefetched into LDS; the layer's in-projection rows run in the same phase (PH_GDNF), each
+//    head's q / k exchanged among its 16 workgroups. Attention: split-context partials per (kv
+//    head, split) with GQA reuse, K/V rows prefetched into LDS through the block table, merged per
+//    (q head, 64 dims) with the sigmoid gate by the split workgroups in the same phase (fold), or
+//    in a combine phase of its own for shapes with fewer splits than 4 per q head;
+//  - the q4 GEMVs run on v_mfma_i32_16x16x64_i8: rows tiled per workgroup, K split over waves, x
+//    as three signed base-256 digits of a 22-bit fixed point per 64 columns;
 //  - the LM head tracks a per-wave argmax; workgroups publish their best and every workgroup
 //    reduces all of them, so the next step needs no separate broadcast.
 #include <cstddef>
