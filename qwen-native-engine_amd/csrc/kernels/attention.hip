@@ -581,8 +581,10 @@ static void launch_prefill(const AttnRowsArgs& a, hipStream_t st) {
 }
 
 bool prefill_attention_supported(int nq, int nkv) {
+    // the groupings the model configurations have (and the tests run); others take the per-row
+    // partials
     const int G = nkv > 0 && nq % nkv == 0 ? nq / nkv : 0;
-    return G == 1 || G == 2 || G == 4;
+    return G == 2 || G == 4;
 }
 
 void launch_attention_rows(const AttnRowsArgs& a, hipStream_t st) {
@@ -594,12 +596,9 @@ void launch_attention_rows(const AttnRowsArgs& a, hipStream_t st) {
             !prefill_attention_supported(a.nq, a.nkv) ||
             (long)a.splits * a.split_len < (long)a.max_blocks * kBlock)
             throw Error(QNE_EINVAL, "prefill attention: rows must share one block table, split_len must be a multiple "
-                                    "of 32 up to 1024 covering the context, and 1, 2 or 4 query heads per kv head");
-        switch (G) {
-            case 1: launch_prefill<1>(a, st); break;
-            case 2: launch_prefill<2>(a, st); break;
-            default: launch_prefill<4>(a, st); break;
-        }
+                                    "of 32 up to 1024 covering the context, and 2 or 4 query heads per kv head");
+        if (G == 2) launch_prefill<2>(a, st);
+        else launch_prefill<4>(a, st);
     } else {
         partial_by_g(G, a.qbuf, a.k_pool, a.v_pool, a.block_table, a.max_blocks, a.bt_stride, a.pos, a.nkv, a.part_ml,
                      a.part_acc, a.splits, a.rows, st, a.order);

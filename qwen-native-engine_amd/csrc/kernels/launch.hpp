@@ -120,7 +120,7 @@ struct AttnRowsArgs {
     int split_len = 0;
 };
 void launch_attention_rows(const AttnRowsArgs& a, hipStream_t st);
-// Whether the query-tile prefill attention takes this head grouping (1, 2 or 4 q heads per kv head).
+// Whether the query-tile prefill attention takes this head grouping (2 or 4 q heads per kv head).
 bool prefill_attention_supported(int nq, int nkv);
 
 // Per-row strides (in floats) of the batched GDN decode step.
