@@ -262,49 +262,63 @@ __global__ __launch_bounds__(256) void k_wy_prep(const float* __restrict__ q, co
     }
 }
 
-// LDS staging of one chunk in the chain workgroup, in floats: W (all tiles), U (the workgroup's four
-// column groups), P, q in A-fragment order, the decayed K^T, L.
-constexpr int kSW = 0, kSU = 8192, kSP = 12288, kSQ = 16384, kSK = 24576, kSL = 32768, kSFloats = 32832;
+// LDS staging of one chunk in the chain workgroup, in floats: W (all tiles), U (the workgroup's two
+// column groups), P, q in A-fragment order, the decayed K^T, L; then the waves' partial sums
+// ([wave 8][tile 4][lane 64][4]: D, later the rows of Q S).
+constexpr int kSW = 0, kSU = 8192, kSP = 10240, kSQ = 14336, kSK = 22528, kSL = 30720, kSX = 30784;
+constexpr int kSFloats = kSX + 8 * 1024;
 
-// The chain over chunks: workgroup = (sequence, head, value columns 64 half .. 64 half + 63), wave =
-// 16 of those columns. Per chunk: D = U - W S, O = diag(gamma) Q S + P D, S = gamma_63 S + Kf D.
-__global__ __launch_bounds__(256) void k_wy_chain(const float* __restrict__ q, const float* __restrict__ ws,
+// The chain over chunks: workgroup = (sequence, head, value columns 32 quarter .. 32 quarter + 31),
+// 8 waves = 2 column groups of 16 (cgl = wave / 4) x 4 key quarters (kq = wave % 4, key tiles
+// 2 kq, 2 kq + 1, the wave's 32 keys of the state slice in 8 VGPRs). Per chunk:
+//  - D = U - W S: each key quarter contracts its 32 keys, the four partials meet in LDS and every
+//    wave of the column group adds them in quarter order (so all four hold the same D);
+//  - O = diag(gamma) Q S + P D: the rows of Q S likewise by key quarter; wave kq then owns output
+//    row tile kq, adds the four partial rows in quarter order and its P D terms (row tile kq needs
+//    position tiles 0..kq of D), and stores them;
+//  - S = gamma_63 S + Kf D on the wave's own key tiles.
+// A chain's MFMA work is split four ways (about 100-112 MFMAs per wave and chunk instead of 424),
+// and a (sequence, head) runs as four workgroups, all on one XCD (workgroups are dealt to XCDs
+// round robin), which share its chunk operands in that XCD's L2.
+__global__ __launch_bounds__(512) void k_wy_chain(const float* __restrict__ q, const float* __restrict__ ws,
                                                   float* __restrict__ state, float* __restrict__ out, int T, int H,
                                                   int BH, int value_major) {
     __shared__ __attribute__((aligned(16))) float sm[kSFloats];
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, lr = lane & 15, lg = lane >> 4;
+    const int cgl = wv >> 2, kq = wv & 3;
     const int id = blockIdx.x, xcd = id & 7, slot = id >> 3;
-    const int bh = (slot >> 1) * 8 + xcd, half = slot & 1, cg = 4 * half + wv;
+    const int bh = (slot >> 2) * 8 + xcd, quarter = slot & 3, cg = 2 * quarter + cgl;
     if (bh >= BH) return;  // the whole workgroup
     const int b = bh / H, h = bh % H, NC = (T + kC - 1) / kC;
     const int col = 16 * cg + lr;
 
-    // Copies of chunk c's operands; each wave copies a quarter of every buffer (1 KiB blocks).
-    // Per wave: W, U, L = 13 instructions, P, q = 12, K = 8.
+    // Copies of chunk c's operands; the 8 waves copy an eighth of every buffer each (1 KiB blocks).
+    // Per wave: W, U, L = 6 instructions, P, q = 6, K = 4.
     auto issue_wul = [&](int c) {
         const float* wc = ws + ((size_t)bh * NC + c) * kWyFloats;
 #pragma unroll
-        for (int u = 0; u < 8; u++) {
-            const int blk = wv + 4 * u;
+        for (int u = 0; u < 4; u++) {
+            const int blk = wv + 8 * u;
             dma16(wc + kWfOff + blk * 256 + lane * 4, sm + kSW + blk * 256);
         }
-#pragma unroll
-        for (int pt = 0; pt < 4; pt++)
-            dma16(wc + kUfOff + ((pt * 8 + 4 * half + wv) * 64 + lane) * 4, sm + kSU + (pt * 4 + wv) * 256);
-        if (lane < 16) dma4(wc + kLfOff + 16 * wv + lane, sm + kSL + 16 * wv);
+        {  // U block (column group wv / 4, position tile wv % 4)
+            const int ucg = wv >> 2, upt = wv & 3;
+            dma16(wc + kUfOff + ((upt * 8 + 2 * quarter + ucg) * 64 + lane) * 4, sm + kSU + (ucg * 4 + upt) * 256);
+        }
+        if (lane < 8) dma4(wc + kLfOff + 8 * wv + lane, sm + kSL + 8 * wv);
     };
     auto issue_qp = [&](int c) {
         const float* wc = ws + ((size_t)bh * NC + c) * kWyFloats;
         const int t0 = c * kC, n = min(kC, T - t0);
 #pragma unroll
-        for (int u = 0; u < 4; u++) {
-            const int blk = wv + 4 * u;
+        for (int u = 0; u < 2; u++) {
+            const int blk = wv + 8 * u;
             dma16(wc + kPfOff + blk * 256 + lane * 4, sm + kSP + blk * 256);
         }
         // q block (pt, kt): lane i <- q[16pt + i%16][16kt + 4(i/16) .. +3]; padding rows repeat a real row
 #pragma unroll
-        for (int u = 0; u < 8; u++) {
-            const int blk = wv + 4 * u, pt = blk >> 3, kt = blk & 7;
+        for (int u = 0; u < 4; u++) {
+            const int blk = wv + 8 * u, pt = blk >> 3, kt = blk & 7;
             const int p = min(16 * pt + lr, n - 1);
             dma16(q + (((size_t)b * T + t0 + p) * H + h) * kD + 16 * kt + 4 * lg, sm + kSQ + blk * 256);
         }
@@ -312,8 +326,8 @@ __global__ __launch_bounds__(256) void k_wy_chain(const float* __restrict__ q, c
     auto issue_k = [&](int c) {
         const float* wc = ws + ((size_t)bh * NC + c) * kWyFloats;
 #pragma unroll
-        for (int u = 0; u < 8; u++) {
-            const int blk = wv + 4 * u;
+        for (int u = 0; u < 4; u++) {
+            const int blk = wv + 8 * u;
             dma16(wc + kKfOff + blk * 256 + lane * 4, sm + kSK + blk * 256);
         }
     };
@@ -321,113 +335,127 @@ __global__ __launch_bounds__(256) void k_wy_chain(const float* __restrict__ q, c
     // state entry (key j, value column col): [dk][dv], or the model's value-major [dv][dk]
     float* S0 = state + (size_t)bh * kD * kD;
     auto sidx = [&](int j) { return value_major ? (size_t)col * kD + j : (size_t)j * kD + col; };
-    f4 S[8];
+    f4 S[2];  // key tiles 2 kq + j
 #pragma unroll
-    for (int kt = 0; kt < 8; kt++)
+    for (int j = 0; j < 2; j++)
 #pragma unroll
-        for (int r = 0; r < 4; r++) S[kt][r] = S0[sidx(16 * kt + 4 * lg + r)];
+        for (int r = 0; r < 4; r++) S[j][r] = S0[sidx(16 * (2 * kq + j) + 4 * lg + r)];
     // the state loads complete before the first copies are counted
     wait_vm<0>();
     issue_wul(0);
     issue_qp(0);
     issue_k(0);
+    f4* X = (f4*)(sm + kSX);  // [wave][tile][lane]
+    const int x0 = 4 * cgl;   // the column group's first wave
 
     for (int c = 0; c < NC; c++) {
         const bool more = c + 1 < NC;
         const int t0 = c * kC, n = min(kC, T - t0);
         const size_t row0 = ((size_t)b * T + t0) * H + h;
 
-        // after W, U, L of c: the stores of chunk c - 1 (issued before the q, P copies), q, P (12), K (8)
-        wait_vm<20>();
+        // after W, U, L of c: the stores of chunk c - 1 (issued before the q, P copies), q, P (6), K (4)
+        wait_vm<10>();
         __syncthreads();
         f4 D[4];
 #pragma unroll
-        for (int pt = 0; pt < 4; pt++) D[pt] = *(const f4*)(sm + kSU + ((pt * 4 + wv) * 64 + lane) * 4);
+        for (int pt = 0; pt < 4; pt++)
+            D[pt] = kq == 0 ? *(const f4*)(sm + kSU + ((cgl * 4 + pt) * 64 + lane) * 4) : f4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int kt = 0; kt < 8; kt++) {
+        for (int j = 0; j < 2; j++) {
+            const int kt = 2 * kq + j;
             f4 a[4];
 #pragma unroll
             for (int pt = 0; pt < 4; pt++) a[pt] = *(const f4*)(sm + kSW + ((pt * 8 + kt) * 64 + lane) * 4);
 #pragma unroll
             for (int r = 0; r < 4; r++)
 #pragma unroll
-                for (int pt = 0; pt < 4; pt++) D[pt] = mfma4(a[pt][r], S[kt][r], D[pt]);
+                for (int pt = 0; pt < 4; pt++) D[pt] = mfma4(a[pt][r], S[j][r], D[pt]);
         }
-        float gq[16];  // gamma of the output rows this lane holds: 16pt + 4lg + r
+#pragma unroll
+        for (int pt = 0; pt < 4; pt++) X[(wv * 4 + pt) * 64 + lane] = D[pt];
+        float gqa[16];  // gamma of the rows this lane holds in every row tile: 16 pt + 4lg + r
 #pragma unroll
         for (int pt = 0; pt < 4; pt++)
 #pragma unroll
-            for (int r = 0; r < 4; r++) gq[pt * 4 + r] = __builtin_amdgcn_exp2f(sm[kSL + 16 * pt + 4 * lg + r]);
+            for (int r = 0; r < 4; r++) gqa[pt * 4 + r] = __builtin_amdgcn_exp2f(sm[kSL + 16 * pt + 4 * lg + r]);
         const float gl = __builtin_amdgcn_exp2f(sm[kSL + kC - 1]);
-        __syncthreads();  // W, U, L are no longer read
+        __syncthreads();  // W, U, L are no longer read; the D partials are in
         if (more) issue_wul(c + 1);
+#pragma unroll
+        for (int pt = 0; pt < 4; pt++) {
+            f4 d = X[((x0 + 0) * 4 + pt) * 64 + lane];
+#pragma unroll
+            for (int w = 1; w < 4; w++) d += X[((x0 + w) * 4 + pt) * 64 + lane];
+            D[pt] = d;
+        }
 
-        // after q, P of c: K of c (8), W, U, L of c + 1 (13)
-        if (more) wait_vm<21>();
-        else wait_vm<8>();
-        __syncthreads();
+        // after q, P of c: K of c (4), W, U, L of c + 1 (6)
+        if (more) wait_vm<10>();
+        else wait_vm<4>();
+        __syncthreads();  // also: every wave has read the D partials
         f4 O[4];
 #pragma unroll
         for (int pt = 0; pt < 4; pt++) O[pt] = f4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int kt = 0; kt < 8; kt++) {
+        for (int j = 0; j < 2; j++) {
+            const int kt = 2 * kq + j;
             f4 a[4];
 #pragma unroll
             for (int pt = 0; pt < 4; pt++) a[pt] = *(const f4*)(sm + kSQ + ((pt * 8 + kt) * 64 + lane) * 4);
 #pragma unroll
             for (int r = 0; r < 4; r++)
 #pragma unroll
-                for (int pt = 0; pt < 4; pt++) O[pt] = mfma4(a[pt][r], S[kt][r], O[pt]);
+                for (int pt = 0; pt < 4; pt++) O[pt] = mfma4(a[pt][r], S[j][r], O[pt]);
         }
         // diag(gamma) on the rows of Q S0: row 16pt + 4lg + r of register r
 #pragma unroll
         for (int pt = 0; pt < 4; pt++)
 #pragma unroll
-            for (int r = 0; r < 4; r++) O[pt][r] *= gq[pt * 4 + r];
+            for (int r = 0; r < 4; r++) O[pt][r] *= gqa[pt * 4 + r];
 #pragma unroll
-        for (int pt = 0; pt < 4; pt++) {
-            f4 a[4];
+        for (int pt = 0; pt < 4; pt++) X[(wv * 4 + pt) * 64 + lane] = O[pt];
+        __syncthreads();
+        // output row tile kq: the four quarters' rows of Q S, then + P D over position tiles 0..kq
+        f4 o = X[((x0 + 0) * 4 + kq) * 64 + lane];
 #pragma unroll
-            for (int it = pt; it < 4; it++) a[it] = *(const f4*)(sm + kSP + ((it * 4 + pt) * 64 + lane) * 4);
+        for (int w = 1; w < 4; w++) o += X[((x0 + w) * 4 + kq) * 64 + lane];
+        for (int pt = 0; pt <= kq; pt++) {  // wave-uniform
+            const f4 a = *(const f4*)(sm + kSP + ((kq * 4 + pt) * 64 + lane) * 4);
 #pragma unroll
-            for (int r = 0; r < 4; r++)
-#pragma unroll
-                for (int it = pt; it < 4; it++) O[it] = mfma4(a[it][r], D[pt][r], O[it]);
+            for (int r = 0; r < 4; r++) o = mfma4(a[r], D[pt][r], o);
         }
 #pragma unroll
-        for (int it = 0; it < 4; it++)
-#pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const int p = 16 * it + 4 * lg + r;
-                if (p < n) out[(row0 + (size_t)p * H) * kD + col] = O[it][r];
-            }
-        __syncthreads();  // q, P are no longer read
+        for (int r = 0; r < 4; r++) {
+            const int p = 16 * kq + 4 * lg + r;
+            if (p < n) out[(row0 + (size_t)p * H) * kD + col] = o[r];
+        }
+        __syncthreads();  // q, P and the partial rows are no longer read
         if (more) issue_qp(c + 1);
 
-        // after K of c: W, U, L of c + 1 (13), this chunk's 16 stores, q, P of c + 1 (12); on the last
+        // after K of c: W, U, L of c + 1 (6), this chunk's 4 stores, q, P of c + 1 (6); on the last
         // chunk everything
-        if (more) wait_vm<41>();
+        if (more) wait_vm<16>();
         else wait_vm<0>();
         __syncthreads();
 #pragma unroll
-        for (int kt = 0; kt < 8; kt++) S[kt] *= gl;
+        for (int j = 0; j < 2; j++) S[j] *= gl;
 #pragma unroll
         for (int pt = 0; pt < 4; pt++) {
-            f4 a[8];
+            f4 a[2];
 #pragma unroll
-            for (int kt = 0; kt < 8; kt++) a[kt] = *(const f4*)(sm + kSK + ((kt * 4 + pt) * 64 + lane) * 4);
+            for (int j = 0; j < 2; j++) a[j] = *(const f4*)(sm + kSK + (((2 * kq + j) * 4 + pt) * 64 + lane) * 4);
 #pragma unroll
             for (int r = 0; r < 4; r++)
 #pragma unroll
-                for (int kt = 0; kt < 8; kt++) S[kt] = mfma4(a[kt][r], D[pt][r], S[kt]);
+                for (int j = 0; j < 2; j++) S[j] = mfma4(a[j][r], D[pt][r], S[j]);
         }
         __syncthreads();  // K is no longer read
         if (more) issue_k(c + 1);
     }
 #pragma unroll
-    for (int kt = 0; kt < 8; kt++)
+    for (int j = 0; j < 2; j++)
 #pragma unroll
-        for (int r = 0; r < 4; r++) S0[sidx(16 * kt + 4 * lg + r)] = S[kt][r];
+        for (int r = 0; r < 4; r++) S0[sidx(16 * (2 * kq + j) + 4 * lg + r)] = S[j][r];
 }
 
 }  // namespace
@@ -441,7 +469,7 @@ void launch_delta_rule_wy(const float* q, const float* k, const float* v, const 
                           int value_major) {
     const int NC = (tokens + kC - 1) / kC, BH = batch * heads;
     hipLaunchKernelGGL(k_wy_prep, dim3(NC, heads, batch), dim3(256), 0, st, q, k, v, beta, g, ws, tokens, heads);
-    hipLaunchKernelGGL(k_wy_chain, dim3(16 * ((BH + 7) / 8)), dim3(256), 0, st, q, ws, state, out, tokens, heads, BH,
+    hipLaunchKernelGGL(k_wy_chain, dim3(32 * ((BH + 7) / 8)), dim3(512), 0, st, q, ws, state, out, tokens, heads, BH,
                        value_major);
 }
 
