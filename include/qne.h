@@ -61,8 +61,8 @@ int qne_prefill(qne_model* m, const uint32_t* ids, size_t n);
 /* Model::prefill_chunk -- model.rs:349 (prefill_batched / prefill_from are start = 0 /
  * finish_logits = 1 forms, model.rs:339-346). Continues the state at `start`. With
  * finish_logits, computes the logits after the last id and the greedy pick (last_token).
- * Like the reference's batched prefill (batch.rs), it runs the prompt in passes of up to 512
- * tokens through the batched MFMA GEMM, the GDN recurrence in the chunk-64 WY form over whole
+ * Like the reference's batched prefill (batch.rs), it runs the prompt in passes of up to 2048
+ * tokens (fewer if max_context is smaller) through the batched MFMA GEMM, the GDN recurrence in the chunk-64 WY form over whole
  * 64-position blocks; the state equals qne_prefill's to f32 rounding. Calls cut at multiples of 64
  * positions give the same bits as one call; other cuts agree to f32 rounding. Models whose shapes
  * the batched kernels do not take run it token by token.
@@ -186,10 +186,10 @@ int qne_paged_attn_decode_noalloc(const float* q, const float* k_new, const floa
                                   const int32_t* ctx, float* out, int batch, int nq, int nkv,
                                   void* stream);
 
-/* The batched form of gemv for m (1..512) rows of x: y[r] = W x[r] for r < m, on f16 MFMA (x split
+/* The batched form of gemv for m (1..2048) rows of x: y[r] = W x[r] for r < m, on f16 MFMA (x split
  * into two f16 halves, so the products keep about 22 bits), with the same norm prologue and
  * epilogues as qne_gemv. The reference's 16-token GEMM (kernels/src/batch.rs:12-99, Gpu::gemm
- * lib.rs:341-347) generalised to M up to 512 (in tiles of 64 rows). x rows at x + r * x_stride (x_stride >= k, a multiple of 4), y
+ * lib.rs:341-347) generalised to M up to 2048 (in tiles of 64 rows). x rows at x + r * x_stride (x_stride >= k, a multiple of 4), y
  * rows at y + r * y_stride. k must be a multiple of 64 and q4 groups a multiple of 64. On the null
  * stream the call returns when the result is ready. The split partials' scratch is kept per device
  * (grown when a call needs more): calls that overlap on one device must not be issued. */

@@ -361,7 +361,7 @@ int qne_gemm(int kind, const void* w, const void* sz, int rows, int k, int group
         need(kind == QNE_MAT_F16 || sz, "q4 needs sz");
         need(epilogue >= QNE_EPI_STORE && epilogue <= QNE_EPI_SWIGLU, "unknown epilogue");
         need(epilogue != QNE_EPI_SWIGLU || rows % 2 == 0, "SwiGlu needs an even row count");
-        need(qne::gemm_shape_ok(kind, rows, k, group, m), "unsupported shape (m 1..512, k a multiple of 64, q4 group a multiple of 64)");
+        need(qne::gemm_shape_ok(kind, rows, k, group, m), "unsupported shape (m 1..2048, k a multiple of 64, q4 group a multiple of 64)");
         const int n_out = epilogue == QNE_EPI_SWIGLU ? rows / 2 : rows;
         need(x_stride >= k && x_stride % 4 == 0, "x_stride must be >= k and a multiple of 4");
         need(y_stride >= n_out, "y_stride must be >= the output count");

@@ -214,7 +214,7 @@ constexpr uint32_t kSampleMaxK = 1024;
 size_t sample_scratch_bytes();
 void launch_sample(const SampleArgs& a, void* scratch, hipStream_t st);
 
-constexpr int kGemmRowsMax = 512;
+constexpr int kGemmRowsMax = 2048;
 size_t gemm_frag_bytes(int K, int m);
 // Split-K count of a GEMM on an N x K matrix: as many splits as keep a grid of N tiles x row_tiles
 // x splits within one workgroup per CU (at least 2 chunks per split, at most 24). A caller passes a

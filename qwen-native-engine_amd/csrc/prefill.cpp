@@ -22,9 +22,11 @@ ChunkPrefill::ChunkPrefill(Model& m) : m_(m), st_(m.stream_) {
     const ModelConfig& c = m.cfg_;
     rows_shapes_check(c);
     size_t part = 0, frag = 0;
-    rows_workspace(m.layers_, m.lm_head_, kChunk, kRowTiles, &part, &frag);
+    pass_ = std::min(kPassMax, (m.max_context_ + 63) / 64 * 64);
+    row_tiles_ = pass_ / 64;
+    rows_workspace(m.layers_, m.lm_head_, pass_, row_tiles_, &part, &frag);
     try {
-        const size_t T = kChunk;
+        const size_t T = pass_;
         proj_w_ = std::max(c.attn_proj(), c.gdn_proj());
         mixed_w_ = std::max(c.attn_out(), c.gdn_out());
         // Attention partials over fixed position ranges (kPrefillSplitLen positions each, cut at the
@@ -89,7 +91,7 @@ void ChunkPrefill::enqueue_chunk(int n, int lead) {
                       first.input_norm, operand_order(first.in), st_);
     auto gemm = [&](const DevMat& W, uint8_t* frag, int norm, float* y, int y_stride, int epi, uint8_t* frag_out,
                     const float* gain_out, int order_out) {
-        rows_gemm(W, n, c.eps, frag, norm, part_, y, y_stride, epi, frag_out, gain_out, order_out, st_, kRowTiles);
+        rows_gemm(W, n, c.eps, frag, norm, part_, y, y_stride, epi, frag_out, gain_out, order_out, st_, row_tiles_);
     };
     const int max_blocks = (m_.max_context_ + 15) / 16;
     for (size_t li = 0; li < m_.layers_.size(); li++) {
@@ -169,8 +171,8 @@ hipGraphExec_t ChunkPrefill::graph_for(int n, int lead) {
 void ChunkPrefill::run(const uint32_t* ids_dev, size_t n, uint32_t start, bool finish_logits) {
     const ModelConfig& c = m_.cfg_;
     int last = 0;
-    for (size_t off = 0; off < n; off += kChunk) {
-        const int t = (int)std::min<size_t>(kChunk, n - off);
+    for (size_t off = 0; off < n; off += (size_t)pass_) {
+        const int t = (int)std::min<size_t>((size_t)pass_, n - off);
         // the previous chunk's graph has read pos_ before these copies run (same stream)
         QNE_HIP(hipStreamSynchronize(st_));
         for (int i = 0; i < t; i++) host_pos_[i] = (int32_t)(start + off + i);

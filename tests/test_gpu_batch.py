@@ -79,8 +79,9 @@ def test_gemm_swiglu_applied_by_the_gemm(norm):
     assert rel_err(got, want) < 2e-5
 
 
-def test_gemm_full_pass_of_512_rows():
-    got, want = run_gemm(Q.MAT_Q4, 64, 256, 512, 512, Q.EPI_ACCUMULATE, True, seed=77)
+@pytest.mark.parametrize("M", [512, 2048])
+def test_gemm_full_pass_of_rows(M):
+    got, want = run_gemm(Q.MAT_Q4, 64, 256, 512, M, Q.EPI_ACCUMULATE, True, seed=77 + M)
     assert rel_err(got, want) < 2e-5
 
 
@@ -123,7 +124,7 @@ def test_gemm_row_result_does_not_depend_on_other_rows():
 
 
 def test_gemm_rejects_bad_shapes():
-    for args in [(Q.MAT_F16, 0, 256, 1000, 4), (Q.MAT_Q4, 32, 256, 1024, 4), (Q.MAT_F16, 0, 256, 1024, 513),
+    for args in [(Q.MAT_F16, 0, 256, 1000, 4), (Q.MAT_Q4, 32, 256, 1024, 4), (Q.MAT_F16, 0, 256, 1024, 2049),
                  (Q.MAT_F16, 0, 256, 1024, 0)]:
         kind, group, rows, k, M = args
         with pytest.raises(Q.QneError) as e:

@@ -187,13 +187,32 @@ def test_chunked_prefill_does_not_depend_on_the_chunking(pair):
 
 def test_chunked_prefill_matches_oracle_over_many_chunks(pair):
     name, m, om, _, _ = pair
-    ids = prompt(m.vocab, 1100, 12)  # passes of 512, 512 and 76 tokens
+    ids = prompt(m.vocab, 1100, 12)  # one pass (passes hold up to 2048 tokens)
     m.reset()
     om.reset()
     m.prefill_batched(ids)
     want = om.prefill_chunk(ids, 0, True)
     assert np.max(np.abs(m.logits() - want)) < 1e-3
     assert m.last_token() == (int(np.argmax(want)), len(ids))
+
+
+def test_chunked_prefill_in_several_passes_matches_oracle():
+    """A pass holds min(2048, max_context rounded up to 64) tokens: a 2200-id prompt in one call runs
+    as passes of 2048 and 152 tokens, and split into calls at 1024 (a multiple of 64: the GDN blocks
+    line up) as 1024 + 1024 + 152."""
+    index, buf = W.synth_model("tiny", seed=11, body="q4", head="f16", norm_jitter=0.1)
+    om = O.OracleModel(index, buf, "f64")
+    ids = prompt(json.loads(index)["config"]["vocab"], 2200, 13)
+    want = om.prefill_chunk(ids, 0, True)
+    with Q.Model.load(index, buf) as m:
+        m.prefill_chunk(ids, 0, True)
+        a = m.logits()
+        assert np.max(np.abs(a - want)) < 1e-3 and m.last_token() == (int(np.argmax(want)), len(ids))
+        m.reset()
+        m.prefill_chunk(ids[:1024], 0, False)
+        m.prefill_chunk(ids[1024:], 1024, True)
+        # the same rows in other passes: the same bits (split counts are fixed per model)
+        assert np.array_equal(m.logits(), a)
 
 
 def test_snapshot_restore_and_reset(pair):
