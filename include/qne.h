@@ -43,7 +43,9 @@ const char* qne_last_error(void);
  * the shapes allow; false keeps them two phases, with identical results), "mfma_gemv" (default
  * true: the persistent decode kernel's q4 GEMVs run on the int8 matrix cores, x as a 22-bit fixed
  * point per 64 columns; false runs them on the vector ALUs, the same results to f32 rounding),
- * "tiles" (a serialised ModelTiles, model.rs:90-98). A serialised ModelTiles may also be passed as the whole object. A tile profile
+ * "gemm_fusion" (default true: a qne_prefill_chunk GEMM with one split applies its SwiGLU or
+ * residual add and stages the next GEMM's operand itself; false runs a separate reduce pass after
+ * it, with identical results), "tiles" (a serialised ModelTiles, model.rs:90-98). A serialised ModelTiles may also be passed as the whole object. A tile profile
  * is validated like ModelTiles::validate (model.rs:101-109, called at model.rs:174, after the index
  * and before any device work): QNE_EINVAL "invalid kernel tile profile: Tile { ... }" for a tile the
  * reference rejects, or for a missing field. A valid profile changes nothing else: kernel shapes

@@ -29,7 +29,8 @@ int attn_splits_for(int max_blocks) {
 int operand_order(const DevMat& W) { return W.kind == KIND_Q4 ? 1 : 0; }
 
 void rows_gemm(const DevMat& W, int n, float eps, uint8_t* frag, int norm, float* part, float* y, int y_stride, int epi,
-               uint8_t* frag_out, const float* gain_out, int order_out, hipStream_t st, int row_tiles, bool partials_only) {
+               uint8_t* frag_out, const float* gain_out, int order_out, hipStream_t st, int row_tiles, bool partials_only,
+               bool fuse) {
     GemmArgs a;
     a.m = n;
     a.frag = frag;
@@ -51,6 +52,7 @@ void rows_gemm(const DevMat& W, int n, float eps, uint8_t* frag, int norm, float
     a.gain_out = gain_out;
     a.order_out = order_out;
     a.partials_only = partials_only ? 1 : 0;
+    a.fuse = fuse ? 0 : -1;
     launch_gemm(a, st);
 }
 

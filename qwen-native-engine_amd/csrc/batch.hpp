@@ -20,10 +20,12 @@ namespace qne {
 // with its reduce, the split count chosen for row_tiles tiles of 64 rows: W applied to the x
 // operand staged in `frag` (norm: its rows carry a deferred RMSNorm), epilogue into y, and with
 // frag_out the result staged for the next GEMM (times gain_out). partials_only: only the split
-// partials are written (into part); the kernel that reads the output sums them.
+// partials are written (into part); the kernel that reads the output sums them. fuse: a GEMM with
+// one split may apply its epilogue and staging itself (false: always the reduce pass; the same
+// results).
 void rows_gemm(const DevMat& W, int n, float eps, uint8_t* frag, int norm, float* part, float* y, int y_stride,
                int epi, uint8_t* frag_out, const float* gain_out, int order_out, hipStream_t st, int row_tiles = 1,
-               bool partials_only = false);
+               bool partials_only = false, bool fuse = true);
 // 1 when a GEMM on W takes its x operand in the q4 column order.
 int operand_order(const DevMat& W);
 // Throws QNE_EFORMAT unless the model's shapes fit the batched kernels.

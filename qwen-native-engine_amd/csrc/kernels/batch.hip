@@ -105,9 +105,10 @@ __device__ __forceinline__ void wait_vm_upto(int n) {
 // computation; with DW = 0 every compute wave sends a share of the W tiles and of x. The row tiles
 // of one W tile read the same W chunks, which the MALL serves after the first.
 // Epilogues: partials (split-K, or an epilogue the GEMM does not apply); `direct` (one split: store
-// or residual add); `fuse` (one split, SwiGLU): tiles [0, TW / 2) are gate rows and [TW / 2, TW) the
-// matching up rows (n_out further), and the workgroup writes silu(gate) * up and stages it as the
-// next GEMM's operand, exactly as k_gemm_reduce does with one split.
+// or residual add); `fuse` 1 (one split, SwiGLU): tiles [0, TW / 2) are gate rows and [TW / 2, TW)
+// the matching up rows (n_out further), and the workgroup writes silu(gate) * up and stages it as
+// the next GEMM's operand; `fuse` 2 (one split, store or residual add with the result staged as the
+// next GEMM's operand). Both compute exactly what k_gemm_reduce does with one split.
 template <int KIND, int WAVES, int D, int DW, int CF>
 __global__ __launch_bounds__(64 * (WAVES + DW)) void k_gemm(const GemmArgs a) {
     constexpr int TW = WAVES * CF;                                  // 32-row W tiles per workgroup
@@ -136,7 +137,7 @@ __global__ __launch_bounds__(64 * (WAVES + DW)) void k_gemm(const GemmArgs a) {
     // W row (= output column) of lane l32 in tile t of this workgroup
     auto wrow = [&](int t) {
         constexpr int half = TW / 2;
-        if (a.fuse) return t < half ? (blockIdx.x * half + t) * 32 + l32 : a.n_out + (blockIdx.x * half + t - half) * 32 + l32;
+        if (a.fuse == 1) return t < half ? (blockIdx.x * half + t) * 32 + l32 : a.n_out + (blockIdx.x * half + t - half) * 32 + l32;
         return (blockIdx.x * TW + t) * 32 + l32;
     };
 
@@ -304,6 +305,51 @@ __global__ __launch_bounds__(64 * (WAVES + DW)) void k_gemm(const GemmArgs a) {
                     store_through(d, a.epi == EPI_ACCUMULATE ? *d + v : v);
                 }
             }
+        }
+        return;
+    }
+    if (a.fuse == 2) {
+        // the tile through LDS ([row][column]) times the rows' 1 / rms, then every wave takes whole
+        // 64-column chunks of rows (lanes = columns): residual add or store, and the staged operand
+        constexpr int kOut = TW * 32;  // output columns of the workgroup
+        static_assert(kOut % kChunk == 0 && (kBM * kOut + kBM) * 4 <= D * kSlot, "fused epilogue tile");
+        float* so = sinv + kBM;  // [kBM][kOut]
+        if (computes) {
+#pragma unroll
+            for (int cf = 0; cf < CF; cf++) {
+                const int col = (w * CF + cf) * 32 + l32;
+#pragma unroll
+                for (int j = 0; j < 16; j++) {
+                    const int m = 8 * (j / 4) + 4 * hf + (j % 4);
+                    so[m * kOut + col] = acc[cf][0][j] * sinv[m];
+                    so[(32 + m) * kOut + col] = acc[cf][1][j] * sinv[32 + m];
+                }
+            }
+        }
+        __syncthreads();
+        if (!computes) return;
+        constexpr int nck = kOut / kChunk;
+        constexpr int kIt = kBM * nck / WAVES;  // (row, chunk) items per wave: item w + WAVES q
+        static_assert(kBM * nck % WAVES == 0, "fused epilogue items");
+        const size_t tile_bytes = (size_t)(a.n_out / kChunk) * kChunkBytes;
+        const int nrow = min(rows, kBM), col0 = blockIdx.x * kOut;
+        // every item's residual and gain loads in flight before the first is used
+        float hv[kIt], gv[kIt];
+#pragma unroll
+        for (int q = 0; q < kIt; q++) {
+            const int it = w + WAVES * q, r = it / nck, ch = it % nck, c = col0 + ch * kChunk + lane;
+            const bool live = r < nrow && col0 + ch * kChunk < a.n_out;  // else a whole chunk past the outputs
+            hv[q] = live && a.epi == EPI_ACCUMULATE ? a.y[(size_t)(kBM * mt + r) * a.y_stride + c] : 0.0f;
+            gv[q] = live && a.gain_out ? a.gain_out[c] : 1.0f;
+        }
+#pragma unroll
+        for (int q = 0; q < kIt; q++) {
+            const int it = w + WAVES * q, r = it / nck, ch = it % nck, c = col0 + ch * kChunk + lane;
+            if (r >= nrow || col0 + ch * kChunk >= a.n_out) continue;  // wave-uniform
+            const float g = so[r * kOut + ch * kChunk + lane];
+            const float v = a.epi == EPI_ACCUMULATE ? hv[q] + g : g;
+            if (a.y) store_through(a.y + (size_t)(kBM * mt + r) * a.y_stride + c, v);
+            emit_x(a.frag_out, tile_bytes, kBM * mt + r, c, v, gv[q], a.order_out, lane);
         }
         return;
     }
@@ -566,10 +612,17 @@ void launch_gemm(GemmArgs a, hipStream_t st) {
     // on every shape (gate_up 68 -> 108 us): each wave then issues 9 LDS DMAs per chunk instead of
     // 5, and a DMA holds its wave for about the transfer time.
     const bool dma_waves = a.mpad == kBM;
-    // SwiGLU with one split over several row tiles: the GEMM applies it and stages the output
-    // itself, with no partials and no reduce pass
-    a.fuse = a.kind == KIND_Q4 && !dma_waves && a.splits == 1 && a.epi == EPI_SWIGLU && !a.partials_only &&
-             a.N == 2 * a.n_out && a.n_out % (32 * waves / 2) == 0 && a.K <= 64 * kChunk && (a.y || a.frag_out);
+    // One split over several row tiles: the GEMM applies the SwiGLU, or the store / residual add,
+    // and stages the output itself, with no partials and no reduce pass
+    const bool one = a.fuse == 0 && a.kind == KIND_Q4 && !dma_waves && a.splits == 1 && !a.partials_only;
+    a.fuse = 0;
+    if (one && a.epi == EPI_SWIGLU && a.N == 2 * a.n_out && a.n_out % (32 * waves / 2) == 0 && a.K <= 64 * kChunk &&
+        (a.y || a.frag_out))
+        a.fuse = 1;
+    // store or residual add staged as the next operand (with a normed input its 1 / rms needs K <= 4096)
+    else if (one && a.epi != EPI_SWIGLU && a.frag_out && a.n_out == a.N && a.N % kChunk == 0 &&
+             (a.epi == EPI_STORE || a.y) && (!a.norm || a.K <= 64 * kChunk))
+        a.fuse = 2;
     a.direct = a.splits == 1 && a.epi != EPI_SWIGLU && !a.frag_out && !a.partials_only;
     if (a.kind == KIND_Q4) {
         // 3 chunk slots (77.6 KiB): deeper rings measured slower, and two workgroups fit a CU

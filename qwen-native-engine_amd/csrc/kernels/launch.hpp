@@ -181,7 +181,8 @@ struct GemmArgs {
     int cps = 0;     // set by launch_gemm: chunks per split
     int mpad = 0;    // set by launch_gemm: m rounded up to a multiple of 64 (rows of the partials)
     int direct = 0;  // set by launch_gemm: the GEMM applies the epilogue itself
-    int fuse = 0;    // set by launch_gemm: the GEMM applies the SwiGLU and stages its output itself
+    int fuse = 0;    // set by launch_gemm: the GEMM applies the epilogue and stages its output itself
+                     // (1: SwiGLU, 2: store or residual add); -1 from the caller: never
     float* part = nullptr;
     int epi = EPI_STORE;
     float* y = nullptr;

@@ -100,6 +100,11 @@ LoadOptions parse_options(const char* json) {
         if (v.type != Json::Bool) throw Error(QNE_EINVAL, "mfma_gemv must be true or false");
         o.mfma_gemv = v.b;
     }
+    if (j.has("gemm_fusion")) {
+        const Json& v = j.at("gemm_fusion");
+        if (v.type != Json::Bool) throw Error(QNE_EINVAL, "gemm_fusion must be true or false");
+        o.gemm_fusion = v.b;
+    }
     if (j.has("gdn_fusion")) {
         const Json& v = j.at("gdn_fusion");
         if (v.type != Json::Bool) throw Error(QNE_EINVAL, "gdn_fusion must be true or false");
@@ -157,6 +162,7 @@ Model::Model(const ModelIndex& ix, const uint8_t* weights, uint64_t /*wlen*/, co
     prefill_graphs_ = opt.prefill_graphs;
     gdn_fusion_ = opt.gdn_fusion;
     mfma_gemv_ = opt.mfma_gemv;
+    gemm_fusion_ = opt.gemm_fusion;
     try {
         upload(ix, weights);
         alloc_state();

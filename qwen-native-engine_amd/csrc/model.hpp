@@ -39,6 +39,7 @@ struct LoadOptions {
     bool prefill_graphs = true;  // prefill_chunk passes replay captured graphs (false: direct launches)
     bool gdn_fusion = true;      // persistent kernel: GDN in-projection and step in one phase where the shapes allow
     bool mfma_gemv = true;       // persistent kernel: q4 GEMVs on the int8 matrix cores where the shapes allow
+    bool gemm_fusion = true;     // prefill GEMMs with one split apply their epilogue and staging themselves
 };
 
 struct EngineRun {
@@ -148,6 +149,7 @@ class Model {
     bool persistent_ = true;
     bool prefill_graphs_ = true;  // ChunkPrefill replays captured graphs (else launches directly)
     bool gdn_fusion_ = true;      // the decode program fuses each GDN layer's in-projection and step
+    bool gemm_fusion_ = true;     // prefill GEMMs with one split apply their epilogue (no reduce pass)
     bool mfma_gemv_ = true;       // the decode program runs q4 GEMVs tiled on the matrix cores
     std::vector<std::string> phase_label_;  // per decode-program phase, for the profile
     int engine_grid_ = 0;

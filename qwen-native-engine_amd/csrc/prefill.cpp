@@ -91,7 +91,8 @@ void ChunkPrefill::enqueue_chunk(int n, int lead) {
                       first.input_norm, operand_order(first.in), st_);
     auto gemm = [&](const DevMat& W, uint8_t* frag, int norm, float* y, int y_stride, int epi, uint8_t* frag_out,
                     const float* gain_out, int order_out) {
-        rows_gemm(W, n, c.eps, frag, norm, part_, y, y_stride, epi, frag_out, gain_out, order_out, st_, row_tiles_);
+        rows_gemm(W, n, c.eps, frag, norm, part_, y, y_stride, epi, frag_out, gain_out, order_out, st_, row_tiles_, false,
+                  m_.gemm_fusion_);
     };
     const int max_blocks = (m_.max_context_ + 15) / 16;
     for (size_t li = 0; li < m_.layers_.size(); li++) {

@@ -215,6 +215,27 @@ def test_chunked_prefill_in_several_passes_matches_oracle():
         assert np.array_equal(m.logits(), a)
 
 
+def test_prefill_gemm_epilogues_equal_the_reduce_pass():
+    """With hidden 2048 and a 2048-token pass every prefill GEMM has one split, so gate_up applies
+    the SwiGLU and the out- and down-projections the residual add, each staging the next GEMM's
+    operand, inside the GEMM; {"gemm_fusion": false} runs the reduce pass after each of them
+    instead. Both compute the same arithmetic in the same order: the logits after a 2100-id prompt
+    (passes of 2048 and 52 tokens) and after a further 1-id call are identical bit for bit."""
+    cfg = dict(layers=4, full_attention_every=4, hidden=2048, intermediate=2048, vocab=4096, n_q_heads=8,
+               n_kv_heads=2, head_dim=256, gdn_heads=16)
+    index, buf = W.synth_model(cfg, seed=23, body="q4", head="f16", norm_jitter=0.1)
+    ids = prompt(cfg["vocab"], 2101, 17)
+    runs = []
+    for fusion in (True, False):
+        with Q.Model.load(index, buf, options={"gemm_fusion": fusion}) as m:
+            m.prefill_chunk(ids[:2100], 0, True)
+            a = m.logits()
+            m.prefill_chunk(ids[2100:], 2100, True)
+            runs.append(np.stack([a, m.logits()]))
+    assert np.all(np.isfinite(runs[0]))
+    assert np.array_equal(runs[0].view(np.uint32), runs[1].view(np.uint32)), float(np.max(np.abs(runs[0] - runs[1])))
+
+
 def test_snapshot_restore_and_reset(pair):
     name, m, om, _, _ = pair
     ids = prompt(m.vocab, 16, 6)
