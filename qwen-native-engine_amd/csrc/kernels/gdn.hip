@@ -27,42 +27,6 @@ struct DeltaShared {
     float kq, g, beta;
 };
 
-// One token of the delta rule on the register tile. Inputs q, k, v, g, beta in `sh`
-// (synchronised by the caller). Returns out[col] = g S^T q + dv (k.q) in quarter-0 threads.
-__device__ __forceinline__ float delta_token(float (&s)[32], DeltaShared& sh, int col, int qq) {
-    const float g = sh.g, beta = sh.beta;
-    float sk = 0.0f, sq = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 32; i++) {
-        sk = fmaf(s[i], sh.k[32 * qq + i], sk);
-        sq = fmaf(s[i], sh.q[32 * qq + i], sq);
-    }
-    sh.part[0][qq][col] = sk;
-    sh.part[1][qq][col] = sq;
-    __syncthreads();
-    float out = 0.0f;
-    if (qq == 0) {
-        sk = sh.part[0][0][col] + sh.part[0][1][col] + sh.part[0][2][col] + sh.part[0][3][col];
-        sq = sh.part[1][0][col] + sh.part[1][1][col] + sh.part[1][2][col] + sh.part[1][3][col];
-        const float d = beta * (sh.v[col] - g * sk);
-        sh.dv[col] = d;
-        out = g * sq + d * sh.kq;
-    }
-    __syncthreads();
-    const float d = sh.dv[col];
-#pragma unroll
-    for (int i = 0; i < 32; i++) s[i] = fmaf(g, s[i], d * sh.k[32 * qq + i]);
-    return out;
-}
-
-__device__ __forceinline__ void load_tile(float (&s)[32], const float* S, int col, int qq) {
-#pragma unroll
-    for (int i = 0; i < 32; i++) s[i] = S[(32 * qq + i) * kDV + col];
-}
-__device__ __forceinline__ void store_tile(const float (&s)[32], float* S, int col, int qq) {
-#pragma unroll
-    for (int i = 0; i < 32; i++) S[(32 * qq + i) * kDV + col] = s[i];
-}
 // The model keeps each head's state value-major, S_T[t][j] = S[j][t]: the 128 keys of one value
 // column are contiguous, so a column (what one wave updates in the persistent decode kernel) is a
 // single 512-byte read.
@@ -189,32 +153,67 @@ __global__ __launch_bounds__(kGdnThreads, 6) void k_gdn_decode(const float* __re
     }
 }
 
-// The bare delta rule for one token of sequence blockIdx.y, head blockIdx.x.
+// The bare delta rule for one token of sequence blockIdx.y, head blockIdx.x, on the key-major
+// tile S[j][c] (key j, value column c): thread t holds columns 4 (t % 32)..+3 of keys t / 32 + 16 r
+// (r = 0..7) as 16-byte pieces, so every wave instruction moves one contiguous KiB. Each thread
+// dots its 8 keys with k and q for its 4 columns; the 16 key groups' partial sums meet in LDS and
+// are added in key-group order; then every thread updates its pieces with the column's dv.
 __global__ __launch_bounds__(kGdnThreads) void k_delta_rule(const float* __restrict__ q, const float* __restrict__ k,
                                                             const float* __restrict__ v, const float* __restrict__ beta,
                                                             const float* __restrict__ g, float* __restrict__ state,
                                                             float* __restrict__ out, int H) {
-    __shared__ DeltaShared sh;
-    const int h = blockIdx.x, b = blockIdx.y, t = threadIdx.x, lane = t % kWave, w = t / kWave;
-    const int col = t & (kDV - 1), qq = t >> 7;
+    constexpr int kGroups = kGdnThreads / 32;  // key groups: 16
+    __shared__ float sq_[kDK], sk_[kDK], sv_[kDV], sdv[kDV];
+    __shared__ f4v spart[2][kGroups][kDV / 4];
+    __shared__ float sred[2], skq;
+    const int h = blockIdx.x, b = blockIdx.y, t = threadIdx.x;
+    const int c4 = t & 31, kg = t >> 5;
     const size_t bh = (size_t)b * H + h;
-    float* S = state + bh * kDK * kDV;
-    float s[32];
-    load_tile(s, S, col, qq);
-    if (t < 128) sh.q[t] = q[bh * kDK + t];
-    else if (t < 256) sh.k[t - 128] = k[bh * kDK + t - 128];
-    else if (t < 384) sh.v[t - 256] = v[bh * kDV + t - 256];
-    if (t == 0) { sh.g = g[bh]; sh.beta = beta[bh]; }
+    f4v* S = (f4v*)(state + bh * kDK * kDV) + c4;
+    f4v s[8];
+#pragma unroll
+    for (int r = 0; r < 8; r++) s[r] = __builtin_nontemporal_load(S + (size_t)(kg + kGroups * r) * (kDV / 4));
+    if (t < 128) sq_[t] = q[bh * kDK + t];
+    else if (t < 256) sk_[t - 128] = k[bh * kDK + t - 128];
+    else if (t < 384) sv_[t - 256] = v[bh * kDV + t - 256];
+    if (t == 0) { sred[0] = g[bh]; sred[1] = beta[bh]; }
     __syncthreads();
-    if (w == 0) {
-        float p = sh.k[lane] * sh.q[lane] + sh.k[lane + 64] * sh.q[lane + 64];
+    if (t < kWave) {
+        float p = sk_[t] * sq_[t] + sk_[t + 64] * sq_[t + 64];
         p = wave_sum(p);
-        if (lane == 0) sh.kq = p;
+        if (t == 0) skq = p;
+    }
+    f4v pk = {0.0f, 0.0f, 0.0f, 0.0f}, pq = pk;
+#pragma unroll
+    for (int r = 0; r < 8; r++) {
+        const float kj = sk_[kg + kGroups * r], qj = sq_[kg + kGroups * r];
+        pk += s[r] * kj;
+        pq += s[r] * qj;
+    }
+    spart[0][kg][c4] = pk;
+    spart[1][kg][c4] = pq;
+    __syncthreads();
+    if (t < kDV) {
+        // column t: S^T k and S^T q summed over the key groups in order
+        float sk = 0.0f, sq = 0.0f;
+#pragma unroll
+        for (int gi = 0; gi < kGroups; gi++) {
+            sk += ((const float*)spart[0][gi])[t];
+            sq += ((const float*)spart[1][gi])[t];
+        }
+        const float gg = sred[0], d = sred[1] * (sv_[t] - gg * sk);
+        sdv[t] = d;
+        out[bh * kDV + t] = gg * sq + d * skq;
     }
     __syncthreads();
-    const float o = delta_token(s, sh, col, qq);
-    store_tile(s, S, col, qq);
-    if (qq == 0) out[bh * kDV + col] = o;
+    const float gg = sred[0];
+    const f4v d4 = *(const f4v*)&sdv[4 * c4];
+#pragma unroll
+    for (int r = 0; r < 8; r++) {
+        const float kj = sk_[kg + kGroups * r];
+        s[r] = gg * s[r] + d4 * kj;
+        __builtin_nontemporal_store(s[r], S + (size_t)(kg + kGroups * r) * (kDV / 4));
+    }
 }
 
 // Sum over the 16 lanes of a DPP row; every lane of the row receives the row's total.
