@@ -969,24 +969,34 @@ __device__ __forceinline__ void tiled_body(const Env& e, CPhase& P, CBufs& B, in
     static_assert(12 * 64 * kNW >= 6144, "the widest q4 GEMV: 12 chunks per wave");
     // B operand of lane (j, kq) for chunk i of tile t: row group j / 8, row j % 8, piece 2 (i % 4) + kq / 2
     const int boff = (j >> 3) * 1024 + (kq >> 1) * 128 + (j & 7) * 16 + 8 * (kq & 1);
-    for (int t = 0; t < T; t++) {
-        float acc = 0.0f;
-        for (int i0 = 0; i0 < Cw; i0 += 4) {
-            // four chunks at a time (one block): every load issued before the first MFMA waits
+    // Blocks of four chunks outside, tiles (T <= 4) inside: a block's x digits and exponents are
+    // read once for every tile, and the tiles' loads and MFMAs are independent of each other. Each
+    // tile still adds its blocks in block order, so the sums are those of a tile-by-tile loop.
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int i0 = 0; i0 < Cw; i0 += 4) {
+        i32x4 A[4];
+        float sxf[4], xf[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int i = min(i0 + u, Cw - 1);
+            const uint8_t* ch = xb + 256 * i;
+            // A rows 3..15 are zero (their lanes read row 0 and drop it)
+            const i32x4 a = *(const i32x4*)(ch + (kq * 3 + (j < 3 ? j : 0)) * 16);
+            A[u] = j < 3 ? a : zero;
+            const u32x2 hx = *(const u32x2*)(ch + 192);
+            sxf[u] = (float)(int)hx.x;
+            xf[u] = __uint_as_float(hx.y);
+        }
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            if (t >= T) break;  // wave-uniform
+            // the tile's four chunks of the block: every load issued before the first MFMA waits
             const uint8_t* blk = cur + (t * NB + (i0 >> 2)) * 2048 + boff;
-            i32x4 A[4], Bv[4];
+            i32x4 Bv[4];
             uint32_t pr[4];
-            float sxf[4], xf[4];
 #pragma unroll
             for (int u = 0; u < 4; u++) {
                 const int i = min(i0 + u, Cw - 1);
-                const uint8_t* ch = xb + 256 * i;
-                // A rows 3..15 are zero (their lanes read row 0 and drop it)
-                const i32x4 a = *(const i32x4*)(ch + (kq * 3 + (j < 3 ? j : 0)) * 16);
-                A[u] = j < 3 ? a : zero;
-                const u32x2 hx = *(const u32x2*)(ch + 192);
-                sxf[u] = (float)(int)hx.x;
-                xf[u] = __uint_as_float(hx.y);
                 pr[u] = *(const uint32_t*)(cur + t_pairs(P) + ((t * Cw + i) * 16 + j) * 4);
                 const u32x2 w = *(const u32x2*)(blk + 256 * (i - i0));
                 Bv[u].x = (int)(w.x & 0x0F0F0F0Fu);
@@ -1002,12 +1012,14 @@ __device__ __forceinline__ void tiled_body(const Env& e, CPhase& P, CBufs& B, in
             for (int u = 0; u < 4; u++) {
                 if (i0 + u < Cw) {
                     const float comb = fmaf(65536.0f, (float)D[u].z, fmaf(256.0f, (float)D[u].y, (float)D[u].x));
-                    acc = fmaf(lo_h(pr[u]) * xf[u], comb - hi_h(pr[u]) * sxf[u], acc);
+                    acc[t] = fmaf(lo_h(pr[u]) * xf[u], comb - hi_h(pr[u]) * sxf[u], acc[t]);
                 }
             }
         }
-        if (lane < 16) s_tsum[(e.wave * 4 + t) * 16 + lane] = acc;
     }
+#pragma unroll
+    for (int t = 0; t < 4; t++)
+        if (t < T && lane < 16) s_tsum[(e.wave * 4 + t) * 16 + lane] = acc[t];
     mark(e, 2);
     bar();
     // one thread per output: the waves' partials in wave order, then the epilogue
