@@ -893,14 +893,16 @@ __device__ __forceinline__ void gemv_body(const Env& e, CPhase& P, CBufs& B, int
 // Chunk layout after the conversion (256 bytes, was 64 floats): [k group 0..3][digit 0..2][16 bytes,
 // columns in the order the nibble unpacking gives: 0 2 4 6 1 3 5 7 8 10 12 14 9 11 13 15], then
 // sum X (int) at byte 192 and 2^(e - 22) (float) at 196.
+// Each wave converts only the Cw chunks its own MFMAs read (chunks wave Cw .. + Cw - 1, four per
+// pass: lanes 16 m .. 16 m + 15 take chunk 4 pass + m), so no workgroup barrier follows.
 __device__ __forceinline__ void tiled_digits(const Env& e, CPhase& P) {
     float* xs = e.xs;
-    const int C = P.k >> 6;
+    const int Cw = P.tcw;
     const bool gdn = P.xnorm == XN_GDN;
-    for (int base = 0; base < 16 * C; base += kT) {
-        const int q = base + (int)threadIdx.x;
-        if (q >= 16 * C) break;  // whole waves: 16 C is a multiple of 64 (K a multiple of 256)
-        const int c = q >> 4, i = q & 15;
+    for (int base = 0; base < Cw; base += 4) {
+        const int row = e.lane >> 4;
+        if (base + row >= Cw) break;  // whole DPP rows (16 lanes per chunk)
+        const int c = e.wave * Cw + base + row, i = e.lane & 15;
         // thread i takes the 4 columns whose digits form one word of the A layout: k group kq = i / 4,
         // columns 16 kq + {0, 2, 4, 6}, {1, 3, 5, 7}, {8, 10, 12, 14} or {9, 11, 13, 15} (sub = i % 4)
         const int kq = i >> 2, sub = i & 3, col = 64 * c + 16 * kq + 8 * (sub >> 1) + (sub & 1);
@@ -957,8 +959,7 @@ __device__ __forceinline__ void tiled_body(const Env& e, CPhase& P, CBufs& B, in
     const int lane = lane_here();
     mark(e, 0);
     wait_all();  // this wave's chunks (issued two region phases ago) are in
-    tiled_digits(e, P);
-    bar();
+    tiled_digits(e, P);  // the wave's own chunks: its LDS writes precede its reads in order
     mark(e, 1);
     int o0, n;
     t_outputs(P, e.wg, o0, n);
