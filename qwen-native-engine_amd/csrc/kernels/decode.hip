@@ -53,6 +53,8 @@ constexpr int kNW = kT / kWave;        // 8 waves
 constexpr int kXs = 6144;              // floats of LDS input staging
 constexpr int kHalf = 8 * 1024;        // bytes of one half of a wave's LDS region
 constexpr int kWaveLds = 2 * kHalf;    // a wave's region: the running phase's half and the next one's
+constexpr int kConvSlots = 5;          // EP_CONV outputs per wave and half whose conv state / weights sit in LDS
+constexpr int kExtraBytes = 2304;      // the workgroup's extra GEMV output slot (rows [nm][rb], then [nm][szb])
 constexpr int kPoll = 6;               // tagged pairs a thread polls at once
 constexpr int kSC1 = 16;               // cache policy: agent-scope coherent access
 constexpr int kNT = 2;                 // cache policy: non-temporal (streamed once; keeps L2 for reused data)
@@ -242,6 +244,7 @@ struct GemvGeo {
     int rb, szb, stride, nm, cap;  // row bytes, scale/zero bytes, bytes per row, rows per output, outputs per half
     int per;                       // DMA instructions per output
     int conv;                      // EP_CONV: bytes of conv state + weights per output (16 + 16)
+    int extra;                     // one output past cap in the workgroup's extra slot (P.extra)
 };
 __device__ __forceinline__ GemvGeo geo(CPhase& P) {
     GemvGeo g;
@@ -252,18 +255,34 @@ __device__ __forceinline__ GemvGeo geo(CPhase& P) {
     g.conv = P.convb;
     g.cap = P.cap;
     g.per = P.dper;
+    g.extra = P.extra;
     return g;
 }
 
 // DMA of outputs [o0, o0 + cnt) (row pairs for SwiGLU) into region slots starting at `slot`.
 // LDS layout of a GEMV phase in a half: the nibble (or f16) rows [nm][cap][rb], then the q4
-// (scale, zero) rows [nm][cap][szb], then (in-projection with the causal conv) the conv states
-// [cap][16 B] and conv weights [cap][16 B]. Row m of the output in slot s:
+// (scale, zero) rows [nm][cap][szb]. With P.extra, output cap of wave 0 sits in the workgroup's
+// extra slot ([nm][rb], then [nm][szb]). The in-projection's conv states and weights sit in the
+// wave's conv area of the half ([kConvSlots][16 B] states, then [kConvSlots][16 B] weights).
+// Row m of the output in slot s:
 __device__ __forceinline__ int lds_w(const GemvGeo& g, int s, int m) { return (m * g.cap + s) * g.rb; }
 __device__ __forceinline__ int lds_sz(const GemvGeo& g, int s, int m) {
     return g.nm * g.cap * g.rb + (m * g.cap + s) * g.szb;
 }
-__device__ __forceinline__ int lds_conv(const GemvGeo& g) { return g.nm * g.cap * g.stride; }
+__device__ __forceinline__ uint8_t* conv_area(uint8_t* conv, int half, int wave) {
+    return conv + (half * kNW + wave) * (kConvSlots * 32);
+}
+
+// DMA of output o into the workgroup's extra slot.
+__device__ __forceinline__ void dma_extra(CPhase& P, CBufs& B, const GemvGeo& g, int o, uint8_t* __restrict__ ex, int lane) {
+    const uint8_t* w = (const uint8_t*)B.w;
+    const uint8_t* sz = (const uint8_t*)B.sz;
+    for (int m = 0; m < g.nm; m++) {
+        const size_t row = (size_t)o + (size_t)m * P.rows;
+        dma_bytes(w + row * g.rb, g.rb, ex + m * g.rb, lane);
+        if (g.szb) dma_bytes(sz + row * g.szb, g.szb, ex + g.nm * g.rb + m * g.szb, lane);
+    }
+}
 
 // DMA of outputs [o0, o0 + cnt) into slots [slot, slot + cnt). Consecutive outputs are consecutive
 // rows of each of the nm matrices, so each block is one contiguous transfer.
@@ -482,6 +501,8 @@ struct Env {
     float* red;
     int* bail;
     unsigned long long* tt;  // profiling: the running phase's sub-step timestamps (thread 0's, in LDS)
+    uint8_t* conv;   // EP_CONV conv state and weights: [half][wave][16 B state x kConvSlots, 16 B weights x kConvSlots]
+    uint8_t* extra;  // the workgroup's extra GEMV output slot (wave 0 of a phase with P.extra)
 };
 
 __device__ __forceinline__ uint32_t tag_of(const DecodeArgs& a, int step, int p) {
@@ -573,7 +594,7 @@ __device__ __forceinline__ int t_pairs(CPhase& P) { return P.ttiles * t_blocks(P
 // GEMV: the wave's first outputs (rows, then their scale/zero pairs; for the GDN in-projection the
 // conv state and conv weights of those rows after them). GDN: the wave's 512-byte state column.
 // Attention: the K/V rows of the wave's positions, through the block table.
-__device__ __forceinline__ void prefetch(const Env& e, CPhase& P, CBufs& B, int step, uint8_t* __restrict__ nxt) {
+__device__ __forceinline__ void prefetch(const Env& e, CPhase& P, CBufs& B, int step, uint8_t* __restrict__ nxt, int half) {
     const DecodeArgs& a = *e.a;
     const int lane = lane_here();
     if (P.kind == PH_GEMV && P.tiled) {
@@ -607,13 +628,15 @@ __device__ __forceinline__ void prefetch(const Env& e, CPhase& P, CBufs& B, int 
         const Rows R = part_p(P, e.gwm);
         const int cnt = min(R.n, g.cap);
         dma_rows(P, B, g, R.r0, cnt, 0, nxt, lane);
-        if (P.epi == EP_CONV && cnt > 0) {
+        const int ex = g.extra && R.n > g.cap ? 1 : 0;  // wave 0 only (rrem <= workgroups)
+        if (ex) dma_extra(P, B, g, R.r0 + g.cap, e.extra, lane);
+        if (P.epi == EP_CONV && cnt + ex > 0) {
             // conv state [ch][4] and weights [ch][4] of the prefetched rows, 16 bytes each
-            uint8_t* cv = nxt + lds_conv(g);
+            uint8_t* cv = conv_area(e.conv, half, e.wave);
             const int row = min(R.r0 + lane, P.conv_ch - 1);
-            if (lane < cnt) {
+            if (lane < cnt + ex) {
                 lds_dma16<false>(B.conv + (size_t)row * 4, cv);
-                lds_dma16<false>((const float*)B.aux + (size_t)row * 4, cv + 16 * g.cap);
+                lds_dma16<false>((const float*)B.aux + (size_t)row * 4, cv + 16 * kConvSlots);
             }
         }
     } else if (P.kind == PH_GDNF) {
@@ -778,7 +801,7 @@ __device__ __forceinline__ void head_phase(const Env& e, CPhase& P, CBufs& B, Wa
 // every step of x, the step's slice is read from LDS once and applied to the whole group, then the
 // group is reduced together. The caller then sends the data of the region phase two ahead into `cur`.
 __device__ __forceinline__ void gemv_body(const Env& e, CPhase& P, CBufs& B, int step, int p, WaveState& ws, float inv,
-                                          uint8_t* cur, const float* xs) {
+                                          uint8_t* cur, const float* xs, int half) {
     const DecodeArgs& a = *e.a;
     const int lane = e.lane;
     mark(e, 0);
@@ -790,10 +813,12 @@ __device__ __forceinline__ void gemv_body(const Env& e, CPhase& P, CBufs& B, int
         uint64_t* out = B.out ? B.out + (size_t)(step & 1) * P.out_stride : nullptr;
         const Step t = make_step(P);
         const int gmax = 8 / g.nm;  // outputs per group
-        const int pre = min(R.n, g.cap);  // outputs prefetched
-        const bool stream = R.n > g.cap;
+        const int ex = g.extra && R.n > g.cap ? 1 : 0;  // output cap in the workgroup's extra slot
+        const int pre = min(R.n, g.cap + ex);  // outputs prefetched
+        const bool stream = R.n > pre;
         const int go = stream ? max(1, min(gmax, g.cap / 2)) : min(gmax, R.n);
-        const uint8_t* cvs = cur + lds_conv(g);  // EP_CONV: conv state / weights of the prefetched rows
+        const uint8_t* cvs = conv_area(e.conv, half, e.wave);  // EP_CONV: conv state / weights of the prefetched rows
+        const int xoff = (int)(e.extra - cur);  // the extra slot relative to this half
         int issued = pre;
         XC X;
         if (t.nsteps == 1) load_step(xs, t, 0, X, lane);
@@ -810,8 +835,13 @@ __device__ __forceinline__ void gemv_body(const Env& e, CPhase& P, CBufs& B, int
             for (int r = 0; r < 8; r++) {
                 int slot = o0 + (r >> ns);
                 if (stream) slot = slot < g.cap ? slot : slot % g.cap;
-                roff[r] = lds_w(g, slot, r & ns);
-                soff[r] = lds_sz(g, slot, r & ns);
+                if (ex && slot == g.cap) {
+                    roff[r] = xoff + (r & ns) * g.rb;
+                    soff[r] = xoff + g.nm * g.rb + (r & ns) * g.szb;
+                } else {
+                    roff[r] = lds_w(g, slot, r & ns);
+                    soff[r] = lds_sz(g, slot, r & ns);
+                }
             }
 #pragma unroll
             for (int r = 1; r < 8; r++) {
@@ -860,7 +890,7 @@ __device__ __forceinline__ void gemv_body(const Env& e, CPhase& P, CBufs& B, int
                     float4 st, cw;
                     if (k < pre) {
                         st = *(const float4*)(cvs + 16 * k);
-                        cw = *(const float4*)(cvs + 16 * g.cap + 16 * k);
+                        cw = *(const float4*)(cvs + 16 * kConvSlots + 16 * k);
                     } else {
                         st = *(const float4*)(B.conv + (size_t)o * 4);
                         cw = *(const float4*)((const float*)B.aux + (size_t)o * 4);
@@ -1569,6 +1599,8 @@ __device__ __forceinline__ void decode_program(const DecodeArgs& a) {
     __shared__ uint32_t redi[kNW];
     __shared__ float rope[2 * 64];  // cos, sin of the step's RoPE angles
     __shared__ int bail;
+    __shared__ __attribute__((aligned(16))) uint8_t s_conv[2 * kNW * kConvSlots * 32];
+    __shared__ __attribute__((aligned(16))) uint8_t s_extra[kExtraBytes];
     Env e;
     e.a = &a;
     e.wg = blockIdx.x;
@@ -1583,6 +1615,8 @@ __device__ __forceinline__ void decode_program(const DecodeArgs& a) {
     e.regs = regs;
     e.red = red;
     e.bail = &bail;
+    e.conv = s_conv;
+    e.extra = s_extra;
     // profiling: thread 0's sub-step timestamps of the running phase (LDS, so that no register
     // holds them for the whole launch)
     __shared__ unsigned long long tts[8];
@@ -1615,8 +1649,8 @@ __device__ __forceinline__ void decode_program(const DecodeArgs& a) {
     uint32_t n_out = a.out_ids && e.wg == 0 && threadIdx.x == 0 ? a.tok[2] : 0u;
     int half = 0;  // half of the next region phase (region phases alternate between the halves)
     // the window's first two region phases (each region phase sends the one two ahead)
-    prefetch(e, shapes[prog[a.reg0].shape], prog[a.reg0], 0, region(0));
-    prefetch(e, shapes[prog[a.reg1].shape], prog[a.reg1], 0, region(1));
+    prefetch(e, shapes[prog[a.reg0].shape], prog[a.reg0], 0, region(0), 0);
+    prefetch(e, shapes[prog[a.reg1].shape], prog[a.reg1], 0, region(1), 1);
     for (int step = 0; step < a.n_steps; step++) {
         const uint32_t pos = a.pos0 + (uint32_t)step;
         const bool head = head_at(a, step);
@@ -1680,7 +1714,7 @@ __device__ __forceinline__ void decode_program(const DecodeArgs& a) {
                     } else if (P.tiled) {
                         tiled_body(e, P, B, step, p, inv, region(rh));
                     } else {
-                        gemv_body(e, P, B, step, p, ws, inv, region(rh), xs);
+                        gemv_body(e, P, B, step, p, ws, inv, region(rh), xs, rh);
                     }
                     break;
                 }
@@ -1714,7 +1748,7 @@ __device__ __forceinline__ void decode_program(const DecodeArgs& a) {
                 // this phase's LDS reads are done: send the data of the region phase two ahead
                 // into its half (the next region phase's data is in the other half)
                 int ns = 0, np = 0;
-                if (region_after(a, P, step, p, 2, ns, np)) prefetch(e, shapes[prog[np].shape], prog[np], ns, region(rh));
+                if (region_after(a, P, step, p, 2, ns, np)) prefetch(e, shapes[prog[np].shape], prog[np], ns, region(rh), rh);
                 mark(e, 7);
                 half ^= 1;
             }
@@ -1810,8 +1844,13 @@ void finalize_phase(Phase& P, int grid) {
         P.szb = P.mkind ? (P.k / P.group) * 4 : 0;
         P.stride = P.rb + P.szb;
         P.nm = P.epi == EP_SWIGLU ? 2 : 1;
-        P.convb = P.epi == EP_CONV ? 32 : 0;
-        P.cap = kHalf / (P.stride * P.nm + P.convb);
+        P.convb = P.epi == EP_CONV ? 32 : 0;  // in the wave's conv area, outside the half
+        P.cap = kHalf / (P.stride * P.nm);
+        if (P.epi == EP_CONV) P.cap = std::min(P.cap, kConvSlots);
+        // one output past cap on wave 0 only: the workgroup's extra slot (the program pass that
+        // keeps consecutive region phases from both using it may clear this)
+        P.extra = P.kind == PH_GEMV && !P.tiled && !P.fast_head && !P.is_head && P.rrem > 0 && P.rper == P.cap &&
+                  P.rrem <= grid && P.stride * P.nm <= kExtraBytes && (P.epi != EP_CONV || P.cap + 1 <= kConvSlots);
         P.dper = P.nm * ((P.rb + 1023) / 1024 + (P.szb + 1023) / 1024);
         int gs = 0;
         while (P.mkind && (1 << gs) < P.group) gs++;

@@ -61,6 +61,8 @@ struct Phase {
     int rper = 0, rrem = 0;  // GEMV outputs per wave: rows / waves and rows % waves
     int rb = 0, szb = 0, stride = 0, nm = 1;  // GEMV row bytes, scale/zero bytes, their sum, rows per output
     int cap = 0, dper = 0, convb = 0;  // outputs per LDS half, DMA instructions per output, conv bytes per output
+    int extra = 0;  // 1: a wave's one output past cap sits in the workgroup's extra slot (only wave 0
+                    // has one: rrem <= workgroups); no two consecutive region phases use the slot
     int gshift = 6;     // log2(group)
     int n4 = 0, n2 = 0, n1 = 0, nsteps = 0;  // x steps: 2048/1024/512-column slabs (q4) or 512 (f16)
     int splits = 0;     // attention: context splits per kv head

@@ -639,6 +639,25 @@ void Model::setup_engine() {
     if (tiled)
         for (Phase& P : prog) P.tiled = gemv_tileable(P, grid) ? 1 : 0;
     for (Phase& P : prog) finalize_phase(P, grid);
+    {
+        // the workgroup's extra GEMV slot is single, and a phase's data is sent two region phases
+        // ahead: no two consecutive region phases (cyclically over steps; the LM head never uses
+        // it, so skipping it changes nothing) may both use it
+        std::vector<int> rp;
+        for (int i = 0; i < (int)prog.size(); i++)
+            if (prog[i].region && !prog[i].is_head) rp.push_back(i);
+        for (bool changed = true; changed;) {
+            changed = false;
+            for (size_t j = 0; j < rp.size(); j++) {
+                Phase& cur = prog[rp[j]];
+                const Phase& prev = prog[rp[(j + rp.size() - 1) % rp.size()]];
+                if (cur.extra && prev.extra) {
+                    cur.extra = 0;
+                    changed = true;
+                }
+            }
+        }
+    }
     DecodeArgs links;
     if (!finalize_program(prog.data(), (int)prog.size(), links)) throw unsupported("too few region phases per step");
     nph_ = (int)prog.size();
