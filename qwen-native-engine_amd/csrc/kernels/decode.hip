@@ -269,9 +269,7 @@ __device__ __forceinline__ int lds_w(const GemvGeo& g, int s, int m) { return (m
 __device__ __forceinline__ int lds_sz(const GemvGeo& g, int s, int m) {
     return g.nm * g.cap * g.rb + (m * g.cap + s) * g.szb;
 }
-__device__ __forceinline__ uint8_t* conv_area(uint8_t* conv, int half, int wave) {
-    return conv + (half * kNW + wave) * (kConvSlots * 32);
-}
+
 
 // DMA of output o into the workgroup's extra slot.
 __device__ __forceinline__ void dma_extra(CPhase& P, CBufs& B, const GemvGeo& g, int o, uint8_t* __restrict__ ex, int lane) {
@@ -501,8 +499,6 @@ struct Env {
     float* red;
     int* bail;
     unsigned long long* tt;  // profiling: the running phase's sub-step timestamps (thread 0's, in LDS)
-    uint8_t* conv;   // EP_CONV conv state and weights: [half][wave][16 B state x kConvSlots, 16 B weights x kConvSlots]
-    uint8_t* extra;  // the workgroup's extra GEMV output slot (wave 0 of a phase with P.extra)
 };
 
 __device__ __forceinline__ uint32_t tag_of(const DecodeArgs& a, int step, int p) {
@@ -574,6 +570,12 @@ typedef int i32x4 __attribute__((ext_vector_type(4)));
 // tiled GEMV [kNW][4 tiles][16 rows]: fixed LDS addresses, no register holds them
 __shared__ float s_hres[kTiledMaxRes];
 __shared__ float s_tsum[kNW * 4 * 16];
+// EP_CONV conv state and weights: [half][wave][16 B state x kConvSlots, 16 B weights x kConvSlots];
+// and the workgroup's extra GEMV output slot (wave 0 of a phase with P.extra). At file scope their
+// LDS addresses are constants, so no register holds them.
+__shared__ __attribute__((aligned(16))) uint8_t s_conv[2 * kNW * kConvSlots * 32];
+__shared__ __attribute__((aligned(16))) uint8_t s_extra[kExtraBytes];
+__device__ __forceinline__ uint8_t* conv_area(int half, int wave) { return s_conv + (half * kNW + wave) * (kConvSlots * 32); }
 __device__ __forceinline__ void t_outputs(CPhase& P, int g, int& o0, int& n) {
     o0 = g * P.rper + min(g, P.rrem);
     n = P.rper + (g < P.rrem ? 1 : 0);
@@ -629,10 +631,10 @@ __device__ __forceinline__ void prefetch(const Env& e, CPhase& P, CBufs& B, int 
         const int cnt = min(R.n, g.cap);
         dma_rows(P, B, g, R.r0, cnt, 0, nxt, lane);
         const int ex = g.extra && R.n > g.cap ? 1 : 0;  // wave 0 only (rrem <= workgroups)
-        if (ex) dma_extra(P, B, g, R.r0 + g.cap, e.extra, lane);
+        if (ex) dma_extra(P, B, g, R.r0 + g.cap, s_extra, lane);
         if (P.epi == EP_CONV && cnt + ex > 0) {
             // conv state [ch][4] and weights [ch][4] of the prefetched rows, 16 bytes each
-            uint8_t* cv = conv_area(e.conv, half, e.wave);
+            uint8_t* cv = conv_area(half, e.wave);
             const int row = min(R.r0 + lane, P.conv_ch - 1);
             if (lane < cnt + ex) {
                 lds_dma16<false>(B.conv + (size_t)row * 4, cv);
@@ -817,8 +819,8 @@ __device__ __forceinline__ void gemv_body(const Env& e, CPhase& P, CBufs& B, int
         const int pre = min(R.n, g.cap + ex);  // outputs prefetched
         const bool stream = R.n > pre;
         const int go = stream ? max(1, min(gmax, g.cap / 2)) : min(gmax, R.n);
-        const uint8_t* cvs = conv_area(e.conv, half, e.wave);  // EP_CONV: conv state / weights of the prefetched rows
-        const int xoff = (int)(e.extra - cur);  // the extra slot relative to this half
+        const uint8_t* cvs = conv_area(half, e.wave);  // EP_CONV: conv state / weights of the prefetched rows
+        const int xoff = (int)(s_extra - cur);  // the extra slot relative to this half
         int issued = pre;
         XC X;
         if (t.nsteps == 1) load_step(xs, t, 0, X, lane);
@@ -1599,8 +1601,6 @@ __device__ __forceinline__ void decode_program(const DecodeArgs& a) {
     __shared__ uint32_t redi[kNW];
     __shared__ float rope[2 * 64];  // cos, sin of the step's RoPE angles
     __shared__ int bail;
-    __shared__ __attribute__((aligned(16))) uint8_t s_conv[2 * kNW * kConvSlots * 32];
-    __shared__ __attribute__((aligned(16))) uint8_t s_extra[kExtraBytes];
     Env e;
     e.a = &a;
     e.wg = blockIdx.x;
@@ -1615,8 +1615,6 @@ __device__ __forceinline__ void decode_program(const DecodeArgs& a) {
     e.regs = regs;
     e.red = red;
     e.bail = &bail;
-    e.conv = s_conv;
-    e.extra = s_extra;
     // profiling: thread 0's sub-step timestamps of the running phase (LDS, so that no register
     // holds them for the whole launch)
     __shared__ unsigned long long tts[8];
