@@ -80,6 +80,7 @@ def cpu_baseline(index, buf, cfg, ctx, tokens):
 
 
 TRAFFIC_PROFILE = ROOT / "profiles" / "k_decode_2b_int4_ctx4000_hbm_traffic.md"
+TRAFFIC_PROFILE_08B = ROOT / "profiles" / "k_decode_08b_f16_ctx128_profile.md"
 ATTN_TRAFFIC_PROFILE = ROOT / "profiles" / "paged_attention_b64_hbm_traffic.md"
 
 
@@ -114,14 +115,14 @@ def profile_values(path) -> dict:
     return vals
 
 
-def profiled_traffic(steps: int):
+def profiled_traffic(steps: int, profile=TRAFFIC_PROFILE):
     """HBM bytes of a `steps`-token decode launch from the FETCH_SIZE / WRITE_SIZE counter passes
     recorded in the profile summary (scaled by a plain copy of known size): the profiled launch's
     bytes per token times `steps`. A token moves the same bytes whatever the window length, except
     for the KV cache's growth with the context (under 0.1 % between a 20- and a 96-token window at
     context 4000). None without the profile."""
     try:
-        text = TRAFFIC_PROFILE.read_text()
+        text = profile.read_text()
     except OSError:
         return None
     vals = {}
@@ -129,6 +130,8 @@ def profiled_traffic(steps: int):
         if line.startswith("traffic_") and ":" in line:
             k, v = line.split(":", 1)
             vals[k.strip()] = float(v)
+    if "traffic_bytes_per_token" in vals:
+        return vals["traffic_bytes_per_token"] * steps
     if vals.get("traffic_steps_per_launch", 0) <= 0 or "traffic_bytes_per_launch" not in vals:
         return None
     return vals["traffic_bytes_per_launch"] / vals["traffic_steps_per_launch"] * steps
@@ -804,7 +807,13 @@ def main():
     bytes_tok = algorithmic_bytes_per_token(cfg, mats, ctx_timed + (args.steps - 1) / 2)
     # one k_decode launch covers the whole timed window: bytes per launch / launch duration
     achieved = bytes_tok["total"] * args.steps / (dev_ms / 1e3) / 1e9
-    traffic = profiled_traffic(args.steps) if args.ctx == 4000 and args.config == "2b" else None
+    if args.config == "2b" and args.ctx == 4000:
+        traffic_profile = TRAFFIC_PROFILE
+    elif args.config == "0.8b" and args.ctx == 128:
+        traffic_profile = TRAFFIC_PROFILE_08B
+    else:
+        traffic_profile = None
+    traffic = profiled_traffic(args.steps, traffic_profile) if traffic_profile else None
     result = {
         "metric": ("decode tok/s @ batch 1, 0.8B f16, 128-id prompt" if small else
                    "decode tok/s @ batch 1, ctx 4096 (2B int4) + % of HBM roofline"),
@@ -827,7 +836,7 @@ def main():
                    "batch": 1, "window": args.steps},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": traffic,
-                     "traffic_source": TRAFFIC_PROFILE.name if traffic else None,
+                     "traffic_source": traffic_profile.name if traffic else None,
                      "kernel": f"k_decode, one launch per {args.steps}-token window"
                                if args.engine == "persistent" else
                                f"decode step ({m.dispatches_per_token()} kernels per token)",
