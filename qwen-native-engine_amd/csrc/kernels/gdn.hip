@@ -299,34 +299,57 @@ __global__ __launch_bounds__(256) void k_delta_rule_cols(const float* __restrict
     for (int j = 0; j < 8; j++) S[j * jstride] = s[j];
 }
 
-// Prefill of a chunk of T tokens of one sequence, before the recurrence. Grid (T, H), 384 threads
-// (the head's q, k, v channels). Token n's projection row is proj + n * proj_stride. Causal conv
-// + SiLU (shaders.rs:457-468) with the inputs of tokens n-3..n-1 taken from the chunk or, before
-// it, from conv_state (read only; k_gdn_chunk_post shifts it); L2 norms of q (times 128^-1/2) and
-// k; g = exp(A_neg_exp ln(1 + e^(a + dt_bias))), beta = sigmoid(b) (:489-496). Outputs in the
-// layouts of k_delta_rule_cols: q, k [T][H][dk], v [T][H][dv], g, beta [T][H].
+// Tokens per workgroup of the chunk prep / post kernels: the conv window slides along them, so a
+// channel's inputs are loaded once each (plus three), and their loads are all in flight at once.
+constexpr int kChunkTok = 8;
+
+// Prefill of a chunk of T tokens of one sequence, before the recurrence. Grid (ceil(T / 8), H),
+// 384 threads (the head's q, k, v channels), tokens 8 blockIdx.x .. + 7. Token n's projection row
+// is proj + n * proj_stride. Causal conv + SiLU (shaders.rs:457-468) with the inputs of tokens
+// n-3..n-1 taken from the chunk or, before it, from conv_state (read only; k_gdn_chunk_post shifts
+// it); L2 norms of q (times 128^-1/2) and k; g = exp(A_neg_exp ln(1 + e^(a + dt_bias))),
+// beta = sigmoid(b) (:489-496). Outputs in the layouts of k_delta_rule_cols: q, k [T][H][dk],
+// v [T][H][dv], g, beta [T][H]. Each token's arithmetic is that of one token per workgroup.
 __global__ __launch_bounds__(384) void k_gdn_chunk_prep(const float* __restrict__ proj, int proj_stride,
                                                         const float* __restrict__ conv_state,
                                                         const float* __restrict__ conv_w, const float* __restrict__ prm,
-                                                        int H, float* __restrict__ qo, float* __restrict__ ko,
+                                                        int H, int T, float* __restrict__ qo, float* __restrict__ ko,
                                                         float* __restrict__ vo, float* __restrict__ go,
                                                         float* __restrict__ bo) {
-    __shared__ float red[8];
-    const int n = blockIdx.x, h = blockIdx.y, t = threadIdx.x, lane = t % kWave, w = t / kWave;
+    __shared__ float red[kChunkTok][8];
+    const int n0 = blockIdx.x * kChunkTok, h = blockIdx.y, t = threadIdx.x, lane = t % kWave, w = t / kWave;
     const int ch = t < 128 ? h * kDK + t : (t < 256 ? H * kDK + h * kDK + (t - 128) : 2 * H * kDK + h * kDV + (t - 256));
     const float* st = conv_state + (size_t)ch * 4;
     const float* cw = conv_w + (size_t)ch * 4;
-    auto input = [&](int m) { return m >= 0 ? proj[(size_t)m * proj_stride + ch] : st[3 + m]; };
-    const float y = input(n - 3) * cw[0] + input(n - 2) * cw[1] + input(n - 1) * cw[2] + input(n) * cw[3];
-    const float val = silu(y);
-    const float ss = wave_sum(val * val);
-    if (lane == 0) red[w] = ss;
+    // inputs of tokens n0 - 3 .. n0 + 7 (before the chunk: the conv state; past T: unused)
+    float in[kChunkTok + 3];
+#pragma unroll
+    for (int j = 0; j < kChunkTok + 3; j++) {
+        const int m = n0 - 3 + j;
+        in[j] = m < 0 ? st[3 + m] : (m < T ? proj[(size_t)m * proj_stride + ch] : 0.0f);
+    }
+    const float w0 = cw[0], w1 = cw[1], w2 = cw[2], w3 = cw[3];
+    float val[kChunkTok];
+#pragma unroll
+    for (int i = 0; i < kChunkTok; i++) {
+        const float y = in[i] * w0 + in[i + 1] * w1 + in[i + 2] * w2 + in[i + 3] * w3;
+        val[i] = silu(y);
+        const float ss = wave_sum(val[i] * val[i]);
+        if (lane == 0) red[i][w] = ss;
+    }
     __syncthreads();
-    const size_t nh = (size_t)n * H + h;
-    if (t < 128) qo[nh * kDK + t] = val * (1.0f / sqrtf(red[0] + red[1] + 1e-6f)) * 0.08838834764831845f;
-    else if (t < 256) ko[nh * kDK + t - 128] = val * (1.0f / sqrtf(red[2] + red[3] + 1e-6f));
-    else vo[nh * kDV + t - 256] = val;
-    if (t == 0) {
+#pragma unroll
+    for (int i = 0; i < kChunkTok; i++) {
+        const int n = n0 + i;
+        if (n >= T) break;
+        const size_t nh = (size_t)n * H + h;
+        if (t < 128) qo[nh * kDK + t] = val[i] * (1.0f / sqrtf(red[i][0] + red[i][1] + 1e-6f)) * 0.08838834764831845f;
+        else if (t < 256) ko[nh * kDK + t - 128] = val[i] * (1.0f / sqrtf(red[i][2] + red[i][3] + 1e-6f));
+        else vo[nh * kDV + t - 256] = val[i];
+    }
+    if (t < kChunkTok && n0 + t < T) {
+        const int n = n0 + t;
+        const size_t nh = (size_t)n * H + h;
         const float* row = proj + (size_t)n * proj_stride;
         const int zoff = 2 * H * kDK + 2 * H * kDV;  // a[H] then b[H] follow z
         const float a = row[zoff + h], b = row[zoff + H + h];
@@ -335,26 +358,40 @@ __global__ __launch_bounds__(384) void k_gdn_chunk_prep(const float* __restrict_
     }
 }
 
-// After the recurrence. Grid (T, H), 384 threads. Gated RMSNorm of token n's head output
-// (shaders.rs:514-516) into mixed + n * mixed_stride; the workgroups of the last token also shift
-// the conv state by the chunk (the inputs of the chunk's last three tokens).
+// After the recurrence. Grid (ceil(T / 8), H), 384 threads, tokens 8 blockIdx.x .. + 7. Gated
+// RMSNorm of token n's head output (shaders.rs:514-516) into mixed + n * mixed_stride; the
+// workgroup of the last token also shifts the conv state by the chunk (the inputs of the chunk's
+// last three tokens).
 __global__ __launch_bounds__(384) void k_gdn_chunk_post(const float* __restrict__ proj, int proj_stride,
                                                         float* __restrict__ conv_state, const float* __restrict__ prm,
                                                         int H, int T, const float* __restrict__ o,
                                                         float* __restrict__ mixed, int mixed_stride) {
-    __shared__ float red[8];
-    const int n = blockIdx.x, h = blockIdx.y, t = threadIdx.x, lane = t % kWave, w = t / kWave;
-    const float* row = proj + (size_t)n * proj_stride;
-    const float v = t < kDV ? o[((size_t)n * H + h) * kDV + t] : 0.0f;
-    const float ss = wave_sum(v * v);
-    if (lane == 0) red[w] = ss;
+    __shared__ float red[kChunkTok][8];
+    const int n0 = blockIdx.x * kChunkTok, h = blockIdx.y, t = threadIdx.x, lane = t % kWave, w = t / kWave;
+    float v[kChunkTok], z[kChunkTok];
+#pragma unroll
+    for (int i = 0; i < kChunkTok; i++) {
+        const int n = n0 + i;
+        const bool live = t < kDV && n < T;
+        v[i] = live ? o[((size_t)n * H + h) * kDV + t] : 0.0f;
+        z[i] = live ? proj[(size_t)n * proj_stride + 2 * H * kDK + H * kDV + h * kDV + t] : 0.0f;
+    }
+#pragma unroll
+    for (int i = 0; i < kChunkTok; i++) {
+        const float ss = wave_sum(v[i] * v[i]);
+        if (lane == 0) red[i][w] = ss;
+    }
     __syncthreads();
     if (t < kDV) {
-        const float inv = 1.0f / sqrtf((red[0] + red[1]) / (float)kDV + 1e-6f);
-        const float z = row[2 * H * kDK + H * kDV + h * kDV + t];
-        mixed[(size_t)n * mixed_stride + h * kDV + t] = v * inv * silu(z) * prm[2 * H + t];
+#pragma unroll
+        for (int i = 0; i < kChunkTok; i++) {
+            const int n = n0 + i;
+            if (n >= T) break;
+            const float inv = 1.0f / sqrtf((red[i][0] + red[i][1]) / (float)kDV + 1e-6f);
+            mixed[(size_t)n * mixed_stride + h * kDV + t] = v[i] * inv * silu(z[i]) * prm[2 * H + t];
+        }
     }
-    if (n == T - 1) {
+    if (n0 <= T - 1 && T - 1 < n0 + kChunkTok) {
         const int ch = t < 128 ? h * kDK + t : (t < 256 ? H * kDK + h * kDK + (t - 128) : 2 * H * kDK + h * kDV + (t - 256));
         float* st = conv_state + (size_t)ch * 4;
         float in[3];
@@ -371,8 +408,9 @@ __global__ __launch_bounds__(384) void k_gdn_chunk_post(const float* __restrict_
 void launch_gdn_chunk(const float* proj, int proj_stride, float* conv_state, const float* conv_w, float* state,
                       const float* prm, int heads, int tokens, float* q, float* k, float* v, float* g, float* beta,
                       float* o, float* mixed, int mixed_stride, hipStream_t st, int lead, float* wy_ws) {
-    hipLaunchKernelGGL(k_gdn_chunk_prep, dim3(tokens, heads), dim3(384), 0, st, proj, proj_stride, conv_state, conv_w,
-                       prm, heads, q, k, v, g, beta);
+    const int tb = (tokens + kChunkTok - 1) / kChunkTok;
+    hipLaunchKernelGGL(k_gdn_chunk_prep, dim3(tb, heads), dim3(384), 0, st, proj, proj_stride, conv_state, conv_w,
+                       prm, heads, tokens, q, k, v, g, beta);
     const int waves = heads * (kDV / 4);
     const size_t hk = (size_t)heads * kDK;  // floats of q, k, v, o per token
     // tokens [t0, t0 + n) in order on the state, one wave per 4 value columns
@@ -389,7 +427,7 @@ void launch_gdn_chunk(const float* proj, int proj_stride, float* conv_state, con
         launch_delta_rule_wy(q + head * hk, k + head * hk, v + head * hk, beta + (size_t)head * heads,
                              g + (size_t)head * heads, state, o + head * hk, 1, 64 * blocks, heads, wy_ws, st, 1);
     sequential(head + 64 * blocks, tokens - head - 64 * blocks);
-    hipLaunchKernelGGL(k_gdn_chunk_post, dim3(tokens, heads), dim3(384), 0, st, proj, proj_stride, conv_state, prm,
+    hipLaunchKernelGGL(k_gdn_chunk_post, dim3(tb, heads), dim3(384), 0, st, proj, proj_stride, conv_state, prm,
                        heads, tokens, o, mixed, mixed_stride);
 }
 
