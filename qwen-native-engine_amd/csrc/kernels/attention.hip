@@ -332,7 +332,7 @@ __device__ __forceinline__ uint32_t pack_hi16(uint32_t a, uint32_t b) { return (
 // Causal attention of the rows of a prompt chunk (consecutive tokens of one sequence, row b at
 // position pos[b], cache rows already appended): the same partials as k_attn_partial, computed for
 // a tile of query rows at a time so that every K/V row is read once per tile instead of once per
-// row. Grid (splits, nkv, tiles), 4 waves; a tile is 16 * (4 / G) rows and wave w takes query head
+// row. Grid (tiles, nkv, splits), 4 waves; a tile is 16 * (4 / G) rows and wave w takes query head
 // g * G + w % G of the 16 rows 16 * (w / G)...; split s covers positions [s * split_len,
 // (s + 1) * split_len), cut at the tile's last position.
 // Per step of 32 positions (two 16-position blocks) the workgroup stages the K rows (as stored,
@@ -359,10 +359,10 @@ __global__ __launch_bounds__(kAttnThreads, 2) void k_attn_prefill(const float* _
     constexpr int RT = 4 / G;  // 16-row subtiles per tile
     __shared__ __attribute__((aligned(16))) uint8_t s_k[2][kPfUnit * kPfKStride];
     __shared__ __attribute__((aligned(16))) uint8_t s_v[2][kHD * kPfVStride];
-    const int split = blockIdx.x, g = blockIdx.y, splits = gridDim.x;
+    const int split = blockIdx.z, g = blockIdx.y, splits = gridDim.z;
     const int t = threadIdx.x, lane = t % kWave, w = t / kWave;
     const int gi = w % G, n = lane & 15, kq = lane >> 4;
-    const int row0 = blockIdx.z * 16 * RT;
+    const int row0 = blockIdx.x * 16 * RT;
     const int b = row0 + 16 * (w / G) + n;  // this lane's row (column of the score tile)
     const int rpos = b < rows ? pos[b] : -1;
     const int tpos = lane < 16 * RT && row0 + lane < rows ? pos[row0 + lane] : -1;
@@ -575,7 +575,10 @@ void launch_attention_model(const AttnModelArgs& a, hipStream_t st) {
 template <int G>
 static void launch_prefill(const AttnRowsArgs& a, hipStream_t st) {
     const int tile = 16 * (4 / G);
-    hipLaunchKernelGGL((k_attn_prefill<G>), dim3(a.splits, a.nkv, (a.rows + tile - 1) / tile), dim3(kAttnThreads), 0, st,
+    // Tiles in x: consecutive workgroups go to different XCDs, so each XCD gets every 8th tile and
+    // an even share of the work. (With splits in x each XCD would hold one split, and the early
+    // splits, which every tile needs, would all land on the same few XCDs.)
+    hipLaunchKernelGGL((k_attn_prefill<G>), dim3((a.rows + tile - 1) / tile, a.nkv, a.splits), dim3(kAttnThreads), 0, st,
                        a.qbuf, a.k_pool, a.v_pool, a.block_table, a.max_blocks, a.pos, a.rows, a.nkv, a.split_len,
                        a.part_ml, a.part_acc);
 }
