@@ -262,14 +262,17 @@ __global__ __launch_bounds__(256) void k_wy_prep(const float* __restrict__ q, co
     }
 }
 
-// LDS staging of one chunk in the chain workgroup, in floats: W (all tiles), U (the workgroup's two
-// column groups), P, q in A-fragment order, the decayed K^T, L; then the waves' partial sums
-// ([wave 8][tile 4][lane 64][4]: D, later the rows of Q S).
-constexpr int kSW = 0, kSU = 8192, kSP = 10240, kSQ = 14336, kSK = 22528, kSL = 30720, kSX = 30784;
-constexpr int kSFloats = kSX + 8 * 1024;
+// LDS staging of one chunk in a chain workgroup of CGW column groups, in floats: W (all tiles), U
+// (the workgroup's column groups), P, q in A-fragment order, the decayed K^T, L; then the waves'
+// partial sums ([wave][tile 4][lane 64][4]: D, later the rows of Q S).
+template <int CGW>
+struct ChainLds {
+    static constexpr int kSW = 0, kSU = 8192, kSP = kSU + CGW * 1024, kSQ = kSP + 4096, kSK = kSQ + 8192,
+                         kSL = kSK + 8192, kSX = kSL + 64, kFloats = kSX + 4 * CGW * 1024;
+};
 
-// The chain over chunks: workgroup = (sequence, head, value columns 32 quarter .. 32 quarter + 31),
-// 8 waves = 2 column groups of 16 (cgl = wave / 4) x 4 key quarters (kq = wave % 4, key tiles
+// The chain over chunks: workgroup = (sequence, head, CGW column groups of 16 value columns),
+// 4 CGW waves = CGW column groups (cgl = wave / 4) x 4 key quarters (kq = wave % 4, key tiles
 // 2 kq, 2 kq + 1, the wave's 32 keys of the state slice in 8 VGPRs). Per chunk:
 //  - D = U - W S: each key quarter contracts its 32 keys, the four partials meet in LDS and every
 //    wave of the column group adds them in quarter order (so all four hold the same D);
@@ -278,47 +281,56 @@ constexpr int kSFloats = kSX + 8 * 1024;
 //    position tiles 0..kq of D), and stores them;
 //  - S = gamma_63 S + Kf D on the wave's own key tiles.
 // A chain's MFMA work is split four ways (about 100-112 MFMAs per wave and chunk instead of 424),
-// and a (sequence, head) runs as four workgroups, all on one XCD (workgroups are dealt to XCDs
-// round robin), which share its chunk operands in that XCD's L2.
-__global__ __launch_bounds__(512) void k_wy_chain(const float* __restrict__ q, const float* __restrict__ ws,
-                                                  float* __restrict__ state, float* __restrict__ out, int T, int H,
-                                                  int BH, int value_major) {
-    __shared__ __attribute__((aligned(16))) float sm[kSFloats];
+// and a (sequence, head) runs as 8 / CGW workgroups, all on one XCD (workgroups are dealt to XCDs
+// round robin), which share its chunk operands in that XCD's L2. CGW = 1 puts one wave on each
+// SIMD of a CU and twice as many CUs to work (for few sequences); CGW = 2 halves the workgroups
+// (for grids that already fill the chip). Both add the same partials in the same order.
+template <int CGW>
+__global__ __launch_bounds__(256 * CGW) void k_wy_chain(const float* __restrict__ q, const float* __restrict__ ws,
+                                                        float* __restrict__ state, float* __restrict__ out, int T,
+                                                        int H, int BH, int value_major) {
+    using Lds = ChainLds<CGW>;
+    constexpr int kSW = Lds::kSW, kSU = Lds::kSU, kSP = Lds::kSP, kSQ = Lds::kSQ, kSK = Lds::kSK, kSL = Lds::kSL,
+                  kSX = Lds::kSX;
+    constexpr int NW = 4 * CGW, PER = 8 / CGW;  // waves; workgroups per (sequence, head)
+    // vector-memory instructions per wave: W + U + L, P + q, K copies; the output stores
+    constexpr int kNWul = 32 / NW + 2, kNQp = 48 / NW, kNK = 32 / NW, kNSt = 4;
+    __shared__ __attribute__((aligned(16))) float sm[Lds::kFloats];
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, lr = lane & 15, lg = lane >> 4;
     const int cgl = wv >> 2, kq = wv & 3;
     const int id = blockIdx.x, xcd = id & 7, slot = id >> 3;
-    const int bh = (slot >> 2) * 8 + xcd, quarter = slot & 3, cg = 2 * quarter + cgl;
+    const int bh = (slot / PER) * 8 + xcd, part = slot % PER, cg = CGW * part + cgl;
     if (bh >= BH) return;  // the whole workgroup
     const int b = bh / H, h = bh % H, NC = (T + kC - 1) / kC;
     const int col = 16 * cg + lr;
 
-    // Copies of chunk c's operands; the 8 waves copy an eighth of every buffer each (1 KiB blocks).
-    // Per wave: W, U, L = 6 instructions, P, q = 6, K = 4.
+    // Copies of chunk c's operands; the NW waves copy 1 / NW of every buffer each (1 KiB blocks).
     auto issue_wul = [&](int c) {
         const float* wc = ws + ((size_t)bh * NC + c) * kWyFloats;
 #pragma unroll
-        for (int u = 0; u < 4; u++) {
-            const int blk = wv + 8 * u;
+        for (int u = 0; u < 32 / NW; u++) {
+            const int blk = wv + NW * u;
             dma16(wc + kWfOff + blk * 256 + lane * 4, sm + kSW + blk * 256);
         }
         {  // U block (column group wv / 4, position tile wv % 4)
             const int ucg = wv >> 2, upt = wv & 3;
-            dma16(wc + kUfOff + ((upt * 8 + 2 * quarter + ucg) * 64 + lane) * 4, sm + kSU + (ucg * 4 + upt) * 256);
+            dma16(wc + kUfOff + ((upt * 8 + CGW * part + ucg) * 64 + lane) * 4, sm + kSU + (ucg * 4 + upt) * 256);
         }
-        if (lane < 8) dma4(wc + kLfOff + 8 * wv + lane, sm + kSL + 8 * wv);
+        constexpr int kL = 64 / NW;  // L values per wave
+        if (lane < kL) dma4(wc + kLfOff + kL * wv + lane, sm + kSL + kL * wv);
     };
     auto issue_qp = [&](int c) {
         const float* wc = ws + ((size_t)bh * NC + c) * kWyFloats;
         const int t0 = c * kC, n = min(kC, T - t0);
 #pragma unroll
-        for (int u = 0; u < 2; u++) {
-            const int blk = wv + 8 * u;
+        for (int u = 0; u < 16 / NW; u++) {
+            const int blk = wv + NW * u;
             dma16(wc + kPfOff + blk * 256 + lane * 4, sm + kSP + blk * 256);
         }
         // q block (pt, kt): lane i <- q[16pt + i%16][16kt + 4(i/16) .. +3]; padding rows repeat a real row
 #pragma unroll
-        for (int u = 0; u < 4; u++) {
-            const int blk = wv + 8 * u, pt = blk >> 3, kt = blk & 7;
+        for (int u = 0; u < 32 / NW; u++) {
+            const int blk = wv + NW * u, pt = blk >> 3, kt = blk & 7;
             const int p = min(16 * pt + lr, n - 1);
             dma16(q + (((size_t)b * T + t0 + p) * H + h) * kD + 16 * kt + 4 * lg, sm + kSQ + blk * 256);
         }
@@ -326,8 +338,8 @@ __global__ __launch_bounds__(512) void k_wy_chain(const float* __restrict__ q, c
     auto issue_k = [&](int c) {
         const float* wc = ws + ((size_t)bh * NC + c) * kWyFloats;
 #pragma unroll
-        for (int u = 0; u < 4; u++) {
-            const int blk = wv + 8 * u;
+        for (int u = 0; u < 32 / NW; u++) {
+            const int blk = wv + NW * u;
             dma16(wc + kKfOff + blk * 256 + lane * 4, sm + kSK + blk * 256);
         }
     };
@@ -353,8 +365,8 @@ __global__ __launch_bounds__(512) void k_wy_chain(const float* __restrict__ q, c
         const int t0 = c * kC, n = min(kC, T - t0);
         const size_t row0 = ((size_t)b * T + t0) * H + h;
 
-        // after W, U, L of c: the stores of chunk c - 1 (issued before the q, P copies), q, P (6), K (4)
-        wait_vm<10>();
+        // after W, U, L of c: the stores of chunk c - 1 (issued before the q, P copies), q, P, K
+        wait_vm<kNQp + kNK>();
         __syncthreads();
         f4 D[4];
 #pragma unroll
@@ -389,9 +401,9 @@ __global__ __launch_bounds__(512) void k_wy_chain(const float* __restrict__ q, c
             D[pt] = d;
         }
 
-        // after q, P of c: K of c (4), W, U, L of c + 1 (6)
-        if (more) wait_vm<10>();
-        else wait_vm<4>();
+        // after q, P of c: K of c, W, U, L of c + 1
+        if (more) wait_vm<kNK + kNWul>();
+        else wait_vm<kNK>();
         __syncthreads();  // also: every wave has read the D partials
         f4 O[4];
 #pragma unroll
@@ -432,9 +444,9 @@ __global__ __launch_bounds__(512) void k_wy_chain(const float* __restrict__ q, c
         __syncthreads();  // q, P and the partial rows are no longer read
         if (more) issue_qp(c + 1);
 
-        // after K of c: W, U, L of c + 1 (6), this chunk's 4 stores, q, P of c + 1 (6); on the last
-        // chunk everything
-        if (more) wait_vm<16>();
+        // after K of c: W, U, L of c + 1, this chunk's stores, q, P of c + 1; on the last chunk
+        // everything
+        if (more) wait_vm<kNWul + kNSt + kNQp>();
         else wait_vm<0>();
         __syncthreads();
 #pragma unroll
@@ -469,8 +481,13 @@ void launch_delta_rule_wy(const float* q, const float* k, const float* v, const 
                           int value_major) {
     const int NC = (tokens + kC - 1) / kC, BH = batch * heads;
     hipLaunchKernelGGL(k_wy_prep, dim3(NC, heads, batch), dim3(256), 0, st, q, k, v, beta, g, ws, tokens, heads);
-    hipLaunchKernelGGL(k_wy_chain, dim3(32 * ((BH + 7) / 8)), dim3(512), 0, st, q, ws, state, out, tokens, heads, BH,
-                       value_major);
+    // one column group per workgroup while that leaves a CU per workgroup (256 CUs), else two
+    if (BH <= 32)
+        hipLaunchKernelGGL((k_wy_chain<1>), dim3(64 * ((BH + 7) / 8)), dim3(256), 0, st, q, ws, state, out, tokens,
+                           heads, BH, value_major);
+    else
+        hipLaunchKernelGGL((k_wy_chain<2>), dim3(32 * ((BH + 7) / 8)), dim3(512), 0, st, q, ws, state, out, tokens,
+                           heads, BH, value_major);
 }
 
 }  // namespace qne
