@@ -359,13 +359,15 @@ __global__ __launch_bounds__(384) void k_gdn_chunk_prep(const float* __restrict_
 }
 
 // After the recurrence. Grid (ceil(T / 8), H), 384 threads, tokens 8 blockIdx.x .. + 7. Gated
-// RMSNorm of token n's head output (shaders.rs:514-516) into mixed + n * mixed_stride; the
+// RMSNorm of token n's head output (shaders.rs:514-516) into mixed + n * mixed_stride (when set)
+// and, with frag_out, staged as the out-projection's GEMM operand (column order order_out); the
 // workgroup of the last token also shifts the conv state by the chunk (the inputs of the chunk's
 // last three tokens).
 __global__ __launch_bounds__(384) void k_gdn_chunk_post(const float* __restrict__ proj, int proj_stride,
                                                         float* __restrict__ conv_state, const float* __restrict__ prm,
                                                         int H, int T, const float* __restrict__ o,
-                                                        float* __restrict__ mixed, int mixed_stride) {
+                                                        float* __restrict__ mixed, int mixed_stride,
+                                                        uint8_t* __restrict__ frag_out, int order_out) {
     __shared__ float red[kChunkTok][8];
     const int n0 = blockIdx.x * kChunkTok, h = blockIdx.y, t = threadIdx.x, lane = t % kWave, w = t / kWave;
     float v[kChunkTok], z[kChunkTok];
@@ -388,7 +390,10 @@ __global__ __launch_bounds__(384) void k_gdn_chunk_post(const float* __restrict_
             const int n = n0 + i;
             if (n >= T) break;
             const float inv = 1.0f / sqrtf((red[i][0] + red[i][1]) / (float)kDV + 1e-6f);
-            mixed[(size_t)n * mixed_stride + h * kDV + t] = v[i] * inv * silu(z[i]) * prm[2 * H + t];
+            const float y = v[i] * inv * silu(z[i]) * prm[2 * H + t];
+            if (mixed) mixed[(size_t)n * mixed_stride + h * kDV + t] = y;
+            if (frag_out)  // waves 0 and 1: the two 64-column chunks of head h in row n
+                emit_x(frag_out, (size_t)(H * kDV / kChunk) * kChunkBytes, n, h * kDV + t, y, 1.0f, order_out, lane);
         }
     }
     if (n0 <= T - 1 && T - 1 < n0 + kChunkTok) {
@@ -407,7 +412,8 @@ __global__ __launch_bounds__(384) void k_gdn_chunk_post(const float* __restrict_
 
 void launch_gdn_chunk(const float* proj, int proj_stride, float* conv_state, const float* conv_w, float* state,
                       const float* prm, int heads, int tokens, float* q, float* k, float* v, float* g, float* beta,
-                      float* o, float* mixed, int mixed_stride, hipStream_t st, int lead, float* wy_ws) {
+                      float* o, float* mixed, int mixed_stride, hipStream_t st, int lead, float* wy_ws,
+                      uint8_t* frag_out, int order_out) {
     const int tb = (tokens + kChunkTok - 1) / kChunkTok;
     hipLaunchKernelGGL(k_gdn_chunk_prep, dim3(tb, heads), dim3(384), 0, st, proj, proj_stride, conv_state, conv_w,
                        prm, heads, tokens, q, k, v, g, beta);
@@ -428,7 +434,7 @@ void launch_gdn_chunk(const float* proj, int proj_stride, float* conv_state, con
                              g + (size_t)head * heads, state, o + head * hk, 1, 64 * blocks, heads, wy_ws, st, 1);
     sequential(head + 64 * blocks, tokens - head - 64 * blocks);
     hipLaunchKernelGGL(k_gdn_chunk_post, dim3(tb, heads), dim3(384), 0, st, proj, proj_stride, conv_state, prm,
-                       heads, tokens, o, mixed, mixed_stride);
+                       heads, tokens, o, mixed, mixed_stride, frag_out, order_out);
 }
 
 void launch_gdn_decode(const float* proj, float* conv_state, const float* conv_w, float* state, float* out,

@@ -128,7 +128,8 @@ struct GdnRowStrides {
     size_t proj = 0, conv = 0, state = 0, out = 0;
 };
 // Prefill of `tokens` consecutive tokens of one sequence: conv + norms + gates, the recurrence on
-// the model's value-major state, the gated RMSNorm into mixed + n * mixed_stride, the conv state
+// the model's value-major state, the gated RMSNorm into mixed + n * mixed_stride (when set) and,
+// with frag_out, into the out-projection's GEMM operand (column order order_out), the conv state
 // shifted by the chunk. q, k, v, o: tokens * heads * 128 floats of scratch; g, beta: tokens * heads.
 // With wy_ws (wy_workspace_bytes(1, tokens, heads)), the recurrence runs in the chunk-64 WY form
 // over every complete block of 64 tokens that starts `lead` tokens in or 64 k after that, and
@@ -136,7 +137,8 @@ struct GdnRowStrides {
 // multiple of 64 positions, the blocks are fixed by absolute position.
 void launch_gdn_chunk(const float* proj, int proj_stride, float* conv_state, const float* conv_w, float* state,
                       const float* prm, int heads, int tokens, float* q, float* k, float* v, float* g, float* beta,
-                      float* o, float* mixed, int mixed_stride, hipStream_t st, int lead = 0, float* wy_ws = nullptr);
+                      float* o, float* mixed, int mixed_stride, hipStream_t st, int lead = 0, float* wy_ws = nullptr,
+                      uint8_t* frag_out = nullptr, int order_out = 0);
 // Where the batched GDN step reads its projection and writes its output. With `part`, the
 // projection is the in-projection's split partials (splits x split_stride floats, rows n apart)
 // summed here in split order times the row's 1 / rms (from the sums of x^2 of its operand x_in,

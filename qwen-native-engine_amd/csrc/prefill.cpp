@@ -28,7 +28,6 @@ ChunkPrefill::ChunkPrefill(Model& m) : m_(m), st_(m.stream_) {
     try {
         const size_t T = pass_;
         proj_w_ = std::max(c.attn_proj(), c.gdn_proj());
-        mixed_w_ = std::max(c.attn_out(), c.gdn_out());
         // Attention partials over fixed position ranges (kPrefillSplitLen positions each, cut at the
         // row's own position), so that a token's result does not depend on how the prompt was
         // chunked; head groupings the query-tile kernel does not take use per-row partials over
@@ -44,7 +43,6 @@ ChunkPrefill::ChunkPrefill(Model& m) : m_(m), st_(m.stream_) {
         pos_ = (int32_t*)dalloc(T * 4);
         h_ = (float*)dalloc(T * c.hidden * 4);
         proj_ = (float*)dalloc(T * proj_w_ * 4);
-        mixed_ = (float*)dalloc(T * mixed_w_ * 4);
         qbuf_ = (float*)dalloc(T * c.n_q_heads * c.head_dim * 4);
         part_ = (float*)dalloc(part * 4);
         const size_t G = (size_t)(c.n_q_heads / c.n_kv_heads);
@@ -60,8 +58,13 @@ ChunkPrefill::ChunkPrefill(Model& m) : m_(m), st_(m.stream_) {
         wy_ws_ = (float*)dalloc(wy_workspace_bytes(1, (int)T, c.gdn_heads));
         frag_a_ = (uint8_t*)dalloc(frag);
         frag_b_ = (uint8_t*)dalloc(frag);
+        frag_c_ = (uint8_t*)dalloc(frag);
         QNE_HIP(hipMemset(frag_a_, 0, frag));
         QNE_HIP(hipMemset(frag_b_, 0, frag));
+        // Only the attention combine and the GDN output write frag_c_ (rows < the pass's tokens), so
+        // the rows of a last row tile past them hold zeros or earlier rows' staged values, always
+        // finite; the out-projection's rows are independent and those rows are never stored.
+        QNE_HIP(hipMemset(frag_c_, 0, frag));
         QNE_HIP(hipHostMalloc((void**)&host_pos_, T * 4, hipHostMallocDefault));
     } catch (...) {
         release();
@@ -113,7 +116,9 @@ void ChunkPrefill::enqueue_chunk(int n, int lead) {
             a.qbuf = qbuf_;
             a.part_ml = attn_ml_;
             a.part_acc = attn_acc_;
-            a.out = mixed_;
+            a.out = nullptr;  // the combine stages the out-projection's operand itself
+            a.frag_out = frag_c_;
+            a.order_out = operand_order(L.out);
             a.nq = c.n_q_heads;
             a.nkv = c.n_kv_heads;
             a.rope_dim = c.rope_dim;
@@ -124,10 +129,9 @@ void ChunkPrefill::enqueue_chunk(int n, int lead) {
             launch_attention_rows(a, st_);
         } else {
             launch_gdn_chunk(proj_, proj_w_, L.conv_state, L.conv_w, L.rec, L.gdn_params, c.gdn_heads, n, gq_, gk_, gv_,
-                             gg_, gb_, go_, mixed_, L.out.k, st_, lead, wy_ws_);
+                             gg_, gb_, go_, nullptr, L.out.k, st_, lead, wy_ws_, frag_c_, operand_order(L.out));
         }
-        launch_stage_x(mixed_, L.out.k, n, L.out.k, nullptr, operand_order(L.out), frag_b_, st_);
-        gemm(L.out, frag_b_, 0, h_, c.hidden, EPI_ACCUMULATE, frag_a_, L.post_norm, operand_order(L.gate_up));
+        gemm(L.out, frag_c_, 0, h_, c.hidden, EPI_ACCUMULATE, frag_a_, L.post_norm, operand_order(L.gate_up));
         gemm(L.gate_up, frag_a_, 1, nullptr, 0, EPI_SWIGLU, frag_b_, nullptr, operand_order(L.down));
         // the last layer's h is read by the LM head of the model (one token), not by a GEMM
         const float* next_gain = last ? nullptr : m_.layers_[li + 1].input_norm;

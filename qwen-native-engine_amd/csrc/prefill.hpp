@@ -62,15 +62,17 @@ class ChunkPrefill {
     std::map<int, std::list<std::pair<int, hipGraphExec_t>>::iterator> graphs_;
     static constexpr int kPrefillSplitLen = 512;  // positions per attention split of the query-tile kernel
     int pass_ = 0, row_tiles_ = 0;  // tokens per pass, its 64-row tiles
-    int proj_w_ = 0, mixed_w_ = 0, splits_ = 1, split_len_ = 0;
+    int proj_w_ = 0, splits_ = 1, split_len_ = 0;
     uint32_t* ids_ = nullptr;  // the chunk's token ids
     int32_t* pos_ = nullptr;   // the chunk's positions
     int32_t* host_pos_ = nullptr;  // pinned
-    float *h_ = nullptr, *proj_ = nullptr, *mixed_ = nullptr, *qbuf_ = nullptr, *part_ = nullptr;
+    float *h_ = nullptr, *proj_ = nullptr, *qbuf_ = nullptr, *part_ = nullptr;
     float *attn_ml_ = nullptr, *attn_acc_ = nullptr;
     float *gq_ = nullptr, *gk_ = nullptr, *gv_ = nullptr, *go_ = nullptr, *gg_ = nullptr, *gb_ = nullptr;
     float* wy_ws_ = nullptr;  // the WY form's per-chunk operands
-    uint8_t *frag_a_ = nullptr, *frag_b_ = nullptr;
+    // GEMM operands: the in-projection and gate_up input (a), the down input (b), the
+    // out-projection input, staged by the attention combine and the GDN output (c)
+    uint8_t *frag_a_ = nullptr, *frag_b_ = nullptr, *frag_c_ = nullptr;
 };
 
 }  // namespace qne
