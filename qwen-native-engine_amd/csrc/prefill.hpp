@@ -60,7 +60,7 @@ class ChunkPrefill {
     // instantiated pass graphs by graph_key, most recently used first (at most kGraphCap)
     std::list<std::pair<int, hipGraphExec_t>> lru_;
     std::map<int, std::list<std::pair<int, hipGraphExec_t>>::iterator> graphs_;
-    static constexpr int kPrefillSplitLen = 512;  // positions per attention split of the query-tile kernel
+    static constexpr int kPrefillSplitLen = 1024;  // positions per attention split of the query-tile kernel
     int pass_ = 0, row_tiles_ = 0;  // tokens per pass, its 64-row tiles
     int proj_w_ = 0, splits_ = 1, split_len_ = 0;
     uint32_t* ids_ = nullptr;  // the chunk's token ids
