@@ -458,12 +458,16 @@ __global__ __launch_bounds__(kAttnThreads, 2) void k_attn_prefill(const float* _
         for (int hb = 0; hb < 2; hb++) {
             f32x4 sh = {0.f, 0.f, 0.f, 0.f}, sl = sh;
             const uint8_t* kb = s_k[buf] + (16 * hb + n) * kPfKStride + 16 * kq;
+            h8v a[8];  // all eight K fragments in flight before the first MFMA needs one
+#pragma unroll
+            for (int i = 0; i < 8; i++) a[i] = *(const h8v*)(kb + 64 * i);
 #pragma unroll
             for (int i = 0; i < 8; i++) {
-                const h8v a = *(const h8v*)(kb + 64 * i);
-                sh = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qh[i], sh, 0, 0, 0);
-                sl = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, ql[i], sl, 0, 0, 0);
+                sh = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i], qh[i], sh, 0, 0, 0);
+                sl = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i], ql[i], sl, 0, 0, 0);
             }
+            __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);  // the 8 LDS reads first,
+            __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);  // then the 16 MFMAs
 #pragma unroll
             for (int r = 0; r < 4; r++) {
                 const int pp = base + 16 * hb + 4 * kq + r;
@@ -498,10 +502,17 @@ __global__ __launch_bounds__(kAttnThreads, 2) void k_attn_prefill(const float* _
         }
         const uint8_t* vb = s_v[buf] + n * kPfVStride + 16 * kq;
 #pragma unroll
-        for (int d = 0; d < 16; d++) {
-            const h8v a = *(const h8v*)(vb + 16 * d * kPfVStride);
-            o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, ph, o[d], 0, 0, 0);
-            o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, pl, o[d], 0, 0, 0);
+        for (int d0 = 0; d0 < 16; d0 += 8) {
+            h8v a[8];  // eight V fragments in flight at a time
+#pragma unroll
+            for (int d = 0; d < 8; d++) a[d] = *(const h8v*)(vb + 16 * (d0 + d) * kPfVStride);
+#pragma unroll
+            for (int d = 0; d < 8; d++) {
+                o[d0 + d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[d], ph, o[d0 + d], 0, 0, 0);
+                o[d0 + d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[d], pl, o[d0 + d], 0, 0, 0);
+            }
+            __builtin_amdgcn_sched_group_barrier(0x100, 8, 1);
+            __builtin_amdgcn_sched_group_barrier(0x008, 16, 1);
         }
     }
     if (b >= rows || rpos < p0) return;  // no partial for a row that attends nothing here
