@@ -39,6 +39,7 @@ void rows_gemm(const DevMat& W, int n, float eps, uint8_t* frag, int norm, float
     a.kind = W.kind;
     a.W = W.w;
     a.SZ = W.sz;
+    a.SZT = W.szt;
     a.N = W.rows;
     a.K = W.k;
     a.group = W.group;

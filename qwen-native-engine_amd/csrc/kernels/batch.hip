@@ -155,7 +155,11 @@ __global__ __launch_bounds__(64 * (WAVES + DW)) void k_gemm(const GemmArgs a) {
             uint8_t* dst = base + kChunkLds + wt * kWBytes;
             if (KIND == KIND_Q4) {
                 dma16((const uint8_t*)a.W + (size_t)nr * (K / 2) + c * 32 + 16 * hf, dst);
-                if (lane < 32) dma4(a.SZ + (size_t)nr * ngroups + c / cpg, dst + 1024);
+                // the tile's 32 words of the chunk's group: one line from the tile-major copy
+                if (lane < 32)
+                    dma4(a.SZT ? a.SZT + ((size_t)(nr >> 5) * ngroups + c / cpg) * 32 + (nr & 31)
+                               : a.SZ + (size_t)nr * ngroups + c / cpg,
+                         dst + 1024);
             } else {
 #pragma unroll
                 for (int s = 0; s < 4; s++) dma16((const uint16_t*)a.W + (size_t)nr * K + c * kChunk + 32 * hf + 8 * s, dst + 1024 * s);

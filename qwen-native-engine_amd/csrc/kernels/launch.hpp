@@ -178,6 +178,7 @@ struct GemmArgs {
     int kind = KIND_Q4;
     const void* W = nullptr;
     const uint32_t* SZ = nullptr;
+    const uint32_t* SZT = nullptr;  // q4: SZ tile-major ([row / 32][group][row % 32]); null: read SZ
     int N = 0, K = 0, group = 64;
     int splits = 1;
     int cps = 0;     // set by launch_gemm: chunks per split

@@ -213,7 +213,7 @@ void Model::upload(const ModelIndex& ix, const uint8_t* weights) {
         seen[key] = d;
         return d;
     };
-    std::map<std::pair<uint64_t, uint64_t>, uint32_t*> seen_sz;
+    std::map<std::pair<uint64_t, uint64_t>, std::pair<uint32_t*, uint32_t*>> seen_sz;
     auto mat = [&](const std::string& name) -> DevMat {
         const MatInfo& m = ix.mat(name);
         DevMat d;
@@ -226,7 +226,8 @@ void Model::upload(const ModelIndex& ix, const uint8_t* weights) {
             auto key = std::make_pair(m.s.offset, m.z.offset);
             auto it = seen_sz.find(key);
             if (it != seen_sz.end()) {
-                d.sz = it->second;
+                d.sz = it->second.first;
+                d.szt = it->second.second;
             } else {
                 const size_t groups_per_row = (size_t)m.k / m.group, n = (size_t)m.rows * groups_per_row;
                 std::vector<uint32_t> sz(n);
@@ -248,8 +249,16 @@ void Model::upload(const ModelIndex& ix, const uint8_t* weights) {
                 }
                 uint32_t* dsz = (uint32_t*)dalloc(n * 4);
                 QNE_HIP(hipMemcpy(dsz, sz.data(), n * 4, hipMemcpyHostToDevice));
-                seen_sz[key] = dsz;
+                const size_t tiles = ((size_t)m.rows + 31) / 32, nt = tiles * groups_per_row * 32;
+                std::vector<uint32_t> szt(nt, 0u);
+                for (size_t r = 0; r < (size_t)m.rows; r++)
+                    for (size_t g = 0; g < groups_per_row; g++)
+                        szt[((r / 32) * groups_per_row + g) * 32 + r % 32] = sz[r * groups_per_row + g];
+                uint32_t* dszt = (uint32_t*)dalloc(nt * 4);
+                QNE_HIP(hipMemcpy(dszt, szt.data(), nt * 4, hipMemcpyHostToDevice));
+                seen_sz[key] = {dsz, dszt};
                 d.sz = dsz;
+                d.szt = dszt;
             }
         }
         return d;

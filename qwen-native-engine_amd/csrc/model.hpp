@@ -15,7 +15,10 @@ struct DevMat {
     int kind = 0;  // 0 f16, 1 q4
     int rows = 0, k = 0, group = 64;
     const void* w = nullptr;
-    const uint32_t* sz = nullptr;  // q4: (scale, zero) f16 pairs per group
+    const uint32_t* sz = nullptr;  // q4: (scale, zero) f16 pairs per group, [row][group]
+    // q4: the same words tile-major, [row / 32][group][row % 32] (rows padded to 32 with zeros), so
+    // that the row-tiled GEMM reads a tile's 32 words of a group from one 128-byte line
+    const uint32_t* szt = nullptr;
 };
 
 struct DevLayer {
