@@ -34,7 +34,6 @@ namespace {
 
 using namespace lds_dma;
 
-constexpr int kChunkLds = kSsOff;  // the part of a chunk the GEMM copies to LDS
 
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
@@ -112,16 +111,21 @@ __device__ __forceinline__ void wait_vm_upto(int n) {
 template <int KIND, int WAVES, int D, int DW, int CF>
 __global__ __launch_bounds__(64 * (WAVES + DW)) void k_gemm(const GemmArgs a) {
     constexpr int TW = WAVES * CF;                                  // 32-row W tiles per workgroup
-    constexpr int kWBytes = KIND == KIND_Q4 ? 1024 + 128 : 4096;  // one W tile's chunk (q4: + scale/zero words)
-    constexpr int kSlot = kChunkLds + TW * kWBytes;
+    // A ring slot: the x chunk's fragments (hi, lo), every W tile's chunk (1 KiB q4 or 4 KiB f16),
+    // then (q4) 256 bytes per tile: its 32 scale/zero words and, for tiles 0 and 1, the x chunk's
+    // row sums of rows 0..31 and 32..63. A tile's words and those sums come in one 64-lane DMA: an
+    // LDS DMA costs its issuing wave about the same however little it moves (one fewer per wave
+    // and chunk: -15 % GEMM time), so the chunk's transfers are as few instructions as the data
+    // allows. The f16 GEMM needs no row sums.
+    constexpr int kWTile = KIND == KIND_Q4 ? 1024 : 4096;           // one W tile's chunk
+    constexpr int kSzOff = 2 * kFragBytes + TW * kWTile;            // q4: per tile 128 B of words + 128 B
+    constexpr int kSlot = kSzOff + (KIND == KIND_Q4 ? TW * 256 : 0);
     constexpr int kSenders = DW > 0 ? DW : WAVES;                   // waves that issue the DMA
     constexpr int kXPart = 2 * kFragBytes / kSenders;               // x bytes each sender copies
     constexpr int kTilesPer = TW / kSenders;                        // W tiles each sender sends
     constexpr int kWDmas = KIND == KIND_Q4 ? 2 : 4;                 // DMAs of one W tile chunk
-    static_assert(kXPart % 1024 == 0 && TW % kSenders == 0, "the senders split x and W evenly");
-    constexpr int kSumLanes = kBM * 4 / 16 / kSenders;              // lanes copying the chunk sums (16 B each)
-    static_assert(kSumLanes >= 1, "every sender copies a part of the chunk sums");
-    constexpr int kPer = kXPart / 1024 + 1 + kTilesPer * kWDmas;    // DMAs per sender per chunk
+    static_assert(kXPart % 1024 == 0 && TW % kSenders == 0 && TW >= 2, "the senders split x and W evenly");
+    constexpr int kPer = kXPart / 1024 + kTilesPer * kWDmas;        // DMAs per sender per chunk
     __shared__ __attribute__((aligned(16))) uint8_t ring[D][kSlot];
     const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const bool computes = w < WAVES;
@@ -146,20 +150,20 @@ __global__ __launch_bounds__(64 * (WAVES + DW)) void k_gemm(const GemmArgs a) {
         const uint8_t* src = xfrag + (size_t)(c0 + j) * kChunkBytes;
 #pragma unroll
         for (int u = 0; u < kXPart / 1024; u++) dma16(src + kXPart * sender + 1024 * u + 16 * lane, base + kXPart * sender + 1024 * u);
-        if (lane < kSumLanes) dma16(src + kXsumOff + 16 * (kSumLanes * sender + lane), base + kXsumOff + 16 * kSumLanes * sender);
         const int c = c0 + j;
 #pragma unroll
         for (int i = 0; i < kTilesPer; i++) {
             const int wt = sender * kTilesPer + i;  // W tile sent
             const int nr = min(wrow(wt), a.N - 1);  // rows past N: row N - 1, not stored
-            uint8_t* dst = base + kChunkLds + wt * kWBytes;
+            uint8_t* dst = base + 2 * kFragBytes + wt * kWTile;
             if (KIND == KIND_Q4) {
                 dma16((const uint8_t*)a.W + (size_t)nr * (K / 2) + c * 32 + 16 * hf, dst);
-                // the tile's 32 words of the chunk's group: one line from the tile-major copy
-                if (lane < 32)
-                    dma4(a.SZT ? a.SZT + ((size_t)(nr >> 5) * ngroups + c / cpg) * 32 + (nr & 31)
-                               : a.SZ + (size_t)nr * ngroups + c / cpg,
-                         dst + 1024);
+                // lanes 0..31: the tile's 32 words of the chunk's group (one line from the
+                // tile-major copy); lanes 32..63 of tiles 0 and 1: x chunk row sums 32 wt + l32
+                const void* sp = lane >= 32 ? (const void*)(src + kXsumOff + 4 * (32 * wt + l32))
+                                 : a.SZT ? (const void*)(a.SZT + ((size_t)(nr >> 5) * ngroups + c / cpg) * 32 + (nr & 31))
+                                         : (const void*)(a.SZ + (size_t)nr * ngroups + c / cpg);
+                if (lane < 32 || wt < 2) dma4(sp, base + kSzOff + wt * 256);
             } else {
 #pragma unroll
                 for (int s = 0; s < 4; s++) dma16((const uint16_t*)a.W + (size_t)nr * K + c * kChunk + 32 * hf + 8 * s, dst + 1024 * s);
@@ -184,11 +188,12 @@ __global__ __launch_bounds__(64 * (WAVES + DW)) void k_gemm(const GemmArgs a) {
         if (sender >= 0 && j + D - 1 < nch) issue(j + D - 1, next_slot);
         if (computes) {
             const uint8_t* xs = ring[slot];
-            const uint8_t* ws = ring[slot] + kChunkLds + w * CF * kWBytes;
+            const uint8_t* ws = ring[slot] + 2 * kFragBytes + w * CF * kWTile;
+            const uint8_t* wsz = ring[slot] + kSzOff + w * CF * 256;
             uint4 wq[CF];
             if (KIND == KIND_Q4)
 #pragma unroll
-                for (int cf = 0; cf < CF; cf++) wq[cf] = *(const uint4*)(ws + cf * kWBytes + 16 * lane);
+                for (int cf = 0; cf < CF; cf++) wq[cf] = *(const uint4*)(ws + cf * kWTile + 16 * lane);
 #pragma unroll
             for (int s = 0; s < 4; s++) {
                 const half8_t a0h = *(const half8_t*)(xs + frag_offset(s, 0, lane));
@@ -199,7 +204,7 @@ __global__ __launch_bounds__(64 * (WAVES + DW)) void k_gemm(const GemmArgs a) {
                 for (int cf = 0; cf < CF; cf++) {
                     half8_t b;
                     if (KIND == KIND_Q4) b = nibbles8(s == 0 ? wq[cf].x : s == 1 ? wq[cf].y : s == 2 ? wq[cf].z : wq[cf].w);
-                    else b = *(const half8_t*)(ws + cf * kWBytes + 1024 * s + 16 * lane);
+                    else b = *(const half8_t*)(ws + cf * kWTile + 1024 * s + 16 * lane);
                     if (KIND == KIND_Q4 && s == 0) {  // a fresh tile per chunk: C = 0
                         const float16_t zero = {};
                         grp[cf][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0h, b, zero, 0, 0, 0);
@@ -214,15 +219,17 @@ __global__ __launch_bounds__(64 * (WAVES + DW)) void k_gemm(const GemmArgs a) {
             }
             if (KIND == KIND_Q4) {
                 // y += s (sum q x) - s z (sum x) over the chunk (scale and zero of the chunk's group)
-                const float* xsum = (const float*)(xs + kXsumOff);
+                // the row sums: rows 0..31 beside tile 0's words, rows 32..63 beside tile 1's
+                const float* xsum0 = (const float*)(xs + kSzOff + 128);
+                const float* xsum1 = (const float*)(xs + kSzOff + 256 + 128);
 #pragma unroll
                 for (int cf = 0; cf < CF; cf++) {
-                    const uint32_t szw = *(const uint32_t*)(ws + cf * kWBytes + 1024 + 4 * l32);
+                    const uint32_t szw = *(const uint32_t*)(wsz + cf * 256 + 4 * l32);
                     const float sc = lo_h(szw), sz = sc * hi_h(szw);
 #pragma unroll
                     for (int q = 0; q < 4; q++) {
-                        const float4 s0 = *(const float4*)(xsum + 8 * q + 4 * hf);
-                        const float4 s1 = *(const float4*)(xsum + 32 + 8 * q + 4 * hf);
+                        const float4 s0 = *(const float4*)(xsum0 + 8 * q + 4 * hf);
+                        const float4 s1 = *(const float4*)(xsum1 + 8 * q + 4 * hf);
                         const float v0[4] = {s0.x, s0.y, s0.z, s0.w}, v1[4] = {s1.x, s1.y, s1.z, s1.w};
 #pragma unroll
                         for (int e = 0; e < 4; e++) {
