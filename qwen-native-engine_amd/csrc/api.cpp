@@ -383,10 +383,17 @@ int qne_gemm(int kind, const void* w, const void* sz, int rows, int k, int group
         a.y_stride = y_stride;
         a.n_out = n_out;
         const size_t part = (size_t)a.splits * ((m + 63) / 64 * 64) * rows;
-        float* ws = workspace(kWsGemm, part * 4 + qne::gemm_frag_bytes(k, m));
+        const size_t frag = (qne::gemm_frag_bytes(k, m) + 255) / 256 * 256;
+        const size_t szt = kind == QNE_MAT_Q4 ? qne::tile_sz_words(rows, k / a.group) : 0;
+        float* ws = workspace(kWsGemm, part * 4 + frag + szt * 4);
         a.part = ws;
         a.frag = (uint8_t*)(ws + part);
         hipStream_t st = (hipStream_t)stream;
+        if (szt) {  // the GEMM reads the words tile-major
+            uint32_t* d = (uint32_t*)(a.frag + frag);
+            qne::launch_tile_sz((const uint32_t*)sz, rows, k / a.group, d, st);
+            a.SZT = d;
+        }
         qne::launch_gemm(a, st);
         check_launch();
         if (!stream) qne::hip_check(hipStreamSynchronize(st), "gemm");

@@ -23,6 +23,7 @@
 //    the epilogue (store, residual add, SwiGLU).
 #include <algorithm>
 
+#include "../error.hpp"
 #include "common.hpp"
 #include "launch.hpp"
 #include "lds_dma.hpp"
@@ -112,20 +113,24 @@ template <int KIND, int WAVES, int D, int DW, int CF>
 __global__ __launch_bounds__(64 * (WAVES + DW)) void k_gemm(const GemmArgs a) {
     constexpr int TW = WAVES * CF;                                  // 32-row W tiles per workgroup
     // A ring slot: the x chunk's fragments (hi, lo), every W tile's chunk (1 KiB q4 or 4 KiB f16),
-    // then (q4) 256 bytes per tile: its 32 scale/zero words and, for tiles 0 and 1, the x chunk's
-    // row sums of rows 0..31 and 32..63. A tile's words and those sums come in one 64-lane DMA: an
-    // LDS DMA costs its issuing wave about the same however little it moves (one fewer per wave
-    // and chunk: -15 % GEMM time), so the chunk's transfers are as few instructions as the data
-    // allows. The f16 GEMM needs no row sums.
+    // then (q4) the x chunk's 64 row sums (256 B) and every tile's 32 scale/zero words (128 B
+    // each). A sender copies its tiles' words with one 16-byte-per-lane DMA from the tile-major
+    // copy (8 lanes a tile), the first sender the row sums in the same DMA (16 lanes in front):
+    // every workgroup of a row tile reads those two lines at about the same time, and 4-byte
+    // lanes would make 4x the requests to them (measured: -9 % GEMM time). An LDS DMA costs its
+    // issuing wave about the same however little it moves, so this adds none. The f16 GEMM needs
+    // no row sums.
     constexpr int kWTile = KIND == KIND_Q4 ? 1024 : 4096;           // one W tile's chunk
-    constexpr int kSzOff = 2 * kFragBytes + TW * kWTile;            // q4: per tile 128 B of words + 128 B
-    constexpr int kSlot = kSzOff + (KIND == KIND_Q4 ? TW * 256 : 0);
+    constexpr int kSzOff = 2 * kFragBytes + TW * kWTile;            // q4: row sums, then words
+    constexpr int kSlot = kSzOff + (KIND == KIND_Q4 ? 256 + TW * 128 : 0);
     constexpr int kSenders = DW > 0 ? DW : WAVES;                   // waves that issue the DMA
     constexpr int kXPart = 2 * kFragBytes / kSenders;               // x bytes each sender copies
     constexpr int kTilesPer = TW / kSenders;                        // W tiles each sender sends
-    constexpr int kWDmas = KIND == KIND_Q4 ? 2 : 4;                 // DMAs of one W tile chunk
-    static_assert(kXPart % 1024 == 0 && TW % kSenders == 0 && TW >= 2, "the senders split x and W evenly");
-    constexpr int kPer = kXPart / 1024 + kTilesPer * kWDmas;        // DMAs per sender per chunk
+    constexpr int kWDmas = KIND == KIND_Q4 ? 1 : 4;                 // DMAs of one W tile chunk
+    static_assert(kXPart % 1024 == 0 && TW % kSenders == 0, "the senders split x and W evenly");
+    static_assert(16 + 8 * kTilesPer <= 64, "the first sender's words DMA holds the row sums and its tiles");
+    // DMAs per sender per chunk: its x part, its W tiles, (q4) its tiles' words (+ row sums)
+    constexpr int kPer = kXPart / 1024 + kTilesPer * kWDmas + (KIND == KIND_Q4 ? 1 : 0);
     __shared__ __attribute__((aligned(16))) uint8_t ring[D][kSlot];
     const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const bool computes = w < WAVES;
@@ -138,12 +143,13 @@ __global__ __launch_bounds__(64 * (WAVES + DW)) void k_gemm(const GemmArgs a) {
     const int nch = max(0, c1 - c0);
     const int mt = blockIdx.z;  // row tile
     const uint8_t* xfrag = a.frag + (size_t)mt * nchunks * kChunkBytes;
-    // W row (= output column) of lane l32 in tile t of this workgroup
-    auto wrow = [&](int t) {
+    // first W row (= output column) of tile t of this workgroup; lane l32 has row + l32
+    auto wrow0 = [&](int t) -> int {
         constexpr int half = TW / 2;
-        if (a.fuse == 1) return t < half ? (blockIdx.x * half + t) * 32 + l32 : a.n_out + (blockIdx.x * half + t - half) * 32 + l32;
-        return (blockIdx.x * TW + t) * 32 + l32;
+        if (a.fuse == 1) return t < half ? (blockIdx.x * half + t) * 32 : a.n_out + (blockIdx.x * half + t - half) * 32;
+        return (blockIdx.x * TW + t) * 32;
     };
+    auto wrow = [&](int t) -> int { return wrow0(t) + l32; };
 
     auto issue = [&](int j, int slot) {  // senders only
         uint8_t* base = ring[slot];
@@ -158,15 +164,20 @@ __global__ __launch_bounds__(64 * (WAVES + DW)) void k_gemm(const GemmArgs a) {
             uint8_t* dst = base + 2 * kFragBytes + wt * kWTile;
             if (KIND == KIND_Q4) {
                 dma16((const uint8_t*)a.W + (size_t)nr * (K / 2) + c * 32 + 16 * hf, dst);
-                // lanes 0..31: the tile's 32 words of the chunk's group (one line from the
-                // tile-major copy); lanes 32..63 of tiles 0 and 1: x chunk row sums 32 wt + l32
-                const void* sp = lane >= 32 ? (const void*)(src + kXsumOff + 4 * (32 * wt + l32))
-                                 : a.SZT ? (const void*)(a.SZT + ((size_t)(nr >> 5) * ngroups + c / cpg) * 32 + (nr & 31))
-                                         : (const void*)(a.SZ + (size_t)nr * ngroups + c / cpg);
-                if (lane < 32 || wt < 2) dma4(sp, base + kSzOff + wt * 256);
             } else {
 #pragma unroll
                 for (int s = 0; s < 4; s++) dma16((const uint16_t*)a.W + (size_t)nr * K + c * kChunk + 32 * hf + 8 * s, dst + 1024 * s);
+            }
+        }
+        if (KIND == KIND_Q4) {
+            // lanes [0, lead): row sums (first sender); then 8 lanes (16 B of words) per tile
+            const int lead = sender == 0 ? 16 : 0, li = lane - lead;
+            if (lane < lead + 8 * kTilesPer) {
+                const int t = sender * kTilesPer + (li >> 3);
+                const int tb = min(wrow0(t), a.N - 1) >> 5;  // tiles past N: the last one, not stored
+                const void* sp = lane < lead ? (const void*)(src + kXsumOff + 16 * lane)
+                                             : (const void*)(a.SZT + ((size_t)tb * ngroups + c / cpg) * 32 + 4 * (li & 7));
+                dma16(sp, base + kSzOff + (sender == 0 ? 0 : 256 + 128 * kTilesPer * sender));
             }
         }
     };
@@ -189,7 +200,7 @@ __global__ __launch_bounds__(64 * (WAVES + DW)) void k_gemm(const GemmArgs a) {
         if (computes) {
             const uint8_t* xs = ring[slot];
             const uint8_t* ws = ring[slot] + 2 * kFragBytes + w * CF * kWTile;
-            const uint8_t* wsz = ring[slot] + kSzOff + w * CF * 256;
+            const uint8_t* wsz = ring[slot] + kSzOff + 256 + w * CF * 128;
             uint4 wq[CF];
             if (KIND == KIND_Q4)
 #pragma unroll
@@ -219,12 +230,11 @@ __global__ __launch_bounds__(64 * (WAVES + DW)) void k_gemm(const GemmArgs a) {
             }
             if (KIND == KIND_Q4) {
                 // y += s (sum q x) - s z (sum x) over the chunk (scale and zero of the chunk's group)
-                // the row sums: rows 0..31 beside tile 0's words, rows 32..63 beside tile 1's
-                const float* xsum0 = (const float*)(xs + kSzOff + 128);
-                const float* xsum1 = (const float*)(xs + kSzOff + 256 + 128);
+                const float* xsum0 = (const float*)(xs + kSzOff);  // rows 0..31
+                const float* xsum1 = xsum0 + 32;                     // rows 32..63
 #pragma unroll
                 for (int cf = 0; cf < CF; cf++) {
-                    const uint32_t szw = *(const uint32_t*)(wsz + cf * 256 + 4 * l32);
+                    const uint32_t szw = *(const uint32_t*)(wsz + cf * 128 + 4 * l32);
                     const float sc = lo_h(szw), sz = sc * hi_h(szw);
 #pragma unroll
                     for (int q = 0; q < 4; q++) {
@@ -605,7 +615,25 @@ void launch_stage_x(const float* x, int x_stride, int m, int K, const float* gai
     hipLaunchKernelGGL(k_stage_x, dim3((K + 255) / 256, mpad), dim3(256), 0, st, x, x_stride, m, K, gain, q4order, frag);
 }
 
+// The tile-major copy of a q4 matrix's (scale, zero) words: szt[(t G + g) 32 + r] = sz[(32 t + r) G + g]
+// (zero for rows past the matrix). Grid (ceil(rows / 32) G / 8), 256 threads.
+__global__ __launch_bounds__(256) void k_tile_sz(const uint32_t* __restrict__ sz, int rows, int ngroups,
+                                                 uint32_t* __restrict__ szt) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x, tiles = ((size_t)rows + 31) / 32;
+    if (i >= tiles * ngroups * 32) return;
+    const size_t r = (i / ((size_t)ngroups * 32)) * 32 + i % 32, g = (i / 32) % ngroups;
+    szt[i] = r < (size_t)rows ? sz[r * ngroups + g] : 0u;
+}
+
+size_t tile_sz_words(int rows, int ngroups) { return ((size_t)rows + 31) / 32 * ngroups * 32; }
+
+void launch_tile_sz(const uint32_t* sz, int rows, int ngroups, uint32_t* szt, hipStream_t st) {
+    const size_t n = tile_sz_words(rows, ngroups);
+    hipLaunchKernelGGL(k_tile_sz, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, sz, rows, ngroups, szt);
+}
+
 void launch_gemm(GemmArgs a, hipStream_t st) {
+    if (a.kind == KIND_Q4 && !a.SZT) throw Error(QNE_EINVAL, "q4 GEMM needs the tile-major scale/zero words");
     const int nch = a.K / kChunk;
     a.cps = (nch + a.splits - 1) / a.splits;
     a.mpad = (a.m + kBM - 1) / kBM * kBM;

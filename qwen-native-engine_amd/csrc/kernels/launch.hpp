@@ -178,7 +178,7 @@ struct GemmArgs {
     int kind = KIND_Q4;
     const void* W = nullptr;
     const uint32_t* SZ = nullptr;
-    const uint32_t* SZT = nullptr;  // q4: SZ tile-major ([row / 32][group][row % 32]); null: read SZ
+    const uint32_t* SZT = nullptr;  // q4: SZ tile-major ([row / 32][group][row % 32]), what k_gemm reads
     int N = 0, K = 0, group = 64;
     int splits = 1;
     int cps = 0;     // set by launch_gemm: chunks per split
@@ -226,6 +226,10 @@ size_t gemm_frag_bytes(int K, int m);
 int gemm_splits(int kind, int N, int K, int group, int row_tiles = 1);
 bool gemm_shape_ok(int kind, int N, int K, int group, int m);
 void launch_gemm(GemmArgs a, hipStream_t st);
+// The tile-major copy of q4 (scale, zero) words the row-tiled GEMM reads (GemmArgs::SZT):
+// tile_sz_words(rows, groups) words.
+size_t tile_sz_words(int rows, int ngroups);
+void launch_tile_sz(const uint32_t* sz, int rows, int ngroups, uint32_t* szt, hipStream_t st);
 // The x operand of a GEMM from f32 rows (rows >= m zero), times gain when set.
 void launch_stage_x(const float* x, int x_stride, int m, int K, const float* gain, int q4order, uint8_t* frag,
                     hipStream_t st);
