@@ -59,8 +59,10 @@ __global__ __launch_bounds__(kGdnThreads, 6) void k_gdn_decode(const float* __re
     // The row's projection values this thread reads: channel ch (q, k or v; threads < 384; z of
     // column t - 384 for threads 384..511) and a (thread 0) or b (thread 1). Stored, or the
     // in-projection's split partials summed in split order times the row's 1 / rms from the sums
-    // of x^2 of its operand, as k_gemm_reduce computes them. Those loads are issued before the
-    // state tile's (loads complete in order).
+    // of x^2 of its operand, as k_gemm_reduce computes them. Loads complete in order: the
+    // channel's partials and its conv state and weights are issued before the state tile, so the
+    // conv does not wait for the tile; the gates' partials (threads 0 and 1) after it, as they are
+    // summed only after the conv's barrier.
     const int zoff = 2 * H * kDK + 2 * H * kDV;  // a[H] then b[H] follow z
     const int ch = t < 128 ? h * kDK + t
                            : (t < 256 ? H * kDK + h * kDK + (t - 128)
@@ -70,9 +72,15 @@ __global__ __launch_bounds__(kGdnThreads, 6) void k_gdn_decode(const float* __re
     const float ss_in = io.part && t < nchunks_in ? ((const float*)(io.x_in + (size_t)t * kChunkBytes))[kSsOff / 4 + b] : 0.0f;
     const float* pbase = io.part ? io.part + (size_t)b * io.n : proj;
     const int nsp = io.part ? io.splits : 1;
-    Split8 pc, pg;
+    Split8 pc;
     pc.load(pbase + ch, nsp, io.split_stride);
-    if (t < 2) pg.load(pbase + gch, nsp, io.split_stride);
+    float* st = conv_state + (size_t)(t < 384 ? ch : 0) * 4;
+    const float* cw = conv_w + (size_t)(t < 384 ? ch : 0) * 4;
+    float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f, w0 = 0.0f, w1 = 0.0f, w2 = 0.0f, w3 = 0.0f;
+    if (t < 384) {
+        s0 = st[0]; s1 = st[1]; s2 = st[2];
+        w0 = cw[0]; w1 = cw[1]; w2 = cw[2]; w3 = cw[3];
+    }
     asm volatile("" ::: "memory");  // keeps the loads above ahead of the tile's
     load_tile_t_issue(tv, S);  // in flight while the conv runs
     float inv = 1.0f;
@@ -82,15 +90,11 @@ __global__ __launch_bounds__(kGdnThreads, 6) void k_gdn_decode(const float* __re
         __syncthreads();  // sh.red is reused below
     }
     const float x = pc.sum(pbase + ch, nsp, io.split_stride) * inv;
-    const float gx = t < 2 ? pg.sum(pbase + gch, nsp, io.split_stride) * inv : 0.0f;
     if (t >= 384) sh.z[t - 384] = x;
 
     float val = 0.0f;
     if (t < 384) {
-        float* st = conv_state + (size_t)ch * 4;
-        const float* cw = conv_w + (size_t)ch * 4;
-        const float s0 = st[0], s1 = st[1], s2 = st[2];
-        const float y = s0 * cw[0] + s1 * cw[1] + s2 * cw[2] + x * cw[3];
+        const float y = s0 * w0 + s1 * w1 + s2 * w2 + x * w3;
         st[0] = s1; st[1] = s2; st[2] = x;
         val = silu(y);
     }
@@ -100,8 +104,13 @@ __global__ __launch_bounds__(kGdnThreads, 6) void k_gdn_decode(const float* __re
     if (t < 128) sh.q[t] = val * (1.0f / sqrtf(sh.red[0] + sh.red[1] + 1e-6f)) * 0.08838834764831845f;
     else if (t < 256) sh.k[t - 128] = val * (1.0f / sqrtf(sh.red[2] + sh.red[3] + 1e-6f));
     else if (t < 384) sh.v[t - 256] = val;
-    if (t == 0) sh.g = expf(prm[H + h] * logf(1.0f + expf(gx + prm[h])));
-    if (t == 1) sh.beta = 1.0f / (1.0f + expf(-gx));
+    if (t < 2) {  // the gates: issued after the tile, summed in split order like the channels
+        Split8 pg;
+        pg.load(pbase + gch, nsp, io.split_stride);
+        const float gx = pg.sum(pbase + gch, nsp, io.split_stride) * inv;
+        if (t == 0) sh.g = expf(prm[H + h] * logf(1.0f + expf(gx + prm[h])));
+        else sh.beta = 1.0f / (1.0f + expf(-gx));
+    }
     __syncthreads();
     if (w == 0) {
         float p = sh.k[lane] * sh.q[lane] + sh.k[lane + 64] * sh.q[lane + 64];
