@@ -842,8 +842,13 @@ def main():
                                f"decode step ({m.dispatches_per_token()} kernels per token)",
                      "bytes_per_launch": bytes_tok["total"] * args.steps, "bytes_per_step": bytes_tok["total"],
                      "device_ms_per_launch": round(dev_ms, 3), "device_ms_per_step": round(dev_ms / args.steps, 4)},
-        "detail": {"bytes_per_token": bytes_tok, "weights_gen_s": round(gen_s, 2), "prefill_s": round(prefill_s, 2),
-                   "prefill_tok_s": round((args.ctx - 1) / prefill_s, 1), "adapter": m.adapter},
+        "detail": {"bytes_per_token": bytes_tok, "weights_gen_s": round(gen_s, 2),
+                   "context_fill_s": round(prefill_s, 2),
+                   "context_fill": (f"{args.ctx - 1} ids through Model::prefill, untimed set-up" if args.prefill == "tokens"
+                                    else f"{args.ctx - 1} ids in 512-id prefill_chunk calls, each the first of its "
+                                         "shape (pass graphs instantiated), untimed set-up; the prefill rate is "
+                                         "bench.py --config prefill"),
+                   "adapter": m.adapter},
     }
     if args.engine == "persistent" and args.prefill != "tokens":
         # the token's dependent phases: one profiled token (not timed) from the prompt state, since
