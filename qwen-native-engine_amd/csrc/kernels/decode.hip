@@ -760,7 +760,11 @@ __device__ __forceinline__ void head_rows(const Env& e, CPhase& P, CBufs& B, Wav
     load_x<KIND, K>(xs, nullptr, 0.0f, xr, lane);
     float xsum[KIND == KIND_Q4 ? Q4Plan<K>::NS : 1];
     if constexpr (KIND == KIND_Q4) slab_sums<K>(xr, xsum);
-    constexpr int NB = 2;
+    // Rows per group, two groups in flight per wave: ~48 registers of rows a group (f16 K = 2048:
+    // 3 rows, 24 KiB in flight per wave). With 2 rows a group the head streamed at 0.78 of HBM,
+    // waiting on load latency; 4 rows of K = 2048 spill.
+    constexpr int kRowRegs = (int)(sizeof(RowRaw<KIND, K>) / 4);
+    constexpr int NB = 48 / kRowRegs < 2 ? 2 : (48 / kRowRegs > 8 ? 8 : 48 / kRowRegs);
     RowRaw<KIND, K> cur[NB], nxt[NB];
 #pragma unroll
     for (int k = 0; k < NB; k++) load_row<KIND, K, 64>(cur[k], B.w, (const uint32_t*)B.sz, R.r0 + min(k, R.n - 1), lane);
