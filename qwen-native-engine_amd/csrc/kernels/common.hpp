@@ -97,6 +97,18 @@ __device__ __forceinline__ float wave_sum(float v) {
     for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, kWave);
     return v;
 }
+// The same butterfly as wave_sum (lane xor 32, 16, 8, 4, 2, 1), so the same bits, with permlane
+// swaps, LDS swizzles and DPP: no per-lane shuffle addresses for the compiler to keep live.
+__device__ __forceinline__ float wave_sum_xor(float v) {
+    const int lane = (int)__lane_id();
+    v += lane_xor32(v, lane);
+    v += lane_xor16(v, lane);
+    v += __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x1F | (8 << 10)));
+    v += __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x1F | (4 << 10)));
+    v += QNE_DPP(v, kDppXor2);
+    v += QNE_DPP(v, kDppXor1);
+    return v;
+}
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
     for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, kWave));

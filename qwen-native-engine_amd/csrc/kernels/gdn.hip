@@ -16,6 +16,7 @@
 namespace qne {
 
 constexpr int kDK = 128, kDV = 128, kGdnThreads = 512;
+constexpr int kNT = 2;  // buffer cache policy: non-temporal (the state is streamed once per step)
 
 struct DeltaShared {
     float q[kDK], k[kDK], v[kDV];
@@ -32,17 +33,30 @@ struct DeltaShared {
 // single 512-byte read.
 // The decode step reads the value-major tile as 16-byte pieces in address order (piece f of the
 // tile: column f / 32, keys 4 (f % 32)..+3; each wave instruction one contiguous KiB) and keeps
-// them in that layout: thread t owns piece t + 512 r (r = 0..7).
+// them in that layout: thread t owns piece t + 512 r (r = 0..7). The pieces go through one buffer
+// resource (the tile's base in scalar registers, piece r at a scalar offset of 8 KiB r),
+// non-temporal: no 64-bit address per piece for the compiler to keep live, which holds the kernel
+// to 64 VGPRs, so four 8-wave workgroups fit a CU and a 64-sequence batch (1024 workgroups) runs
+// in one round.
 typedef float f4v __attribute__((ext_vector_type(4)));
-__device__ __forceinline__ void load_tile_t_issue(f4v (&v)[8], const float* S) {
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(float* S) {
+    return __builtin_amdgcn_make_buffer_rsrc(S, (short)0, kDK * kDV * 4, 0x00020000);
+}
+__device__ __forceinline__ void load_tile_rs(f4v (&v)[8], __amdgpu_buffer_rsrc_t rs) {
 #pragma unroll
-    for (int r = 0; r < 8; r++) v[r] = __builtin_nontemporal_load((const f4v*)S + threadIdx.x + kGdnThreads * r);
+    for (int r = 0; r < 8; r++)
+        v[r] = __builtin_bit_cast(f4v, __builtin_amdgcn_raw_buffer_load_b128(rs, 16 * threadIdx.x, 16 * kGdnThreads * r, kNT));
+}
+__device__ __forceinline__ void store_tile_rs(const f4v (&v)[8], __amdgpu_buffer_rsrc_t rs) {
+#pragma unroll
+    for (int r = 0; r < 8; r++)
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v[r]), rs, 16 * threadIdx.x, 16 * kGdnThreads * r, kNT);
 }
 
 // Model decode step for head blockIdx.x: conv + SiLU on the head's q, k, v channels, L2 norms,
 // gates, delta rule, gated RMSNorm (shaders.rs:436-520).
 // proj = [q(H*dk) k(H*dk) v(H*dv) z(H*dv) a(H) b(H)], prm = [dt_bias(H) A_neg_exp(H) norm_w(dv)].
-__global__ __launch_bounds__(kGdnThreads, 6) void k_gdn_decode(const float* __restrict__ proj, float* __restrict__ conv_state,
+__global__ __launch_bounds__(kGdnThreads, 8) void k_gdn_decode(const float* __restrict__ proj, float* __restrict__ conv_state,
                                                             const float* __restrict__ conv_w, float* __restrict__ state,
                                                             float* __restrict__ out, const float* __restrict__ prm, int H,
                                                             GdnRowStrides rs, GdnRowsIO io) {
@@ -82,7 +96,8 @@ __global__ __launch_bounds__(kGdnThreads, 6) void k_gdn_decode(const float* __re
         w0 = cw[0]; w1 = cw[1]; w2 = cw[2]; w3 = cw[3];
     }
     asm volatile("" ::: "memory");  // keeps the loads above ahead of the tile's
-    load_tile_t_issue(tv, S);  // in flight while the conv runs
+    const __amdgpu_buffer_rsrc_t trs = tile_rsrc(S);
+    load_tile_rs(tv, trs);  // in flight while the conv runs
     float inv = 1.0f;
     if (io.part) {
         // row_inv_rms: one chunk sum per thread (nchunks_in <= 256), the block sum in wave order
@@ -98,7 +113,7 @@ __global__ __launch_bounds__(kGdnThreads, 6) void k_gdn_decode(const float* __re
         st[0] = s1; st[1] = s2; st[2] = x;
         val = silu(y);
     }
-    const float ss = wave_sum(val * val);
+    const float ss = wave_sum_xor(val * val);
     if (lane == 0) sh.red[w] = ss;
     __syncthreads();
     if (t < 128) sh.q[t] = val * (1.0f / sqrtf(sh.red[0] + sh.red[1] + 1e-6f)) * 0.08838834764831845f;
@@ -114,7 +129,7 @@ __global__ __launch_bounds__(kGdnThreads, 6) void k_gdn_decode(const float* __re
     __syncthreads();
     if (w == 0) {
         float p = sh.k[lane] * sh.q[lane] + sh.k[lane + 64] * sh.q[lane + 64];
-        p = wave_sum(p);
+        p = wave_sum_xor(p);
         if (lane == 0) sh.kq = p;
     }
     __syncthreads();
@@ -144,13 +159,12 @@ __global__ __launch_bounds__(kGdnThreads, 6) void k_gdn_decode(const float* __re
             tv[r].w = fmaf(g, tv[r].w, d * k4.w);
             if ((t & 31) == 0) sh.o[c] = g * sq + d * kq;
         }
-#pragma unroll
-        for (int r = 0; r < 8; r++) __builtin_nontemporal_store(tv[r], (f4v*)S + t + kGdnThreads * r);
+        store_tile_rs(tv, trs);
     }
     __syncthreads();
     // gated RMSNorm over the head's dv outputs (threads 0..127 = waves 0 and 1, one column each)
     const float o = t < kDV ? sh.o[t] : 0.0f;
-    const float oo = wave_sum(o * o);
+    const float oo = wave_sum_xor(o * o);
     if (lane == 0) sh.red[w] = oo;
     __syncthreads();
     if (t < kDV) {
