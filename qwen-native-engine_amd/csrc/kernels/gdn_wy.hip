@@ -13,8 +13,9 @@
 // chunk at once and the chain over chunks is four small GEMMs per chunk.
 //
 // Design for gfx950:
-//  - k_wy_prep: one 256-thread workgroup per (sequence, head, chunk). K, Q, V of the chunk sit in
-//    LDS; K K^T and K Q^T run on v_mfma_f32_16x16x4f32 (only the lower-triangle tiles: each wave
+//  - k_wy_prep: one 256-thread workgroup per (sequence, head, chunk). K and Q of the chunk sit in
+//    LDS (A and T then take Q's place), V in registers, 66 KiB of LDS: two workgroups per CU;
+//    K K^T and K Q^T run on v_mfma_f32_16x16x4f32 (only the lower-triangle tiles: each wave
 //    gets five), T is inverted in 16 x 16 blocks (forward substitution on the diagonal blocks, MFMA
 //    for the rest), and U, W^T are again MFMA over the triangular T. The results are written
 //    in the exact register-fragment order in which the chain kernel feeds them to the MFMA.
@@ -43,7 +44,6 @@ using namespace lds_dma;
 constexpr int kC = 64;     // positions per chunk
 constexpr int kD = 128;    // dk = dv
 constexpr int kKS = 132;   // LDS row stride (floats) of K and Q: rows 16 apart x 4 columns on distinct banks
-constexpr int kVS = 144;   // LDS row stride of V: 4 rows x 16 columns on distinct banks
 constexpr int kAS = 68;    // LDS row stride of the A / T matrix
 // Per (sequence, head, chunk) workspace, in floats:
 //  Wf [pt 4][kt 8][lane 64][4]: -W[16pt + lane%16][16kt + 4(lane/16) + r]
@@ -70,8 +70,11 @@ __global__ __launch_bounds__(256) void k_wy_prep(const float* __restrict__ q, co
                                                  const float* __restrict__ v, const float* __restrict__ beta,
                                                  const float* __restrict__ g, float* __restrict__ ws, int T, int H) {
     __shared__ __attribute__((aligned(16))) float Ks[kC * kKS];
-    __shared__ __attribute__((aligned(16))) float Qs[kC * kVS];  // q (stride kKS), then v (stride kVS)
-    __shared__ __attribute__((aligned(16))) float As[kC * kAS];  // A, then T
+    // q, then A and T (stride kAS) once every wave has read q: 66 KiB in all, so two workgroups
+    // share a CU. V goes to registers instead (each lane's 32 values of its wave's U columns).
+    __shared__ __attribute__((aligned(16))) float Qs[kC * kKS];
+    float* const As = Qs;
+    static_assert(kAS <= kKS, "A / T fit the q buffer");
     __shared__ float Ls[kC], Bs[kC], BGs[kC], Ds[kC];
     const int c = blockIdx.x, h = blockIdx.y, b = blockIdx.z, NC = gridDim.x;
     const int t0 = c * kC, n = min(kC, T - t0);
@@ -116,6 +119,16 @@ __global__ __launch_bounds__(256) void k_wy_prep(const float* __restrict__ q, co
     }
     wait_vm<0>();  // this wave's K, Q rows
     __syncthreads();
+    // V for U (below): lane (lr, lg) of wave w takes V[4 s + lg][32 w + lr] and V[4 s + lg][32 w + 16 + lr],
+    // s = 0..15, loaded now and used after T is inverted
+    float vr0[16], vr1[16];
+#pragma unroll
+    for (int s = 0; s < 16; s++) {
+        const int p = 4 * s + lg;
+        const float* vp = v + (row0 + (size_t)min(p, n - 1) * H) * kD + 32 * w + lr;
+        vr0[s] = p < n ? vp[0] : 0.0f;
+        vr1[s] = p < n ? vp[16] : 0.0f;
+    }
 
     // K K^T tiles (w, t <= w) -> A;  K Q^T tiles (w, t >= w) -> P. Five tiles per wave.
     {
@@ -143,6 +156,7 @@ __global__ __launch_bounds__(256) void k_wy_prep(const float* __restrict__ q, co
 #pragma unroll
                 for (int x = 0; x < 5; x++) acc[x] = mfma4(a[j], bb[x][j], acc[x]);
         }
+        __syncthreads();  // every wave has read q: A overwrites it
 #pragma unroll
         for (int x = 0; x < 5; x++) {
             const int t = bt[x];
@@ -165,19 +179,7 @@ __global__ __launch_bounds__(256) void k_wy_prep(const float* __restrict__ q, co
             }
         }
     }
-    __syncthreads();  // Q is no longer read: V takes its place
-
-    // V rows into the freed buffer by LDS DMA (one row per instruction, 32 lanes), landing while T is
-    // inverted; padding rows are zeroed by plain stores
-#pragma unroll
-    for (int u = 0; u < kC / 4; u++) {
-        const int t = w * (kC / 4) + u;
-        if (t < n) {
-            if (lane < 32) dma16(v + (row0 + (size_t)t * H) * kD + 4 * lane, Qs + t * kVS);
-        } else if (lane < 32) {
-            *(f4*)(Qs + t * kVS + 4 * lane) = f4{0.0f, 0.0f, 0.0f, 0.0f};
-        }
-    }
+    __syncthreads();  // A is complete
 
     // T = (I + A)^-1 in 16 x 16 blocks (A_ij, T_ij: block row i, block column j).
     //  (1) T_ww = (I + A_ww)^-1 by forward substitution, wave w on diagonal block w: lane = (column
@@ -225,8 +227,7 @@ __global__ __launch_bounds__(256) void k_wy_prep(const float* __restrict__ q, co
         __syncthreads();
     }
 
-    wait_vm<0>();  // this wave's V rows (and its P stores)
-    __syncthreads();
+    wait_vm<0>();  // this wave's V values (and its P stores)
     // U (row tiles pt, column tiles cg = 2w, 2w + 1) and W^T (key tiles kt = 2w, 2w + 1, position
     // tiles pt) over the lower-triangular T: tile pt contracts positions < 16 (pt + 1).
 #pragma unroll
@@ -238,8 +239,8 @@ __global__ __launch_bounds__(256) void k_wy_prep(const float* __restrict__ q, co
             const int p = 4 * s + lg;
             const float tval = ta[4 * s];
             const float bv = Bs[p], bg = BGs[p];
-            u0 = mfma4(tval, bv * Qs[p * kVS + 16 * (2 * w) + lr], u0);
-            u1 = mfma4(tval, bv * Qs[p * kVS + 16 * (2 * w + 1) + lr], u1);
+            u0 = mfma4(tval, bv * vr0[s], u0);
+            u1 = mfma4(tval, bv * vr1[s], u1);
             // W^T[key][pos] = sum_p (beta gamma K)[p][key] T[pos][p]: A = (beta gamma K)^T, B = T^T
             w0 = mfma4(bg * Ks[p * kKS + 16 * (2 * w) + lr], tval, w0);
             w1 = mfma4(bg * Ks[p * kKS + 16 * (2 * w + 1) + lr], tval, w1);
