@@ -381,23 +381,25 @@ __global__ __launch_bounds__(384) void k_gdn_chunk_prep(const float* __restrict_
     }
 }
 
-// After the recurrence. Grid (ceil(T / 8), H), 384 threads, tokens 8 blockIdx.x .. + 7. Gated
+// After the recurrence. Grid (ceil(T / 8), H), 128 threads (one per value column), tokens
+// 8 blockIdx.x .. + 7: two waves a workgroup, so every workgroup of a 2048-token pass is resident at
+// once (the q, k, v channels of the conv-state shift are three per thread). Gated
 // RMSNorm of token n's head output (shaders.rs:514-516) into mixed + n * mixed_stride (when set)
 // and, with frag_out, staged as the out-projection's GEMM operand (column order order_out); the
 // workgroup of the last token also shifts the conv state by the chunk (the inputs of the chunk's
 // last three tokens).
-__global__ __launch_bounds__(384) void k_gdn_chunk_post(const float* __restrict__ proj, int proj_stride,
+__global__ __launch_bounds__(kDV) void k_gdn_chunk_post(const float* __restrict__ proj, int proj_stride,
                                                         float* __restrict__ conv_state, const float* __restrict__ prm,
                                                         int H, int T, const float* __restrict__ o,
                                                         float* __restrict__ mixed, int mixed_stride,
                                                         uint8_t* __restrict__ frag_out, int order_out) {
-    __shared__ float red[kChunkTok][8];
+    __shared__ float red[kChunkTok][2];
     const int n0 = blockIdx.x * kChunkTok, h = blockIdx.y, t = threadIdx.x, lane = t % kWave, w = t / kWave;
     float v[kChunkTok], z[kChunkTok];
 #pragma unroll
     for (int i = 0; i < kChunkTok; i++) {
         const int n = n0 + i;
-        const bool live = t < kDV && n < T;
+        const bool live = n < T;
         v[i] = live ? o[((size_t)n * H + h) * kDV + t] : 0.0f;
         z[i] = live ? proj[(size_t)n * proj_stride + 2 * H * kDK + H * kDV + h * kDV + t] : 0.0f;
     }
@@ -407,29 +409,35 @@ __global__ __launch_bounds__(384) void k_gdn_chunk_post(const float* __restrict_
         if (lane == 0) red[i][w] = ss;
     }
     __syncthreads();
-    if (t < kDV) {
 #pragma unroll
-        for (int i = 0; i < kChunkTok; i++) {
-            const int n = n0 + i;
-            if (n >= T) break;
-            const float inv = 1.0f / sqrtf((red[i][0] + red[i][1]) / (float)kDV + 1e-6f);
-            const float y = v[i] * inv * silu(z[i]) * prm[2 * H + t];
-            if (mixed) mixed[(size_t)n * mixed_stride + h * kDV + t] = y;
-            if (frag_out)  // waves 0 and 1: the two 64-column chunks of head h in row n
-                emit_x(frag_out, (size_t)(H * kDV / kChunk) * kChunkBytes, n, h * kDV + t, y, 1.0f, order_out, lane);
-        }
+    for (int i = 0; i < kChunkTok; i++) {
+        const int n = n0 + i;
+        if (n >= T) break;
+        const float inv = 1.0f / sqrtf((red[i][0] + red[i][1]) / (float)kDV + 1e-6f);
+        const float y = v[i] * inv * silu(z[i]) * prm[2 * H + t];
+        if (mixed) mixed[(size_t)n * mixed_stride + h * kDV + t] = y;
+        if (frag_out)  // the two waves: the two 64-column chunks of head h in row n
+            emit_x(frag_out, (size_t)(H * kDV / kChunk) * kChunkBytes, n, h * kDV + t, y, 1.0f, order_out, lane);
     }
     if (n0 <= T - 1 && T - 1 < n0 + kChunkTok) {
-        const int ch = t < 128 ? h * kDK + t : (t < 256 ? H * kDK + h * kDK + (t - 128) : 2 * H * kDK + h * kDV + (t - 256));
-        float* st = conv_state + (size_t)ch * 4;
-        float in[3];
+        // channels q t, k t, v t of head h
+        const int chs[3] = {h * kDK + t, H * kDK + h * kDK + t, 2 * H * kDK + h * kDV + t};
+        float in[3][3];
 #pragma unroll
-        for (int j = 0; j < 3; j++) {
-            const int m = T - 3 + j;
-            in[j] = m >= 0 ? proj[(size_t)m * proj_stride + ch] : st[3 + m];
+        for (int u = 0; u < 3; u++) {
+            const float* st = conv_state + (size_t)chs[u] * 4;
+#pragma unroll
+            for (int j = 0; j < 3; j++) {
+                const int m = T - 3 + j;
+                in[u][j] = m >= 0 ? proj[(size_t)m * proj_stride + chs[u]] : st[3 + m];
+            }
         }
 #pragma unroll
-        for (int j = 0; j < 3; j++) st[j] = in[j];
+        for (int u = 0; u < 3; u++) {
+            float* st = conv_state + (size_t)chs[u] * 4;
+#pragma unroll
+            for (int j = 0; j < 3; j++) st[j] = in[u][j];
+        }
     }
 }
 
@@ -456,7 +464,7 @@ void launch_gdn_chunk(const float* proj, int proj_stride, float* conv_state, con
         launch_delta_rule_wy(q + head * hk, k + head * hk, v + head * hk, beta + (size_t)head * heads,
                              g + (size_t)head * heads, state, o + head * hk, 1, 64 * blocks, heads, wy_ws, st, 1);
     sequential(head + 64 * blocks, tokens - head - 64 * blocks);
-    hipLaunchKernelGGL(k_gdn_chunk_post, dim3(tb, heads), dim3(384), 0, st, proj, proj_stride, conv_state, prm,
+    hipLaunchKernelGGL(k_gdn_chunk_post, dim3(tb, heads), dim3(kDV), 0, st, proj, proj_stride, conv_state, prm,
                        heads, tokens, o, mixed, mixed_stride, frag_out, order_out);
 }
 
