@@ -326,22 +326,25 @@ __global__ __launch_bounds__(256) void k_delta_rule_cols(const float* __restrict
 // channel's inputs are loaded once each (plus three), and their loads are all in flight at once.
 constexpr int kChunkTok = 8;
 
-// Prefill of a chunk of T tokens of one sequence, before the recurrence. Grid (ceil(T / 8), H),
-// 384 threads (the head's q, k, v channels), tokens 8 blockIdx.x .. + 7. Token n's projection row
-// is proj + n * proj_stride. Causal conv + SiLU (shaders.rs:457-468) with the inputs of tokens
-// n-3..n-1 taken from the chunk or, before it, from conv_state (read only; k_gdn_chunk_post shifts
-// it); L2 norms of q (times 128^-1/2) and k; g = exp(A_neg_exp ln(1 + e^(a + dt_bias))),
-// beta = sigmoid(b) (:489-496). Outputs in the layouts of k_delta_rule_cols: q, k [T][H][dk],
-// v [T][H][dv], g, beta [T][H]. Each token's arithmetic is that of one token per workgroup.
-__global__ __launch_bounds__(384) void k_gdn_chunk_prep(const float* __restrict__ proj, int proj_stride,
+// Prefill of a chunk of T tokens of one sequence, before the recurrence. Grid (ceil(T / 8), H, 3),
+// 128 threads: workgroup (x, h, z) takes tokens 8 x .. + 7 of head h's q (z = 0), k (1) or v (2)
+// channels, one per thread, so a 2048-token pass's 12288 two-wave workgroups run in three full
+// rounds. Token n's projection row is proj + n * proj_stride. Causal conv + SiLU
+// (shaders.rs:457-468) with the inputs of tokens n-3..n-1 taken from the chunk or, before it, from
+// conv_state (read only; k_gdn_chunk_post shifts it); L2 norms of q (times 128^-1/2) and k; the q
+// workgroup also computes g = exp(A_neg_exp ln(1 + e^(a + dt_bias))), beta = sigmoid(b)
+// (:489-496). Outputs in the layouts of k_delta_rule_cols: q, k [T][H][dk], v [T][H][dv], g, beta
+// [T][H]. Each token's arithmetic is that of one token per workgroup.
+__global__ __launch_bounds__(kDK) void k_gdn_chunk_prep(const float* __restrict__ proj, int proj_stride,
                                                         const float* __restrict__ conv_state,
                                                         const float* __restrict__ conv_w, const float* __restrict__ prm,
                                                         int H, int T, float* __restrict__ qo, float* __restrict__ ko,
                                                         float* __restrict__ vo, float* __restrict__ go,
                                                         float* __restrict__ bo) {
-    __shared__ float red[kChunkTok][8];
-    const int n0 = blockIdx.x * kChunkTok, h = blockIdx.y, t = threadIdx.x, lane = t % kWave, w = t / kWave;
-    const int ch = t < 128 ? h * kDK + t : (t < 256 ? H * kDK + h * kDK + (t - 128) : 2 * H * kDK + h * kDV + (t - 256));
+    __shared__ float red[kChunkTok][2];
+    const int n0 = blockIdx.x * kChunkTok, h = blockIdx.y, z = blockIdx.z, t = threadIdx.x, lane = t % kWave,
+              w = t / kWave;
+    const int ch = z == 0 ? h * kDK + t : (z == 1 ? H * kDK + h * kDK + t : 2 * H * kDK + h * kDV + t);
     const float* st = conv_state + (size_t)ch * 4;
     const float* cw = conv_w + (size_t)ch * 4;
     // inputs of tokens n0 - 3 .. n0 + 7 (before the chunk: the conv state; past T: unused)
@@ -357,8 +360,10 @@ __global__ __launch_bounds__(384) void k_gdn_chunk_prep(const float* __restrict_
     for (int i = 0; i < kChunkTok; i++) {
         const float y = in[i] * w0 + in[i + 1] * w1 + in[i + 2] * w2 + in[i + 3] * w3;
         val[i] = silu(y);
-        const float ss = wave_sum(val[i] * val[i]);
-        if (lane == 0) red[i][w] = ss;
+        if (z < 2) {
+            const float ss = wave_sum(val[i] * val[i]);
+            if (lane == 0) red[i][w] = ss;
+        }
     }
     __syncthreads();
 #pragma unroll
@@ -366,11 +371,11 @@ __global__ __launch_bounds__(384) void k_gdn_chunk_prep(const float* __restrict_
         const int n = n0 + i;
         if (n >= T) break;
         const size_t nh = (size_t)n * H + h;
-        if (t < 128) qo[nh * kDK + t] = val[i] * (1.0f / sqrtf(red[i][0] + red[i][1] + 1e-6f)) * 0.08838834764831845f;
-        else if (t < 256) ko[nh * kDK + t - 128] = val[i] * (1.0f / sqrtf(red[i][2] + red[i][3] + 1e-6f));
-        else vo[nh * kDV + t - 256] = val[i];
+        if (z == 0) qo[nh * kDK + t] = val[i] * (1.0f / sqrtf(red[i][0] + red[i][1] + 1e-6f)) * 0.08838834764831845f;
+        else if (z == 1) ko[nh * kDK + t] = val[i] * (1.0f / sqrtf(red[i][0] + red[i][1] + 1e-6f));
+        else vo[nh * kDV + t] = val[i];
     }
-    if (t < kChunkTok && n0 + t < T) {
+    if (z == 0 && t < kChunkTok && n0 + t < T) {
         const int n = n0 + t;
         const size_t nh = (size_t)n * H + h;
         const float* row = proj + (size_t)n * proj_stride;
@@ -446,7 +451,7 @@ void launch_gdn_chunk(const float* proj, int proj_stride, float* conv_state, con
                       float* o, float* mixed, int mixed_stride, hipStream_t st, int lead, float* wy_ws,
                       uint8_t* frag_out, int order_out) {
     const int tb = (tokens + kChunkTok - 1) / kChunkTok;
-    hipLaunchKernelGGL(k_gdn_chunk_prep, dim3(tb, heads), dim3(384), 0, st, proj, proj_stride, conv_state, conv_w,
+    hipLaunchKernelGGL(k_gdn_chunk_prep, dim3(tb, heads, 3), dim3(kDK), 0, st, proj, proj_stride, conv_state, conv_w,
                        prm, heads, tokens, q, k, v, g, beta);
     const int waves = heads * (kDV / 4);
     const size_t hk = (size_t)heads * kDK;  // floats of q, k, v, o per token
